@@ -1,0 +1,406 @@
+"""Prefix KV cache, step functions and the Fast-dLLM v2 decode loop over the HIP function table.
+
+Mirror of fast_dllm_relax/runtime.py with ``vm`` a ``HipVM``: the same names, arguments, cache
+contract, window checks and exceptions, so the reference's loop reads the same here.
+  PrefixCache / allocate_prefix_cache / _check_write        runtime.py:196-263
+  build_prefix_cache_from_ids / _prefill / _embed            runtime.py:266-330
+  _forward_cached                                            runtime.py:333-343
+  shifted_confidence                                         runtime.py:158-181 (device confidence path)
+  score_active_block_cached_fast / _refine / _partial        runtime.py:346-436
+  score_sequence_block / score_masked_continuation           runtime.py:439-588
+  relax_greedy_generate                                      runtime.py:591-880
+Differences: prefill passes no host-built bias (the kernels apply the same block-causal rule
+arithmetically, build_prefix_block_attention_bias semantics, cuda.py:148-177); the cached-step
+confidence always runs on the device (fused lm_head + argmax + max-softmax), reading back 2 x rows values.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import time
+from typing import Any
+
+import numpy as np
+import torch
+
+from .vm import HipVM
+
+
+@dataclasses.dataclass(frozen=True)
+class CacheSpec:
+    num_layers: int
+    num_kv_heads: int
+    head_dim: int
+    dtype: str
+
+
+def cache_spec_of(vm: HipVM) -> CacheSpec:
+    c = vm.cfg
+    return CacheSpec(c.num_hidden_layers, c.num_key_value_heads, c.head_dim, vm.dtype)
+
+
+@dataclasses.dataclass
+class PrefixCache:
+    """In-place KV cache of one sequence: k / v [num_layers, 1, capacity, num_kv_heads, head_dim].
+    Rows [0, prefix_len) hold the committed prefix and are never rewritten."""
+
+    k: torch.Tensor
+    v: torch.Tensor
+    prefix_len: int
+    spec: CacheSpec
+
+    @property
+    def capacity(self) -> int:
+        return int(self.k.shape[2])
+
+    def commit(self, rows: int) -> None:
+        if self.prefix_len + rows > self.capacity:
+            raise ValueError(f"commit past capacity: {self.prefix_len} + {rows} > {self.capacity}")
+        self.prefix_len += rows
+
+    def ensure_capacity(self, rows: int, dev: Any = None) -> None:
+        """Grow (reallocate, copy the committed rows) so that ``rows`` rows fit."""
+        if rows <= self.capacity:
+            return
+        bigger = allocate_prefix_cache(self.spec, self.k.device, rows)
+        bigger.k[:, :, :self.prefix_len].copy_(self.k[:, :, :self.prefix_len])
+        bigger.v[:, :, :self.prefix_len].copy_(self.v[:, :, :self.prefix_len])
+        self.k, self.v = bigger.k, bigger.v
+
+
+def allocate_prefix_cache(spec: CacheSpec, dev: Any, rows: int, *, block_size: int = 32) -> PrefixCache:
+    """An empty PrefixCache with capacity ``rows`` rounded up to a multiple of block_size."""
+    from .params import TORCH_DTYPES
+
+    capacity = -(-max(int(rows), 1) // block_size) * block_size
+    shape = (spec.num_layers, 1, capacity, spec.num_kv_heads, spec.head_dim)
+    td = TORCH_DTYPES[spec.dtype]
+    return PrefixCache(k=torch.empty(shape, dtype=td, device=dev), v=torch.empty(shape, dtype=td, device=dev),
+                       prefix_len=0, spec=spec)
+
+
+def _check_write(cache: PrefixCache, write_start: int, attend_len: int) -> None:
+    if write_start < cache.prefix_len:
+        raise ValueError(f"KV write at row {write_start} would overwrite the committed prefix [0, {cache.prefix_len})")
+    if attend_len > cache.capacity:
+        raise ValueError(f"cached call needs {attend_len} rows; cache capacity is {cache.capacity}")
+
+
+def _ids_tensor(vm: HipVM, ids) -> torch.Tensor:
+    arr = np.asarray(ids, dtype=np.int64)
+    if arr.size and (arr.min() < 0 or arr.max() >= vm.cfg.vocab_size):
+        raise ValueError(f"token id out of range [0, {vm.cfg.vocab_size})")
+    return torch.from_numpy(arr.astype(np.int32)).pin_memory().to("cuda", non_blocking=True)
+
+
+def _embed(vm: HipVM, ids) -> torch.Tensor:
+    """vm.embed of ``ids`` reshaped to [1, len(ids), hidden] (runtime.py:326-330)."""
+    return vm.embed_unchecked(_ids_tensor(vm, ids))[None]
+
+
+def _offset_tensor(value: int) -> torch.Tensor:
+    return torch.tensor(int(value), dtype=torch.int32).pin_memory().to("cuda", non_blocking=True)
+
+
+def build_prefix_cache_from_ids(vm: HipVM, prefix_ids, *, block_size: int, cache_spec: CacheSpec | None = None,
+                                capacity: int | None = None, chunked_prefill: bool = False) -> PrefixCache:
+    spec = cache_spec or cache_spec_of(vm)
+    prefix_len = len(prefix_ids)
+    cache = allocate_prefix_cache(spec, "cuda", max(prefix_len, capacity or 0), block_size=block_size)
+    if prefix_len == 0:
+        return cache
+    if chunked_prefill and prefix_len > block_size:
+        if prefix_len % block_size != 0:
+            raise ValueError(f"chunked_prefill requires a block-aligned prefix; got {prefix_len} tokens "
+                             f"with block_size={block_size}.")
+        _prefill(vm, list(prefix_ids[:block_size]), cache)
+        for start in range(block_size, prefix_len, block_size):
+            _forward_cached(vm, list(prefix_ids[start:start + block_size]), cache)
+            cache.commit(block_size)
+        return cache
+    _prefill(vm, list(prefix_ids), cache)
+    return cache
+
+
+def _prefill(vm: HipVM, prefix_ids, cache: PrefixCache) -> None:
+    if cache.prefix_len != 0:
+        raise ValueError("build_prefix_cache writes from row 0; the cache already has a prefix")
+    _check_write(cache, 0, len(prefix_ids))
+    vm.build_prefix_cache(_embed(vm, prefix_ids), None, cache.k, cache.v)
+    cache.commit(len(prefix_ids))
+
+
+def _forward_cached(vm: HipVM, active_ids, cache: PrefixCache) -> torch.Tensor:
+    _check_write(cache, cache.prefix_len, cache.prefix_len + len(active_ids))
+    return vm.forward_cached(_embed(vm, active_ids), cache.k, cache.v, _offset_tensor(cache.prefix_len),
+                             cache.prefix_len)
+
+
+def shifted_confidence(vm: HipVM, hidden: torch.Tensor) -> tuple[np.ndarray, np.ndarray, int]:
+    """(shifted ids [rows] int64, shifted max probs [rows] fp32, unshifted last-row argmax).
+
+    Device path of runtime.py:168-174: the fused lm_head + confidence kernel reduces the logits, only
+    2 x rows values come back."""
+    ids_d, maxp_d = vm.get_confidence(hidden)
+    both = torch.cat([ids_d.view(torch.float32), maxp_d], dim=1).cpu().numpy()[0]
+    rows = ids_d.shape[1]
+    ids = both[:rows].view(np.int32).astype(np.int64)
+    maxp = both[rows:].astype(np.float32)
+    return np.concatenate([ids[:1], ids[:-1]]), np.concatenate([maxp[:1], maxp[:-1]]), int(ids[-1])
+
+
+def score_active_block_cached_fast(vm: HipVM, active_ids, prefix_cache: PrefixCache):
+    hidden = _forward_cached(vm, active_ids, prefix_cache)
+    prefix_cache.commit(len(active_ids))
+    ids, probs, last = shifted_confidence(vm, hidden)
+    return ids, probs, last, prefix_cache
+
+
+def score_active_block_refine(vm: HipVM, active_ids, prefix_cache: PrefixCache):
+    ids, probs, _ = shifted_confidence(vm, _forward_cached(vm, active_ids, prefix_cache))
+    return ids, probs
+
+
+def score_active_block_partial_perlayer(vm: HipVM, small_block_ids, prefix_cache: PrefixCache,
+                                        replace_position: int, *, block_size: int):
+    write_start = prefix_cache.prefix_len + replace_position
+    _check_write(prefix_cache, write_start, prefix_cache.prefix_len + block_size)
+    fn = vm[f"forward_block_partial_rp{replace_position}"]
+    hidden = fn(_embed(vm, small_block_ids), prefix_cache.k, prefix_cache.v, _offset_tensor(write_start),
+                prefix_cache.prefix_len)
+    ids, probs, _ = shifted_confidence(vm, hidden)
+    return ids, probs
+
+
+def build_prefix_block_attention_bias(prefix_len: int, block_len: int, *, block_size: int | None = None,
+                                      blocked_value: float = -1e9) -> np.ndarray:
+    """[1, 1, T, T] block-causal bias (cuda.py:148-177)."""
+    if prefix_len < 0:
+        raise ValueError("prefix_len must be non-negative")
+    if block_len <= 0:
+        raise ValueError("block_len must be positive")
+    total = prefix_len + block_len
+    bs = block_len if block_size is None else int(block_size)
+    if bs <= 0:
+        raise ValueError("block_size must be positive when provided")
+    pos = np.arange(total, dtype=np.int32)
+    allowed = (pos[:, None] // bs) >= (pos[None, :] // bs)
+    return np.where(allowed, 0.0, blocked_value).astype(np.float32)[None, None]
+
+
+def extract_shifted_block_logits(logits, *, prefix_len: int, block_len: int):
+    """Position i is predicted from logits at i-1 (cuda.py:180-204)."""
+    if logits.ndim != 3:
+        raise ValueError(f"Expected logits to have rank 3, got shape {tuple(logits.shape)}")
+    if block_len <= 0:
+        raise ValueError("block_len must be positive")
+    if prefix_len + block_len > logits.shape[1]:
+        raise ValueError(f"Requested prefix_len={prefix_len} and block_len={block_len} "
+                         f"for logits of length {logits.shape[1]}")
+    src = ([prefix_len - 1] + list(range(prefix_len, prefix_len + block_len - 1)) if prefix_len > 0
+           else [0] + list(range(0, block_len - 1)))
+    return logits[:, src, :]
+
+
+def score_sequence_block(vm: HipVM, sequence_ids, *, block_size: int):
+    """Raw active-block logits and shifted block logits of a token sequence (runtime.py:439-482),
+    as host numpy arrays."""
+    if len(sequence_ids) <= block_size:
+        prefix_ids, active = [], list(sequence_ids)
+    else:
+        plen = ((len(sequence_ids) - 1) // block_size) * block_size
+        prefix_ids, active = list(sequence_ids[:plen]), list(sequence_ids[plen:])
+    bias = torch.from_numpy(build_prefix_block_attention_bias(len(prefix_ids), len(active),
+                                                              block_size=block_size)).cuda()
+    hidden = vm.forward_hidden(_embed(vm, prefix_ids + active), bias)
+    logits = vm.get_logits(hidden).cpu().numpy()
+    cur = logits[:, -len(active):, :]
+    shifted = extract_shifted_block_logits(logits, prefix_len=len(prefix_ids), block_len=len(active))
+    return cur, shifted
+
+
+def score_masked_continuation(vm: HipVM, prefix_ids, continuation_ids, *, block_size: int, mask_id: int,
+                              eos_token_id: int | None = None, cached_prefix=None, chunked_prefill: bool = False):
+    """Masked-continuation scoring (runtime.py:485-588): returns (logits [len(cont), vocab] numpy,
+    (aligned prefix ids, PrefixCache) or None)."""
+    if not continuation_ids:
+        return np.empty((0, 0), dtype=np.float32), cached_prefix
+    pcl = (len(prefix_ids) // block_size) * block_size
+    if pcl == 0:
+        seq = list(prefix_ids) + [mask_id] * len(continuation_ids)
+        _, shifted = score_sequence_block(vm, seq, block_size=block_size)
+        return shifted[0, -len(continuation_ids):, :], None
+    aligned = list(prefix_ids[:pcl])
+    tail_rows = max(len(prefix_ids) - pcl + len(continuation_ids), block_size)
+    if cached_prefix is not None and cached_prefix[0] == aligned:
+        cache = cached_prefix[1]
+        cache.ensure_capacity(pcl + tail_rows)
+    else:
+        cache = build_prefix_cache_from_ids(vm, aligned, block_size=block_size, capacity=pcl + tail_rows,
+                                            chunked_prefill=chunked_prefill)
+    real = list(prefix_ids[cache.prefix_len:])
+    active = real + [mask_id] * len(continuation_ids)
+    if len(active) <= block_size:
+        pad = block_size - len(active)
+        if pad:
+            active = active + [mask_id] * pad
+            if eos_token_id is not None:
+                active[len(real) + len(continuation_ids)] = eos_token_id
+    hidden = _forward_cached(vm, active, cache)
+    logits = vm.get_logits(hidden)
+    shifted = torch.cat([logits[:, :1, :], logits[:, :-1, :]], dim=1)
+    end = len(real) + len(continuation_ids)
+    return shifted[0, len(real):end, :].cpu().numpy(), (aligned, cache)
+
+
+def relax_greedy_generate(vm: HipVM, prompt_token_ids, *, max_new_tokens: int, block_size: int = 32,
+                          small_block_size: int = 8, threshold: float = 0.9, temperature: float = 0.0,
+                          top_p: float = 0.95, use_block_cache: bool = True, mask_id: int,
+                          stop_token: int | None, timing: dict | None = None, chunked_prefill: bool = False,
+                          trace: list | None = None):
+    """Fast-dLLM v2 block-diffusion generation (runtime.py:591-880), temperature 0.
+
+    ``trace`` (optional) receives one tuple per model call, as oracle.runtime.greedy_generate logs."""
+    if temperature != 0.0:
+        raise NotImplementedError("Fast-dLLM Relax runner currently supports only temperature=0.")
+    if top_p <= 0:
+        raise ValueError("top_p must be positive.")
+    if max_new_tokens < 0:
+        raise ValueError("max_new_tokens must be non-negative.")
+    if block_size <= 0 or small_block_size <= 0:
+        raise ValueError("block_size and small_block_size must be positive.")
+
+    t_start = time.perf_counter()
+    prefill_recorded = False
+    generated = list(prompt_token_ids)
+    plen0 = len(generated)
+    unmask_updates = block_recomputes = partial_recomputes = block_appends = 0
+    prefix_cache: PrefixCache | None = None
+    block_kv_valid = False
+    capacity = -(-(plen0 + max_new_tokens) // block_size) * block_size + block_size
+
+    def has_completed_stop(seq, plen):
+        if stop_token is None:
+            return False
+        suffix = seq[plen:]
+        if stop_token not in suffix:
+            return False
+        return mask_id not in suffix[:suffix.index(stop_token)]
+
+    def make_continuation(tokens):
+        raw = tokens[plen0:plen0 + max_new_tokens]
+        first = next((i for i, t in enumerate(raw) if t == mask_id), len(raw))
+        return raw[:first]
+
+    def stats():
+        return {"unmask_updates": unmask_updates, "block_recomputes": block_recomputes,
+                "partial_recomputes": partial_recomputes, "block_appends": block_appends}
+
+    def log(*item):
+        if trace is not None:
+            trace.append(item)
+
+    if plen0 % block_size == 0 and plen0 > 0 and max_new_tokens > 0:
+        last_start = plen0 - block_size
+        prefix_cache = build_prefix_cache_from_ids(vm, generated[:last_start], block_size=block_size,
+                                                   capacity=capacity, chunked_prefill=chunked_prefill)
+        _, _, nxt, prefix_cache = score_active_block_cached_fast(vm, generated[last_start:], prefix_cache)
+        log("append", prefix_cache.prefix_len, nxt)
+        block_recomputes += 1
+        block_appends += 1
+        generated.append(nxt)
+        if stop_token is not None and nxt == int(stop_token):
+            if timing is not None:
+                timing["prefill_latency_s"] = time.perf_counter() - t_start
+            return make_continuation(generated), stats()
+
+    while len(generated) - plen0 < max_new_tokens:
+        prompt_length = len(generated)
+        x_t = generated + [mask_id] * (block_size - prompt_length % block_size)
+        a0 = len(x_t) - block_size
+        if a0 == 0:
+            use_cache = False
+        else:
+            use_cache = True
+            if a0 != (prefix_cache.prefix_len if prefix_cache is not None else 0):
+                prefix_cache = build_prefix_cache_from_ids(vm, x_t[:a0], block_size=block_size, capacity=capacity,
+                                                           chunked_prefill=chunked_prefill)
+                block_kv_valid = False
+        if not prefill_recorded:
+            if timing is not None:
+                torch.cuda.synchronize()
+                timing["prefill_latency_s"] = time.perf_counter() - t_start
+            prefill_recorded = True
+
+        for s0 in range(0, block_size, small_block_size):
+            s1 = min(block_size, s0 + small_block_size)
+            while True:
+                local = [i for i, t in enumerate(x_t[a0 + s0:a0 + s1]) if t == mask_id]
+                if not local:
+                    break
+                if has_completed_stop(x_t, prompt_length):
+                    return make_continuation(x_t), stats()
+                if use_cache:
+                    use_partial = use_block_cache and block_kv_valid and x_t[a0 + s0] != mask_id
+                    if use_partial:
+                        ids, probs = score_active_block_partial_perlayer(vm, x_t[a0 + s0:a0 + s1], prefix_cache,
+                                                                         s0, block_size=block_size)
+                    else:
+                        ids, probs = score_active_block_refine(vm, x_t[a0:], prefix_cache)
+                        block_kv_valid = use_block_cache
+                    block_recomputes += 1
+                    if use_partial:
+                        partial_recomputes += 1
+                    bids = ids if use_partial else ids[s0:s1]
+                    bp = probs if use_partial else probs[s0:s1]
+                    rows = [r for r in local if bp[r] > threshold]
+                    if not rows:
+                        rows = [local[int(np.argmax([bp[r] for r in local]))]]
+                    for r in rows:
+                        x_t[a0 + s0 + r] = int(bids[r])
+                        unmask_updates += 1
+                    log("partial" if use_partial else "full", s0, tuple(rows), tuple(int(bids[r]) for r in rows))
+                else:
+                    _, shifted = score_sequence_block(vm, x_t, block_size=block_size)
+                    block_recomputes += 1
+                    small = shifted[:, s0:s1, :][0]
+                    chosen = small.argmax(axis=-1)
+                    cp = np.empty(small.shape[0], dtype=np.float64)
+                    for r in range(small.shape[0]):
+                        z = small[r].astype(np.float64)
+                        e = np.exp(z - z.max())
+                        cp[r] = e[chosen[r]] / e.sum()
+                    gated = np.full_like(cp, -np.inf, dtype=np.float64)
+                    for r in local:
+                        gated[r] = cp[r]
+                    rows = [r for r in local if gated[r] > threshold]
+                    if not rows:
+                        rows = [int(np.argmax(gated))]
+                    for r in rows:
+                        x_t[a0 + s0 + r] = int(chosen[r])
+                        unmask_updates += 1
+                    log("stateless", s0, tuple(rows), tuple(int(chosen[r]) for r in rows))
+                if len(x_t) - plen0 >= max_new_tokens:
+                    break
+            if len(x_t) - plen0 >= max_new_tokens:
+                break
+
+        generated = x_t
+        if len(generated) - plen0 >= max_new_tokens:
+            break
+        if has_completed_stop(generated, plen0):
+            break
+        if use_cache:
+            _, _, nxt, prefix_cache = score_active_block_cached_fast(vm, generated[a0:], prefix_cache)
+            block_kv_valid = False
+        else:
+            cur, _ = score_sequence_block(vm, generated, block_size=block_size)
+            nxt = int(cur[0, -1, :].argmax())
+        log("append", prefix_cache.prefix_len if use_cache else 0, nxt)
+        block_recomputes += 1
+        generated.append(nxt)
+        block_appends += 1
+        if stop_token is not None and nxt == int(stop_token):
+            break
+
+    return make_continuation(generated), stats()

@@ -1,0 +1,131 @@
+/* C ABI of the MI355X-native cached block-diffusion step (libfdllm.so).
+ *
+ * Replaces the reference's TVM Relax VM function table for Fast-dLLM v2: the artifact exposes
+ * REQUIRED_FNS (fast_dllm_relax/export_utils.py:13-17), called as vm["name"](..., params) by
+ * fast_dllm_relax/runtime.py.  Every entry point below keeps the argument meaning, shapes and error
+ * behaviour of the reference function it names; shapes are passed as plain ints and tensors as device
+ * pointers (the caller owns every buffer; the KV caches are mutated in place, as in the reference).
+ *
+ * Conventions
+ *   - All pointers are device pointers unless stated; `stream` is a hipStream_t (NULL = default).
+ *   - Activations/weights/caches are in the context's dtype (bf16 or fp16, 2-byte elements);
+ *     logits are fp32; token ids are int32.
+ *   - KV caches: [num_layers, 1, cap, num_kv_heads, head_dim] rows (contract "inplace_bsnh_v1",
+ *     export_utils.py:21-34).
+ *   - Return value: 0 on success; FDLLM_EINVAL for a rejected argument (the reference raises
+ *     ValueError / a VM shape error); FDLLM_EHIP for a HIP runtime failure; FDLLM_ESTATE when weights
+ *     are not bound.  fdllm_last_error() returns this thread's message for the last failure.
+ *   - All work is enqueued on `stream`; nothing synchronises the host unless stated.  One context
+ *     per stream; a context is not thread-safe.
+ */
+#ifndef FDLLM_H
+#define FDLLM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FDLLM_OK 0
+#define FDLLM_EINVAL 1
+#define FDLLM_EHIP 2
+#define FDLLM_ESTATE 3
+
+#define FDLLM_DTYPE_BF16 0
+#define FDLLM_DTYPE_F16 1
+
+typedef struct fdllm_ctx fdllm_ctx;
+
+/* Model constants; mirror of FastDLLMRelaxConfig (fast_dllm_relax/model/cuda.py:15-29). */
+typedef struct fdllm_config {
+  int32_t vocab_size;
+  int32_t hidden_size;
+  int32_t intermediate_size;
+  int32_t num_hidden_layers;
+  int32_t num_attention_heads;
+  int32_t num_key_value_heads;
+  int32_t head_dim;            /* 128 for the HIP attention kernel */
+  float rms_norm_eps;
+  float rope_theta;
+  int32_t tie_word_embeddings;
+  int32_t bd_size;             /* block size (32); partial steps use bd_size / 4 rows */
+  int32_t dtype;               /* FDLLM_DTYPE_* */
+  int32_t max_rows;            /* rows the workspace is sized for at creation (grown on demand) */
+} fdllm_config;
+
+/* Replaces tvm.relax.VirtualMachine(load_module(...)) (fast_dllm_relax/runners.py:614-615). */
+int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out);
+void fdllm_destroy(fdllm_ctx* ctx);
+
+/* Number of packed parameters and their names, in param_names.txt order
+ * (fast_dllm_relax/runners.py:947-972; 198 for the tied 1.5B model). */
+int fdllm_num_params(const fdllm_ctx* ctx);
+const char* fdllm_param_name(const fdllm_ctx* ctx, int index);
+
+/* Binds the packed `params` list (cuda.py:807, "param_mode": "packed"): n device pointers in
+ * fdllm_param_name order.  The caller keeps them alive while the context uses them. */
+int fdllm_bind_weights(fdllm_ctx* ctx, const void* const* ptrs, int n);
+
+/* embed (cuda.py:698-699): ids [seq_len] int32 -> out [seq_len, hidden]. */
+int fdllm_embed(fdllm_ctx* ctx, const int32_t* ids, int seq_len, void* out, void* stream);
+
+/* forward_hidden (cuda.py:604-608, 701-702): stateless forward of [1, seq_len, hidden] with the
+ * additive attention bias [1, 1, seq_len, seq_len] fp32; bias == NULL means the block-causal bias of
+ * build_prefix_block_attention_bias(0, seq_len, block_size=bd_size) (cuda.py:148-177). */
+int fdllm_forward_hidden(fdllm_ctx* ctx, const void* input_embed, int seq_len, const float* attention_bias,
+                         void* out, void* stream);
+
+/* get_logits (cuda.py:704-711): hidden [rows, hidden] -> logits [rows, vocab] fp32 (rounded to the
+ * model dtype first, as the reference's model-dtype GEMM output is). */
+int fdllm_get_logits(fdllm_ctx* ctx, const void* hidden, int rows, float* logits, void* stream);
+
+/* build_prefix_cache (cuda.py:610-637, 713-721): writes rows [0, prefix_len) of every layer of the
+ * caches in place; prefix_bias as in fdllm_forward_hidden (NULL = block-causal). */
+int fdllm_build_prefix_cache(fdllm_ctx* ctx, const void* prefix_embed, int prefix_len, const float* prefix_bias,
+                             void* k_cache, void* v_cache, int cap, void* stream);
+
+/* forward_cached (cuda.py:723-738, 639-666 with fast_dllm.attn_inplace, runtime.py:63-73): writes the
+ * block's K/V at rows [prefix_len, prefix_len + block_len) and attends over [0, prefix_len + block_len).
+ * cache_offset: device int32 scalar, RoPE position of row 0.  out [block_len, hidden]. */
+int fdllm_forward_cached(fdllm_ctx* ctx, const void* active_embed, int block_len, void* k_cache, void* v_cache,
+                         int cap, const int32_t* cache_offset, int64_t prefix_len, void* out, void* stream);
+
+/* forward_block_partial_rp{0,8,16,24} (cuda.py:740-788): bd_size/4 rows written at
+ * [prefix_len + rp, + bd_size/4), attending over [0, prefix_len + bd_size). */
+int fdllm_forward_block_partial(fdllm_ctx* ctx, int replace_position, const void* active_embed, int rows,
+                                void* k_cache, void* v_cache, int cap, const int32_t* cache_offset,
+                                int64_t prefix_len, void* out, void* stream);
+int fdllm_forward_block_partial_rp0(fdllm_ctx* ctx, const void* active_embed, int rows, void* k_cache,
+                                    void* v_cache, int cap, const int32_t* cache_offset, int64_t prefix_len,
+                                    void* out, void* stream);
+int fdllm_forward_block_partial_rp8(fdllm_ctx* ctx, const void* active_embed, int rows, void* k_cache,
+                                    void* v_cache, int cap, const int32_t* cache_offset, int64_t prefix_len,
+                                    void* out, void* stream);
+int fdllm_forward_block_partial_rp16(fdllm_ctx* ctx, const void* active_embed, int rows, void* k_cache,
+                                     void* v_cache, int cap, const int32_t* cache_offset, int64_t prefix_len,
+                                     void* out, void* stream);
+int fdllm_forward_block_partial_rp24(fdllm_ctx* ctx, const void* active_embed, int rows, void* k_cache,
+                                     void* v_cache, int cap, const int32_t* cache_offset, int64_t prefix_len,
+                                     void* out, void* stream);
+
+/* Fused lm_head + confidence: the device restatement of get_confidence_m{rows}
+ * (fast_dllm_relax/model/metal.py:505-528, dispatch runtime.py:136-174).  ids [rows] int32 = first
+ * argmax of each row's logits; maxp [rows] fp32 = 1 / sum exp(logit - max).  Unshifted; the caller
+ * applies the shift of runtime.py:172-174.  logits may be NULL, or [rows, vocab] fp32 to also receive
+ * exactly what fdllm_get_logits returns. */
+int fdllm_get_confidence(fdllm_ctx* ctx, const void* hidden, int rows, int32_t* ids, float* maxp, float* logits,
+                         void* stream);
+
+/* The same confidence of given fp32 logits [rows, ld] (the host reduction of runtime.py:176-181). */
+int fdllm_confidence_from_logits(fdllm_ctx* ctx, const float* logits, int rows, int vocab, int ld, int32_t* ids,
+                                 float* maxp, void* stream);
+
+/* Message of this thread's last failure ("" if none). */
+const char* fdllm_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FDLLM_H */

@@ -1,0 +1,182 @@
+"""HIP path vs the CPU oracle on the same seeded weights and inputs (calls go through the C ABI)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import TINY, WIDE2, log, make_pair, to_np
+from oracle import confidence as oconf
+from oracle.model import build_prefix_block_attention_bias
+
+pytestmark = pytest.mark.gpu
+
+TOL = dict(rtol=2e-2, atol=2e-2)  # bf16 activations; the reference's own tests use 2e-2 (test_tiny_compile.py:282)
+
+
+def _ids(rng, n, vocab):
+    return rng.integers(0, vocab - 1, n)
+
+
+def _dev_ids(ids):
+    return torch.tensor(np.asarray(ids), dtype=torch.int32, device="cuda")
+
+
+def _off(v):
+    return torch.tensor(int(v), dtype=torch.int32, device="cuda")
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    log("setup: tiny bf16 model seed 0")
+    return make_pair(TINY, 0)
+
+
+def test_embed_bit_exact(tiny):
+    ref, vm = tiny
+    ids = _ids(np.random.default_rng(1), 37, TINY["vocab_size"])
+    log("case: embed 37 rows")
+    got = to_np(vm.embed(_dev_ids(ids)))
+    np.testing.assert_array_equal(got, ref.embed(ids))
+
+
+def test_get_logits_matches_oracle(tiny):
+    ref, vm = tiny
+    rng = np.random.default_rng(2)
+    for rows in (8, 32, 45):
+        log(f"case: get_logits rows={rows}")
+        h = ref.rnd(rng.standard_normal((1, rows, TINY["hidden_size"])).astype(np.float32))
+        got = to_np(vm.get_logits(torch.from_numpy(h).to("cuda", torch.bfloat16)))
+        want = ref.get_logits(h)
+        # fp32 accumulation order differs; the bf16 rounding of the logits may flip by one ulp
+        np.testing.assert_allclose(got, want, rtol=1e-2, atol=1e-2)
+        assert np.mean(got == want) > 0.98
+
+
+def test_prefill_and_cached_step_match_oracle(tiny):
+    ref, vm = tiny
+    rng = np.random.default_rng(3)
+    P, R, cap = 64, 32, 128
+    ids = _ids(rng, P + R, TINY["vocab_size"])
+    kc = np.full((2, 1, cap, 2, 128), 7.0, np.float32)
+    vc = kc.copy()
+    ref.build_prefix_cache(ref.embed(ids[:P])[None], build_prefix_block_attention_bias(0, P, block_size=32), kc, vc)
+    h_ref = ref.forward_cached(ref.embed(ids[P:])[None], kc, vc, P, P)
+    k = torch.full((2, 1, cap, 2, 128), 7.0, dtype=torch.bfloat16, device="cuda")
+    v = k.clone()
+    log("case: build_prefix_cache P=64 (arithmetic block-causal)")
+    vm.build_prefix_cache(vm.embed(_dev_ids(ids[:P]))[None], None, k, v)
+    kn = to_np(k)
+    np.testing.assert_allclose(kn[:, :, :P], kc[:, :, :P], **TOL)
+    assert (kn[:, :, P:] == 7.0).all(), "build_prefix_cache wrote past the prefix"
+    log("case: forward_cached R=32 at P=64")
+    h = to_np(vm.forward_cached(vm.embed(_dev_ids(ids[P:]))[None], k, v, _off(P), P))
+    np.testing.assert_allclose(h, h_ref, **TOL)
+    kn = to_np(k)
+    np.testing.assert_allclose(kn[:, :, P:P + R], kc[:, :, P:P + R], **TOL)
+    assert (kn[:, :, P + R:] == 7.0).all(), "forward_cached wrote past the block"
+    for rp in (0, 8, 16, 24):
+        log(f"case: forward_block_partial_rp{rp}")
+        small = ids[P + rp:P + rp + 8]
+        kc2, vc2 = kc.copy(), vc.copy()
+        h_ref_p = ref.forward_block_partial(rp, ref.embed(small)[None], kc2, vc2, P + rp, P)
+        before = to_np(k)
+        h_p = to_np(vm[f"forward_block_partial_rp{rp}"](vm.embed(_dev_ids(small))[None], k, v, _off(P + rp), P))
+        np.testing.assert_allclose(h_p, h_ref_p, **TOL)
+        # same tokens at the same rows: the partial step reproduces the full step's rows (cuda.py:740-756)
+        np.testing.assert_allclose(h_p, h_ref[:, rp:rp + 8], **TOL)
+        after = to_np(k)
+        outside = np.ones(cap, bool)
+        outside[P + rp:P + rp + 8] = False
+        np.testing.assert_array_equal(after[:, :, outside], before[:, :, outside])
+
+
+def test_forward_hidden_matches_oracle_and_dense_equals_cached(tiny):
+    ref, vm = tiny
+    rng = np.random.default_rng(4)
+    S = 96
+    ids = _ids(rng, S, TINY["vocab_size"])
+    bias = build_prefix_block_attention_bias(0, S, block_size=32)
+    log("case: forward_hidden S=96 with explicit bias")
+    h_ref = ref.forward_hidden(ref.embed(ids)[None], bias)
+    x = vm.embed(_dev_ids(ids))[None]
+    h = to_np(vm.forward_hidden(x, torch.from_numpy(bias).cuda()))
+    np.testing.assert_allclose(h, h_ref, **TOL)
+    log("case: forward_hidden S=96 arithmetic block-causal")
+    h2 = to_np(vm.forward_hidden(x, None))
+    np.testing.assert_allclose(h2, h, rtol=1e-2, atol=1e-2)
+
+
+def test_write_window_errors(tiny):
+    _, vm = tiny
+    k = torch.zeros((2, 1, 64, 2, 128), dtype=torch.bfloat16, device="cuda")
+    v = torch.zeros_like(k)
+    x = torch.zeros((1, 32, TINY["hidden_size"]), dtype=torch.bfloat16, device="cuda")
+    log("case: window errors")
+    with pytest.raises(ValueError, match="outside cache capacity"):
+        vm.forward_cached(x, k, v, _off(48), 48)
+    with pytest.raises(ValueError):
+        vm.forward_block_partial_rp8(x, k, v, _off(8), 0)  # 32 rows where 8 are required
+    xs = torch.zeros((1, 8, TINY["hidden_size"]), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="outside cache capacity"):
+        vm.forward_block_partial_rp24(xs, k, v, _off(56), 40)
+
+
+def test_confidence_bit_exact_given_logits(tiny):
+    ref, vm = tiny
+    rng = np.random.default_rng(5)
+    for rows, scale in ((32, 1.0), (8, 20.0), (3, 0.01)):
+        log(f"case: confidence_from_logits rows={rows} scale={scale}")
+        logits = ref.rnd(scale * rng.standard_normal((1, rows, TINY["vocab_size"])).astype(np.float32))
+        logits[0, 0, 17] = logits[0, 0].max()  # a tie: the first index wins
+        ids, maxp = vm.confidence_from_logits(torch.from_numpy(logits).cuda())
+        wid, wp = oconf.confidence(logits[0])
+        np.testing.assert_array_equal(ids.cpu().numpy()[0], wid)
+        np.testing.assert_array_equal(maxp.cpu().numpy()[0].view(np.uint32), wp.view(np.uint32))
+
+
+def test_fused_confidence_equals_confidence_of_get_logits(tiny):
+    ref, vm = tiny
+    rng = np.random.default_rng(6)
+    for rows in (32, 8):
+        log(f"case: fused lm_head+confidence rows={rows}")
+        h = torch.from_numpy(ref.rnd(rng.standard_normal((1, rows, TINY["hidden_size"])).astype(np.float32)))
+        h = h.to("cuda", torch.bfloat16)
+        logits = torch.empty((1, rows, TINY["vocab_size"]), dtype=torch.float32, device="cuda")
+        ids, maxp = vm.get_confidence(h, logits=logits)
+        np.testing.assert_array_equal(to_np(logits), to_np(vm.get_logits(h)))
+        wid, wp = oconf.confidence(to_np(logits)[0])
+        np.testing.assert_array_equal(ids.cpu().numpy()[0], wid)
+        np.testing.assert_array_equal(maxp.cpu().numpy()[0].view(np.uint32), wp.view(np.uint32))
+
+
+@pytest.fixture(scope="module")
+def wide2():
+    log("setup: 1.5B-shape 2-layer bf16 model seed 1")
+    return make_pair(WIDE2, 1)
+
+
+def test_wide_cached_step_and_logits(wide2):
+    """1.5B layer shapes: cached 32-row step at P=512 and its logits / confidence vs the oracle."""
+    ref, vm = wide2
+    rng = np.random.default_rng(7)
+    P, R, cap = 512, 32, 576
+    ids = _ids(rng, P + R, WIDE2["vocab_size"])
+    kc = np.zeros((2, 1, cap, 2, 128), np.float32)
+    vc = kc.copy()
+    ref.build_prefix_cache(ref.embed(ids[:P])[None], build_prefix_block_attention_bias(0, P, block_size=32), kc, vc)
+    h_ref = ref.forward_cached(ref.embed(ids[P:])[None], kc, vc, P, P)
+    k = torch.zeros((2, 1, cap, 2, 128), dtype=torch.bfloat16, device="cuda")
+    v = torch.zeros_like(k)
+    log("case: wide build_prefix_cache P=512")
+    vm.build_prefix_cache(vm.embed(_dev_ids(ids[:P]))[None], None, k, v)
+    log("case: wide forward_cached R=32")
+    h = vm.forward_cached(vm.embed(_dev_ids(ids[P:]))[None], k, v, _off(P), P)
+    np.testing.assert_allclose(to_np(h), h_ref, **TOL)
+    log("case: wide logits")
+    lg = to_np(vm.get_logits(h))
+    lref = ref.get_logits(h_ref)
+    err = np.abs(lg - lref).max()
+    log(f"  max |dlogit| = {err:.4g}")
+    assert err <= 3e-2
