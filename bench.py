@@ -1,0 +1,252 @@
+#!/usr/bin/env python3
+"""Benchmark of Fast-dLLM v2's cached block-diffusion step on one MI355X.
+
+Workload (the metric's configuration): the 1.5B architecture in bf16 with random-init weights, seed 2,
+lm_head N(0, 0.5), a 2048-token random prompt and 256 new tokens decoded by the block-diffusion loop
+(blocks of 32 refined in sub-blocks of 8, threshold 0.9, block cache on; the loop of
+fast_dllm_relax/runtime.py:591-880).  One bench step = one such generation.  The headline value is
+decode tokens/s = new tokens / (generation time - prefill time), the reference's definition
+(fast_dllm_relax/runners.py:748-750), summed over the timed steps.
+
+Beside it the JSON line carries:
+  block_step      synced medians (HIP events on the kernels' stream) of one 32-row refinement step
+                  (forward_cached + fused lm_head/confidence) and one 8-row partial step at prefix 2048,
+                  with their algorithmic HBM bytes and GB/s (weights + KV read + KV write + rows);
+  roofline        the dominant kernel (the gate_up projection with the SiLU epilogue) timed alone with
+                  HIP events over launches that walk the 28 layers;
+  cpu_baseline    the CPU oracle's 32-row refinement step (numpy fp32 with the bf16 rounding points) at
+                  the same prefix on the host's cores, scaled to tokens/s with the GPU loop's tokens per
+                  model call.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import statistics
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0
+PREFIX = 2048
+NEW_TOKENS = 256
+SEED = 2
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def event_ms(fn, iters: int, warmup: int = 2) -> float:
+    """Median of per-call times measured with HIP events on torch's current stream."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(iters):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        b.synchronize()
+        times.append(a.elapsed_time(b))
+    return statistics.median(times)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--new-tokens", type=int, default=NEW_TOKENS)
+    ap.add_argument("--prefix", type=int, default=PREFIX)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-iters", type=int, default=2)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: the cached block step is batch-1 and this build has no "
+              f"multi-GPU path (asked for --gpus {args.gpus})", file=sys.stderr, flush=True)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import __graft_entry__
+
+    __graft_entry__.load_package()
+    from fast_dllm_relax_amd import _lib
+    from fast_dllm_relax_amd.config import DEFAULT_MASK_ID, fast_dllm_v2_1p5b
+    from fast_dllm_relax_amd.params import random_params_torch
+    from fast_dllm_relax_amd.runtime import (allocate_prefix_cache, build_prefix_cache_from_ids, cache_spec_of,
+                                             relax_greedy_generate, score_active_block_partial_perlayer,
+                                             score_active_block_refine)
+    from fast_dllm_relax_amd.vm import HipVM
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    torch.cuda.set_device(0)
+
+    # lm_head N(0, 0.5) is an untied head: scaling a tied embedding would also scale every input row,
+    # and each masked row would then predict its own (mask) token.
+    cfg = fast_dllm_v2_1p5b(tie_word_embeddings=False)
+    log("generating random weights on the GPU")
+    params = random_params_torch(cfg, SEED, dtype="bfloat16", device="cuda", std=0.02, lm_head_std=0.5)
+    vm = HipVM(cfg, params, dtype="bfloat16", max_rows=PREFIX)
+    rng = np.random.default_rng(SEED)
+    prompt = rng.integers(0, 150000, args.prefix).tolist()
+    P = args.prefix
+
+    # ---- decode loop: the headline --------------------------------------------------------------
+    def generate():
+        timing: dict = {}
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out, stats = relax_greedy_generate(vm, prompt, max_new_tokens=args.new_tokens, block_size=32,
+                                           small_block_size=8, threshold=0.9, mask_id=DEFAULT_MASK_ID,
+                                           stop_token=None, timing=timing)
+        torch.cuda.synchronize()
+        total = time.perf_counter() - t0
+        return out, stats, total, timing["prefill_latency_s"]
+
+    for i in range(args.warmup):
+        log(f"warmup generation {i + 1}/{args.warmup}")
+        generate()
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    runs = []
+    for i in range(args.steps):
+        out, stats, total, prefill = generate()
+        runs.append((len(out), stats, total, prefill))
+        log(f"step {i + 1}/{args.steps}: {len(out)} tokens, total {total * 1e3:.1f} ms, prefill "
+            f"{prefill * 1e3:.1f} ms, calls {stats['block_recomputes']} (partial {stats['partial_recomputes']})")
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    tokens = sum(r[0] for r in runs)
+    decode_s = sum(r[2] - r[3] for r in runs)
+    value = tokens / decode_s
+    calls = sum(r[1]["block_recomputes"] for r in runs)
+    tokens_per_call = tokens / calls
+
+    # ---- single cached block steps at prefix P ----------------------------------------------------
+    log(f"block steps at prefix {P}")
+    cache = build_prefix_cache_from_ids(vm, prompt, block_size=32, capacity=P + 32)
+    block = rng.integers(0, 150000, 32).tolist()
+    refine_ms = event_ms(lambda: score_active_block_refine(vm, block, cache), 20)
+    partial_ms = event_ms(lambda: score_active_block_partial_perlayer(vm, block[8:16], cache, 8, block_size=32), 20)
+    bytes_r32 = cfg.step_bytes(32, P)
+    bytes_r8 = cfg.step_bytes(8, P)
+
+    # ---- dominant kernel alone (gate_up + SiLU), events on the launch stream ------------------------
+    stream = torch.cuda.current_stream().cuda_stream
+    lib = vm.lib
+    iters = 4 * cfg.num_hidden_layers
+
+    def gate_up():
+        _lib.check(lib.fdllm_bench_op(vm.ctx, _lib.OP_GATE_UP, 32, 0, iters, None, None, 0, 0, stream))
+
+    gu_ms = event_ms(gate_up, 10) / iters
+    H, I = cfg.hidden_size, cfg.intermediate_size
+    gu_bytes = 2 * I * H * 2 + 32 * H * 2 + 32 * I * 2  # weights + input rows + output rows
+    gu_gbps = gu_bytes / (gu_ms * 1e-3) / 1e9
+
+    # ---- CPU baseline: the oracle's refinement step on the host ------------------------------------
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(vm, params, cache, block, P, args.cpu_iters, tokens_per_call)
+
+    line = {
+        "metric": "decode tokens/s (1.5B bf16, bs1); block-step ms + achieved HBM GB/s",
+        "value": round(value, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights N(0,0.02), lm_head N(0,0.5), seed 2; random prompt ids)",
+        "config": {
+            "workload": f"Fast-dLLM v2 block-diffusion decode: 1.5B bf16, batch 1, prompt {P}, "
+                        f"{args.new_tokens} new tokens, block 32 / sub-block 8, threshold 0.9, block cache on",
+            "global_batch": 1, "seq_len": P + args.new_tokens, "parallelism": "single GPU",
+        },
+        "decode": {"tokens": tokens, "decode_s": round(decode_s, 4), "model_calls": calls,
+                   "tokens_per_call": round(tokens_per_call, 3),
+                   "prefill_ms_mean": round(statistics.mean(r[3] for r in runs) * 1e3, 2)},
+        "block_step": {
+            "prefix": P,
+            "refine_r32_ms": round(refine_ms, 4), "refine_r32_bytes": bytes_r32,
+            "refine_r32_gbps": round(bytes_r32 / (refine_ms * 1e-3) / 1e9, 1),
+            "partial_r8_ms": round(partial_ms, 4), "partial_r8_bytes": bytes_r8,
+            "partial_r8_gbps": round(bytes_r8 / (partial_ms * 1e-3) / 1e9, 1),
+        },
+        "roofline": {"kernel": "gemm_skinny_kernel<bf16, EPI_SILU> (gate_up, 32 rows)", "bound": "hbm",
+                     "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "avg_launch_us": round(gu_ms * 1e3, 2), "bytes_per_launch": gu_bytes},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_baseline(vm, params, cache, block, P, iters, tokens_per_call):
+    """Time the CPU oracle's 32-row refinement step (28 layers + lm_head + confidence) at prefix P on
+    the same weights and KV cache as the GPU run."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_info
+
+    from oracle import confidence as oconf
+    from oracle.model import OracleConfig, OracleModel, param_names
+
+    c = vm.cfg
+    ocfg = OracleConfig(vocab_size=c.vocab_size, hidden_size=c.hidden_size, intermediate_size=c.intermediate_size,
+                        num_hidden_layers=c.num_hidden_layers, num_attention_heads=c.num_attention_heads,
+                        num_key_value_heads=c.num_key_value_heads, head_dim=c.head_dim,
+                        tie_word_embeddings=c.tie_word_embeddings)
+    log("cpu baseline: copying weights and cache to the host")
+    arrays = {n: p.float().cpu().numpy() for n, p in zip(param_names(ocfg), params)}
+    model = OracleModel(ocfg, arrays, "bfloat16")
+    kc = cache.k[:, :, :P + 32].float().cpu().numpy()
+    vc = cache.v[:, :, :P + 32].float().cpu().numpy()
+    emb = model.embed(block)[None]
+
+    def step():
+        h = model.forward_cached(emb, kc, vc, P, P)
+        return oconf.shifted_confidence(model.get_logits(h)[0])
+
+    step()  # warm-up
+    times = []
+    for i in range(iters):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+        log(f"cpu baseline step {i + 1}/{iters}: {times[-1]:.2f} s")
+    sec = statistics.median(times)
+    threads = max([d.get("num_threads", 1) for d in threadpool_info()] or [1])
+    del arrays, model
+    torch.cuda.empty_cache()
+    return {"value": round(tokens_per_call / sec, 3), "unit": "tokens/s", "cores": int(threads), "kind": "port",
+            "step_s": round(sec, 3), "host_cpus": os.cpu_count(),
+            "sample": f"oracle (numpy fp32 + bf16 rounding) 32-row refinement step at prefix {P}, 28 layers + "
+                      f"lm_head + confidence, median of {iters} after 1 warm-up; tokens/s = "
+                      f"{tokens_per_call:.3f} tokens per model call (the GPU loop's) / step time"}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

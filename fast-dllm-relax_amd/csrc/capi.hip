@@ -450,6 +450,64 @@ int fdllm_get_confidence(fdllm_ctx* c, const void* hidden, int rows, int32_t* id
   return FDLLM_OK;
 }
 
+int fdllm_bench_op(fdllm_ctx* c, int op, int rows, int layer, int iters, void* k, void* v, int cap, int attend_len,
+                   void* stream) {
+  int rc = check_ready(c);
+  if (rc) return rc;
+  const fdllm_config& f = c->cfg;
+  if (rows <= 0 || iters <= 0 || layer < 0 || layer >= f.num_hidden_layers)
+    return fail(FDLLM_EINVAL, "invalid bench_op arguments");
+  rc = ensure_rows(c, rows);
+  if (rc == FDLLM_OK) rc = ensure_stats(c, rows);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  const int H = f.hidden_size, I = f.intermediate_size;
+  for (int it = 0; it < iters && rc == FDLLM_OK; ++it) {
+    // consecutive launches walk the layers, as a step does, so no weight is re-read from cache
+    const int li = (layer + it) % f.num_hidden_layers;
+    const Layer& L = c->layers[li];
+    switch (op) {
+      case FDLLM_OP_QKV:
+        rc = run_gemm(c, EPI_BIAS, c->xn, H, rows, L.wqkv, c->qkv_dim(), H, c->qkv, c->qkv_dim(), L.bqkv, nullptr, 0,
+                      nullptr, 0, false, st);
+        break;
+      case FDLLM_OP_O_PROJ:
+        rc = run_gemm(c, EPI_RESID, c->attn, c->q_dim(), rows, L.wo, H, c->q_dim(), c->h, H, nullptr, c->h, H, nullptr,
+                      0, false, st);
+        break;
+      case FDLLM_OP_GATE_UP:
+        rc = run_gemm(c, EPI_SILU, c->xn, H, rows, L.wgu, 2 * I, H, c->act, I, nullptr, nullptr, 0, nullptr, 0, false,
+                      st);
+        break;
+      case FDLLM_OP_DOWN:
+        rc = run_gemm(c, EPI_RESID, c->act, I, rows, L.wd, H, I, c->h, H, nullptr, c->h, H, nullptr, 0, false, st);
+        break;
+      case FDLLM_OP_ATTENTION: {
+        if (!k || !v || attend_len <= 0 || attend_len > cap) return fail(FDLLM_EINVAL, "attention needs a cache");
+        size_t stride = (size_t)cap * f.num_key_value_heads * f.head_dim;
+        rc = run_attention(c, rows, (uint16_t*)k + (size_t)li * stride, (uint16_t*)v + (size_t)li * stride,
+                           attend_len, 0, 0, nullptr, 0, st);
+        break;
+      }
+      case FDLLM_OP_LM_HEAD_CONFIDENCE: {
+        rc = run_gemm(c, EPI_LOGITS, c->xn, H, rows, c->lm_head, f.vocab_size, H, nullptr, 0, nullptr, nullptr, 0,
+                      nullptr, f.vocab_size, true, st);
+        if (rc) break;
+        int T = c->tiles();
+        char* base = (char*)c->stats;
+        int32_t* ids = (int32_t*)c->qkv;
+        float* maxp = (float*)(c->qkv + 64);
+        HIPCHK(launch_confidence_combine((float*)base, (int32_t*)(base + c->stats_rows * T * 4),
+                                         (float*)(base + c->stats_rows * T * 8), T, rows, ids, maxp, st));
+        break;
+      }
+      default:
+        return fail(FDLLM_EINVAL, "unknown op %d", op);
+    }
+  }
+  return rc;
+}
+
 int fdllm_confidence_from_logits(fdllm_ctx* c, const float* logits, int rows, int vocab, int ld, int32_t* ids,
                                  float* maxp, void* stream) {
   if (!c) return fail(FDLLM_EINVAL, "null context");

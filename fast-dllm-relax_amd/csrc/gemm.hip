@@ -295,12 +295,14 @@ static hipError_t launch_one(const GemmArgs& a, int nblocks, int ksplit, int mch
   size_t lds = (size_t)16 * MT * (a.kc + 8) * 2;
   if (EPI == EPI_LOGITS && lds < (size_t)16 * MT * 256 * 4) lds = (size_t)16 * MT * 256 * 4;
   auto kern = gemm_skinny_kernel<DT, EPI, TPW, MT>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    // raise the dynamic LDS limit once; a runtime that rejects the attribute keeps its default
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              160 * 1024);
-    attr_set = true;
+  static size_t attr_lds = 64 * 1024;  // the launch limit without the attribute
+  if (lds > attr_lds) {
+    // a runtime that needs no attribute for LDS up to the device limit may reject it: clear that
+    // error and let the launch itself report whether the size fits
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess)
+      (void)hipGetLastError();
+    attr_lds = lds;
   }
   hipLaunchKernelGGL(kern, dim3(nblocks, ksplit, mchunks), dim3(256), lds, st, a);
   return hipGetLastError();

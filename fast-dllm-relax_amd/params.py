@@ -50,10 +50,11 @@ def param_shapes(cfg: FastDLLMConfig) -> dict[str, tuple[int, ...]]:
 
 
 def random_params_torch(cfg: FastDLLMConfig, seed: int, *, dtype: str = "bfloat16", device: str = "cuda",
-                        std: float = 0.02, embed_std: float | None = None) -> list[torch.Tensor]:
+                        std: float = 0.02, embed_std: float | None = None,
+                        lm_head_std: float | None = None) -> list[torch.Tensor]:
     """Synthetic weights N(0, std) (norm weights = 1, the reference's test convention,
     tests/test_tiny_compile.py:45-55) generated on ``device`` from ``seed``; ``embed_std`` scales the
-    tied embedding / lm_head separately."""
+    embedding (the lm_head too when tied) and ``lm_head_std`` an untied lm_head separately."""
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
     td = TORCH_DTYPES[dtype]
@@ -64,7 +65,11 @@ def random_params_torch(cfg: FastDLLMConfig, seed: int, *, dtype: str = "bfloat1
         if name.endswith("norm.weight"):
             out.append(torch.ones(shape, dtype=td, device=device))
             continue
-        s = embed_std if (embed_std is not None and name == "model.embed_tokens.weight") else std
+        s = std
+        if embed_std is not None and name == "model.embed_tokens.weight":
+            s = embed_std
+        elif lm_head_std is not None and name == "lm_head.weight":
+            s = lm_head_std
         t = torch.empty(shape, dtype=torch.float32, device=device)
         t.normal_(0.0, 1.0, generator=gen)
         out.append((t * s).to(td))

@@ -121,6 +121,20 @@ int fdllm_get_confidence(fdllm_ctx* ctx, const void* hidden, int rows, int32_t* 
 int fdllm_confidence_from_logits(fdllm_ctx* ctx, const float* logits, int rows, int vocab, int ld, int32_t* ids,
                                  float* maxp, void* stream);
 
+/* Profiling hook; it has no counterpart in the reference.  Launches one operator of the cached step
+ * `iters` times back to back on `stream`, reading and writing the context's own workspace (the values
+ * are not meaningful); launch i uses layer (layer + i) % num_layers, as a step walks the layers, so a
+ * benchmark can time one kernel with events on the stream it runs on without re-reading one layer's
+ * weights from cache.  FDLLM_OP_ATTENTION attends rows [0, attend_len) of each layer of the caches. */
+#define FDLLM_OP_QKV 0
+#define FDLLM_OP_O_PROJ 1
+#define FDLLM_OP_GATE_UP 2
+#define FDLLM_OP_DOWN 3
+#define FDLLM_OP_ATTENTION 4
+#define FDLLM_OP_LM_HEAD_CONFIDENCE 5
+int fdllm_bench_op(fdllm_ctx* ctx, int op, int rows, int layer, int iters, void* k_cache, void* v_cache, int cap,
+                   int attend_len, void* stream);
+
 /* Message of this thread's last failure ("" if none). */
 const char* fdllm_last_error(void);
 

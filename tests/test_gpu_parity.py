@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import TINY, WIDE2, log, make_pair, to_np
+from helpers import TINY, WIDE2, bf16_parity, log, make_pair, to_np
 from oracle import confidence as oconf
 from oracle.model import build_prefix_block_attention_bias
 
@@ -158,25 +158,37 @@ def wide2():
 
 
 def test_wide_cached_step_and_logits(wide2):
-    """1.5B layer shapes: cached 32-row step at P=512 and its logits / confidence vs the oracle."""
+    """1.5B layer shapes: cached 32-row step at P=512 and its logits vs the bf16 oracle and the fp32
+    oracle (same bf16-representable weights, no rounding anywhere)."""
+    from oracle.model import OracleModel
+
     ref, vm = wide2
+    ref32 = OracleModel(ref.cfg, ref.p, "float32")
     rng = np.random.default_rng(7)
     P, R, cap = 512, 32, 576
     ids = _ids(rng, P + R, WIDE2["vocab_size"])
-    kc = np.zeros((2, 1, cap, 2, 128), np.float32)
-    vc = kc.copy()
-    ref.build_prefix_cache(ref.embed(ids[:P])[None], build_prefix_block_attention_bias(0, P, block_size=32), kc, vc)
-    h_ref = ref.forward_cached(ref.embed(ids[P:])[None], kc, vc, P, P)
+    outs = {}
+    for name, model in (("bf16", ref), ("f32", ref32)):
+        kc = np.zeros((2, 1, cap, 2, 128), np.float32)
+        vc = kc.copy()
+        model.build_prefix_cache(model.embed(ids[:P])[None], build_prefix_block_attention_bias(0, P, block_size=32),
+                                 kc, vc)
+        h = model.forward_cached(model.embed(ids[P:])[None], kc, vc, P, P)
+        outs[name] = (h, model.get_logits(h), kc)
     k = torch.zeros((2, 1, cap, 2, 128), dtype=torch.bfloat16, device="cuda")
     v = torch.zeros_like(k)
     log("case: wide build_prefix_cache P=512")
     vm.build_prefix_cache(vm.embed(_dev_ids(ids[:P]))[None], None, k, v)
+    bf16_parity("prefix K", to_np(k)[:, :, :P], outs["bf16"][2][:, :, :P], outs["f32"][2][:, :, :P])
     log("case: wide forward_cached R=32")
     h = vm.forward_cached(vm.embed(_dev_ids(ids[P:]))[None], k, v, _off(P), P)
-    np.testing.assert_allclose(to_np(h), h_ref, **TOL)
+    bf16_parity("hidden", to_np(h), outs["bf16"][0], outs["f32"][0])
     log("case: wide logits")
     lg = to_np(vm.get_logits(h))
-    lref = ref.get_logits(h_ref)
-    err = np.abs(lg - lref).max()
-    log(f"  max |dlogit| = {err:.4g}")
-    assert err <= 3e-2
+    # The reference's own bf16 precision order is ~0.04 from fp32 at the max over 4.9M logits (bf16
+    # hidden-state rounding through the layers), so the bound is relative to it, not an absolute 3e-2.
+    bf16_parity("logits", lg, outs["bf16"][1], outs["f32"][1])
+    ids_d, maxp_d = vm.get_confidence(h)
+    wid, wp = oconf.confidence(lg[0])
+    np.testing.assert_array_equal(ids_d.cpu().numpy()[0], wid)
+    np.testing.assert_array_equal(maxp_d.cpu().numpy()[0].view(np.uint32), wp.view(np.uint32))
