@@ -194,7 +194,7 @@ def main() -> int:
             "partial_r8_ms": round(partial_ms, 4), "partial_r8_bytes": bytes_r8,
             "partial_r8_gbps": round(bytes_r8 / (partial_ms * 1e-3) / 1e9, 1),
         },
-        "roofline": {"kernel": "gemm_skinny_kernel<bf16, EPI_SILU> (gate_up, 32 rows)", "bound": "hbm",
+        "roofline": {"kernel": "gemm_pk_kernel<bf16, EPI_SILU_PAIR> (gate_up + SiLU*up, 32 rows)", "bound": "hbm",
                      "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
                      "avg_launch_us": round(gu_ms * 1e3, 2), "bytes_per_launch": gu_bytes},

@@ -1,85 +1,183 @@
-// GQA attention of the block rows against the in-place KV cache (fast_dllm.attn_inplace,
-// fast_dllm_relax/runtime.py:63-73; in-graph restatement model/metal.py:378-408): query head h uses
-// kv head h / (nq / nkv); scores q.k * scale in fp32, softmax in fp32, P.V with fp32 accumulation.
+// GQA attention of a block of rows against the in-place KV cache, with RoPE and the KV append fused in
+// (fast_dllm.attn_inplace, fast_dllm_relax/runtime.py:51-73; RoPE cuda.py:278-316; in-graph restatement
+// model/metal.py:255-302, 378-408).  Query head h uses kv head h / (nq / nkv); scores q.k * scale in
+// fp32, online softmax in fp32, P rounded to the model dtype for P.V on MFMA with fp32 accumulation
+// (the flash-attention precision the reference's callback uses), one rounding of the output.
 //
-// Work split: blockIdx.y = kv head, blockIdx.z = key split, blockIdx.x = group of 4 query tiles.
-// The group's query rows of all heads sharing the kv head are stacked (row qi = head_in_group * R + r),
-// so one K/V stream serves all of them.  Each wave owns 16 query rows:
-//   S^T = K . Q^T   (A = 16 keys x 32 dims straight from the cache rows, B = the wave's queries)
-// leaves lane l with 4 keys of query l % 16, which is exactly the A-operand layout P needs for
-//   O = P . V       (B = V^T from LDS, keys permuted consistently with P's register order).
-// Online softmax inside a split; the splits are merged by attn_combine_kernel.
+// Rows [ws, ws + rows) of the cache belong to this call: their K (after RoPE) and V are taken straight
+// from this call's qkv projection, and workgroup column 0 writes them to the cache.  Every other key
+// row comes from the cache.  Queries are RoPE'd in registers at positions pos_offset + r.
+//
+// Work split: blockIdx.y = kv head g, blockIdx.z = key split c, blockIdx.x = group of QPW query tiles
+// (the query rows of the grp heads sharing g are stacked: row qi = head_in_group * rows + r, 16 per
+// tile).  The workgroup's QPW x KSW waves are QPW query-tile slots times KSW key groups; key group kg
+// stages blocks of 32 keys (K row-major, V transposed four keys at a time) in its own LDS buffers and
+// its waves run the scores S^T = K . Q^T and O += P . V for their query tiles.  Key groups are merged
+// in LDS in fixed order; key splits (S > 1) leave agent-coherent partials and the workgroup that
+// arrives last merges them in split order, so results are deterministic.
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace fdllm {
 
 constexpr int HD = 128;
-constexpr int KSUB = 64;      // keys per inner step
-constexpr int VT_LD = KSUB + 8;
+constexpr int KB = 32;        // keys per block
+constexpr int KLD = HD + 8;   // u16 stride of a K row in LDS
+constexpr int VLD = KB + 8;   // u16 stride of a transposed V row (one head dimension)
+constexpr int PSZ = 16 * HD + 32;  // floats per split partial of one query tile: O, m, l
 
+template <int DT> __device__ __forceinline__ float elem(const u32x4& v, int e) {
+  return (e & 1) ? hi_f32<DT>(v[e >> 1]) : lo_f32<DT>(v[e >> 1]);
+}
+
+// RoPE of 8 rotation pairs: lo holds dims i0 .. i0 + 7 (< 64), hi the partner dims + 64
+// (cuda.py:288-299 tables: inv_freq = exp(-ln(theta) * i / 64), emb = [f, f]; apply 314-315 with
+// _rotate_half 207-209, every product and sum rounded to the model dtype).
 template <int DT>
-__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
-  __shared__ __align__(16) u16 vt[HD * VT_LD];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int lr = lane & 15, lg = lane >> 4;
-  const int g = blockIdx.y, split = blockIdx.z;
-  const int grp = a.nq / a.nkv;
-  const int QR = grp * a.rows;
-  const int qt = blockIdx.x * 4 + w;
-  const bool active = qt * 16 < QR;
-  const size_t krow = (size_t)a.nkv * HD;
+__device__ __forceinline__ void rope_pair(u32x4& lo, u32x4& hi, int i0, float pos, float nlt) {
+  u16 o1[8], o2[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float ex = (nlt * (float)(i0 + e)) / 64.0f;
+    const float fr = pos * expf(ex);
+    const float cs = rnd<DT>(cosf(fr)), sn = rnd<DT>(sinf(fr));
+    const float x1 = elem<DT>(lo, e), x2 = elem<DT>(hi, e);
+    o1[e] = from_f32<DT>(rnd<DT>(x1 * cs) + rnd<DT>(-x2 * sn));
+    o2[e] = from_f32<DT>(rnd<DT>(x2 * cs) + rnd<DT>(x1 * sn));
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    lo[c] = pack2(o1[2 * c], o1[2 * c + 1]);
+    hi[c] = pack2(o2[2 * c], o2[2 * c + 1]);
+  }
+}
 
+template <int DT, int QPW, int KSW>
+__global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
+  constexpr int NT = 64 * QPW;  // threads of one key group
+  constexpr int KBUF = KB * KLD, VBUF = HD * VLD;
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int flag_s;
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int qw = w % QPW, kg = w / QPW;
+  const int tid = threadIdx.x - kg * NT;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int g = blockIdx.y, c = blockIdx.z;
+  const int grp = a.nq / a.nkv, QR = grp * a.rows, QT = (QR + 15) / 16;
+  const int qt = blockIdx.x * QPW + qw;
+  const bool tile_ok = qt < QT;
+  const int pos_base = *a.pos_offset;
+  const size_t krow = (size_t)a.nkv * HD;
+  u16* kbuf = reinterpret_cast<u16*>(smem) + kg * KBUF;
+  u16* vbuf = reinterpret_cast<u16*>(smem) + KSW * KBUF + kg * VBUF;
+
+  // this lane's query row: qi = 16 qt + lr
   const int qi = qt * 16 + lr;
-  const bool qvalid = qi < QR;
+  const bool qvalid = tile_ok && qi < QR;
   const int hh = qvalid ? qi / a.rows : 0;
   const int r = qvalid ? qi - hh * a.rows : 0;
-  u32x4 qf[HD / 32];
+  u32x4 qf[4];
   {
-    const u16* qp = a.q + (size_t)r * a.nq * HD + (g * grp + hh) * HD + 8 * lg;
+    const u16* qp = a.qkv + (size_t)r * a.ldq + (g * grp + hh) * HD + 8 * lg;
 #pragma unroll
-    for (int ds = 0; ds < HD / 32; ++ds)
+    for (int ds = 0; ds < 4; ++ds)
       qf[ds] = qvalid ? *reinterpret_cast<const u32x4*>(qp + 32 * ds) : u32x4{0u, 0u, 0u, 0u};
+    const float pos = (float)(pos_base + r);
+    rope_pair<DT>(qf[0], qf[2], 8 * lg, pos, a.neg_log_theta);
+    rope_pair<DT>(qf[1], qf[3], 8 * lg + 32, pos, a.neg_log_theta);
   }
-  const int qpos_blk = (a.q_pos0 + r) / (a.block > 0 ? a.block : 1);
+  const int qpos_blk = a.mask == 1 ? (a.q_pos0 + r) / a.block : 0;
   const float* brow = a.mask == 2 ? a.bias + (long long)r * a.bias_ld : nullptr;
 
-  const int kbeg = split * a.chunk;
+  const int kbeg = c * a.chunk;
   const int kend = min(kbeg + a.chunk, a.Lk);
+  const int nblk = (kend - kbeg + KB - 1) / KB;
+  const int iters = (nblk + KSW - 1) / KSW;
+  const bool writer = blockIdx.x == 0;
+  const u16* kq_base = a.qkv + a.nq * HD + g * HD;
+  const u16* vq_base = a.qkv + (a.nq + a.nkv) * HD + g * HD;
 
   float m_run = -INFINITY, l_run = 0.f;
   f32x4 o[HD / 16];
 #pragma unroll
   for (int dt = 0; dt < HD / 16; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int kb = kbeg; kb < kend; kb += KSUB) {
+  for (int it = 0; it < iters; ++it) {
+    const int b = it * KSW + kg;
+    const int kb = kbeg + b * KB;
+    const bool bvalid = b < nblk;
     __syncthreads();
-    for (int idx = threadIdx.x; idx < KSUB * (HD / 8); idx += 256) {
-      const int key = idx % KSUB, dblk = idx / KSUB;
-      const int kk = kb + key;
-      u32x4 val = {0u, 0u, 0u, 0u};
-      if (kk < kend) val = *reinterpret_cast<const u32x4*>(a.v + kk * krow + g * HD + dblk * 8);
+    if (bvalid) {
+      // K: 32 keys x 8 rotation-pair chunks
+      for (int item = tid; item < KB * 8; item += NT) {
+        const int j = item >> 3, p = item & 7;
+        const int key = kb + j;
+        u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
+        if (key < kend) {
+          if (key >= a.ws && key < a.ws + a.rows) {
+            const u16* src = kq_base + (size_t)(key - a.ws) * a.ldq;
+            lo = *reinterpret_cast<const u32x4*>(src + 8 * p);
+            hi = *reinterpret_cast<const u32x4*>(src + 64 + 8 * p);
+            rope_pair<DT>(lo, hi, 8 * p, (float)(pos_base + key - a.ws), a.neg_log_theta);
+            if (writer) {
+              u16* dst = a.kc + key * krow + g * HD;
+              *reinterpret_cast<u32x4*>(dst + 8 * p) = lo;
+              *reinterpret_cast<u32x4*>(dst + 64 + 8 * p) = hi;
+            }
+          } else {
+            const u16* src = a.kc + key * krow + g * HD;
+            lo = *reinterpret_cast<const u32x4*>(src + 8 * p);
+            hi = *reinterpret_cast<const u32x4*>(src + 64 + 8 * p);
+          }
+        }
+        *reinterpret_cast<u32x4*>(kbuf + j * KLD + 8 * p) = lo;
+        *reinterpret_cast<u32x4*>(kbuf + j * KLD + 64 + 8 * p) = hi;
+      }
+      // V: 8 key quads x 16 dim chunks, stored transposed (vbuf[dim][key], four keys per 8-byte word)
+      for (int item = tid; item < 8 * 16; item += NT) {
+        const int kq = item >> 4, dc = item & 15;
+        u32x4 v[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) vt[(dblk * 8 + e) * VT_LD + key] = (u16)(val[e >> 1] >> (16 * (e & 1)));
+        for (int qq = 0; qq < 4; ++qq) {
+          const int key = kb + 4 * kq + qq;
+          v[qq] = u32x4{0u, 0u, 0u, 0u};
+          if (key < kend) {
+            if (key >= a.ws && key < a.ws + a.rows) {
+              v[qq] = *reinterpret_cast<const u32x4*>(vq_base + (size_t)(key - a.ws) * a.ldq + 8 * dc);
+              if (writer) *reinterpret_cast<u32x4*>(a.vc + key * krow + g * HD + 8 * dc) = v[qq];
+            } else {
+              v[qq] = *reinterpret_cast<const u32x4*>(a.vc + key * krow + g * HD + 8 * dc);
+            }
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int sh = 16 * (e & 1);
+          const unsigned long long wd =
+              (unsigned long long)((v[0][e >> 1] >> sh) & 0xffffu) |
+              ((unsigned long long)((v[1][e >> 1] >> sh) & 0xffffu) << 16) |
+              ((unsigned long long)((v[2][e >> 1] >> sh) & 0xffffu) << 32) |
+              ((unsigned long long)((v[3][e >> 1] >> sh) & 0xffffu) << 48);
+          *reinterpret_cast<unsigned long long*>(vbuf + (8 * dc + e) * VLD + 4 * kq) = wd;
+        }
+      }
     }
     __syncthreads();
-    if (!active) continue;
+    if (!bvalid || !tile_ok) continue;
 
-    f32x4 s[KSUB / 16];
+    f32x4 s[2];
 #pragma unroll
-    for (int kt = 0; kt < KSUB / 16; ++kt) {
+    for (int kt = 0; kt < 2; ++kt) {
       s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      int key = kb + 16 * kt + lr;
-      key = key < kend ? key : kend - 1;
-      const u16* kp = a.k + key * krow + g * HD + 8 * lg;
+      const u16* kp = kbuf + (16 * kt + lr) * KLD + 8 * lg;
 #pragma unroll
-      for (int ds = 0; ds < HD / 32; ++ds)
-        s[kt] = mfma16<DT>(*reinterpret_cast<const u32x4*>(kp + 32 * ds), qf[ds], s[kt]);
+      for (int ds = 0; ds < 4; ++ds) s[kt] = mfma16<DT>(*reinterpret_cast<const u32x4*>(kp + 32 * ds), qf[ds], s[kt]);
     }
     // lane holds S^T[key = kb + 16 kt + 4 lg + i][query lr]
     float mx = -INFINITY;
 #pragma unroll
-    for (int kt = 0; kt < KSUB / 16; ++kt)
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int key = kb + 16 * kt + 4 * lg + i;
@@ -101,10 +199,10 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const float alpha = expf(m_run - m_use);
     float ps = 0.f;
 #pragma unroll
-    for (int kt = 0; kt < KSUB / 16; ++kt)
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float p = expf(s[kt][i] - m_use);
+        const float p = expf(s[kt][i] - m_use);
         s[kt][i] = p;
         ps += p;
       }
@@ -118,65 +216,199 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 #pragma unroll
       for (int dt = 0; dt < HD / 16; ++dt) o[dt][i] *= al;
     }
+    // P as the A operand: k slot 8 lg + e holds key 4 lg + e (e < 4) or 16 + 4 lg + e - 4 (e >= 4);
+    // the V fragment below reads the same keys, so the contraction is over the same 32 keys.
+    const u32x4 pa = {pack2(from_f32<DT>(s[0][0]), from_f32<DT>(s[0][1])),
+                      pack2(from_f32<DT>(s[0][2]), from_f32<DT>(s[0][3])),
+                      pack2(from_f32<DT>(s[1][0]), from_f32<DT>(s[1][1])),
+                      pack2(from_f32<DT>(s[1][2]), from_f32<DT>(s[1][3]))};
 #pragma unroll
-    for (int ks = 0; ks < KSUB / 32; ++ks) {
-      u16 pv[8];
+    for (int dt = 0; dt < HD / 16; ++dt) {
+      const u16* vrow = vbuf + (16 * dt + lr) * VLD + 4 * lg;
+      const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
+      const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 16);
+      o[dt] = mfma16<DT>(pa, u32x4{lo[0], lo[1], hi[0], hi[1]}, o[dt]);
+    }
+  }
+
+  // ---- merge the key groups in LDS (fixed order kg = 0, 1, ...) ----
+  // lane holds O rows q = 4 lg + i (dims 16 dt + lr); m_run / l_run belong to query lr.
+  float Mq[4], Lq[4];
+  __syncthreads();
+  {
+    float* cm = reinterpret_cast<float*>(smem);
+    float* cl = cm + KSW * QPW * 16;
+    f32x4* co = reinterpret_cast<f32x4*>(cl + KSW * QPW * 16);
+    if (lg == 0) {
+      cm[(kg * QPW + qw) * 16 + lr] = m_run;
+      cl[(kg * QPW + qw) * 16 + lr] = l_run;
+    }
+    if (KSW > 1 && kg > 0) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pv[e] = from_f32<DT>(s[2 * ks + (e >> 2)][e & 3]);
-      u32x4 pa = {(uint32_t)pv[0] | ((uint32_t)pv[1] << 16), (uint32_t)pv[2] | ((uint32_t)pv[3] << 16),
-                  (uint32_t)pv[4] | ((uint32_t)pv[5] << 16), (uint32_t)pv[6] | ((uint32_t)pv[7] << 16)};
+      for (int dt = 0; dt < HD / 16; ++dt) co[(((kg - 1) * QPW + qw) * (HD / 16) + dt) * 64 + lane] = o[dt];
+    }
+    __syncthreads();
+    if (kg == 0) {
 #pragma unroll
-      for (int dt = 0; dt < HD / 16; ++dt) {
-        const u16* vrow = vt + (16 * dt + lr) * VT_LD + 32 * ks + 4 * lg;
-        u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
-        u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 16);
-        u32x4 vb = {lo[0], lo[1], hi[0], hi[1]};
-        o[dt] = mfma16<DT>(pa, vb, o[dt]);
+      for (int i = 0; i < 4; ++i) {
+        const int q = 4 * lg + i;
+        float M = -INFINITY;
+        for (int k = 0; k < KSW; ++k) M = fmaxf(M, cm[(k * QPW + qw) * 16 + q]);
+        const float Mu = M == -INFINITY ? 0.f : M;
+        float L = 0.f;
+        for (int k = 0; k < KSW; ++k) L += cl[(k * QPW + qw) * 16 + q] * expf(cm[(k * QPW + qw) * 16 + q] - Mu);
+        const float f0 = expf(cm[qw * 16 + q] - Mu);
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; ++dt) o[dt][i] *= f0;
+        for (int k = 1; k < KSW; ++k) {
+          const float fk = expf(cm[(k * QPW + qw) * 16 + q] - Mu);
+#pragma unroll
+          for (int dt = 0; dt < HD / 16; ++dt) o[dt][i] += co[(((k - 1) * QPW + qw) * (HD / 16) + dt) * 64 + lane][i] * fk;
+        }
+        Mq[i] = M;
+        Lq[i] = L;
       }
     }
   }
-  if (!active) return;
-  const size_t base = (size_t)(split * a.nkv + g) * a.QRp;
+
+  auto store_out = [&](int q, int dim, float v) {
+    const int row = qt * 16 + q;
+    if (row >= QR) return;
+    const int h2 = row / a.rows, r2 = row - h2 * a.rows;
+    a.out[(size_t)r2 * a.nq * HD + (g * grp + h2) * HD + dim] = from_f32<DT>(v);
+  };
+
+  if (a.S == 1) {
+    if (kg == 0 && tile_ok) {
 #pragma unroll
-  for (int dt = 0; dt < HD / 16; ++dt)
+      for (int dt = 0; dt < HD / 16; ++dt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a.o_part[(base + qt * 16 + 4 * lg + i) * HD + 16 * dt + lr] = o[dt][i];
-  if (lg == 0) {
-    a.m_part[base + qt * 16 + lr] = m_run;
-    a.l_part[base + qt * 16 + lr] = l_run;
+        for (int i = 0; i < 4; ++i) store_out(4 * lg + i, 16 * dt + lr, o[dt][i] / Lq[i]);
+    }
+    return;
   }
+
+  // ---- key splits: agent-coherent partials, merged by the last workgroup in split order ----
+  if (kg == 0 && tile_ok) {
+    float* pp = a.part + ((size_t)(g * QT + qt) * a.S + c) * PSZ;
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) st_agent(pp + (dt * 4 + i) * 64 + lane, o[dt][i]);
+    if (lr == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        st_agent(pp + 16 * HD + 4 * lg + i, Mq[i]);
+        st_agent(pp + 16 * HD + 16 + 4 * lg + i, Lq[i]);
+      }
+    }
+  }
+  if (!arrive_last(a.counters + g * gridDim.x + blockIdx.x, a.S, &flag_s)) return;
+  // the splits' m and l of this workgroup's query tiles, staged in LDS with all loads in flight at once
+  float* ml = reinterpret_cast<float*>(smem);  // [QPW][S][32]: m of rows 0..15, then l
+  const int nml = QPW * a.S * 32;
+  for (int idx = threadIdx.x; idx < nml; idx += blockDim.x) {
+    const int q = idx / (a.S * 32), rem = idx - q * (a.S * 32);
+    const int qt2 = blockIdx.x * QPW + q;
+    ml[idx] = qt2 < QT ? ld_agent(a.part + ((size_t)(g * QT + qt2) * a.S + (rem >> 5)) * PSZ + 16 * HD + (rem & 31))
+                       : 0.f;
+  }
+  __syncthreads();
+  if (!tile_ok) return;
+  // every wave of the last workgroup merges its query tile for dims [128 kg / KSW, 128 (kg + 1) / KSW)
+  const float* mlq = ml + qw * a.S * 32;
+  const float* pt = a.part + (size_t)(g * QT + qt) * a.S * PSZ;
+  constexpr int DPW = (HD / 16) / KSW;  // dim tiles per wave
+  float M[4], L[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = 4 * lg + i;
+    M[i] = -INFINITY;
+    for (int sp = 0; sp < a.S; ++sp) M[i] = fmaxf(M[i], mlq[sp * 32 + q]);
+    if (M[i] == -INFINITY) M[i] = 0.f;
+    L[i] = 0.f;
+    for (int sp = 0; sp < a.S; ++sp) L[i] += mlq[sp * 32 + 16 + q] * expf(mlq[sp * 32 + q] - M[i]);
+  }
+  float acc[DPW][4];
+#pragma unroll
+  for (int d = 0; d < DPW; ++d)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[d][i] = 0.f;
+  constexpr int SB = 8;  // splits whose partial O is requested before any is added
+  for (int s0 = 0; s0 < a.S; s0 += SB) {
+    float v[SB][DPW][4];
+#pragma unroll
+    for (int q = 0; q < SB; ++q)
+#pragma unroll
+      for (int d = 0; d < DPW; ++d)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          v[q][d][i] = s0 + q < a.S ? ld_agent(pt + (s0 + q) * PSZ + ((kg * DPW + d) * 4 + i) * 64 + lane) : 0.f;
+#pragma unroll
+    for (int q = 0; q < SB; ++q) {
+      if (s0 + q >= a.S) break;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float f = expf(mlq[(s0 + q) * 32 + 4 * lg + i] - M[i]);
+#pragma unroll
+        for (int d = 0; d < DPW; ++d) acc[d][i] += v[q][d][i] * f;
+      }
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < DPW; ++d)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) store_out(4 * lg + i, 16 * (kg * DPW + d) + lr, acc[d][i] / L[i]);
 }
 
-// Merge the key splits: out = sum_s exp(m_s - M) O_s / sum_s exp(m_s - M) l_s, cast once.
-template <int DT>
-__global__ __launch_bounds__(128) void attn_combine_kernel(AttnArgs a) {
-  const int r = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
-  const int grp = a.nq / a.nkv;
-  const int g = h / grp, hh = h - g * grp;
-  const int qi = hh * a.rows + r;
-  float M = -INFINITY;
-  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, a.m_part[(size_t)(s * a.nkv + g) * a.QRp + qi]);
-  const float Mu = M == -INFINITY ? 0.f : M;
-  float L = 0.f, acc = 0.f;
-  for (int s = 0; s < a.nsplit; ++s) {
-    const size_t b = (size_t)(s * a.nkv + g) * a.QRp + qi;
-    const float wgt = expf(a.m_part[b] - Mu);
-    L += a.l_part[b] * wgt;
-    acc += a.o_part[b * HD + d] * wgt;
-  }
-  a.out[(size_t)r * a.nq * HD + h * HD + d] = from_f32<DT>(acc / L);
+AttnShape attn_shape(int rows, int nq, int nkv) {
+  const int QT = ((nq / nkv) * rows + 15) / 16;
+  if (QT >= 32) return AttnShape{4, 1};  // long row blocks (prefill): many workgroups already
+  if (QT >= 3) return AttnShape{4, 2};
+  if (QT == 2) return AttnShape{2, 4};
+  return AttnShape{1, 4};
 }
 
-hipError_t launch_attention(int dt, const AttnArgs& a, int nqgroups, hipStream_t st) {
-  if (a.hd != HD) return hipErrorInvalidValue;
-  if (dt == DT_BF16) {
-    hipLaunchKernelGGL(attn_kernel<DT_BF16>, dim3(nqgroups, a.nkv, a.nsplit), dim3(256), 0, st, a);
-    hipLaunchKernelGGL(attn_combine_kernel<DT_BF16>, dim3(a.rows, a.nq), dim3(HD), 0, st, a);
-  } else {
-    hipLaunchKernelGGL(attn_kernel<DT_F16>, dim3(nqgroups, a.nkv, a.nsplit), dim3(256), 0, st, a);
-    hipLaunchKernelGGL(attn_combine_kernel<DT_F16>, dim3(a.rows, a.nq), dim3(HD), 0, st, a);
+size_t attn_partial_floats(const AttnP& a) {
+  const int QT = ((a.nq / a.nkv) * a.rows + 15) / 16;
+  return (size_t)a.nkv * QT * a.S * PSZ;
+}
+
+template <int DT, int QPW, int KSW>
+static hipError_t launch_shape(const AttnP& a, hipStream_t st) {
+  const int QT = ((a.nq / a.nkv) * a.rows + 15) / 16;
+  const int qg = (QT + QPW - 1) / QPW;
+  const size_t loop_lds = (size_t)KSW * (KB * KLD + HD * VLD) * 2;
+  const size_t merge_lds = (size_t)2 * KSW * QPW * 16 * 4 + (size_t)(KSW - 1) * QPW * (HD / 16) * 64 * 16;
+  const size_t split_lds = a.S > 1 ? (size_t)QPW * a.S * 32 * 4 : 0;
+  size_t lds = loop_lds > merge_lds ? loop_lds : merge_lds;
+  if (split_lds > lds) lds = split_lds;
+  auto kern = attn_kernel<DT, QPW, KSW>;
+  static size_t attr_lds = 64 * 1024;
+  if (lds > attr_lds) {
+    // a runtime that needs no attribute for LDS up to the device limit may reject it: clear that
+    // error and let the launch report whether the size fits
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess)
+      (void)hipGetLastError();
+    attr_lds = lds;
   }
+  hipLaunchKernelGGL(kern, dim3(qg, a.nkv, a.S), dim3(64 * QPW * KSW), lds, st, a);
   return hipGetLastError();
+}
+
+template <int DT>
+static hipError_t launch_dt(const AttnP& a, hipStream_t st) {
+  const AttnShape sh = attn_shape(a.rows, a.nq, a.nkv);
+  if (sh.q_tiles_per_wg == 4 && sh.key_groups == 1) return launch_shape<DT, 4, 1>(a, st);
+  if (sh.q_tiles_per_wg == 4) return launch_shape<DT, 4, 2>(a, st);
+  if (sh.q_tiles_per_wg == 2) return launch_shape<DT, 2, 4>(a, st);
+  return launch_shape<DT, 1, 4>(a, st);
+}
+
+hipError_t launch_attention(int dt, const AttnP& a, hipStream_t st) {
+  if (dt == DT_BF16) return launch_dt<DT_BF16>(a, st);
+  return launch_dt<DT_F16>(a, st);
 }
 
 }  // namespace fdllm

@@ -35,10 +35,12 @@ int fail(int code, const char* fmt, ...) {
   } while (0)
 
 struct Layer {
-  const uint16_t *wqkv, *bqkv, *wo, *wgu, *wd, *ln_in, *ln_post;
+  const uint16_t *wqkv, *bqkv, *wo, *wgu, *wd, *ln_in, *ln_post;  // caller's tensors
+  const uint16_t *pqkv, *po, *pgu, *pd;                           // packed copies (context-owned)
 };
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+int round_up(int x, int a) { return (x + a - 1) / a * a; }
 
 }  // namespace
 
@@ -52,24 +54,30 @@ struct fdllm_ctx {
   const uint16_t* embed = nullptr;
   const uint16_t* final_norm = nullptr;
   const uint16_t* lm_head = nullptr;
+  uint16_t* packed = nullptr;        // every packed weight matrix, one allocation
+  const uint16_t* plm = nullptr;     // packed lm_head
+  int lm_tiles = 0;
 
   // row workspace (grown on demand)
   int ws_rows = 0;
   void* ws = nullptr;
-  uint16_t *h = nullptr, *xn = nullptr, *qkv = nullptr, *qrot = nullptr, *attn = nullptr, *act = nullptr;
+  uint16_t *h = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr;
   uint16_t *kscr = nullptr, *vscr = nullptr;  // K/V of a stateless forward (one layer at a time)
-  // split-K partials / attention partials / confidence statistics (grown on demand)
+  float* ssq = nullptr;                       // [hidden / 16][ws_rows] row sums of squares per 16 columns
+  // split partials / confidence statistics (grown on demand)
   float* gpart = nullptr; size_t gpart_floats = 0;
   float* apart = nullptr; size_t apart_floats = 0;
   void* stats = nullptr; size_t stats_rows = 0;
-  int* counters = nullptr; int n_counters = 0;
+  unsigned* counters = nullptr; int n_counters = 0;
   int32_t* zero_i32 = nullptr;
-  int wg_target = 256;
+  int attn_target = 48;   // attention workgroups aimed for when splitting the keys
+  int down_split = 10;    // cross-workgroup k splits of the down projection (largest divisor of K/32 <= this)
 
   int qkv_dim() const { return (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim; }
   int q_dim() const { return cfg.num_attention_heads * cfg.head_dim; }
   int kv_dim() const { return cfg.num_key_value_heads * cfg.head_dim; }
   int tiles() const { return (cfg.vocab_size + 255) / 256; }
+  int ssq_tiles() const { return cfg.hidden_size / 16; }
 };
 
 namespace {
@@ -80,22 +88,29 @@ int ensure_rows(fdllm_ctx* c, int rows) {
   const fdllm_config& f = c->cfg;
   size_t e_h = (size_t)R * f.hidden_size, e_qkv = (size_t)R * c->qkv_dim(), e_q = (size_t)R * c->q_dim();
   size_t e_act = (size_t)R * f.intermediate_size, e_kv = (size_t)R * c->kv_dim();
-  size_t bytes = 2 * (align_up(e_h, 64) * 2 + align_up(e_qkv, 64) + align_up(e_q, 64) * 2 + align_up(e_act, 64) +
-                      align_up(e_kv, 64) * 2);
-  if (c->ws) HIPCHK(hipFree(c->ws));
+  size_t e_ssq = (size_t)c->ssq_tiles() * R * 2;  // floats as u16 pairs
+  size_t bytes = 2 * (align_up(e_h, 64) + align_up(e_qkv, 64) + align_up(e_q, 64) + align_up(e_act, 64) +
+                      align_up(e_kv, 64) * 2 + align_up(e_ssq, 64));
+  if (c->ws) {
+    HIPCHK(hipDeviceSynchronize());
+    HIPCHK(hipFree(c->ws));
+  }
   c->ws = nullptr;
   HIPCHK(hipMalloc(&c->ws, bytes));
   uint16_t* p = (uint16_t*)c->ws;
   auto take = [&](size_t n) { uint16_t* r = p; p += align_up(n, 64); return r; };
-  c->h = take(e_h); c->xn = take(e_h); c->qkv = take(e_qkv); c->qrot = take(e_q); c->attn = take(e_q);
-  c->act = take(e_act); c->kscr = take(e_kv); c->vscr = take(e_kv);
+  c->h = take(e_h); c->qkv = take(e_qkv); c->attn = take(e_q); c->act = take(e_act);
+  c->kscr = take(e_kv); c->vscr = take(e_kv); c->ssq = (float*)take(e_ssq);
   c->ws_rows = R;
   return FDLLM_OK;
 }
 
 int ensure_floats(float** buf, size_t* have, size_t need) {
   if (need <= *have) return FDLLM_OK;
-  if (*buf) HIPCHK(hipFree(*buf));
+  if (*buf) {
+    HIPCHK(hipDeviceSynchronize());
+    HIPCHK(hipFree(*buf));
+  }
   *buf = nullptr;
   size_t n = align_up(need, 1 << 20);
   HIPCHK(hipMalloc((void**)buf, n * sizeof(float)));
@@ -106,68 +121,59 @@ int ensure_floats(float** buf, size_t* have, size_t need) {
 int ensure_stats(fdllm_ctx* c, int rows) {
   if ((size_t)rows <= c->stats_rows) return FDLLM_OK;
   size_t R = align_up((size_t)std::max(rows, 32), 32);
-  if (c->stats) HIPCHK(hipFree(c->stats));
+  if (c->stats) {
+    HIPCHK(hipDeviceSynchronize());
+    HIPCHK(hipFree(c->stats));
+  }
   c->stats = nullptr;
   HIPCHK(hipMalloc(&c->stats, R * c->tiles() * 12));
   c->stats_rows = R;
   return FDLLM_OK;
 }
 
-// ---- launch planning -----------------------------------------------------------------------------
-struct Plan {
-  int tpw, mt, nblocks, ksplit, mchunks, kc, wg_rows, tile_stride;
-};
+// Packed tile counts of each projection (padded to whole workgroups of its launch configuration).
+int qkv_tiles(const fdllm_ctx* c) { return round_up(c->qkv_dim() / 16, gemm_shape(CFG_QKV).tiles_per_wg); }
+int o_tiles(const fdllm_ctx* c) { return round_up(c->cfg.hidden_size / 16, gemm_shape(CFG_OPROJ).tiles_per_wg); }
+int gu_tiles(const fdllm_ctx* c) { return round_up(2 * c->cfg.intermediate_size / 16, gemm_shape(CFG_GATE_UP).tiles_per_wg); }
+int d_tiles(const fdllm_ctx* c) { return round_up(c->cfg.hidden_size / 16, gemm_shape(CFG_DOWN).tiles_per_wg); }
+int lm_tiles_of(const fdllm_ctx* c) { return round_up((c->cfg.vocab_size + 15) / 16, gemm_shape(CFG_LM_HEAD).tiles_per_wg); }
 
-Plan plan_gemm(const fdllm_ctx* c, int M, int N, int K, int epi) {
-  Plan p{};
-  p.mt = M <= 16 ? 1 : 2;
-  p.mchunks = (M + 16 * p.mt - 1) / (16 * p.mt);
-  if (epi == EPI_SILU) {
-    p.tpw = 2; p.wg_rows = 64; p.tile_stride = N / 2; p.nblocks = (N / 2 + 63) / 64;
-  } else if (epi == EPI_LOGITS) {
-    p.tpw = 4; p.wg_rows = 256; p.tile_stride = 64; p.nblocks = (N + 255) / 256;
-  } else {
-    p.tpw = 2; p.wg_rows = 128; p.tile_stride = 64; p.nblocks = (N + 127) / 128;
-  }
-  if (epi == EPI_LOGITS) {  // one workgroup per 256-column confidence tile, whole K in LDS
-    p.ksplit = 1;
-    p.kc = K;
-    return p;
-  }
-  const int steps = K / 128;
-  int best = -1;
-  long best_cost = 0;
-  for (int d = 1; d <= steps; ++d) {
-    if (steps % d) continue;
-    int kc = K / d;
-    if (kc > 1024) continue;
-    long total = (long)p.nblocks * p.mchunks * d;
-    long cost = std::labs(total - c->wg_target) + (d > 1 ? (long)d * 4 : 0);
-    if (best < 0 || cost < best_cost) { best = d; best_cost = cost; }
-  }
-  p.ksplit = best < 0 ? 1 : best;
-  p.kc = K / p.ksplit;
-  return p;
+// Largest divisor of n that is <= cap (>= 1).
+int divisor_at_most(int n, int cap) {
+  for (int d = std::max(1, std::min(n, cap)); d > 1; --d)
+    if (n % d == 0) return d;
+  return 1;
 }
 
-int run_gemm(fdllm_ctx* c, int epi, const uint16_t* X, int ldx, int M, const uint16_t* W, int N, int K,
-             uint16_t* Y, int ldy, const uint16_t* bias, const uint16_t* resid, int ldr, float* logits, int ldl,
-             bool stats, hipStream_t st) {
-  if (K % 128 != 0) return fail(FDLLM_EINVAL, "GEMM K=%d is not a multiple of 128", K);
-  Plan p = plan_gemm(c, M, N, K, epi);
-  if (epi == EPI_LOGITS && p.kc > 2048) return fail(FDLLM_EINVAL, "hidden size %d too large for the lm_head kernel", K);
-  GemmArgs a{};
-  a.X = X; a.ldx = ldx; a.M = M; a.W = W; a.N = N; a.K = K; a.kc = p.kc;
-  a.wg_rows = p.wg_rows; a.tile_stride = p.tile_stride;
-  a.Y = Y; a.ldy = ldy; a.bias = bias; a.resid = resid; a.ldr = ldr; a.logits = logits; a.ldl = ldl;
-  if (p.ksplit > 1) {
-    size_t need = (size_t)p.nblocks * p.mchunks * p.ksplit * 4 * p.tpw * p.mt * 64 * 4;
+int run_gemm(fdllm_ctx* c, int cfg, GemmP a, int ksplit, hipStream_t st) {
+  const fdllm_config& f = c->cfg;
+  if (ksplit < 1 || a.KS % ksplit) return fail(FDLLM_EINVAL, "k split %d does not divide %d k steps", ksplit, a.KS);
+  a.kps = a.KS / ksplit;
+  const GemmShape sh = gemm_shape(cfg);
+  const int groups = (a.ntiles + sh.tiles_per_wg - 1) / sh.tiles_per_wg;
+  const int mchunks = (a.M + 31) / 32;
+  if (ksplit > 1) {
+    size_t need = (size_t)groups * mchunks * ksplit * sh.tiles_per_wg * 2 * 64 * 4;
     int rc = ensure_floats(&c->gpart, &c->gpart_floats, need);
     if (rc) return rc;
-    if (p.nblocks * p.mchunks > c->n_counters) return fail(FDLLM_EINVAL, "too many GEMM column blocks (%d)", p.nblocks * p.mchunks);
-    a.partial = c->gpart;
+    if (groups * mchunks > c->n_counters) return fail(FDLLM_EINVAL, "too many GEMM workgroup groups (%d)", groups * mchunks);
+    a.part = c->gpart;
     a.counters = c->counters;
   }
+  HIPCHK(launch_gemm(f.dtype, cfg, a, ksplit, st));
+  return FDLLM_OK;
+}
+
+GemmP gemm_args(const uint16_t* W, int ntiles, int N, int K, const uint16_t* X, int ldx, int M) {
+  GemmP a{};
+  a.W = W; a.KS = K / 32; a.ntiles = ntiles; a.N = N; a.X = X; a.ldx = ldx; a.M = M; a.kps = a.KS;
+  return a;
+}
+
+int run_lm_head(fdllm_ctx* c, const uint16_t* hidden, int rows, float* logits, bool stats, hipStream_t st) {
+  const fdllm_config& f = c->cfg;
+  GemmP a = gemm_args(c->plm, c->lm_tiles, f.vocab_size, f.hidden_size, hidden, f.hidden_size, rows);
+  a.logits = logits; a.ldl = f.vocab_size;
   if (stats) {
     int T = c->tiles();
     char* base = (char*)c->stats;
@@ -176,71 +182,82 @@ int run_gemm(fdllm_ctx* c, int epi, const uint16_t* X, int ldx, int M, const uin
     a.stat_s = (float*)(base + c->stats_rows * T * 8);
     a.stat_tiles = T;
   }
-  HIPCHK(launch_gemm(c->cfg.dtype, epi, p.tpw, p.mt, a, p.nblocks, p.ksplit, p.mchunks, st));
-  return FDLLM_OK;
+  return run_gemm(c, CFG_LM_HEAD, a, 1, st);
 }
 
-int run_attention(fdllm_ctx* c, int rows, const uint16_t* kc, const uint16_t* vc, int Lk, int mask, int q_pos0,
+int run_attention(fdllm_ctx* c, int rows, const int32_t* pos, uint16_t* kc, uint16_t* vc, int ws, int Lk, int mask,
                   const float* bias, long long bias_ld, hipStream_t st) {
   const fdllm_config& f = c->cfg;
-  AttnArgs a{};
-  a.q = c->qrot; a.k = kc; a.v = vc;
-  a.rows = rows; a.nq = f.num_attention_heads; a.nkv = f.num_key_value_heads; a.hd = f.head_dim;
-  a.Lk = Lk; a.scale = 1.0f / std::sqrt((float)f.head_dim);
-  a.mask = mask; a.q_pos0 = q_pos0; a.block = f.bd_size; a.bias = bias; a.bias_ld = bias_ld;
-  const int grp = a.nq / a.nkv;
-  const int QR = grp * rows;
-  const int qtiles = (QR + 15) / 16;
-  const int nqg = (qtiles + 3) / 4;
-  a.QRp = qtiles * 16;
-  int base = nqg * a.nkv;
-  int nsplit = std::max(1, std::min((c->wg_target + base - 1) / base, (Lk + 255) / 256));
-  int chunk = (int)align_up((size_t)((Lk + nsplit - 1) / nsplit), 64);
-  nsplit = (Lk + chunk - 1) / chunk;
-  a.nsplit = nsplit; a.chunk = chunk;
-  size_t per = (size_t)nsplit * a.nkv * a.QRp;
-  int rc = ensure_floats(&c->apart, &c->apart_floats, per * (a.hd + 2));
-  if (rc) return rc;
-  a.o_part = c->apart; a.m_part = c->apart + per * a.hd; a.l_part = a.m_part + per;
+  AttnP a{};
+  a.qkv = c->qkv; a.ldq = c->qkv_dim(); a.rows = rows; a.nq = f.num_attention_heads; a.nkv = f.num_key_value_heads;
+  a.pos_offset = pos; a.neg_log_theta = (float)(-std::log((double)f.rope_theta));
+  a.kc = kc; a.vc = vc; a.ws = ws; a.Lk = Lk; a.scale = 1.0f / std::sqrt((float)f.head_dim);
+  a.mask = mask; a.q_pos0 = 0; a.block = f.bd_size; a.bias = bias; a.bias_ld = bias_ld;
+  const AttnShape sh = attn_shape(rows, a.nq, a.nkv);
+  const int QT = ((a.nq / a.nkv) * rows + 15) / 16;
+  const int base = ((QT + sh.q_tiles_per_wg - 1) / sh.q_tiles_per_wg) * a.nkv;
+  const int max_splits = std::max(1, (Lk + 32 * sh.key_groups - 1) / (32 * sh.key_groups));
+  int S = std::min(max_splits, std::max(1, (c->attn_target + base - 1) / base));
+  int chunk = (int)align_up((size_t)((Lk + S - 1) / S), 32);
+  S = (Lk + chunk - 1) / chunk;
+  a.S = S; a.chunk = chunk;
+  if (S > 1) {
+    int rc = ensure_floats(&c->apart, &c->apart_floats, attn_partial_floats(a));
+    if (rc) return rc;
+    if (base > c->n_counters) return fail(FDLLM_EINVAL, "too many attention workgroup groups (%d)", base);
+    a.part = c->apart;
+    a.counters = c->counters;
+  }
   a.out = c->attn;
-  HIPCHK(launch_attention(f.dtype, a, nqg, st));
+  HIPCHK(launch_attention(f.dtype, a, st));
   return FDLLM_OK;
 }
 
 // The decoder-layer loop (cuda.py:561-579 per layer, 639-666 for the model).
-// kv: per-layer cache base pointers come from k/v + layer * layer_stride (elements).
+//   per layer: qkv (RMSNorm on load, + bias) -> attention (RoPE, KV append, GQA) -> o_proj + residual
+//              -> gate_up (RMSNorm on load, SiLU * up) -> down + residual
+// kv: per-layer cache base pointers are k/v + layer * layer_stride (elements).  out == nullptr skips
+// the final norm (build_prefix_cache returns only the caches).
 int run_layers(fdllm_ctx* c, const void* x_in, int rows, uint16_t* kbase, uint16_t* vbase, size_t layer_stride,
                int write_start, const int32_t* pos_dev, int attend_len, int mask, const float* bias,
                long long bias_ld, void* out, hipStream_t st) {
   const fdllm_config& f = c->cfg;
   const int H = f.hidden_size, I = f.intermediate_size;
-  HIPCHK(hipMemcpyAsync(c->h, x_in, (size_t)rows * H * 2, hipMemcpyDeviceToDevice, st));
+  const int ssq_ld = c->ws_rows;
+  HIPCHK(launch_load_rows(f.dtype, (const uint16_t*)x_in, rows, H, c->h, c->ssq, ssq_ld, st));
+  const int dsplit = divisor_at_most(I / 32, c->down_split);
   for (int l = 0; l < f.num_hidden_layers; ++l) {
     const Layer& L = c->layers[l];
     uint16_t* kc = kbase + (size_t)l * layer_stride;
     uint16_t* vc = vbase + (size_t)l * layer_stride;
-    HIPCHK(launch_rmsnorm(f.dtype, c->h, H, rows, H, L.ln_in, f.rms_norm_eps, c->xn, H, st));
-    int rc = run_gemm(c, EPI_BIAS, c->xn, H, rows, L.wqkv, c->qkv_dim(), H, c->qkv, c->qkv_dim(), L.bqkv, nullptr, 0,
-                      nullptr, 0, false, st);
+
+    GemmP q = gemm_args(L.pqkv, qkv_tiles(c), c->qkv_dim(), H, c->h, H, rows);
+    q.ssq = c->ssq; q.ssq_tiles = c->ssq_tiles(); q.ssq_ld = ssq_ld; q.nw = L.ln_in; q.eps = f.rms_norm_eps; q.H = H;
+    q.Y = c->qkv; q.ldy = c->qkv_dim(); q.bias = L.bqkv;
+    int rc = run_gemm(c, CFG_QKV, q, 1, st);
     if (rc) return rc;
-    RopeArgs ra{};
-    ra.qkv = c->qkv; ra.ld = c->qkv_dim(); ra.rows = rows; ra.nq = f.num_attention_heads;
-    ra.nkv = f.num_key_value_heads; ra.hd = f.head_dim; ra.pos_offset = pos_dev;
-    ra.neg_log_theta = (float)(-std::log((double)f.rope_theta));
-    ra.q_out = c->qrot; ra.k_cache = kc; ra.v_cache = vc; ra.write_start = write_start;
-    HIPCHK(launch_rope_kv(f.dtype, ra, st));
-    rc = run_attention(c, rows, kc, vc, attend_len, mask, 0, bias, bias_ld, st);
+
+    rc = run_attention(c, rows, pos_dev, kc, vc, write_start, attend_len, mask, bias, bias_ld, st);
     if (rc) return rc;
-    rc = run_gemm(c, EPI_RESID, c->attn, c->q_dim(), rows, L.wo, H, c->q_dim(), c->h, H, nullptr, c->h, H, nullptr, 0,
-                  false, st);
+
+    GemmP o = gemm_args(L.po, o_tiles(c), H, c->q_dim(), c->attn, c->q_dim(), rows);
+    o.Y = c->h; o.ldy = H; o.ssq_out = c->ssq; o.ssq_ld = ssq_ld;
+    rc = run_gemm(c, CFG_OPROJ, o, 1, st);
     if (rc) return rc;
-    HIPCHK(launch_rmsnorm(f.dtype, c->h, H, rows, H, L.ln_post, f.rms_norm_eps, c->xn, H, st));
-    rc = run_gemm(c, EPI_SILU, c->xn, H, rows, L.wgu, 2 * I, H, c->act, I, nullptr, nullptr, 0, nullptr, 0, false, st);
+
+    GemmP gu = gemm_args(L.pgu, gu_tiles(c), I, H, c->h, H, rows);
+    gu.ssq = c->ssq; gu.ssq_tiles = c->ssq_tiles(); gu.ssq_ld = ssq_ld; gu.nw = L.ln_post; gu.eps = f.rms_norm_eps;
+    gu.H = H; gu.Y = c->act; gu.ldy = I;
+    rc = run_gemm(c, CFG_GATE_UP, gu, 1, st);
     if (rc) return rc;
-    rc = run_gemm(c, EPI_RESID, c->act, I, rows, L.wd, H, I, c->h, H, nullptr, c->h, H, nullptr, 0, false, st);
+
+    GemmP d = gemm_args(L.pd, d_tiles(c), H, I, c->act, I, rows);
+    d.Y = c->h; d.ldy = H; d.ssq_out = c->ssq; d.ssq_ld = ssq_ld;
+    rc = run_gemm(c, CFG_DOWN, d, dsplit, st);
     if (rc) return rc;
   }
-  HIPCHK(launch_rmsnorm(f.dtype, c->h, H, rows, H, c->final_norm, f.rms_norm_eps, (uint16_t*)out, H, st));
+  if (out != nullptr)
+    HIPCHK(launch_norm_rows(f.dtype, c->h, rows, H, c->ssq, ssq_ld, c->final_norm, f.rms_norm_eps, (uint16_t*)out, st));
   return FDLLM_OK;
 }
 
@@ -275,6 +292,32 @@ int cached_step(fdllm_ctx* c, const void* x, int rows, void* k, void* v, int cap
                     nullptr, 0, out, (hipStream_t)stream);
 }
 
+int pack_all(fdllm_ctx* c) {
+  const fdllm_config& f = c->cfg;
+  const int H = f.hidden_size, I = f.intermediate_size;
+  const size_t per_layer = (size_t)qkv_tiles(c) * (H / 32) * 512 + (size_t)o_tiles(c) * (c->q_dim() / 32) * 512 +
+                           (size_t)gu_tiles(c) * (H / 32) * 512 + (size_t)d_tiles(c) * (I / 32) * 512;
+  c->lm_tiles = lm_tiles_of(c);
+  const size_t lm = (size_t)c->lm_tiles * (H / 32) * 512;
+  if (c->packed == nullptr) HIPCHK(hipMalloc((void**)&c->packed, (per_layer * f.num_hidden_layers + lm) * 2));
+  uint16_t* p = c->packed;
+  for (int l = 0; l < f.num_hidden_layers; ++l) {
+    Layer& L = c->layers[l];
+    HIPCHK(launch_pack(L.wqkv, c->qkv_dim(), H, qkv_tiles(c), PACK_ROWS, p, nullptr));
+    L.pqkv = p; p += (size_t)qkv_tiles(c) * (H / 32) * 512;
+    HIPCHK(launch_pack(L.wo, H, c->q_dim(), o_tiles(c), PACK_ROWS, p, nullptr));
+    L.po = p; p += (size_t)o_tiles(c) * (c->q_dim() / 32) * 512;
+    HIPCHK(launch_pack(L.wgu, 2 * I, H, gu_tiles(c), PACK_PAIRS, p, nullptr));
+    L.pgu = p; p += (size_t)gu_tiles(c) * (H / 32) * 512;
+    HIPCHK(launch_pack(L.wd, H, I, d_tiles(c), PACK_ROWS, p, nullptr));
+    L.pd = p; p += (size_t)d_tiles(c) * (I / 32) * 512;
+  }
+  HIPCHK(launch_pack(c->lm_head, f.vocab_size, H, c->lm_tiles, PACK_ROWS, p, nullptr));
+  c->plm = p;
+  HIPCHK(hipDeviceSynchronize());
+  return FDLLM_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -296,7 +339,8 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   fdllm_ctx* c = new fdllm_ctx();
   c->cfg = f;
   (void)hipGetDevice(&c->dev);
-  if (const char* e = std::getenv("FDLLM_WG_TARGET")) c->wg_target = std::max(1, atoi(e));
+  if (const char* e = std::getenv("FDLLM_ATTN_TARGET")) c->attn_target = std::max(1, atoi(e));
+  if (const char* e = std::getenv("FDLLM_DOWN_SPLIT")) c->down_split = std::max(1, atoi(e));
   c->names.push_back("model.embed_tokens.weight");
   for (int i = 0; i < f.num_hidden_layers; ++i) {
     std::string p = "model.layers." + std::to_string(i);
@@ -332,7 +376,7 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
 void fdllm_destroy(fdllm_ctx* c) {
   if (!c) return;
   (void)hipDeviceSynchronize();
-  for (void* p : {c->ws, (void*)c->gpart, (void*)c->apart, c->stats, (void*)c->counters})
+  for (void* p : {c->ws, (void*)c->gpart, (void*)c->apart, c->stats, (void*)c->counters, (void*)c->packed})
     if (p) (void)hipFree(p);
   delete c;
 }
@@ -354,10 +398,13 @@ int fdllm_bind_weights(fdllm_ctx* c, const void* const* ptrs, int n) {
   c->layers.resize(c->cfg.num_hidden_layers);
   for (int i = 0; i < c->cfg.num_hidden_layers; ++i) {
     const uint16_t* const* p = &c->params[1 + 7 * i];
-    c->layers[i] = Layer{p[0], p[1], p[2], p[3], p[4], p[5], p[6]};
+    c->layers[i] = Layer{p[0], p[1], p[2], p[3], p[4], p[5], p[6], nullptr, nullptr, nullptr, nullptr};
   }
   c->final_norm = c->params[1 + 7 * c->cfg.num_hidden_layers];
   c->lm_head = c->cfg.tie_word_embeddings ? c->embed : c->params[2 + 7 * c->cfg.num_hidden_layers];
+  c->bound = false;
+  int rc = pack_all(c);
+  if (rc) return rc;
   c->bound = true;
   return FDLLM_OK;
 }
@@ -385,9 +432,7 @@ int fdllm_get_logits(fdllm_ctx* c, const void* hidden, int rows, float* logits, 
   int rc = check_ready(c);
   if (rc) return rc;
   if (rows <= 0 || !hidden || !logits) return fail(FDLLM_EINVAL, "invalid get_logits arguments");
-  const fdllm_config& f = c->cfg;
-  return run_gemm(c, EPI_LOGITS, (const uint16_t*)hidden, f.hidden_size, rows, c->lm_head, f.vocab_size,
-                  f.hidden_size, nullptr, 0, nullptr, nullptr, 0, logits, f.vocab_size, false, (hipStream_t)stream);
+  return run_lm_head(c, (const uint16_t*)hidden, rows, logits, false, (hipStream_t)stream);
 }
 
 int fdllm_build_prefix_cache(fdllm_ctx* c, const void* x, int P, const float* bias, void* k, void* v, int cap,
@@ -400,8 +445,8 @@ int fdllm_build_prefix_cache(fdllm_ctx* c, const void* x, int P, const float* bi
   if (rc) return rc;
   const fdllm_config& f = c->cfg;
   size_t stride = (size_t)cap * f.num_key_value_heads * f.head_dim;
-  // build_prefix_cache returns only the caches; the final hidden goes to scratch
-  return run_layers(c, x, P, (uint16_t*)k, (uint16_t*)v, stride, 0, c->zero_i32, P, bias ? 2 : 1, bias, P, c->xn,
+  // build_prefix_cache returns only the caches: no final norm
+  return run_layers(c, x, P, (uint16_t*)k, (uint16_t*)v, stride, 0, c->zero_i32, P, bias ? 2 : 1, bias, P, nullptr,
                     (hipStream_t)stream);
 }
 
@@ -438,10 +483,8 @@ int fdllm_get_confidence(fdllm_ctx* c, const void* hidden, int rows, int32_t* id
   if (rows <= 0 || !hidden || !ids || !maxp) return fail(FDLLM_EINVAL, "invalid get_confidence arguments");
   rc = ensure_stats(c, rows);
   if (rc) return rc;
-  const fdllm_config& f = c->cfg;
   hipStream_t st = (hipStream_t)stream;
-  rc = run_gemm(c, EPI_LOGITS, (const uint16_t*)hidden, f.hidden_size, rows, c->lm_head, f.vocab_size, f.hidden_size,
-                nullptr, 0, nullptr, nullptr, 0, logits, f.vocab_size, true, st);
+  rc = run_lm_head(c, (const uint16_t*)hidden, rows, logits, true, st);
   if (rc) return rc;
   int T = c->tiles();
   char* base = (char*)c->stats;
@@ -457,43 +500,54 @@ int fdllm_bench_op(fdllm_ctx* c, int op, int rows, int layer, int iters, void* k
   const fdllm_config& f = c->cfg;
   if (rows <= 0 || iters <= 0 || layer < 0 || layer >= f.num_hidden_layers)
     return fail(FDLLM_EINVAL, "invalid bench_op arguments");
+  if (op == FDLLM_OP_ATTENTION && (!k || !v || attend_len < rows || attend_len > cap))
+    return fail(FDLLM_EINVAL, "attention needs a cache holding attend_len >= rows rows");
   rc = ensure_rows(c, rows);
   if (rc == FDLLM_OK) rc = ensure_stats(c, rows);
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
-  const int H = f.hidden_size, I = f.intermediate_size;
+  const int H = f.hidden_size, I = f.intermediate_size, ssq_ld = c->ws_rows;
+  const size_t stride = (size_t)cap * f.num_key_value_heads * f.head_dim;
   for (int it = 0; it < iters && rc == FDLLM_OK; ++it) {
     // consecutive launches walk the layers, as a step does, so no weight is re-read from cache
     const int li = (layer + it) % f.num_hidden_layers;
     const Layer& L = c->layers[li];
     switch (op) {
-      case FDLLM_OP_QKV:
-        rc = run_gemm(c, EPI_BIAS, c->xn, H, rows, L.wqkv, c->qkv_dim(), H, c->qkv, c->qkv_dim(), L.bqkv, nullptr, 0,
-                      nullptr, 0, false, st);
-        break;
-      case FDLLM_OP_O_PROJ:
-        rc = run_gemm(c, EPI_RESID, c->attn, c->q_dim(), rows, L.wo, H, c->q_dim(), c->h, H, nullptr, c->h, H, nullptr,
-                      0, false, st);
-        break;
-      case FDLLM_OP_GATE_UP:
-        rc = run_gemm(c, EPI_SILU, c->xn, H, rows, L.wgu, 2 * I, H, c->act, I, nullptr, nullptr, 0, nullptr, 0, false,
-                      st);
-        break;
-      case FDLLM_OP_DOWN:
-        rc = run_gemm(c, EPI_RESID, c->act, I, rows, L.wd, H, I, c->h, H, nullptr, c->h, H, nullptr, 0, false, st);
-        break;
-      case FDLLM_OP_ATTENTION: {
-        if (!k || !v || attend_len <= 0 || attend_len > cap) return fail(FDLLM_EINVAL, "attention needs a cache");
-        size_t stride = (size_t)cap * f.num_key_value_heads * f.head_dim;
-        rc = run_attention(c, rows, (uint16_t*)k + (size_t)li * stride, (uint16_t*)v + (size_t)li * stride,
-                           attend_len, 0, 0, nullptr, 0, st);
+      case FDLLM_OP_QKV: {
+        GemmP q = gemm_args(L.pqkv, qkv_tiles(c), c->qkv_dim(), H, c->h, H, rows);
+        q.ssq = c->ssq; q.ssq_tiles = c->ssq_tiles(); q.ssq_ld = ssq_ld; q.nw = L.ln_in; q.eps = f.rms_norm_eps;
+        q.H = H; q.Y = c->qkv; q.ldy = c->qkv_dim(); q.bias = L.bqkv;
+        rc = run_gemm(c, CFG_QKV, q, 1, st);
         break;
       }
+      case FDLLM_OP_O_PROJ: {
+        GemmP o = gemm_args(L.po, o_tiles(c), H, c->q_dim(), c->attn, c->q_dim(), rows);
+        o.Y = c->h; o.ldy = H; o.ssq_out = c->ssq; o.ssq_ld = ssq_ld;
+        rc = run_gemm(c, CFG_OPROJ, o, 1, st);
+        break;
+      }
+      case FDLLM_OP_GATE_UP: {
+        GemmP gu = gemm_args(L.pgu, gu_tiles(c), I, H, c->h, H, rows);
+        gu.ssq = c->ssq; gu.ssq_tiles = c->ssq_tiles(); gu.ssq_ld = ssq_ld; gu.nw = L.ln_post;
+        gu.eps = f.rms_norm_eps; gu.H = H; gu.Y = c->act; gu.ldy = I;
+        rc = run_gemm(c, CFG_GATE_UP, gu, 1, st);
+        break;
+      }
+      case FDLLM_OP_DOWN: {
+        GemmP d = gemm_args(L.pd, d_tiles(c), H, I, c->act, I, rows);
+        d.Y = c->h; d.ldy = H; d.ssq_out = c->ssq; d.ssq_ld = ssq_ld;
+        rc = run_gemm(c, CFG_DOWN, d, divisor_at_most(I / 32, c->down_split), st);
+        break;
+      }
+      case FDLLM_OP_ATTENTION:
+        // the block's rows sit at the end of the attended range, as in a full cached step
+        rc = run_attention(c, rows, c->zero_i32, (uint16_t*)k + li * stride, (uint16_t*)v + li * stride,
+                           attend_len - rows, attend_len, 0, nullptr, 0, st);
+        break;
       case FDLLM_OP_LM_HEAD_CONFIDENCE: {
-        rc = run_gemm(c, EPI_LOGITS, c->xn, H, rows, c->lm_head, f.vocab_size, H, nullptr, 0, nullptr, nullptr, 0,
-                      nullptr, f.vocab_size, true, st);
+        rc = run_lm_head(c, c->h, rows, nullptr, true, st);
         if (rc) break;
-        int T = c->tiles();
+        const int T = c->tiles();
         char* base = (char*)c->stats;
         int32_t* ids = (int32_t*)c->qkv;
         float* maxp = (float*)(c->qkv + 64);

@@ -11,6 +11,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
 enum DType : int { DT_BF16 = 0, DT_F16 = 1 };
 
@@ -19,12 +20,8 @@ constexpr int WAVE = 64;
 // ---- scalar conversions (round to nearest even, as torch / cuBLAS casts do) -------------------
 __device__ __forceinline__ float bf16_to_f32(u16 h) { return __uint_as_float(((uint32_t)h) << 16); }
 
-__device__ __forceinline__ u16 f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u16)0x7fc0;  // NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (u16)(u >> 16);
-}
+// round to nearest even (v_cvt_pk_bf16_f32 on gfx950); NaN stays NaN
+__device__ __forceinline__ u16 f32_to_bf16(float f) { return __builtin_bit_cast(u16, (__bf16)f); }
 
 __device__ __forceinline__ float f16_to_f32(u16 h) {
   _Float16 v;
@@ -98,23 +95,56 @@ __device__ __forceinline__ float fd_exp_neg(float x) {
   return p * scale;
 }
 
-// ---- split-K fix-up: the last workgroup of a group to arrive reduces --------------------------
-// Returns true in every thread of the workgroup that arrived last.  Writers publish their partials
-// with a device-scope release before the arrival count; the last arriver acquires before reading.
-// The counter returns to zero, so a later launch (or a graph replay) starts from a clean state.
-__device__ __forceinline__ bool arrive_last(int* counter, int expected, int* lds_flag) {
-  __threadfence();
+// ---- agent-coherent exchange between workgroups of one launch ---------------------------------
+// Each XCD has its own write-back L2, so data one workgroup hands to another inside a launch is
+// written and read with agent-scope relaxed atomics (the sc1 cache policy: written through to memory,
+// read past a possibly stale L2 line) instead of plain accesses plus a release fence, whose L2
+// write-back costs ~20 us per launch on MI355X.  A writer waits for its stores to be acknowledged
+// (s_waitcnt vmcnt(0)) before it signals.
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent4(f32x4* p, f32x4 v) {
+  typedef unsigned long long u64;
+  u64* q = reinterpret_cast<u64*>(p);
+  __hip_atomic_store(q, __builtin_bit_cast(u64, f32x2_t{v[0], v[1]}), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(q + 1, __builtin_bit_cast(u64, f32x2_t{v[2], v[3]}), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ f32x4 ld_agent4(const f32x4* p) {
+  typedef unsigned long long u64;
+  u64* q = reinterpret_cast<u64*>(const_cast<f32x4*>(p));
+  f32x2_t lo = __builtin_bit_cast(f32x2_t, __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  f32x2_t hi = __builtin_bit_cast(f32x2_t, __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  return f32x4{lo[0], lo[1], hi[0], hi[1]};
+}
+__device__ __forceinline__ void wait_memory() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Split fix-up: returns true in every thread of the workgroup that arrived last of `expected`.
+// Callers write their partials with st_agent* first; the last arriver reads them with ld_agent*.
+// The counter is returned to zero, so the next launch starts clean.
+__device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned expected, int* lds_flag) {
+  wait_memory();
   __syncthreads();
   if (threadIdx.x == 0) {
-    int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     int last = (old == expected - 1);
-    if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *lds_flag = last;
   }
   __syncthreads();
-  bool last = *lds_flag != 0;
-  if (last) __threadfence();
-  return last;
+  return *lds_flag != 0;
 }
+
+// ---- bf16/fp16 pairs packed in 32-bit words ---------------------------------------------------
+template <int DT> __device__ __forceinline__ float lo_f32(uint32_t w) { return to_f32<DT>((u16)(w & 0xffffu)); }
+template <int DT> __device__ __forceinline__ float hi_f32(uint32_t w) { return to_f32<DT>((u16)(w >> 16)); }
+__device__ __forceinline__ uint32_t pack2(u16 a, u16 b) { return (uint32_t)a | ((uint32_t)b << 16); }
 
 }  // namespace fdllm

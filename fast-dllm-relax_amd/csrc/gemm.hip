@@ -1,147 +1,229 @@
-// Skinny projection GEMMs of the cached step: Y[M, N] = X[M, K] . W[N, K]^T, M <= 32 per m-chunk.
+// Skinny projection GEMMs of the cached step over packed weights: Y[M, N] = X[M, K] . W[N, K]^T with
+// M <= 32 rows per m-chunk (gridDim.z), fp32 accumulation on MFMA 16x16x32.
 //
-// The weights stream from HBM once; the activations of one k-slice sit in LDS.  Each wave owns TPW
-// tiles of 16 weight rows and all m-chunk rows; per 32-wide k step a lane loads 16 contiguous bytes of
-// one weight row (A operand) and 16 bytes of one activation row from LDS (B operand), so the MFMA
-// produces C^T[n, m] and each lane ends with 4 consecutive output columns of one row.
-// Split-K over gridDim.y: partials go to a workspace and the last workgroup of a column block to
-// arrive sums them in split order (deterministic) and runs the epilogue.
+// Work split.  A workgroup owns TW x TPW consecutive 16-row weight tiles and the k steps of one
+// cross-workgroup split (gridDim.y).  Its TW x KW waves are arranged as TW tile columns times KW k
+// partitions: wave (tw, kw) streams its TPW tiles' packed 1 KB blocks for its share of the k steps,
+// U steps per load group, double-buffered, and multiplies them with the matching activation
+// fragments (B operand, read from the row-major activations and transformed on the fly).  The KW
+// partial sums are added in LDS in fixed order; gridDim.y > 1 splits are added by the workgroup that
+// arrives last, in split order, so every result is deterministic.
 //
 // Epilogues follow the reference's rounding points (fast_dllm_relax/model/cuda.py):
-//   EPI_STORE   y = rnd(acc)                                  o_proj alone, down alone
-//   EPI_BIAS    y = rnd(acc + b[n])                           qkv_proj + bias (cuda.py:389-399)
-//   EPI_RESID   y = rnd(r + rnd(acc))                         o_proj / down_proj + residual (cuda.py:577-578)
-//   EPI_SILU    y = rnd(rnd(silu(rnd(g))) * rnd(u))           gate_up + _silu_fp32 * up (cuda.py:319-348)
-//   EPI_LOGITS  logits fp32 = rnd(acc), plus per-256-column confidence tile statistics (cuda.py:704-711)
+//   EPI_BIAS       y = rnd(acc + b[n])                              qkv_proj + bias (cuda.py:389-399)
+//   EPI_RESID      h = rnd(h + rnd(acc)), plus row sums of squares  o_proj / down_proj + residual
+//                  of the new h per 16-column tile for the next RMSNorm   (cuda.py:561-579)
+//   EPI_SILU_PAIR  act = rnd(rnd(silu(rnd(g))) * rnd(u))             gate_up + _silu_fp32 * up (cuda.py:319-348)
+//   EPI_LOGITS     logits fp32 = rnd(acc) and per-256-column confidence statistics (cuda.py:704-711)
+// XF_RMS applies FastDLLMRMSNorm (cuda.py:269-275) to the activations as they are loaded:
+//   x' = rnd(w[k] * rnd(x * inv_rms[m])), inv_rms from the sums of squares the producer left.
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace fdllm {
 
-template <int DT, int EPI, int TPW, int MT>
-__global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs a) {
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  u16* xs = reinterpret_cast<u16*>(smem_raw);
-  __shared__ int last_flag;
+__device__ __forceinline__ const u32x4* wblock(const u16* W, int KS, int t, int s) {
+  return reinterpret_cast<const u32x4*>(W + ((size_t)t * KS + s) * 512) + (threadIdx.x & 63);
+}
+
+template <int DT, int XF>
+__device__ __forceinline__ u32x4 xform(u32x4 raw, u32x4 wv, float inv) {
+  if constexpr (XF == XF_NONE) {
+    return raw;
+  } else {
+    u32x4 o;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float y0 = lo_f32<DT>(wv[c]) * rnd<DT>(lo_f32<DT>(raw[c]) * inv);
+      float y1 = hi_f32<DT>(wv[c]) * rnd<DT>(hi_f32<DT>(raw[c]) * inv);
+      o[c] = pack2(from_f32<DT>(y0), from_f32<DT>(y1));
+    }
+    return o;
+  }
+}
+
+template <int DT, int EPI, int XF, int MT, int TPW, int TW, int KW, int U>
+__global__ __launch_bounds__(64 * TW * KW) void gemm_pk_kernel(GemmP a) {
+  __shared__ float inv_s[32];
+  __shared__ int flag_s;
+  extern __shared__ __align__(16) unsigned char smem[];
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int tw = w % TW, kw = w / TW;
   const int lr = lane & 15, lg = lane >> 4;
-  const int kc = a.kc;
-  const int k0 = blockIdx.y * kc;
-  const int m0 = blockIdx.z * 16 * MT;
-  const int xld = kc + 8;
+  const int m0 = blockIdx.z * 32;
+  const int t0 = (blockIdx.x * TW + tw) * TPW;
+  const int kq = a.kps / KW, kr = a.kps % KW;
+  const int wb = blockIdx.y * a.kps + kw * kq + min(kw, kr);
+  const int wn = kq + (kw < kr ? 1 : 0);
 
-  // stage the activation k-slice: rows m0 .. m0 + 16 MT (zero past M)
-  {
-    const int per_row = kc / 8;
-    for (int idx = threadIdx.x; idx < 16 * MT * per_row; idx += 256) {
-      int m = idx / per_row, c = idx - m * per_row;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (m0 + m < a.M) v = *reinterpret_cast<const u32x4*>(a.X + (size_t)(m0 + m) * a.ldx + k0 + c * 8);
-      *reinterpret_cast<u32x4*>(xs + m * xld + c * 8) = v;
-    }
-  }
-
-  const int row_base = blockIdx.x * a.wg_rows + w * 16;
-  const u16* wp[TPW];
+  // Every load below is unconditional and in bounds, so the compiler can count outstanding loads
+  // exactly and keep the next group in flight while this one is multiplied: rows past M read row M - 1
+  // (their products land in output rows that are discarded) and the prefetch past the last group
+  // re-reads the last group.
+  const int ngf = wn / U;  // full groups of U k steps; the rest run one step at a time
+  const int mlast = a.M - 1;
+  // a group's operands: weight blocks A, activation fragments X and (XF_RMS) the norm weights N
+  constexpr int UN = XF == XF_RMS ? U : 1;
+  u32x4 A0[U][TPW], A1[U][TPW], X0[U][MT], X1[U][MT], N0[UN], N1[UN];
+  auto load = [&](int g, u32x4(&A)[U][TPW], u32x4(&X)[U][MT], u32x4(&Nw)[UN]) {
 #pragma unroll
-  for (int j = 0; j < TPW; ++j) {
-    int r = row_base + j * a.tile_stride + lr;
-    r = r < a.N ? r : a.N - 1;
-    wp[j] = a.W + (size_t)r * a.K + k0 + lg * 8;
+    for (int u = 0; u < U; ++u) {
+      const int s = wb + g * U + u;
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) A[u][j] = __builtin_nontemporal_load(wblock(a.W, a.KS, t0 + j, s));
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = min(m0 + 16 * mt + lr, mlast);
+        X[u][mt] = *reinterpret_cast<const u32x4*>(a.X + (size_t)m * a.ldx + 32 * s + 8 * lg);
+      }
+      if constexpr (XF == XF_RMS) Nw[u] = *reinterpret_cast<const u32x4*>(a.nw + 32 * s + 8 * lg);
+    }
+  };
+  if (ngf > 0) load(0, A0, X0, N0);
+
+  float inv[MT];
+  if constexpr (XF == XF_RMS) {
+    // inv_rms of the chunk's 32 rows: 8 threads per row each add every 8th tile's sum of squares (all
+    // loads in flight at once), then a fixed-order butterfly over the 8
+    static_assert(64 * TW * KW >= 256, "the RMS prologue needs 256 threads");
+    if (threadIdx.x < 256) {
+      const int mr = threadIdx.x >> 3, pp = threadIdx.x & 7;
+      const int m = m0 + mr;
+      float v[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int t = pp + 8 * q;
+        v[q] = (m < a.M && t < a.ssq_tiles) ? a.ssq[(size_t)t * a.ssq_ld + m] : 0.f;
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) ss += v[q];
+      for (int q = 16; pp + 8 * q < a.ssq_tiles; ++q) ss += (m < a.M) ? a.ssq[(size_t)(pp + 8 * q) * a.ssq_ld + m] : 0.f;
+      ss += __shfl_xor(ss, 1, WAVE);
+      ss += __shfl_xor(ss, 2, WAVE);
+      ss += __shfl_xor(ss, 4, WAVE);
+      if (pp == 0) inv_s[mr] = 1.0f / sqrtf(ss / (float)a.H + a.eps);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) inv[mt] = inv_s[16 * mt + lr];
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) inv[mt] = 1.f;
   }
-  __syncthreads();
 
   f32x4 acc[TPW][MT];
 #pragma unroll
   for (int j = 0; j < TPW; ++j)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[j][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  constexpr int U = 4;  // k steps per group
-  const int ng = kc / (32 * U);
-  u32x4 A0[U][TPW], A1[U][TPW];
-  auto load = [&](int g, u32x4(&dst)[U][TPW]) {
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int j = 0; j < TPW; ++j)
-        dst[u][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp[j] + (g * U + u) * 32));
-  };
-  auto comp = [&](int g, u32x4(&src)[U][TPW]) {
+  auto comp = [&](u32x4(&A)[U][TPW], u32x4(&X)[U][MT], u32x4(&Nw)[UN]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       u32x4 b[MT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        b[mt] = *reinterpret_cast<const u32x4*>(xs + (16 * mt + lr) * xld + (g * U + u) * 32 + lg * 8);
+      for (int mt = 0; mt < MT; ++mt) b[mt] = xform<DT, XF>(X[u][mt], Nw[XF == XF_RMS ? u : 0], inv[mt]);
 #pragma unroll
       for (int j = 0; j < TPW; ++j)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[j][mt] = mfma16<DT>(src[u][j], b[mt], acc[j][mt]);
+        for (int mt = 0; mt < MT; ++mt) acc[j][mt] = mfma16<DT>(A[u][j], b[mt], acc[j][mt]);
     }
   };
-  load(0, A0);
-  int g = 0;
-  for (; g + 1 < ng; g += 2) {
-    load(g + 1, A1);
-    comp(g, A0);
-    if (g + 2 < ng) load(g + 2, A0);
-    comp(g + 1, A1);
+  // the scheduling barriers keep each prefetch ahead of the multiply it overlaps (the scheduler would
+  // otherwise sink the loads below it and leave only one group in flight)
+  for (int g = 0; g < ngf; g += 2) {
+    load(min(g + 1, ngf - 1), A1, X1, N1);
+    __builtin_amdgcn_sched_barrier(0);
+    comp(A0, X0, N0);
+    __builtin_amdgcn_sched_barrier(0);
+    load(min(g + 2, ngf - 1), A0, X0, N0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (g + 1 < ngf) comp(A1, X1, N1);
+    __builtin_amdgcn_sched_barrier(0);
   }
-  if (g < ng) comp(g, A0);
+  for (int s = wb + ngf * U; s < wb + wn; ++s) {  // remainder, one k step at a time
+    u32x4 A[TPW], b[MT];
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) A[j] = __builtin_nontemporal_load(wblock(a.W, a.KS, t0 + j, s));
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = min(m0 + 16 * mt + lr, mlast);
+      const u32x4 wv = XF == XF_RMS ? *reinterpret_cast<const u32x4*>(a.nw + 32 * s + 8 * lg) : u32x4{0u, 0u, 0u, 0u};
+      b[mt] = xform<DT, XF>(*reinterpret_cast<const u32x4*>(a.X + (size_t)m * a.ldx + 32 * s + 8 * lg), wv, inv[mt]);
+    }
+#pragma unroll
+    for (int j = 0; j < TPW; ++j)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[j][mt] = mfma16<DT>(A[j], b[mt], acc[j][mt]);
+  }
 
-  // ---- split-K fix-up ----
+  // ---- k partitions of the workgroup, added in LDS in fixed order ----
+  if constexpr (KW > 1) {
+    f32x4* red = reinterpret_cast<f32x4*>(smem);
+    if (kw > 0) {
+#pragma unroll
+      for (int j = 0; j < TPW; ++j)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) red[((((kw - 1) * TW + tw) * TPW + j) * MT + mt) * 64 + lane] = acc[j][mt];
+    }
+    __syncthreads();
+    if (kw == 0) {
+      for (int q = 1; q < KW; ++q)
+#pragma unroll
+        for (int j = 0; j < TPW; ++j)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) acc[j][mt] += red[((((q - 1) * TW + tw) * TPW + j) * MT + mt) * 64 + lane];
+    }
+  }
+
+  // ---- cross-workgroup k splits: the last arriver adds them in split order ----
   if (gridDim.y > 1) {
-    const size_t per_wg = (size_t)4 * TPW * MT * 64;  // f32x4 per workgroup
     const size_t grp = (size_t)blockIdx.z * gridDim.x + blockIdx.x;
-    f32x4* part = reinterpret_cast<f32x4*>(a.partial) + (grp * gridDim.y) * per_wg;
+    const size_t per = (size_t)TW * TPW * MT * 64;
+    f32x4* part = reinterpret_cast<f32x4*>(a.part) + grp * gridDim.y * per;
+    if (kw == 0) {
 #pragma unroll
-    for (int j = 0; j < TPW; ++j)
+      for (int j = 0; j < TPW; ++j)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        part[blockIdx.y * per_wg + ((w * TPW + j) * MT + mt) * 64 + lane] = acc[j][mt];
-    if (!arrive_last(a.counters + grp, gridDim.y, &last_flag)) return;
+        for (int mt = 0; mt < MT; ++mt)
+          st_agent4(part + blockIdx.y * per + ((tw * TPW + j) * MT + mt) * 64 + lane, acc[j][mt]);
+    }
+    if (!arrive_last(a.counters + grp, gridDim.y, &flag_s)) return;
+    if (kw == 0) {
+      // every split's partial is requested before any is added (one memory round trip per 16 splits)
+      constexpr int SB = 16;
 #pragma unroll
-    for (int j = 0; j < TPW; ++j)
+      for (int j = 0; j < TPW; ++j)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        f32x4 s = part[((w * TPW + j) * MT + mt) * 64 + lane];
-        for (int y = 1; y < (int)gridDim.y; ++y) s += part[y * per_wg + ((w * TPW + j) * MT + mt) * 64 + lane];
-        acc[j][mt] = s;
-      }
+        for (int mt = 0; mt < MT; ++mt) {
+          const size_t o = ((tw * TPW + j) * MT + mt) * 64 + lane;
+          f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int y0 = 0; y0 < (int)gridDim.y; y0 += SB) {
+            f32x4 v[SB];
+#pragma unroll
+            for (int q = 0; q < SB; ++q)
+              v[q] = y0 + q < (int)gridDim.y ? ld_agent4(part + (y0 + q) * per + o) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int q = 0; q < SB; ++q)
+              if (y0 + q < (int)gridDim.y) s = (y0 + q == 0) ? v[q] : s + v[q];
+          }
+          acc[j][mt] = s;
+        }
+    }
   }
 
   // ---- epilogues ----
-  if constexpr (EPI == EPI_SILU) {
-    // tile 0 = gate rows n, tile 1 = up rows n + tile_stride
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      int m = m0 + 16 * mt + lr;
-      int n = row_base + 4 * lg;
-      if (m >= a.M || n >= a.tile_stride) continue;
-      u16 out[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float gt = rnd<DT>(acc[0][mt][i]);
-        float up = rnd<DT>(acc[1][mt][i]);
-        float s = rnd<DT>(gt * (1.0f / (1.0f + expf(-gt))));
-        out[i] = from_f32<DT>(s * up);
-      }
-      u32x2 pk = {(uint32_t)out[0] | ((uint32_t)out[1] << 16), (uint32_t)out[2] | ((uint32_t)out[3] << 16)};
-      *reinterpret_cast<u32x2*>(a.Y + (size_t)m * a.ldy + n) = pk;
-    }
-  } else if constexpr (EPI == EPI_LOGITS) {
-    // logits (optional) and 256-column confidence tile statistics; one workgroup = one tile
-    float* tile = reinterpret_cast<float*>(smem_raw);  // [16 MT][256], reuses the activation slice
-    __syncthreads();
+  if constexpr (EPI == EPI_LOGITS) {
+    // one workgroup = one 256-column confidence tile (TW * TPW == 16)
+    float* tile = reinterpret_cast<float*>(smem);  // [32][256]
 #pragma unroll
     for (int j = 0; j < TPW; ++j)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        int m = 16 * mt + lr;
-        int nl = w * 16 + j * a.tile_stride + 4 * lg;  // column inside the 256-wide tile
-        int n = blockIdx.x * a.wg_rows + nl;
+        const int m = 16 * mt + lr;
+        const int nl = 16 * (tw * TPW + j) + 4 * lg;
+        const int n = blockIdx.x * 256 + nl;
         float v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = rnd<DT>(acc[j][mt][i]);
@@ -151,6 +233,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs a) {
           if (n + 3 < a.N) {
             *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
           } else {
+#pragma unroll
             for (int i = 0; i < 4; ++i)
               if (n + i < a.N) dst[i] = v[i];
           }
@@ -159,23 +242,22 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs a) {
     if (a.stat_m == nullptr) return;
     __syncthreads();
     const int n0 = blockIdx.x * 256;
-    const int tiles = a.stat_tiles;
-    for (int m = w; m < 16 * MT; m += 4) {
+    for (int m = w; m < 16 * MT; m += TW * KW) {
       if (m0 + m >= a.M) break;
       const float* row = tile + m * 256;
       float vmax = -INFINITY;
       int amax = 0x7fffffff;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        int c = lane + 64 * i;
+        const int c = lane + 64 * i;
         if (n0 + c < a.N) {
-          float x = row[c];
+          const float x = row[c];
           if (x > vmax) { vmax = x; amax = n0 + c; }
         }
       }
       for (int k = 32; k >= 1; k >>= 1) {
-        float ov = __shfl_xor(vmax, k, WAVE);
-        int oa = __shfl_xor(amax, k, WAVE);
+        const float ov = __shfl_xor(vmax, k, WAVE);
+        const int oa = __shfl_xor(amax, k, WAVE);
         if (ov > vmax || (ov == vmax && oa < amax)) { vmax = ov; amax = oa; }
       }
       float s;
@@ -184,39 +266,68 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs a) {
         s = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          int c = lane + 64 * i;
+          const int c = lane + 64 * i;
           if (n0 + c < a.N) s = s + fd_exp_neg(row[c] - vmax);
         }
         for (int k = 32; k >= 1; k >>= 1) s = s + __shfl_xor(s, k, WAVE);
       }
       if (lane == 0) {
-        size_t o = (size_t)(m0 + m) * tiles + blockIdx.x;
+        const size_t o = (size_t)(m0 + m) * a.stat_tiles + blockIdx.x;
         a.stat_m[o] = vmax;
         a.stat_a[o] = amax;
         a.stat_s[o] = s;
       }
     }
+  } else if constexpr (EPI == EPI_SILU_PAIR) {
+    if (kw != 0) return;
+    const int p = t0 / 2;  // tiles t0 (gate) and t0 + 1 (up) of pair p
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = m0 + 16 * mt + lr;
+      const int n = 16 * p + 4 * lg;
+      if (m >= a.M || n >= a.N) continue;
+      u16 out[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float gt = rnd<DT>(acc[0][mt][i]);
+        const float up = rnd<DT>(acc[1][mt][i]);
+        const float sl = rnd<DT>(gt * (1.0f / (1.0f + expf(-gt))));
+        out[i] = from_f32<DT>(sl * up);
+      }
+      *reinterpret_cast<u32x2*>(a.Y + (size_t)m * a.ldy + n) = u32x2{pack2(out[0], out[1]), pack2(out[2], out[3])};
+    }
   } else {
+    if (kw != 0) return;
 #pragma unroll
     for (int j = 0; j < TPW; ++j)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        int m = m0 + 16 * mt + lr;
-        int n = row_base + j * a.tile_stride + 4 * lg;
-        if (m >= a.M || n >= a.N) continue;
+        const int m = m0 + 16 * mt + lr;
+        const int n = 16 * (t0 + j) + 4 * lg;
+        const bool ok = m < a.M && n < a.N;
         u16 out[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float v = acc[j][mt][i];
+        float ss = 0.f;
+        if (ok) {
           if constexpr (EPI == EPI_BIAS) {
-            v = rnd<DT>(v + to_f32<DT>(a.bias[n + i]));
-          } else if constexpr (EPI == EPI_RESID) {
-            v = to_f32<DT>(a.resid[(size_t)m * a.ldr + n + i]) + rnd<DT>(v);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) out[i] = from_f32<DT>(acc[j][mt][i] + to_f32<DT>(a.bias[n + i]));
+          } else {
+            const u32x2 hv = *reinterpret_cast<const u32x2*>(a.Y + (size_t)m * a.ldy + n);
+            const float hf[4] = {lo_f32<DT>(hv[0]), hi_f32<DT>(hv[0]), lo_f32<DT>(hv[1]), hi_f32<DT>(hv[1])};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              out[i] = from_f32<DT>(hf[i] + rnd<DT>(acc[j][mt][i]));
+              const float y = to_f32<DT>(out[i]);
+              ss += y * y;
+            }
           }
-          out[i] = from_f32<DT>(v);
+          *reinterpret_cast<u32x2*>(a.Y + (size_t)m * a.ldy + n) = u32x2{pack2(out[0], out[1]), pack2(out[2], out[3])};
         }
-        u32x2 pk = {(uint32_t)out[0] | ((uint32_t)out[1] << 16), (uint32_t)out[2] | ((uint32_t)out[3] << 16)};
-        *reinterpret_cast<u32x2*>(a.Y + (size_t)m * a.ldy + n) = pk;
+        if constexpr (EPI == EPI_RESID) {
+          ss += __shfl_xor(ss, 16, WAVE);
+          ss += __shfl_xor(ss, 32, WAVE);
+          if (lg == 0 && m < a.M && 16 * (t0 + j) < a.N) a.ssq_out[(size_t)(t0 + j) * a.ssq_ld + m] = ss;
+        }
       }
   }
 }
@@ -234,17 +345,17 @@ __global__ __launch_bounds__(64) void confidence_combine_kernel(const float* sta
   float vmax = -INFINITY;
   int amax = 0x7fffffff;
   for (int t = lane; t < tiles; t += 64) {
-    float x = m[t];
+    const float x = m[t];
     if (x > vmax) { vmax = x; amax = am[t]; }
   }
   for (int k = 32; k >= 1; k >>= 1) {
-    float ov = __shfl_xor(vmax, k, WAVE);
-    int oa = __shfl_xor(amax, k, WAVE);
+    const float ov = __shfl_xor(vmax, k, WAVE);
+    const int oa = __shfl_xor(amax, k, WAVE);
     if (ov > vmax || (ov == vmax && oa < amax)) { vmax = ov; amax = oa; }
   }
   float acc = 0.0f;
   for (int t = lane; t < tiles; t += 64) {
-    float wgt = s[t] * fd_exp_neg(m[t] - vmax);
+    const float wgt = s[t] * fd_exp_neg(m[t] - vmax);
     acc = acc + wgt;
   }
   for (int k = 32; k >= 1; k >>= 1) acc = acc + __shfl_xor(acc, k, WAVE);
@@ -264,68 +375,120 @@ __global__ __launch_bounds__(64) void confidence_tiles_kernel(const float* logit
   float vmax = -INFINITY;
   int amax = 0x7fffffff;
   for (int i = 0; i < 4; ++i) {
-    int c = n0 + lane + 64 * i;
+    const int c = n0 + lane + 64 * i;
     if (c < vocab) {
-      float x = row[c];
+      const float x = row[c];
       if (x > vmax) { vmax = x; amax = c; }
     }
   }
   for (int k = 32; k >= 1; k >>= 1) {
-    float ov = __shfl_xor(vmax, k, WAVE);
-    int oa = __shfl_xor(amax, k, WAVE);
+    const float ov = __shfl_xor(vmax, k, WAVE);
+    const int oa = __shfl_xor(amax, k, WAVE);
     if (ov > vmax || (ov == vmax && oa < amax)) { vmax = ov; amax = oa; }
   }
   float s = 0.0f;
   for (int i = 0; i < 4; ++i) {
-    int c = n0 + lane + 64 * i;
+    const int c = n0 + lane + 64 * i;
     if (c < vocab) s = s + fd_exp_neg(row[c] - vmax);
   }
   for (int k = 32; k >= 1; k >>= 1) s = s + __shfl_xor(s, k, WAVE);
   if (lane == 0) {
-    size_t o = (size_t)r * tiles + t;
+    const size_t o = (size_t)r * tiles + t;
     stat_m[o] = vmax;
     stat_a[o] = amax;
     stat_s[o] = s;
   }
 }
 
-// ---- launchers ---------------------------------------------------------------------------------
-template <int DT, int EPI, int TPW, int MT>
-static hipError_t launch_one(const GemmArgs& a, int nblocks, int ksplit, int mchunks, hipStream_t st) {
-  size_t lds = (size_t)16 * MT * (a.kc + 8) * 2;
-  if (EPI == EPI_LOGITS && lds < (size_t)16 * MT * 256 * 4) lds = (size_t)16 * MT * 256 * 4;
-  auto kern = gemm_skinny_kernel<DT, EPI, TPW, MT>;
-  static size_t attr_lds = 64 * 1024;  // the launch limit without the attribute
-  if (lds > attr_lds) {
-    // a runtime that needs no attribute for LDS up to the device limit may reject it: clear that
-    // error and let the launch itself report whether the size fits
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)lds) != hipSuccess)
-      (void)hipGetLastError();
-    attr_lds = lds;
+// Weight repack into fragment order (one thread per 16-byte output chunk).
+__global__ __launch_bounds__(256) void pack_kernel(const u16* src, int N, int K, size_t total, int mode, u16* dst) {
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= total) return;
+  const int KS = K / 32;
+  const int l = (int)(idx & 63);
+  const size_t ts = idx >> 6;
+  const int s = (int)(ts % KS);
+  const int t = (int)(ts / KS);
+  const int r = l & 15, g = l >> 4;
+  int row;
+  bool ok;
+  if (mode == PACK_PAIRS) {
+    const int half = N / 2;
+    const int i = 16 * (t >> 1) + r;
+    ok = i < half;
+    row = (t & 1) ? half + i : i;
+  } else {
+    row = 16 * t + r;
+    ok = row < N;
   }
-  hipLaunchKernelGGL(kern, dim3(nblocks, ksplit, mchunks), dim3(256), lds, st, a);
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (ok) v = *reinterpret_cast<const u32x4*>(src + (size_t)row * K + 32 * s + 8 * g);
+  *reinterpret_cast<u32x4*>(dst + idx * 8) = v;
+}
+
+// ---- launchers ---------------------------------------------------------------------------------
+template <int EPI, int XF, int TPW, int TW, int KW, int U>
+struct Cfg {
+  static constexpr int epi = EPI, xf = XF, tpw = TPW, tw = TW, kw = KW, u = U;
+};
+using CfgQkv = Cfg<EPI_BIAS, XF_RMS, 1, 1, 8, 3>;
+using CfgOproj = Cfg<EPI_RESID, XF_NONE, 1, 1, 8, 3>;
+using CfgGateUp = Cfg<EPI_SILU_PAIR, XF_RMS, 2, 2, 2, 4>;
+using CfgDown = Cfg<EPI_RESID, XF_NONE, 1, 4, 2, 4>;
+using CfgLmHead = Cfg<EPI_LOGITS, XF_NONE, 4, 4, 1, 2>;
+
+template <class C> constexpr GemmShape shape_of() { return GemmShape{C::tpw * C::tw, C::tw * C::kw}; }
+
+GemmShape gemm_shape(int cfg) {
+  switch (cfg) {
+    case CFG_QKV: return shape_of<CfgQkv>();
+    case CFG_OPROJ: return shape_of<CfgOproj>();
+    case CFG_GATE_UP: return shape_of<CfgGateUp>();
+    case CFG_DOWN: return shape_of<CfgDown>();
+    default: return shape_of<CfgLmHead>();
+  }
+}
+
+template <int DT, class C, int MT>
+static hipError_t launch_cfg(const GemmP& a, int ksplit, hipStream_t st) {
+  constexpr int tiles = C::tpw * C::tw;
+  const int groups = (a.ntiles + tiles - 1) / tiles;
+  const int mchunks = (a.M + 31) / 32;
+  size_t lds = 0;
+  if (C::kw > 1) lds = (size_t)(C::kw - 1) * C::tw * C::tpw * MT * 64 * 16;
+  if (C::epi == EPI_LOGITS) lds = (size_t)32 * 256 * 4;
+  auto kern = gemm_pk_kernel<DT, C::epi, C::xf, MT, C::tpw, C::tw, C::kw, C::u>;
+  hipLaunchKernelGGL(kern, dim3(groups, ksplit, mchunks), dim3(64 * C::tw * C::kw), lds, st, a);
   return hipGetLastError();
 }
 
-template <int DT>
-static hipError_t gemm_dispatch(int epi, int tpw, int mt, const GemmArgs& a, int nblocks, int ksplit, int mchunks,
-                                hipStream_t st) {
-#define FD_CASE(E, T, M_) \
-  if (epi == E && tpw == T && mt == M_) return launch_one<DT, E, T, M_>(a, nblocks, ksplit, mchunks, st);
-  FD_CASE(EPI_STORE, 2, 1) FD_CASE(EPI_STORE, 2, 2)
-  FD_CASE(EPI_BIAS, 2, 1) FD_CASE(EPI_BIAS, 2, 2)
-  FD_CASE(EPI_RESID, 2, 1) FD_CASE(EPI_RESID, 2, 2)
-  FD_CASE(EPI_SILU, 2, 1) FD_CASE(EPI_SILU, 2, 2)
-  FD_CASE(EPI_LOGITS, 4, 1) FD_CASE(EPI_LOGITS, 4, 2)
-#undef FD_CASE
-  return hipErrorInvalidValue;
+template <int DT, class C>
+static hipError_t launch_mt(const GemmP& a, int ksplit, hipStream_t st) {
+  if (a.M <= 16) return launch_cfg<DT, C, 1>(a, ksplit, st);
+  return launch_cfg<DT, C, 2>(a, ksplit, st);
 }
 
-hipError_t launch_gemm(int dt, int epi, int tpw, int mt, const GemmArgs& a, int nblocks, int ksplit, int mchunks,
-                       hipStream_t st) {
-  if (dt == DT_BF16) return gemm_dispatch<DT_BF16>(epi, tpw, mt, a, nblocks, ksplit, mchunks, st);
-  return gemm_dispatch<DT_F16>(epi, tpw, mt, a, nblocks, ksplit, mchunks, st);
+template <int DT>
+static hipError_t launch_dt(int cfg, const GemmP& a, int ksplit, hipStream_t st) {
+  switch (cfg) {
+    case CFG_QKV: return launch_mt<DT, CfgQkv>(a, ksplit, st);
+    case CFG_OPROJ: return launch_mt<DT, CfgOproj>(a, ksplit, st);
+    case CFG_GATE_UP: return launch_mt<DT, CfgGateUp>(a, ksplit, st);
+    case CFG_DOWN: return launch_mt<DT, CfgDown>(a, ksplit, st);
+    case CFG_LM_HEAD: return launch_mt<DT, CfgLmHead>(a, ksplit, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_gemm(int dt, int cfg, const GemmP& a, int ksplit, hipStream_t st) {
+  if (dt == DT_BF16) return launch_dt<DT_BF16>(cfg, a, ksplit, st);
+  return launch_dt<DT_F16>(cfg, a, ksplit, st);
+}
+
+hipError_t launch_pack(const uint16_t* src, int N, int K, int ntiles, int mode, uint16_t* dst, hipStream_t st) {
+  const size_t total = (size_t)ntiles * (K / 32) * 64;
+  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, src, N, K, total, mode, dst);
+  return hipGetLastError();
 }
 
 hipError_t launch_confidence_combine(const float* sm, const int32_t* sa, const float* ss, int tiles, int rows,
@@ -336,7 +499,7 @@ hipError_t launch_confidence_combine(const float* sm, const int32_t* sa, const f
 
 hipError_t launch_confidence_tiles(const float* logits, int ld, int vocab, int rows, float* sm, int32_t* sa,
                                    float* ss, hipStream_t st) {
-  int tiles = (vocab + 255) / 256;
+  const int tiles = (vocab + 255) / 256;
   hipLaunchKernelGGL(confidence_tiles_kernel, dim3(tiles, rows), dim3(64), 0, st, logits, ld, vocab, tiles, sm, sa, ss);
   return hipGetLastError();
 }

@@ -5,61 +5,79 @@
 
 namespace fdllm {
 
-enum Epilogue : int { EPI_STORE = 0, EPI_BIAS = 1, EPI_RESID = 2, EPI_SILU = 3, EPI_LOGITS = 4 };
+// ---- packed weights ----------------------------------------------------------------------------
+// A weight matrix W [N, K] (nn.Linear layout) is repacked once, at bind time, into MFMA fragment
+// order: tile t (16 rows), k step s (32 columns) is one contiguous 1 KB block in which lane l holds
+// W[16 t + l % 16][32 s + 8 (l / 16) .. + 8].  A wave then streams whole 1 KB blocks with one
+// coalesced load each.  Tiles past the last row are zero.  PACK_PAIRS interleaves the two halves of
+// the fused gate_up matrix: packed tile 2p = gate rows [16p, 16p + 16), tile 2p + 1 = the matching
+// up rows [I + 16p, ...), so one wave holds both operands of the SiLU * up product.
+enum PackMode : int { PACK_ROWS = 0, PACK_PAIRS = 1 };
+hipError_t launch_pack(const uint16_t* src, int N, int K, int ntiles, int mode, uint16_t* dst, hipStream_t st);
 
-struct GemmArgs {
+// ---- skinny GEMM over packed weights ------------------------------------------------------------
+// Y[M, N] = X[M, K] . W[N, K]^T for M <= 32 per m-chunk (gridDim.z chunks of 32 rows).
+enum Epilogue : int { EPI_BIAS = 0, EPI_RESID = 1, EPI_SILU_PAIR = 2, EPI_LOGITS = 3 };
+enum XForm : int { XF_NONE = 0, XF_RMS = 1 };
+
+struct GemmP {
+  const uint16_t* W; int KS;          // packed weights, k steps (K / 32)
+  int ntiles;                         // packed tiles (the launch covers them all)
+  int N;                              // output columns written (rows of W; gate_up: I)
   const uint16_t* X; int ldx; int M;  // activations [M][ldx]
-  const uint16_t* W; int N; int K;    // weights [N][K] (nn.Linear layout)
-  int kc;                             // k elements per split (multiple of 128)
-  int wg_rows;                        // weight rows advanced per workgroup along blockIdx.x
-  int tile_stride;                    // row distance between the tiles of one wave
-  float* partial;                     // split-K partials
-  int* counters;                      // split-K arrival counters (zero between launches)
-  uint16_t* Y; int ldy;               // output
+  int kps;                            // k steps per cross-workgroup split (KS / gridDim.y)
+  // XF_RMS: X is normalized on the fly with inv_rms[m] = 1 / sqrt(sum_t ssq[t][m] / H + eps)
+  const float* ssq; int ssq_tiles; int ssq_ld; const uint16_t* nw; float eps; int H;
+  uint16_t* Y; int ldy;               // EPI_BIAS / EPI_SILU_PAIR output
   const uint16_t* bias;               // EPI_BIAS
-  const uint16_t* resid; int ldr;     // EPI_RESID (may alias Y)
+  float* ssq_out;                     // EPI_RESID: Y (= h, updated in place) + per-tile row sums of squares
   float* logits; int ldl;             // EPI_LOGITS (optional)
-  float* stat_m; int32_t* stat_a; float* stat_s; int stat_tiles;  // EPI_LOGITS confidence tiles
+  float* stat_m; int32_t* stat_a; float* stat_s; int stat_tiles;  // EPI_LOGITS confidence statistics
+  float* part; unsigned* counters;    // cross-workgroup split partials / arrival counters
 };
 
-hipError_t launch_gemm(int dt, int epi, int tpw, int mt, const GemmArgs& a, int nblocks, int ksplit, int mchunks,
-                       hipStream_t st);
+// Launch configurations (see gemm.hip); the host picks one per projection.
+enum GemmCfg : int { CFG_QKV = 0, CFG_OPROJ = 1, CFG_GATE_UP = 2, CFG_DOWN = 3, CFG_LM_HEAD = 4 };
+struct GemmShape { int tiles_per_wg; int waves; };
+GemmShape gemm_shape(int cfg);
+hipError_t launch_gemm(int dt, int cfg, const GemmP& a, int ksplit, hipStream_t st);
+
+// ---- confidence ---------------------------------------------------------------------------------
 hipError_t launch_confidence_combine(const float* sm, const int32_t* sa, const float* ss, int tiles, int rows,
                                      int32_t* ids, float* maxp, hipStream_t st);
 hipError_t launch_confidence_tiles(const float* logits, int ld, int vocab, int rows, float* sm, int32_t* sa,
                                    float* ss, hipStream_t st);
 
+// ---- row kernels --------------------------------------------------------------------------------
 hipError_t launch_embed(const int32_t* ids, int n, const uint16_t* table, int vocab, int hidden, uint16_t* out,
                         hipStream_t st);
-hipError_t launch_rmsnorm(int dt, const uint16_t* x, int ldx, int rows, int hidden, const uint16_t* w, float eps,
-                          uint16_t* y, int ldy, hipStream_t st);
+// copy the input rows into the residual stream and emit their per-16-column sums of squares
+hipError_t launch_load_rows(int dt, const uint16_t* x, int rows, int hidden, uint16_t* h, float* ssq, int ssq_ld,
+                            hipStream_t st);
+// y = RMSNorm(h) from the sums of squares the producer left (final norm)
+hipError_t launch_norm_rows(int dt, const uint16_t* h, int rows, int hidden, const float* ssq, int ssq_ld,
+                            const uint16_t* w, float eps, uint16_t* y, hipStream_t st);
 
-struct RopeArgs {
-  const uint16_t* qkv; int ld;       // [R][ld]: q | k | v, pre-RoPE, bias added
-  int rows, nq, nkv, hd;
-  const int32_t* pos_offset;         // device int32: absolute position of row 0
-  float neg_log_theta;               // (float)(-ln(theta))
-  uint16_t* q_out;                   // [R][nq * hd]
-  uint16_t* k_cache; uint16_t* v_cache;  // this layer's [cap][nkv][hd]
-  int write_start;                   // first cache row written
-};
-hipError_t launch_rope_kv(int dt, const RopeArgs& a, hipStream_t st);
-
-struct AttnArgs {
-  const uint16_t* q;                 // [R][nq * hd] rotated queries
-  const uint16_t* k; const uint16_t* v;  // this layer's cache [>= Lk][nkv][hd]
-  int rows, nq, nkv, hd;
-  int Lk;                            // attended rows [0, Lk)
+// ---- attention ----------------------------------------------------------------------------------
+struct AttnP {
+  const uint16_t* qkv; int ldq;       // [rows][ldq]: q | k | v, bias added, before RoPE
+  int rows, nq, nkv;
+  const int32_t* pos_offset;          // device int32: RoPE position of row 0
+  float neg_log_theta;                // (float)(-ln(theta))
+  uint16_t* kc; uint16_t* vc;         // this layer's cache [cap][nkv][128]
+  int ws;                             // rows [ws, ws + rows) are this call's: taken from qkv, written to the cache
+  int Lk;                             // attended keys [0, Lk)
   float scale;
-  int mask;                          // 0 none, 1 block-causal, 2 additive bias
-  int q_pos0;                        // absolute position of query row 0 (block-causal)
-  int block;                         // block size (block-causal)
-  const float* bias; long long bias_ld;  // bias[r * ld + key] (mask 2)
-  int nsplit, chunk;                 // key splits (gridDim.z) and keys per split (multiple of 64)
-  float* o_part; float* m_part; float* l_part;  // [nsplit][nkv][QRp][hd], [nsplit][nkv][QRp]
-  int QRp;                           // padded rows per kv head (multiple of 16)
-  uint16_t* out;                     // [R][nq * hd]
+  int mask;                           // 0 none, 1 block-causal, 2 additive bias
+  int q_pos0; int block;              // block-causal: query row r sits at q_pos0 + r
+  const float* bias; long long bias_ld;
+  int S, chunk;                       // key splits (gridDim.z), keys per split (multiple of 32)
+  float* part; unsigned* counters;    // split partials / arrival counters
+  uint16_t* out;                      // [rows][nq * 128]
 };
-hipError_t launch_attention(int dt, const AttnArgs& a, int nqgroups, hipStream_t st);
+struct AttnShape { int q_tiles_per_wg; int key_groups; };
+AttnShape attn_shape(int rows, int nq, int nkv);
+hipError_t launch_attention(int dt, const AttnP& a, hipStream_t st);
+size_t attn_partial_floats(const AttnP& a);
 
 }  // namespace fdllm

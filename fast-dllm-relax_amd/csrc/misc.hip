@@ -1,4 +1,4 @@
-// Row kernels of the cached step: embedding gather, RMSNorm, RoPE + KV-cache append.
+// Row kernels of the cached step: embedding gather, residual-stream load, final RMSNorm.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -16,64 +16,50 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t* ids, const u1
   for (int c = threadIdx.x; c < hidden / 8; c += blockDim.x) dst[c] = src[c];
 }
 
-// FastDLLMRMSNorm (cuda.py:269-275): fp32 mean of squares, x * 1/sqrt(var + eps) cast to the model
-// dtype, then the weight multiply in the model dtype.
+// The residual stream h starts as a copy of the input rows; each thread of the first H / 16 also
+// leaves the sum of squares of one 16-column tile of its row for the first layer's RMSNorm (the
+// layers' own residual epilogues leave the same statistics for the next norm).
 template <int DT>
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const u16* x, int ldx, int hidden, const u16* w, float eps,
-                                                      u16* y, int ldy) {
-  __shared__ float red[4];
+__global__ __launch_bounds__(256) void load_rows_kernel(const u16* x, int hidden, u16* h, float* ssq, int ssq_ld) {
   const int r = blockIdx.x;
-  const u16* xr = x + (size_t)r * ldx;
-  float ss = 0.f;
-  for (int c = threadIdx.x; c < hidden; c += 256) {
-    float v = to_f32<DT>(xr[c]);
-    ss += v * v;
-  }
-  ss = wave_sum(ss);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-  __syncthreads();
-  float tot = (red[0] + red[1]) + (red[2] + red[3]);
-  float inv = 1.0f / sqrtf(tot / (float)hidden + eps);
-  u16* yr = y + (size_t)r * ldy;
-  for (int c = threadIdx.x; c < hidden; c += 256) {
-    float n = rnd<DT>(to_f32<DT>(xr[c]) * inv);
-    yr[c] = from_f32<DT>(to_f32<DT>(w[c]) * n);
+  const u32x4* src = reinterpret_cast<const u32x4*>(x + (size_t)r * hidden);
+  u32x4* dst = reinterpret_cast<u32x4*>(h + (size_t)r * hidden);
+  for (int c = threadIdx.x; c < hidden / 8; c += blockDim.x) dst[c] = src[c];
+  for (int t = threadIdx.x; t < hidden / 16; t += blockDim.x) {
+    const u32x4 a = src[2 * t], b = src[2 * t + 1];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float a0 = lo_f32<DT>(a[c]), a1 = hi_f32<DT>(a[c]);
+      ss += a0 * a0;
+      ss += a1 * a1;
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float b0 = lo_f32<DT>(b[c]), b1 = hi_f32<DT>(b[c]);
+      ss += b0 * b0;
+      ss += b1 * b1;
+    }
+    ssq[(size_t)t * ssq_ld + r] = ss;
   }
 }
 
-// RoPE at absolute positions pos_offset + r (cuda.py:278-316) for q and k, then the in-place KV-cache
-// append of k and v at rows [write_start, write_start + rows) (runtime.py:51-60).
+// FastDLLMRMSNorm (cuda.py:269-275) from the producer's sums of squares: fp32 mean of squares,
+// x * 1/sqrt(var + eps) cast to the model dtype, then the weight multiply in the model dtype.
 template <int DT>
-__global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs a) {
+__global__ __launch_bounds__(256) void norm_rows_kernel(const u16* h, int hidden, const float* ssq, int ssq_ld,
+                                                        const u16* w, float eps, u16* y) {
+  __shared__ float part_s[4];
   const int r = blockIdx.x;
-  const int half = a.hd / 2;
-  const float pos = (float)r + (float)(*a.pos_offset);
-  const u16* row = a.qkv + (size_t)r * a.ld;
-  const int nrot = (a.nq + a.nkv) * half;
-  const size_t crow = (size_t)(a.write_start + r) * a.nkv * a.hd;
-  for (int t = threadIdx.x; t < nrot; t += 256) {
-    const int head = t / half, i = t - head * half;
-    float e = (a.neg_log_theta * (float)i) / (float)half;
-    float inv_freq = expf(e);
-    float fr = pos * inv_freq;
-    float c = rnd<DT>(cosf(fr));
-    float s = rnd<DT>(sinf(fr));
-    const u16* src = row + head * a.hd;  // q heads, then k heads (contiguous in the qkv row)
-    float x1 = to_f32<DT>(src[i]), x2 = to_f32<DT>(src[i + half]);
-    u16 o1 = from_f32<DT>(rnd<DT>(x1 * c) + rnd<DT>(-x2 * s));
-    u16 o2 = from_f32<DT>(rnd<DT>(x2 * c) + rnd<DT>(x1 * s));
-    if (head < a.nq) {
-      u16* dst = a.q_out + (size_t)r * a.nq * a.hd + head * a.hd;
-      dst[i] = o1;
-      dst[i + half] = o2;
-    } else {
-      u16* dst = a.k_cache + crow + (head - a.nq) * a.hd;
-      dst[i] = o1;
-      dst[i + half] = o2;
-    }
-  }
-  const u16* vsrc = row + (a.nq + a.nkv) * a.hd;
-  for (int t = threadIdx.x; t < a.nkv * a.hd; t += 256) a.v_cache[crow + t] = vsrc[t];
+  float ss = 0.f;
+  for (int t = threadIdx.x; t < hidden / 16; t += 256) ss += ssq[(size_t)t * ssq_ld + r];
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part_s[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float inv = 1.0f / sqrtf(((part_s[0] + part_s[1]) + (part_s[2] + part_s[3])) / (float)hidden + eps);
+  const u16* hr = h + (size_t)r * hidden;
+  u16* yr = y + (size_t)r * hidden;
+  for (int c = threadIdx.x; c < hidden; c += 256) yr[c] = from_f32<DT>(to_f32<DT>(w[c]) * rnd<DT>(to_f32<DT>(hr[c]) * inv));
 }
 
 hipError_t launch_embed(const int32_t* ids, int n, const uint16_t* table, int vocab, int hidden, uint16_t* out,
@@ -82,20 +68,21 @@ hipError_t launch_embed(const int32_t* ids, int n, const uint16_t* table, int vo
   return hipGetLastError();
 }
 
-hipError_t launch_rmsnorm(int dt, const uint16_t* x, int ldx, int rows, int hidden, const uint16_t* w, float eps,
-                          uint16_t* y, int ldy, hipStream_t st) {
+hipError_t launch_load_rows(int dt, const uint16_t* x, int rows, int hidden, uint16_t* h, float* ssq, int ssq_ld,
+                            hipStream_t st) {
   if (dt == DT_BF16)
-    hipLaunchKernelGGL(rmsnorm_kernel<DT_BF16>, dim3(rows), dim3(256), 0, st, x, ldx, hidden, w, eps, y, ldy);
+    hipLaunchKernelGGL(load_rows_kernel<DT_BF16>, dim3(rows), dim3(256), 0, st, x, hidden, h, ssq, ssq_ld);
   else
-    hipLaunchKernelGGL(rmsnorm_kernel<DT_F16>, dim3(rows), dim3(256), 0, st, x, ldx, hidden, w, eps, y, ldy);
+    hipLaunchKernelGGL(load_rows_kernel<DT_F16>, dim3(rows), dim3(256), 0, st, x, hidden, h, ssq, ssq_ld);
   return hipGetLastError();
 }
 
-hipError_t launch_rope_kv(int dt, const RopeArgs& a, hipStream_t st) {
+hipError_t launch_norm_rows(int dt, const uint16_t* h, int rows, int hidden, const float* ssq, int ssq_ld,
+                            const uint16_t* w, float eps, uint16_t* y, hipStream_t st) {
   if (dt == DT_BF16)
-    hipLaunchKernelGGL(rope_kv_kernel<DT_BF16>, dim3(a.rows), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(norm_rows_kernel<DT_BF16>, dim3(rows), dim3(256), 0, st, h, hidden, ssq, ssq_ld, w, eps, y);
   else
-    hipLaunchKernelGGL(rope_kv_kernel<DT_F16>, dim3(a.rows), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(norm_rows_kernel<DT_F16>, dim3(rows), dim3(256), 0, st, h, hidden, ssq, ssq_ld, w, eps, y);
   return hipGetLastError();
 }
 

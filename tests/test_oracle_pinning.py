@@ -1,0 +1,233 @@
+"""Pins the CPU oracle to checks independent of its own formulas (CPU only).
+
+* the local ``transformers`` Qwen2 implementation (an independent restatement of the architecture the
+  reference's model/cuda.py follows) on the same weights, in fp32: dense block-causal forward and a
+  cached block step against a DynamicCache prefix;
+* the reference's own invariants (tests/test_tiny_compile.py:264-290): cached rows equal the dense
+  block-causal rows, and each partial rp step equals the full step's rows for the same tokens;
+* closed forms: RoPE at position 0 is the identity, preserves norms and makes q.k depend only on the
+  position difference; RMSNorm with unit weights has unit RMS; torch's GQA scaled_dot_product_attention;
+* the confidence / unmask rules against float64 softmax, numpy argmax and a brute-force restatement of
+  runtime.py:794-805.
+A planted mistake in the oracle (a dropped bias, a wrong RoPE sign, a transposed projection, the wrong
+KV head for a query head, a shift in the wrong direction) fails at least one of these.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import confidence as oconf
+from oracle.model import (OracleConfig, OracleModel, build_prefix_block_attention_bias, extract_shifted_block_logits,
+                          random_params)
+from oracle.runtime import greedy_generate
+
+CFG1 = dict(vocab_size=512, hidden_size=64, intermediate_size=128, num_hidden_layers=2, num_attention_heads=4,
+            num_key_value_heads=2, head_dim=16)
+
+
+@pytest.fixture(scope="module")
+def tiny32():
+    cfg = OracleConfig(**CFG1)
+    arrays = random_params(cfg, 0, "float32")
+    return cfg, arrays, OracleModel(cfg, arrays, "float32")
+
+
+def _hf_model(cfg: OracleConfig, arrays):
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    hc = Qwen2Config(vocab_size=cfg.vocab_size, hidden_size=cfg.hidden_size, intermediate_size=cfg.intermediate_size,
+                     num_hidden_layers=cfg.num_hidden_layers, num_attention_heads=cfg.num_attention_heads,
+                     num_key_value_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim, rms_norm_eps=cfg.rms_norm_eps,
+                     rope_theta=cfg.rope_theta, tie_word_embeddings=True, max_position_embeddings=4096,
+                     attn_implementation="eager")
+    model = Qwen2ForCausalLM(hc).eval()
+    qd, kd, inter = cfg.num_attention_heads * cfg.head_dim, cfg.num_key_value_heads * cfg.head_dim, cfg.intermediate_size
+    sd = {"model.embed_tokens.weight": arrays["model.embed_tokens.weight"], "model.norm.weight": arrays["model.norm.weight"]}
+    for i in range(cfg.num_hidden_layers):
+        p = f"model.layers.{i}"
+        w, b = arrays[f"{p}.self_attn.qkv_proj.weight"], arrays[f"{p}.self_attn.qkv_proj.bias"]
+        sd[f"{p}.self_attn.q_proj.weight"], sd[f"{p}.self_attn.q_proj.bias"] = w[:qd], b[:qd]
+        sd[f"{p}.self_attn.k_proj.weight"], sd[f"{p}.self_attn.k_proj.bias"] = w[qd:qd + kd], b[qd:qd + kd]
+        sd[f"{p}.self_attn.v_proj.weight"], sd[f"{p}.self_attn.v_proj.bias"] = w[qd + kd:], b[qd + kd:]
+        sd[f"{p}.self_attn.o_proj.weight"] = arrays[f"{p}.self_attn.o_proj.weight"]
+        gu = arrays[f"{p}.mlp.gate_up_proj.weight"]
+        sd[f"{p}.mlp.gate_proj.weight"], sd[f"{p}.mlp.up_proj.weight"] = gu[:inter], gu[inter:]
+        sd[f"{p}.mlp.down_proj.weight"] = arrays[f"{p}.mlp.down_proj.weight"]
+        sd[f"{p}.input_layernorm.weight"] = arrays[f"{p}.input_layernorm.weight"]
+        sd[f"{p}.post_attention_layernorm.weight"] = arrays[f"{p}.post_attention_layernorm.weight"]
+    missing, unexpected = model.load_state_dict({k: torch.from_numpy(np.ascontiguousarray(v)) for k, v in sd.items()},
+                                                strict=False)
+    assert not unexpected and set(missing) <= {"lm_head.weight"}
+    return model
+
+
+def test_dense_forward_matches_transformers_qwen2(tiny32):
+    cfg, arrays, model = tiny32
+    hf = _hf_model(cfg, arrays)
+    ids = np.random.default_rng(0).integers(0, 510, 48)
+    bias = build_prefix_block_attention_bias(0, 48, block_size=32)
+    logits = model.get_logits(model.forward_hidden(model.embed(ids)[None], bias))
+    with torch.no_grad():
+        want = hf(input_ids=torch.from_numpy(ids)[None], attention_mask={"full_attention": torch.from_numpy(bias)},
+                  position_ids=torch.arange(48)[None]).logits.numpy()
+    # RoPE inverse frequencies differ by formula (exp(-ln theta * i / 64) vs theta^(-2i/d)) at fp32 rounding
+    np.testing.assert_allclose(logits, want, rtol=0, atol=1e-5)
+
+
+def test_cached_step_matches_transformers_dynamic_cache(tiny32):
+    from transformers import DynamicCache
+
+    cfg, arrays, model = tiny32
+    hf = _hf_model(cfg, arrays)
+    P, R = 32, 32
+    ids = np.random.default_rng(1).integers(0, 510, P + R)
+    kc = np.zeros((cfg.num_hidden_layers, 1, P + R, cfg.num_key_value_heads, cfg.head_dim), np.float32)
+    vc = np.zeros_like(kc)
+    model.build_prefix_cache(model.embed(ids[:P])[None], build_prefix_block_attention_bias(0, P, block_size=32), kc, vc)
+    got = model.get_logits(model.forward_cached(model.embed(ids[P:])[None], kc, vc, P, P))
+    with torch.no_grad():
+        cache = DynamicCache()
+        pre_bias = torch.from_numpy(build_prefix_block_attention_bias(0, P, block_size=32))
+        hf(input_ids=torch.from_numpy(ids[:P])[None], attention_mask={"full_attention": pre_bias},
+           position_ids=torch.arange(P)[None], past_key_values=cache, use_cache=True)
+        # the cached block sees the whole prefix and the whole block: an all-zero additive mask
+        want = hf(input_ids=torch.from_numpy(ids[P:])[None],
+                  attention_mask={"full_attention": torch.zeros((1, 1, R, P + R))},
+                  position_ids=torch.arange(P, P + R)[None], past_key_values=cache, use_cache=True).logits.numpy()
+    np.testing.assert_allclose(got, want, rtol=0, atol=1e-5)
+
+
+def test_cached_rows_equal_dense_block_causal_rows(tiny32):
+    """tests/test_tiny_compile.py:264-290, in fp32 (where the two paths agree to rounding)."""
+    cfg, _, model = tiny32
+    P, R = 64, 32
+    ids = np.random.default_rng(2).integers(0, 510, P + R)
+    dense = model.forward_hidden(model.embed(ids)[None], build_prefix_block_attention_bias(0, P + R, block_size=32))
+    kc = np.zeros((cfg.num_hidden_layers, 1, P + R, cfg.num_key_value_heads, cfg.head_dim), np.float32)
+    vc = np.zeros_like(kc)
+    model.build_prefix_cache(model.embed(ids[:P])[None], build_prefix_block_attention_bias(0, P, block_size=32), kc, vc)
+    cached = model.forward_cached(model.embed(ids[P:])[None], kc, vc, P, P)
+    np.testing.assert_allclose(cached, dense[:, P:], rtol=0, atol=2e-6)
+    for rp in (0, 8, 16, 24):
+        part = model.forward_block_partial(rp, model.embed(ids[P + rp:P + rp + 8])[None], kc, vc, P + rp, P)
+        np.testing.assert_allclose(part, cached[:, rp:rp + 8], rtol=0, atol=2e-6)
+
+
+def test_rope_closed_forms(tiny32):
+    cfg, _, model = tiny32
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((1, 2, cfg.head_dim)).astype(np.float32)
+    cos, sin = model.rope_tables(1, 0)
+    np.testing.assert_array_equal(model.apply_rope(x, cos, sin), x)  # position 0: identity
+    cos, sin = model.rope_tables(1, 777)
+    y = model.apply_rope(x, cos, sin)
+    np.testing.assert_allclose(np.linalg.norm(y, axis=-1), np.linalg.norm(x, axis=-1), rtol=1e-5)
+    # q(m).k(n) depends on m - n only, and the rotation direction matters (a sign flip breaks this)
+    q, k = rng.standard_normal((2, 1, 1, cfg.head_dim)).astype(np.float32)
+
+    def dot(m, n):
+        cm, sm = model.rope_tables(1, m)
+        cn, sn = model.rope_tables(1, n)
+        return float((model.apply_rope(q, cm, sm) * model.apply_rope(k, cn, sn)).sum())
+
+    assert abs(dot(10, 3) - dot(107, 100)) < 1e-4
+    # against the textbook rotation with theta^(-2i/d) frequencies
+    m = 5
+    half = cfg.head_dim // 2
+    inv = cfg.rope_theta ** (-np.arange(half, dtype=np.float64) * 2 / cfg.head_dim)
+    ang = m * inv
+    x1, x2 = x[0, 0, :half].astype(np.float64), x[0, 0, half:].astype(np.float64)
+    want = np.concatenate([x1 * np.cos(ang) - x2 * np.sin(ang), x2 * np.cos(ang) + x1 * np.sin(ang)])
+    cos, sin = model.rope_tables(1, m)
+    np.testing.assert_allclose(model.apply_rope(x[:, :1], cos, sin)[0, 0], want, rtol=0, atol=2e-5)
+
+
+def test_rmsnorm_unit_rms(tiny32):
+    cfg, _, model = tiny32
+    x = np.random.default_rng(4).standard_normal((5, cfg.hidden_size)).astype(np.float32) * 3
+    y = model.rmsnorm(x, np.ones(cfg.hidden_size, np.float32))
+    np.testing.assert_allclose(np.sqrt(np.mean(y.astype(np.float64) ** 2, axis=-1)), 1.0, rtol=1e-5)
+
+
+def test_attention_matches_torch_sdpa_gqa(tiny32):
+    cfg, _, model = tiny32
+    rng = np.random.default_rng(5)
+    n, m = 7, 19
+    q = rng.standard_normal((n, cfg.num_attention_heads, cfg.head_dim)).astype(np.float32)
+    k = rng.standard_normal((m, cfg.num_key_value_heads, cfg.head_dim)).astype(np.float32)
+    v = rng.standard_normal((m, cfg.num_key_value_heads, cfg.head_dim)).astype(np.float32)
+    got = model.attend(q, k, v)
+    want = torch.nn.functional.scaled_dot_product_attention(
+        torch.from_numpy(q).transpose(0, 1)[None], torch.from_numpy(k).transpose(0, 1)[None],
+        torch.from_numpy(v).transpose(0, 1)[None], enable_gqa=True)[0].transpose(0, 1).numpy()
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-6)
+
+
+def test_shift_and_block_bias_closed_forms():
+    bias = build_prefix_block_attention_bias(0, 96, block_size=32)[0, 0]
+    q, k = np.meshgrid(np.arange(96), np.arange(96), indexing="ij")
+    np.testing.assert_array_equal(bias == 0, (q // 32) >= (k // 32))
+    logits = np.arange(2 * 6 * 3, dtype=np.float32).reshape(1, 6, 6)[:, :, :3]
+    sh = extract_shifted_block_logits(logits, prefix_len=2, block_len=4)
+    np.testing.assert_array_equal(sh[0], logits[0, [1, 2, 3, 4]])
+    sh0 = extract_shifted_block_logits(logits, prefix_len=0, block_len=4)
+    np.testing.assert_array_equal(sh0[0], logits[0, [0, 0, 1, 2]])
+
+
+def test_exp_within_two_ulp_of_float64():
+    x = np.concatenate([-np.logspace(-8, math.log10(86.0), 2000), [0.0, -1e-30, -85.99]]).astype(np.float32)
+    got = oconf.exp_neg_array(x).astype(np.float64)
+    want = np.exp(x.astype(np.float64))
+    ulp = np.spacing(want.astype(np.float32)).astype(np.float64)
+    assert np.max(np.abs(got - want) / ulp) <= 2.0
+    assert oconf.exp_neg(-87.0) == 0.0
+
+
+@pytest.mark.parametrize("scale", [0.01, 1.0, 20.0])
+def test_confidence_against_float64_softmax(scale):
+    rng = np.random.default_rng(7)
+    rows, vocab = 9, 151936
+    x = (scale * rng.standard_normal((rows, vocab))).astype(np.float32)
+    x[3, 5] = x[3, 100000] = x[3].max() + 1  # tie: the first index wins
+    ids, maxp = oconf.confidence(x)
+    np.testing.assert_array_equal(ids, np.argmax(x, axis=-1))
+    z = x.astype(np.float64)
+    p = np.exp(z - z.max(-1, keepdims=True))
+    np.testing.assert_allclose(maxp, p.max(-1) / p.sum(-1), rtol=2e-6)
+
+
+def test_unmask_rule_brute_force():
+    rng = np.random.default_rng(8)
+    for _ in range(2000):
+        n = int(rng.integers(1, 9))
+        p = rng.random(n).astype(np.float32)
+        if rng.random() < 0.3:
+            p[rng.integers(0, n)] = np.float32(0.9)  # exactly at the threshold: not selected
+        masked = rng.random(n) < 0.6
+        got = oconf.unmask(p, masked, 0.9)
+        local = [i for i in range(n) if masked[i]]
+        rows = [r for r in local if p[r] > 0.9]
+        if not rows and local:
+            rows = [local[int(np.argmax([p[r] for r in local]))]]
+        want = np.zeros(n, bool)
+        want[rows] = True
+        np.testing.assert_array_equal(got, want)
+
+
+def test_decode_loop_block_cache_on_off_agree(tiny32):
+    """In fp32 the partial (block-cache) steps reproduce the full steps' rows, so the decode loop must
+    pick the same tokens with the block cache on or off (runtime.py:762-766)."""
+    cfg, _, model = tiny32
+    prompt = list(np.random.default_rng(9).integers(0, 510, 40))
+    common = dict(max_new_tokens=40, block_size=32, small_block_size=8, threshold=0.9, mask_id=511, stop_token=None)
+    on, st_on = greedy_generate(model, prompt, use_block_cache=True, **common)
+    off, st_off = greedy_generate(model, prompt, use_block_cache=False, **common)
+    # random weights may predict the mask id itself; the continuation then ends at it (runtime.py make_continuation)
+    assert on == off and len(on) > 0 and 511 not in on
+    assert st_on["partial_recomputes"] > 0 and st_off["partial_recomputes"] == 0
+    assert st_on["unmask_updates"] == st_off["unmask_updates"]
