@@ -18,6 +18,8 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <algorithm>
+
 namespace fdllm {
 
 constexpr int HD = 128;
@@ -361,12 +363,354 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
     for (int i = 0; i < 4; ++i) store_out(4 * lg + i, 16 * (kg * DPW + d) + lr, acc[d][i] / L[i]);
 }
 
-AttnShape attn_shape(int rows, int nq, int nkv) {
+// ---- one-shot variant for short key chunks (the cached decode step) -------------------------------
+// Same arithmetic as attn_kernel, but a workgroup requests every K/V row of its chunk (CH keys) at
+// once, so the chunk costs one memory latency instead of one per 32-key block.  Waves are QPW query
+// tiles times KH key parts; the key parts are merged in LDS; key splits (gridDim.z) are merged by the
+// last workgroup to arrive, with all of its waves sharing the merge.
+template <int DT, int QPW, int KH, int CH>
+__global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP a) {
+  constexpr int NT = 64 * QPW * KH;
+  constexpr int KIT = (CH * 8 + NT - 1) / NT;        // K items (rotation-pair chunks) per thread
+  constexpr int VIT = ((CH / 4) * 16 + NT - 1) / NT;  // V items (key quad x dim chunk) per thread
+  constexpr int VLDC = CH + 8;                        // u16 stride of a transposed V row
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int flag_s;
+  u16* kbuf = reinterpret_cast<u16*>(smem);           // [CH][KLD]
+  u16* vbuf = kbuf + CH * KLD;                        // [HD][VLDC]
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int qw = w % QPW, kh = w / QPW;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int g = blockIdx.y, c = blockIdx.z;
+  const int grp = a.nq / a.nkv, QR = grp * a.rows, QT = (QR + 15) / 16;
+  const int qt = blockIdx.x * QPW + qw;
+  const bool tile_ok = qt < QT;
+  const int pos_base = *a.pos_offset;
+  const size_t krow = (size_t)a.nkv * HD;
+  const int kbeg = c * a.chunk;
+  const int kend = min(kbeg + a.chunk, a.Lk);
+  const bool writer = blockIdx.x == 0;
+  const u16* kq_base = a.qkv + a.nq * HD + g * HD;
+  const u16* vq_base = a.qkv + (a.nq + a.nkv) * HD + g * HD;
+
+  // ---- request the whole chunk (rows past kend read row kbeg and are masked or zeroed later) ----
+  u32x4 klo[KIT], khi[KIT], vv[VIT][4];
+#pragma unroll
+  for (int it = 0; it < KIT; ++it) {
+    const int item = threadIdx.x + it * NT;
+    const int j = min(item >> 3, CH - 1), p = item & 7;
+    int key = kbeg + j;
+    key = key < kend ? key : kbeg;
+    const bool win = key >= a.ws && key < a.ws + a.rows;
+    const u16* src = win ? kq_base + (size_t)(key - a.ws) * a.ldq : a.kc + key * krow + g * HD;
+    klo[it] = *reinterpret_cast<const u32x4*>(src + 8 * p);
+    khi[it] = *reinterpret_cast<const u32x4*>(src + 64 + 8 * p);
+  }
+#pragma unroll
+  for (int it = 0; it < VIT; ++it) {
+    const int item = threadIdx.x + it * NT;
+    const int kq = min(item >> 4, CH / 4 - 1), dc = item & 15;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      int key = kbeg + 4 * kq + qq;
+      key = key < kend ? key : kbeg;
+      const bool win = key >= a.ws && key < a.ws + a.rows;
+      vv[it][qq] = *reinterpret_cast<const u32x4*>(win ? vq_base + (size_t)(key - a.ws) * a.ldq + 8 * dc
+                                                       : a.vc + key * krow + g * HD + 8 * dc);
+    }
+  }
+
+  // this lane's query row (qi = 16 qt + lr), RoPE'd in registers while the chunk is in flight
+  const int qi = qt * 16 + lr;
+  const bool qvalid = tile_ok && qi < QR;
+  const int hh = qvalid ? qi / a.rows : 0;
+  const int r = qvalid ? qi - hh * a.rows : 0;
+  u32x4 qf[4];
+  {
+    const u16* qp = a.qkv + (size_t)r * a.ldq + (g * grp + hh) * HD + 8 * lg;
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) qf[ds] = *reinterpret_cast<const u32x4*>(qp + 32 * ds);
+    const float pos = (float)(pos_base + r);
+    rope_pair<DT>(qf[0], qf[2], 8 * lg, pos, a.neg_log_theta);
+    rope_pair<DT>(qf[1], qf[3], 8 * lg + 32, pos, a.neg_log_theta);
+  }
+  const int qpos_blk = a.mask == 1 ? (a.q_pos0 + r) / a.block : 0;
+  const float* brow = a.mask == 2 ? a.bias + (long long)r * a.bias_ld : nullptr;
+
+  // ---- stage: K rows (window rows RoPE'd and appended to the cache), V transposed ----
+#pragma unroll
+  for (int it = 0; it < KIT; ++it) {
+    const int item = threadIdx.x + it * NT;
+    if (item >= CH * 8) break;
+    const int j = item >> 3, p = item & 7;
+    const int key = kbeg + j;
+    u32x4 lo = klo[it], hi = khi[it];
+    if (key >= kend) {
+      lo = hi = u32x4{0u, 0u, 0u, 0u};
+    } else if (key >= a.ws && key < a.ws + a.rows) {
+      rope_pair<DT>(lo, hi, 8 * p, (float)(pos_base + key - a.ws), a.neg_log_theta);
+      if (writer) {
+        u16* dst = a.kc + key * krow + g * HD;
+        *reinterpret_cast<u32x4*>(dst + 8 * p) = lo;
+        *reinterpret_cast<u32x4*>(dst + 64 + 8 * p) = hi;
+      }
+    }
+    *reinterpret_cast<u32x4*>(kbuf + j * KLD + 8 * p) = lo;
+    *reinterpret_cast<u32x4*>(kbuf + j * KLD + 64 + 8 * p) = hi;
+  }
+#pragma unroll
+  for (int it = 0; it < VIT; ++it) {
+    const int item = threadIdx.x + it * NT;
+    if (item >= (CH / 4) * 16) break;
+    const int kq = item >> 4, dc = item & 15;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      const int key = kbeg + 4 * kq + qq;
+      if (key >= kend) {
+        vv[it][qq] = u32x4{0u, 0u, 0u, 0u};
+      } else if (writer && key >= a.ws && key < a.ws + a.rows) {
+        *reinterpret_cast<u32x4*>(a.vc + key * krow + g * HD + 8 * dc) = vv[it][qq];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int sh = 16 * (e & 1);
+      const unsigned long long wd = (unsigned long long)((vv[it][0][e >> 1] >> sh) & 0xffffu) |
+                                    ((unsigned long long)((vv[it][1][e >> 1] >> sh) & 0xffffu) << 16) |
+                                    ((unsigned long long)((vv[it][2][e >> 1] >> sh) & 0xffffu) << 32) |
+                                    ((unsigned long long)((vv[it][3][e >> 1] >> sh) & 0xffffu) << 48);
+      *reinterpret_cast<unsigned long long*>(vbuf + (8 * dc + e) * VLDC + 4 * kq) = wd;
+    }
+  }
+  __syncthreads();
+
+  // ---- scores and P.V over this wave's key part ----
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4 o[HD / 16];
+#pragma unroll
+  for (int dt = 0; dt < HD / 16; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  constexpr int KPW = CH / KH;  // keys per wave
+  if (tile_ok) {
+    for (int b = 0; b < KPW / 32; ++b) {
+      const int kl = kh * KPW + 32 * b;  // chunk-local first key of the block
+      const int kb = kbeg + kl;
+      if (kb >= kend) break;
+      f32x4 s[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const u16* kp = kbuf + (kl + 16 * kt + lr) * KLD + 8 * lg;
+#pragma unroll
+        for (int ds = 0; ds < 4; ++ds) s[kt] = mfma16<DT>(*reinterpret_cast<const u32x4*>(kp + 32 * ds), qf[ds], s[kt]);
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = kb + 16 * kt + 4 * lg + i;
+          float v = s[kt][i] * a.scale;
+          if (key >= kend) {
+            v = -INFINITY;
+          } else if (a.mask == 1) {
+            if (qpos_blk < key / a.block) v = -INFINITY;
+          } else if (a.mask == 2) {
+            v += brow[key];
+          }
+          s[kt][i] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+      const float m_new = fmaxf(m_run, mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = expf(m_run - m_use);
+      float ps = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float pe = expf(s[kt][i] - m_use);
+          s[kt][i] = pe;
+          ps += pe;
+        }
+      ps += __shfl_xor(ps, 16, WAVE);
+      ps += __shfl_xor(ps, 32, WAVE);
+      l_run = l_run * alpha + ps;
+      m_run = m_new;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float al = __shfl(alpha, 4 * lg + i, WAVE);
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; ++dt) o[dt][i] *= al;
+      }
+      const u32x4 pa = {pack2(from_f32<DT>(s[0][0]), from_f32<DT>(s[0][1])),
+                        pack2(from_f32<DT>(s[0][2]), from_f32<DT>(s[0][3])),
+                        pack2(from_f32<DT>(s[1][0]), from_f32<DT>(s[1][1])),
+                        pack2(from_f32<DT>(s[1][2]), from_f32<DT>(s[1][3]))};
+#pragma unroll
+      for (int dt = 0; dt < HD / 16; ++dt) {
+        const u16* vrow = vbuf + (16 * dt + lr) * VLDC + kl + 4 * lg;
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 16);
+        o[dt] = mfma16<DT>(pa, u32x4{lo[0], lo[1], hi[0], hi[1]}, o[dt]);
+      }
+    }
+  }
+
+  // ---- merge the key parts in LDS (fixed order kh = 0, 1, ...) ----
+  float Mq[4], Lq[4];
+  __syncthreads();
+  {
+    float* cm = reinterpret_cast<float*>(smem);
+    float* cl = cm + KH * QPW * 16;
+    f32x4* co = reinterpret_cast<f32x4*>(cl + KH * QPW * 16);
+    if (lg == 0) {
+      cm[(kh * QPW + qw) * 16 + lr] = m_run;
+      cl[(kh * QPW + qw) * 16 + lr] = l_run;
+    }
+    if (KH > 1 && kh > 0) {
+#pragma unroll
+      for (int dt = 0; dt < HD / 16; ++dt) co[(((kh - 1) * QPW + qw) * (HD / 16) + dt) * 64 + lane] = o[dt];
+    }
+    __syncthreads();
+    if (kh == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int q = 4 * lg + i;
+        float M = -INFINITY;
+        for (int k = 0; k < KH; ++k) M = fmaxf(M, cm[(k * QPW + qw) * 16 + q]);
+        const float Mu = M == -INFINITY ? 0.f : M;
+        float L = 0.f;
+        for (int k = 0; k < KH; ++k) L += cl[(k * QPW + qw) * 16 + q] * expf(cm[(k * QPW + qw) * 16 + q] - Mu);
+        const float f0 = expf(cm[qw * 16 + q] - Mu);
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; ++dt) o[dt][i] *= f0;
+        for (int k = 1; k < KH; ++k) {
+          const float fk = expf(cm[(k * QPW + qw) * 16 + q] - Mu);
+#pragma unroll
+          for (int dt = 0; dt < HD / 16; ++dt) o[dt][i] += co[(((k - 1) * QPW + qw) * (HD / 16) + dt) * 64 + lane][i] * fk;
+        }
+        Mq[i] = M;
+        Lq[i] = L;
+      }
+    }
+  }
+
+  auto store_out = [&](int q, int dim, float v) {
+    const int row = qt * 16 + q;
+    if (row >= QR) return;
+    const int h2 = row / a.rows, r2 = row - h2 * a.rows;
+    a.out[(size_t)r2 * a.nq * HD + (g * grp + h2) * HD + dim] = from_f32<DT>(v);
+  };
+  if (a.S == 1) {
+    if (kh == 0 && tile_ok) {
+#pragma unroll
+      for (int dt = 0; dt < HD / 16; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) store_out(4 * lg + i, 16 * dt + lr, o[dt][i] / Lq[i]);
+    }
+    return;
+  }
+  if (kh == 0 && tile_ok) {
+    float* pp = a.part + ((size_t)(g * QT + qt) * a.S + c) * PSZ;
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) st_agent(pp + (dt * 4 + i) * 64 + lane, o[dt][i]);
+    if (lr == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        st_agent(pp + 16 * HD + 4 * lg + i, Mq[i]);
+        st_agent(pp + 16 * HD + 16 + 4 * lg + i, Lq[i]);
+      }
+    }
+  }
+  if (!arrive_last(a.counters + g * gridDim.x + blockIdx.x, a.S, &flag_s)) return;
+  float* ml = reinterpret_cast<float*>(smem);  // [QPW][S][32]
+  const int nml = QPW * a.S * 32;
+  for (int idx = threadIdx.x; idx < nml; idx += NT) {
+    const int q = idx / (a.S * 32), rem = idx - q * (a.S * 32);
+    const int qt2 = blockIdx.x * QPW + q;
+    ml[idx] = qt2 < QT ? ld_agent(a.part + ((size_t)(g * QT + qt2) * a.S + (rem >> 5)) * PSZ + 16 * HD + (rem & 31))
+                       : 0.f;
+  }
+  __syncthreads();
+  if (!tile_ok) return;
+  const float* mlq = ml + qw * a.S * 32;
+  const float* pt = a.part + (size_t)(g * QT + qt) * a.S * PSZ;
+  constexpr int DPW = (HD / 16) / KH;
+  float M[4], L[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = 4 * lg + i;
+    M[i] = -INFINITY;
+    for (int sp = 0; sp < a.S; ++sp) M[i] = fmaxf(M[i], mlq[sp * 32 + q]);
+    if (M[i] == -INFINITY) M[i] = 0.f;
+    L[i] = 0.f;
+    for (int sp = 0; sp < a.S; ++sp) L[i] += mlq[sp * 32 + 16 + q] * expf(mlq[sp * 32 + q] - M[i]);
+  }
+  float acc[DPW][4];
+#pragma unroll
+  for (int d = 0; d < DPW; ++d)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[d][i] = 0.f;
+  constexpr int SB = 8;
+  for (int s0 = 0; s0 < a.S; s0 += SB) {
+    float v[SB][DPW][4];
+#pragma unroll
+    for (int q = 0; q < SB; ++q)
+#pragma unroll
+      for (int d = 0; d < DPW; ++d)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          v[q][d][i] = ld_agent(pt + min(s0 + q, a.S - 1) * PSZ + ((kh * DPW + d) * 4 + i) * 64 + lane);
+#pragma unroll
+    for (int q = 0; q < SB; ++q) {
+      if (s0 + q >= a.S) break;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float f = expf(mlq[(s0 + q) * 32 + 4 * lg + i] - M[i]);
+#pragma unroll
+        for (int d = 0; d < DPW; ++d) acc[d][i] += v[q][d][i] * f;
+      }
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < DPW; ++d)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) store_out(4 * lg + i, 16 * (kh * DPW + d) + lr, acc[d][i] / L[i]);
+}
+
+// Launch plan: short row blocks (the cached decode step) use attn_chunk_kernel with one key chunk of
+// CH keys per workgroup; long row blocks (prefill, stateless forward) use attn_kernel with few, long
+// key ranges per workgroup.
+AttnPlan attn_plan(int rows, int nq, int nkv, int Lk, int target_wgs) {
+  AttnPlan p{};
   const int QT = ((nq / nkv) * rows + 15) / 16;
-  if (QT >= 32) return AttnShape{4, 1};  // long row blocks (prefill): many workgroups already
-  if (QT >= 3) return AttnShape{4, 2};
-  if (QT == 2) return AttnShape{2, 4};
-  return AttnShape{1, 4};
+  // chunked: 128 keys per workgroup unless that leaves fewer workgroups than aimed for; at most 64
+  // chunks, so the split merge stays small (longer contexts take the loop kernel)
+  if (QT <= 12 && (Lk + 127) / 128 <= 64) {
+    p.chunked = 1;
+    p.q_tiles_per_wg = 4;
+    p.key_groups = 2;
+    p.qg = (QT + 3) / 4;
+    p.chunk = 128;
+    if (p.qg * nkv * ((Lk + 127) / 128) < target_wgs && (Lk + 63) / 64 <= 64) p.chunk = 64;
+    p.S = (Lk + p.chunk - 1) / p.chunk;
+    return p;
+  }
+  p.chunked = 0;
+  if (QT >= 32) { p.q_tiles_per_wg = 4; p.key_groups = 1; }
+  else { p.q_tiles_per_wg = 4; p.key_groups = 2; }
+  p.qg = (QT + p.q_tiles_per_wg - 1) / p.q_tiles_per_wg;
+  const int base = p.qg * nkv;
+  const int max_splits = std::max(1, (Lk + 32 * p.key_groups - 1) / (32 * p.key_groups));
+  int S = std::min(max_splits, std::max(1, (target_wgs + base - 1) / base));
+  p.chunk = (((Lk + S - 1) / S) + 31) / 32 * 32;
+  p.S = (Lk + p.chunk - 1) / p.chunk;
+  return p;
 }
 
 size_t attn_partial_floats(const AttnP& a) {
@@ -374,36 +718,53 @@ size_t attn_partial_floats(const AttnP& a) {
   return (size_t)a.nkv * QT * a.S * PSZ;
 }
 
+template <typename K>
+static void raise_lds(K kern, size_t lds) {
+  // a runtime that needs no attribute for LDS up to the device limit may reject it: clear that error
+  // and let the launch report whether the size fits
+  if (lds > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+          hipSuccess)
+    (void)hipGetLastError();
+}
+
 template <int DT, int QPW, int KSW>
-static hipError_t launch_shape(const AttnP& a, hipStream_t st) {
-  const int QT = ((a.nq / a.nkv) * a.rows + 15) / 16;
-  const int qg = (QT + QPW - 1) / QPW;
+static hipError_t launch_loop(const AttnP& a, const AttnPlan& p, hipStream_t st) {
   const size_t loop_lds = (size_t)KSW * (KB * KLD + HD * VLD) * 2;
   const size_t merge_lds = (size_t)2 * KSW * QPW * 16 * 4 + (size_t)(KSW - 1) * QPW * (HD / 16) * 64 * 16;
   const size_t split_lds = a.S > 1 ? (size_t)QPW * a.S * 32 * 4 : 0;
-  size_t lds = loop_lds > merge_lds ? loop_lds : merge_lds;
-  if (split_lds > lds) lds = split_lds;
+  const size_t lds = std::max(loop_lds, std::max(merge_lds, split_lds));
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
   auto kern = attn_kernel<DT, QPW, KSW>;
-  static size_t attr_lds = 64 * 1024;
-  if (lds > attr_lds) {
-    // a runtime that needs no attribute for LDS up to the device limit may reject it: clear that
-    // error and let the launch report whether the size fits
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)lds) != hipSuccess)
-      (void)hipGetLastError();
-    attr_lds = lds;
-  }
-  hipLaunchKernelGGL(kern, dim3(qg, a.nkv, a.S), dim3(64 * QPW * KSW), lds, st, a);
+  raise_lds(kern, lds);
+  hipLaunchKernelGGL(kern, dim3(p.qg, a.nkv, a.S), dim3(64 * QPW * KSW), lds, st, a);
+  return hipGetLastError();
+}
+
+template <int DT, int CH>
+static hipError_t launch_chunk(const AttnP& a, const AttnPlan& p, hipStream_t st) {
+  constexpr int QPW = 4, KH = 2;
+  const size_t loop_lds = (size_t)CH * KLD * 2 + (size_t)HD * (CH + 8) * 2;
+  const size_t merge_lds = (size_t)2 * KH * QPW * 16 * 4 + (size_t)(KH - 1) * QPW * (HD / 16) * 64 * 16;
+  const size_t split_lds = a.S > 1 ? (size_t)QPW * a.S * 32 * 4 : 0;
+  const size_t lds = std::max(loop_lds, std::max(merge_lds, split_lds));
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  auto kern = attn_chunk_kernel<DT, QPW, KH, CH>;
+  raise_lds(kern, lds);
+  hipLaunchKernelGGL(kern, dim3(p.qg, a.nkv, a.S), dim3(64 * QPW * KH), lds, st, a);
   return hipGetLastError();
 }
 
 template <int DT>
 static hipError_t launch_dt(const AttnP& a, hipStream_t st) {
-  const AttnShape sh = attn_shape(a.rows, a.nq, a.nkv);
-  if (sh.q_tiles_per_wg == 4 && sh.key_groups == 1) return launch_shape<DT, 4, 1>(a, st);
-  if (sh.q_tiles_per_wg == 4) return launch_shape<DT, 4, 2>(a, st);
-  if (sh.q_tiles_per_wg == 2) return launch_shape<DT, 2, 4>(a, st);
-  return launch_shape<DT, 1, 4>(a, st);
+  const AttnPlan p = attn_plan(a.rows, a.nq, a.nkv, a.Lk, a.target_wgs);
+  if (p.S != a.S || p.chunk != a.chunk) return hipErrorInvalidValue;
+  if (p.chunked) {
+    if (p.chunk == 128) return launch_chunk<DT, 128>(a, p, st);
+    return launch_chunk<DT, 64>(a, p, st);
+  }
+  if (p.key_groups == 1) return launch_loop<DT, 4, 1>(a, p, st);
+  return launch_loop<DT, 4, 2>(a, p, st);
 }
 
 hipError_t launch_attention(int dt, const AttnP& a, hipStream_t st) {

@@ -70,7 +70,7 @@ struct fdllm_ctx {
   void* stats = nullptr; size_t stats_rows = 0;
   unsigned* counters = nullptr; int n_counters = 0;
   int32_t* zero_i32 = nullptr;
-  int attn_target = 48;   // attention workgroups aimed for when splitting the keys
+  int attn_target = 64;   // attention workgroups aimed for when splitting the keys
   int down_split = 10;    // cross-workgroup k splits of the down projection (largest divisor of K/32 <= this)
 
   int qkv_dim() const { return (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim; }
@@ -193,15 +193,10 @@ int run_attention(fdllm_ctx* c, int rows, const int32_t* pos, uint16_t* kc, uint
   a.pos_offset = pos; a.neg_log_theta = (float)(-std::log((double)f.rope_theta));
   a.kc = kc; a.vc = vc; a.ws = ws; a.Lk = Lk; a.scale = 1.0f / std::sqrt((float)f.head_dim);
   a.mask = mask; a.q_pos0 = 0; a.block = f.bd_size; a.bias = bias; a.bias_ld = bias_ld;
-  const AttnShape sh = attn_shape(rows, a.nq, a.nkv);
-  const int QT = ((a.nq / a.nkv) * rows + 15) / 16;
-  const int base = ((QT + sh.q_tiles_per_wg - 1) / sh.q_tiles_per_wg) * a.nkv;
-  const int max_splits = std::max(1, (Lk + 32 * sh.key_groups - 1) / (32 * sh.key_groups));
-  int S = std::min(max_splits, std::max(1, (c->attn_target + base - 1) / base));
-  int chunk = (int)align_up((size_t)((Lk + S - 1) / S), 32);
-  S = (Lk + chunk - 1) / chunk;
-  a.S = S; a.chunk = chunk;
-  if (S > 1) {
+  const AttnPlan pl = attn_plan(rows, a.nq, a.nkv, Lk, c->attn_target);
+  const int base = pl.qg * a.nkv;
+  a.S = pl.S; a.chunk = pl.chunk; a.target_wgs = c->attn_target;
+  if (a.S > 1) {
     int rc = ensure_floats(&c->apart, &c->apart_floats, attn_partial_floats(a));
     if (rc) return rc;
     if (base > c->n_counters) return fail(FDLLM_EINVAL, "too many attention workgroup groups (%d)", base);

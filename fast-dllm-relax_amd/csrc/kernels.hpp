@@ -72,11 +72,12 @@ struct AttnP {
   int q_pos0; int block;              // block-causal: query row r sits at q_pos0 + r
   const float* bias; long long bias_ld;
   int S, chunk;                       // key splits (gridDim.z), keys per split (multiple of 32)
+  int target_wgs;                     // workgroups the plan aims for (attn_plan)
   float* part; unsigned* counters;    // split partials / arrival counters
   uint16_t* out;                      // [rows][nq * 128]
 };
-struct AttnShape { int q_tiles_per_wg; int key_groups; };
-AttnShape attn_shape(int rows, int nq, int nkv);
+struct AttnPlan { int chunked; int q_tiles_per_wg; int key_groups; int qg; int S; int chunk; };
+AttnPlan attn_plan(int rows, int nq, int nkv, int Lk, int target_wgs);
 hipError_t launch_attention(int dt, const AttnP& a, hipStream_t st);
 size_t attn_partial_floats(const AttnP& a);
 
