@@ -32,20 +32,21 @@ template <int DT> __device__ __forceinline__ float elem(const u32x4& v, int e) {
   return (e & 1) ? hi_f32<DT>(v[e >> 1]) : lo_f32<DT>(v[e >> 1]);
 }
 
-// RoPE of 8 rotation pairs: lo holds dims i0 .. i0 + 7 (< 64), hi the partner dims + 64
-// (cuda.py:288-299 tables: inv_freq = exp(-ln(theta) * i / 64), emb = [f, f]; apply 314-315 with
-// _rotate_half 207-209, every product and sum rounded to the model dtype).
+// RoPE of 8 rotation pairs: lo holds dims i0 .. i0 + 7 (< 64), hi the partner dims + 64; cs points at
+// the (cos, sin) entries i0 .. i0 + 7 of the position's table row (cuda.py:314-315 with _rotate_half
+// 207-209: q' = q cos + rot(q) sin, every product and sum rounded to the model dtype).
 template <int DT>
-__device__ __forceinline__ void rope_pair(u32x4& lo, u32x4& hi, int i0, float pos, float nlt) {
+__device__ __forceinline__ void rope_tab(u32x4& lo, u32x4& hi, const float* cs) {
+  f32x4 t[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) t[c] = *reinterpret_cast<const f32x4*>(cs + 4 * c);
   u16 o1[8], o2[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float ex = (nlt * (float)(i0 + e)) / 64.0f;
-    const float fr = pos * expf(ex);
-    const float cs = rnd<DT>(cosf(fr)), sn = rnd<DT>(sinf(fr));
+    const float c = t[e >> 1][2 * (e & 1)], sn = t[e >> 1][2 * (e & 1) + 1];
     const float x1 = elem<DT>(lo, e), x2 = elem<DT>(hi, e);
-    o1[e] = from_f32<DT>(rnd<DT>(x1 * cs) + rnd<DT>(-x2 * sn));
-    o2[e] = from_f32<DT>(rnd<DT>(x2 * cs) + rnd<DT>(x1 * sn));
+    o1[e] = from_f32<DT>(rnd<DT>(x1 * c) + rnd<DT>(-x2 * sn));
+    o2[e] = from_f32<DT>(rnd<DT>(x2 * c) + rnd<DT>(x1 * sn));
   }
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
@@ -69,7 +70,6 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
   const int grp = a.nq / a.nkv, QR = grp * a.rows, QT = (QR + 15) / 16;
   const int qt = blockIdx.x * QPW + qw;
   const bool tile_ok = qt < QT;
-  const int pos_base = *a.pos_offset;
   const size_t krow = (size_t)a.nkv * HD;
   u16* kbuf = reinterpret_cast<u16*>(smem) + kg * KBUF;
   u16* vbuf = reinterpret_cast<u16*>(smem) + KSW * KBUF + kg * VBUF;
@@ -85,9 +85,9 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds)
       qf[ds] = qvalid ? *reinterpret_cast<const u32x4*>(qp + 32 * ds) : u32x4{0u, 0u, 0u, 0u};
-    const float pos = (float)(pos_base + r);
-    rope_pair<DT>(qf[0], qf[2], 8 * lg, pos, a.neg_log_theta);
-    rope_pair<DT>(qf[1], qf[3], 8 * lg + 32, pos, a.neg_log_theta);
+    const float* cs = a.rope + (size_t)r * 128;
+    rope_tab<DT>(qf[0], qf[2], cs + 16 * lg);
+    rope_tab<DT>(qf[1], qf[3], cs + 16 * lg + 64);
   }
   const int qpos_blk = a.mask == 1 ? (a.q_pos0 + r) / a.block : 0;
   const float* brow = a.mask == 2 ? a.bias + (long long)r * a.bias_ld : nullptr;
@@ -121,7 +121,7 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
             const u16* src = kq_base + (size_t)(key - a.ws) * a.ldq;
             lo = *reinterpret_cast<const u32x4*>(src + 8 * p);
             hi = *reinterpret_cast<const u32x4*>(src + 64 + 8 * p);
-            rope_pair<DT>(lo, hi, 8 * p, (float)(pos_base + key - a.ws), a.neg_log_theta);
+            rope_tab<DT>(lo, hi, a.rope + (size_t)(key - a.ws) * 128 + 16 * p);
             if (writer) {
               u16* dst = a.kc + key * krow + g * HD;
               *reinterpret_cast<u32x4*>(dst + 8 * p) = lo;
@@ -363,19 +363,55 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
     for (int i = 0; i < 4; ++i) store_out(4 * lg + i, 16 * (kg * DPW + d) + lr, acc[d][i] / L[i]);
 }
 
+// Waits until `expected` workgroups (this one included) have arrived at ctr[0].  Every store this
+// workgroup made before the call is complete and agent-visible first.  The wait is bounded: if the
+// group's workgroups are not all resident it gives up, sets *err and carries on (the results are then
+// wrong, and the host reports the flag), so a wave never spins forever.
+__device__ __forceinline__ void group_wait(unsigned* ctr, unsigned expected, unsigned* err) {
+  wait_memory();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int spins = 0;
+    while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < expected) {
+      __builtin_amdgcn_s_sleep(2);
+      if (++spins > (1 << 22)) {
+        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// The group's last workgroup to leave returns both counters (ctr[0] arrivals, ctr[1] departures) to
+// zero; every workgroup has passed its wait by then, so the next launch starts from zero.
+__device__ __forceinline__ void group_leave(unsigned* ctr, unsigned expected) {
+  if (threadIdx.x == 0) {
+    const unsigned old = __hip_atomic_fetch_add(ctr + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == expected - 1) {
+      __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(ctr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
 // ---- one-shot variant for short key chunks (the cached decode step) -------------------------------
 // Same arithmetic as attn_kernel, but a workgroup requests every K/V row of its chunk (CH keys) at
 // once, so the chunk costs one memory latency instead of one per 32-key block.  Waves are QPW query
-// tiles times KH key parts; the key parts are merged in LDS; key splits (gridDim.z) are merged by the
-// last workgroup to arrive, with all of its waves sharing the merge.
+// tiles times KH key parts.  The output is accumulated transposed, O^T = V^T P^T, so that a lane holds
+// one query (its softmax statistics stay in-lane) and the row reductions use row-swap permutes.  The
+// key parts are merged in LDS; key splits (gridDim.z) store their partials, wait for the rest of their
+// group and merge one (query tile, 16-dim slice) per wave, with the split weights computed once per
+// query.
 template <int DT, int QPW, int KH, int CH>
 __global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP a) {
   constexpr int NT = 64 * QPW * KH;
   constexpr int KIT = (CH * 8 + NT - 1) / NT;        // K items (rotation-pair chunks) per thread
   constexpr int VIT = ((CH / 4) * 16 + NT - 1) / NT;  // V items (key quad x dim chunk) per thread
   constexpr int VLDC = CH + 8;                        // u16 stride of a transposed V row
+  constexpr int DT16 = HD / 16;
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ int flag_s;
   u16* kbuf = reinterpret_cast<u16*>(smem);           // [CH][KLD]
   u16* vbuf = kbuf + CH * KLD;                        // [HD][VLDC]
 
@@ -386,7 +422,6 @@ __global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP a) {
   const int grp = a.nq / a.nkv, QR = grp * a.rows, QT = (QR + 15) / 16;
   const int qt = blockIdx.x * QPW + qw;
   const bool tile_ok = qt < QT;
-  const int pos_base = *a.pos_offset;
   const size_t krow = (size_t)a.nkv * HD;
   const int kbeg = c * a.chunk;
   const int kend = min(kbeg + a.chunk, a.Lk);
@@ -431,9 +466,9 @@ __global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP a) {
     const u16* qp = a.qkv + (size_t)r * a.ldq + (g * grp + hh) * HD + 8 * lg;
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) qf[ds] = *reinterpret_cast<const u32x4*>(qp + 32 * ds);
-    const float pos = (float)(pos_base + r);
-    rope_pair<DT>(qf[0], qf[2], 8 * lg, pos, a.neg_log_theta);
-    rope_pair<DT>(qf[1], qf[3], 8 * lg + 32, pos, a.neg_log_theta);
+    const float* cs = a.rope + (size_t)r * 128;
+    rope_tab<DT>(qf[0], qf[2], cs + 16 * lg);
+    rope_tab<DT>(qf[1], qf[3], cs + 16 * lg + 64);
   }
   const int qpos_blk = a.mask == 1 ? (a.q_pos0 + r) / a.block : 0;
   const float* brow = a.mask == 2 ? a.bias + (long long)r * a.bias_ld : nullptr;
@@ -449,7 +484,7 @@ __global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP a) {
     if (key >= kend) {
       lo = hi = u32x4{0u, 0u, 0u, 0u};
     } else if (key >= a.ws && key < a.ws + a.rows) {
-      rope_pair<DT>(lo, hi, 8 * p, (float)(pos_base + key - a.ws), a.neg_log_theta);
+      rope_tab<DT>(lo, hi, a.rope + (size_t)(key - a.ws) * 128 + 16 * p);
       if (writer) {
         u16* dst = a.kc + key * krow + g * HD;
         *reinterpret_cast<u32x4*>(dst + 8 * p) = lo;
@@ -486,10 +521,11 @@ __global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP a) {
   __syncthreads();
 
   // ---- scores and P.V over this wave's key part ----
+  // lane (lr, lg) holds S^T[key kb + 16 kt + 4 lg + i][query lr] and O^T[dim 16 dt + 4 lg + i][query lr]
   float m_run = -INFINITY, l_run = 0.f;
-  f32x4 o[HD / 16];
+  f32x4 o[DT16];
 #pragma unroll
-  for (int dt = 0; dt < HD / 16; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int dt = 0; dt < DT16; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   constexpr int KPW = CH / KH;  // keys per wave
   if (tile_ok) {
     for (int b = 0; b < KPW / 32; ++b) {
@@ -521,8 +557,7 @@ __global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP a) {
           s[kt][i] = v;
           mx = fmaxf(mx, v);
         }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+      mx = rows_max(mx);
       const float m_new = fmaxf(m_run, mx);
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
       const float alpha = expf(m_run - m_use);
@@ -535,33 +570,28 @@ __global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP a) {
           s[kt][i] = pe;
           ps += pe;
         }
-      ps += __shfl_xor(ps, 16, WAVE);
-      ps += __shfl_xor(ps, 32, WAVE);
+      ps = rows_sum(ps);
       l_run = l_run * alpha + ps;
       m_run = m_new;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float al = __shfl(alpha, 4 * lg + i, WAVE);
-#pragma unroll
-        for (int dt = 0; dt < HD / 16; ++dt) o[dt][i] *= al;
-      }
-      const u32x4 pa = {pack2(from_f32<DT>(s[0][0]), from_f32<DT>(s[0][1])),
+      // P^T as the B operand: k slot 8 lg + e holds key 4 lg + e (e < 4) or 16 + 4 lg + e - 4; the V^T
+      // fragment (A operand) reads the same keys
+      const u32x4 pb = {pack2(from_f32<DT>(s[0][0]), from_f32<DT>(s[0][1])),
                         pack2(from_f32<DT>(s[0][2]), from_f32<DT>(s[0][3])),
                         pack2(from_f32<DT>(s[1][0]), from_f32<DT>(s[1][1])),
                         pack2(from_f32<DT>(s[1][2]), from_f32<DT>(s[1][3]))};
 #pragma unroll
-      for (int dt = 0; dt < HD / 16; ++dt) {
+      for (int dt = 0; dt < DT16; ++dt) {
         const u16* vrow = vbuf + (16 * dt + lr) * VLDC + kl + 4 * lg;
         const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
         const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 16);
-        o[dt] = mfma16<DT>(pa, u32x4{lo[0], lo[1], hi[0], hi[1]}, o[dt]);
+        o[dt] = mfma16<DT>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb, o[dt] * alpha);
       }
     }
   }
 
-  // ---- merge the key parts in LDS (fixed order kh = 0, 1, ...) ----
-  float Mq[4], Lq[4];
+  // ---- merge the key parts in LDS (fixed order kh = 0, 1, ...); wave kh = 0 keeps the result ----
   __syncthreads();
+  float Mq, Lq;
   {
     float* cm = reinterpret_cast<float*>(smem);
     float* cl = cm + KH * QPW * 16;
@@ -572,115 +602,103 @@ __global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP a) {
     }
     if (KH > 1 && kh > 0) {
 #pragma unroll
-      for (int dt = 0; dt < HD / 16; ++dt) co[(((kh - 1) * QPW + qw) * (HD / 16) + dt) * 64 + lane] = o[dt];
+      for (int dt = 0; dt < DT16; ++dt) co[(((kh - 1) * QPW + qw) * DT16 + dt) * 64 + lane] = o[dt];
     }
     __syncthreads();
     if (kh == 0) {
+      float M = -INFINITY;
+      for (int k = 0; k < KH; ++k) M = fmaxf(M, cm[(k * QPW + qw) * 16 + lr]);
+      const float Mu = M == -INFINITY ? 0.f : M;
+      float L = 0.f;
+      for (int k = 0; k < KH; ++k) L += cl[(k * QPW + qw) * 16 + lr] * expf(cm[(k * QPW + qw) * 16 + lr] - Mu);
+      const float f0 = expf(cm[qw * 16 + lr] - Mu);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int q = 4 * lg + i;
-        float M = -INFINITY;
-        for (int k = 0; k < KH; ++k) M = fmaxf(M, cm[(k * QPW + qw) * 16 + q]);
-        const float Mu = M == -INFINITY ? 0.f : M;
-        float L = 0.f;
-        for (int k = 0; k < KH; ++k) L += cl[(k * QPW + qw) * 16 + q] * expf(cm[(k * QPW + qw) * 16 + q] - Mu);
-        const float f0 = expf(cm[qw * 16 + q] - Mu);
+      for (int dt = 0; dt < DT16; ++dt) o[dt] *= f0;
+      for (int k = 1; k < KH; ++k) {
+        const float fk = expf(cm[(k * QPW + qw) * 16 + lr] - Mu);
 #pragma unroll
-        for (int dt = 0; dt < HD / 16; ++dt) o[dt][i] *= f0;
-        for (int k = 1; k < KH; ++k) {
-          const float fk = expf(cm[(k * QPW + qw) * 16 + q] - Mu);
-#pragma unroll
-          for (int dt = 0; dt < HD / 16; ++dt) o[dt][i] += co[(((k - 1) * QPW + qw) * (HD / 16) + dt) * 64 + lane][i] * fk;
-        }
-        Mq[i] = M;
-        Lq[i] = L;
+        for (int dt = 0; dt < DT16; ++dt) o[dt] += co[(((k - 1) * QPW + qw) * DT16 + dt) * 64 + lane] * fk;
       }
+      Mq = M;
+      Lq = L;
     }
   }
 
-  auto store_out = [&](int q, int dim, float v) {
-    const int row = qt * 16 + q;
-    if (row >= QR) return;
-    const int h2 = row / a.rows, r2 = row - h2 * a.rows;
-    a.out[(size_t)r2 * a.nq * HD + (g * grp + h2) * HD + dim] = from_f32<DT>(v);
+  // lane output: query row qi (head hh, row r), dims 16 dt + 4 lg .. + 3
+  auto store4 = [&](int dt, f32x4 v) {
+    u16* dst = a.out + (size_t)r * a.nq * HD + (g * grp + hh) * HD + 16 * dt + 4 * lg;
+    *reinterpret_cast<u32x2*>(dst) =
+        u32x2{pack2(from_f32<DT>(v[0]), from_f32<DT>(v[1])), pack2(from_f32<DT>(v[2]), from_f32<DT>(v[3]))};
   };
   if (a.S == 1) {
-    if (kh == 0 && tile_ok) {
+    if (kh == 0 && qvalid) {
+      const float inv = 1.0f / Lq;
 #pragma unroll
-      for (int dt = 0; dt < HD / 16; ++dt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) store_out(4 * lg + i, 16 * dt + lr, o[dt][i] / Lq[i]);
+      for (int dt = 0; dt < DT16; ++dt) store4(dt, o[dt] * inv);
     }
     return;
   }
+
+  // ---- key splits: partials, a wait for the whole group, then a parallel merge ----
+  // partial of (g, qt, c): O^T as f32x4 [HD / 16][64 lanes], then m and l of the tile's 16 queries
   if (kh == 0 && tile_ok) {
     float* pp = a.part + ((size_t)(g * QT + qt) * a.S + c) * PSZ;
 #pragma unroll
-    for (int dt = 0; dt < HD / 16; ++dt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) st_agent(pp + (dt * 4 + i) * 64 + lane, o[dt][i]);
-    if (lr == 0) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        st_agent(pp + 16 * HD + 4 * lg + i, Mq[i]);
-        st_agent(pp + 16 * HD + 16 + 4 * lg + i, Lq[i]);
-      }
+    for (int dt = 0; dt < DT16; ++dt) st_agent4(reinterpret_cast<f32x4*>(pp) + dt * 64 + lane, o[dt]);
+    if (lg == 0) {
+      st_agent(pp + 16 * HD + lr, Mq);
+      st_agent(pp + 16 * HD + 16 + lr, Lq);
     }
   }
-  if (!arrive_last(a.counters + g * gridDim.x + blockIdx.x, a.S, &flag_s)) return;
-  float* ml = reinterpret_cast<float*>(smem);  // [QPW][S][32]
-  const int nml = QPW * a.S * 32;
-  for (int idx = threadIdx.x; idx < nml; idx += NT) {
-    const int q = idx / (a.S * 32), rem = idx - q * (a.S * 32);
-    const int qt2 = blockIdx.x * QPW + q;
-    ml[idx] = qt2 < QT ? ld_agent(a.part + ((size_t)(g * QT + qt2) * a.S + (rem >> 5)) * PSZ + 16 * HD + (rem & 31))
-                       : 0.f;
-  }
-  __syncthreads();
-  if (!tile_ok) return;
-  const float* mlq = ml + qw * a.S * 32;
-  const float* pt = a.part + (size_t)(g * QT + qt) * a.S * PSZ;
-  constexpr int DPW = (HD / 16) / KH;
-  float M[4], L[4];
+  unsigned* grp_ctr = a.counters + 2 * ((size_t)g * gridDim.x + blockIdx.x);
+  group_wait(grp_ctr, (unsigned)a.S, a.err);
+
+  // merge unit = (query tile of the group, 16-dim slice): one wave.  The split weights
+  // exp(m_c - M) depend only on the query, so each lane computes them once for its query lr.
+  constexpr int NW = QPW * KH, SB = 8;
+  for (int u = c * NW + w; u < QPW * DT16; u += a.S * NW) {
+    const int ql = u / DT16, dt = u - ql * DT16;
+    const int qt2 = blockIdx.x * QPW + ql;
+    if (qt2 >= QT) continue;
+    const float* pt = a.part + (size_t)(g * QT + qt2) * a.S * PSZ;
+    float M = -INFINITY;
+    for (int s0 = 0; s0 < a.S; s0 += SB) {
+      float mv[SB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int q = 4 * lg + i;
-    M[i] = -INFINITY;
-    for (int sp = 0; sp < a.S; ++sp) M[i] = fmaxf(M[i], mlq[sp * 32 + q]);
-    if (M[i] == -INFINITY) M[i] = 0.f;
-    L[i] = 0.f;
-    for (int sp = 0; sp < a.S; ++sp) L[i] += mlq[sp * 32 + 16 + q] * expf(mlq[sp * 32 + q] - M[i]);
-  }
-  float acc[DPW][4];
+      for (int q = 0; q < SB; ++q) mv[q] = ld_agent(pt + (size_t)min(s0 + q, a.S - 1) * PSZ + 16 * HD + lr);
 #pragma unroll
-  for (int d = 0; d < DPW; ++d)
+      for (int q = 0; q < SB; ++q) M = fmaxf(M, mv[q]);
+    }
+    const float Mu = M == -INFINITY ? 0.f : M;
+    float L = 0.f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < a.S; s0 += SB) {
+      f32x4 ov[SB];
+      float mv[SB], lv[SB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[d][i] = 0.f;
-  constexpr int SB = 8;
-  for (int s0 = 0; s0 < a.S; s0 += SB) {
-    float v[SB][DPW][4];
+      for (int q = 0; q < SB; ++q) {
+        const float* ps = pt + (size_t)min(s0 + q, a.S - 1) * PSZ;
+        ov[q] = ld_agent4(reinterpret_cast<const f32x4*>(ps) + dt * 64 + lane);
+        mv[q] = ld_agent(ps + 16 * HD + lr);
+        lv[q] = ld_agent(ps + 16 * HD + 16 + lr);
+      }
 #pragma unroll
-    for (int q = 0; q < SB; ++q)
-#pragma unroll
-      for (int d = 0; d < DPW; ++d)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          v[q][d][i] = ld_agent(pt + min(s0 + q, a.S - 1) * PSZ + ((kh * DPW + d) * 4 + i) * 64 + lane);
-#pragma unroll
-    for (int q = 0; q < SB; ++q) {
-      if (s0 + q >= a.S) break;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float f = expf(mlq[(s0 + q) * 32 + 4 * lg + i] - M[i]);
-#pragma unroll
-        for (int d = 0; d < DPW; ++d) acc[d][i] += v[q][d][i] * f;
+      for (int q = 0; q < SB; ++q) {
+        const float e = s0 + q < a.S ? expf(mv[q] - Mu) : 0.f;
+        L += lv[q] * e;
+        acc += ov[q] * e;
       }
     }
+    const int qi2 = qt2 * 16 + lr;
+    if (qi2 < QR) {
+      const int h2 = qi2 / a.rows, r2 = qi2 - h2 * a.rows;
+      const float inv = 1.0f / L;
+      u16* dst = a.out + (size_t)r2 * a.nq * HD + (g * grp + h2) * HD + 16 * dt + 4 * lg;
+      *reinterpret_cast<u32x2*>(dst) = u32x2{pack2(from_f32<DT>(acc[0] * inv), from_f32<DT>(acc[1] * inv)),
+                                             pack2(from_f32<DT>(acc[2] * inv), from_f32<DT>(acc[3] * inv))};
+    }
   }
-#pragma unroll
-  for (int d = 0; d < DPW; ++d)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) store_out(4 * lg + i, 16 * (kh * DPW + d) + lr, acc[d][i] / L[i]);
+  group_leave(grp_ctr, (unsigned)a.S);
 }
 
 // Launch plan: short row blocks (the cached decode step) use attn_chunk_kernel with one key chunk of
@@ -746,8 +764,7 @@ static hipError_t launch_chunk(const AttnP& a, const AttnPlan& p, hipStream_t st
   constexpr int QPW = 4, KH = 2;
   const size_t loop_lds = (size_t)CH * KLD * 2 + (size_t)HD * (CH + 8) * 2;
   const size_t merge_lds = (size_t)2 * KH * QPW * 16 * 4 + (size_t)(KH - 1) * QPW * (HD / 16) * 64 * 16;
-  const size_t split_lds = a.S > 1 ? (size_t)QPW * a.S * 32 * 4 : 0;
-  const size_t lds = std::max(loop_lds, std::max(merge_lds, split_lds));
+  const size_t lds = std::max(loop_lds, merge_lds);
   if (lds > 160 * 1024) return hipErrorInvalidValue;
   auto kern = attn_chunk_kernel<DT, QPW, KH, CH>;
   raise_lds(kern, lds);

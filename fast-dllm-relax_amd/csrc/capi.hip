@@ -70,6 +70,8 @@ struct fdllm_ctx {
   void* stats = nullptr; size_t stats_rows = 0;
   unsigned* counters = nullptr; int n_counters = 0;
   int32_t* zero_i32 = nullptr;
+  float* rope = nullptr; size_t rope_floats = 0;  // RoPE (cos, sin) table of the current call's rows
+  unsigned* host_err = nullptr;                  // pinned, device-written: a bounded group wait gave up
   int attn_target = 64;   // attention workgroups aimed for when splitting the keys
   int down_split = 10;    // cross-workgroup k splits of the down projection (largest divisor of K/32 <= this)
 
@@ -185,12 +187,21 @@ int run_lm_head(fdllm_ctx* c, const uint16_t* hidden, int rows, float* logits, b
   return run_gemm(c, CFG_LM_HEAD, a, 1, st);
 }
 
-int run_attention(fdllm_ctx* c, int rows, const int32_t* pos, uint16_t* kc, uint16_t* vc, int ws, int Lk, int mask,
+// RoPE table of `rows` rows at positions *pos + r, shared by every layer of the call.
+int rope_table(fdllm_ctx* c, int rows, const int32_t* pos, hipStream_t st) {
+  int rc = ensure_floats(&c->rope, &c->rope_floats, (size_t)rows * 128);
+  if (rc) return rc;
+  HIPCHK(launch_rope_table(c->cfg.dtype, pos, rows, (float)(-std::log((double)c->cfg.rope_theta)), c->rope, st));
+  return FDLLM_OK;
+}
+
+// Attention of the call's rows; the RoPE table (rope_table) must hold the call's positions.
+int run_attention(fdllm_ctx* c, int rows, uint16_t* kc, uint16_t* vc, int ws, int Lk, int mask,
                   const float* bias, long long bias_ld, hipStream_t st) {
   const fdllm_config& f = c->cfg;
   AttnP a{};
   a.qkv = c->qkv; a.ldq = c->qkv_dim(); a.rows = rows; a.nq = f.num_attention_heads; a.nkv = f.num_key_value_heads;
-  a.pos_offset = pos; a.neg_log_theta = (float)(-std::log((double)f.rope_theta));
+  a.rope = c->rope; a.err = c->host_err;
   a.kc = kc; a.vc = vc; a.ws = ws; a.Lk = Lk; a.scale = 1.0f / std::sqrt((float)f.head_dim);
   a.mask = mask; a.q_pos0 = 0; a.block = f.bd_size; a.bias = bias; a.bias_ld = bias_ld;
   const AttnPlan pl = attn_plan(rows, a.nq, a.nkv, Lk, c->attn_target);
@@ -199,7 +210,7 @@ int run_attention(fdllm_ctx* c, int rows, const int32_t* pos, uint16_t* kc, uint
   if (a.S > 1) {
     int rc = ensure_floats(&c->apart, &c->apart_floats, attn_partial_floats(a));
     if (rc) return rc;
-    if (base > c->n_counters) return fail(FDLLM_EINVAL, "too many attention workgroup groups (%d)", base);
+    if (2 * base > c->n_counters) return fail(FDLLM_EINVAL, "too many attention workgroup groups (%d)", base);
     a.part = c->apart;
     a.counters = c->counters;
   }
@@ -220,6 +231,8 @@ int run_layers(fdllm_ctx* c, const void* x_in, int rows, uint16_t* kbase, uint16
   const int H = f.hidden_size, I = f.intermediate_size;
   const int ssq_ld = c->ws_rows;
   HIPCHK(launch_load_rows(f.dtype, (const uint16_t*)x_in, rows, H, c->h, c->ssq, ssq_ld, st));
+  int rc = rope_table(c, rows, pos_dev, st);
+  if (rc) return rc;
   const int dsplit = divisor_at_most(I / 32, c->down_split);
   for (int l = 0; l < f.num_hidden_layers; ++l) {
     const Layer& L = c->layers[l];
@@ -229,10 +242,10 @@ int run_layers(fdllm_ctx* c, const void* x_in, int rows, uint16_t* kbase, uint16
     GemmP q = gemm_args(L.pqkv, qkv_tiles(c), c->qkv_dim(), H, c->h, H, rows);
     q.ssq = c->ssq; q.ssq_tiles = c->ssq_tiles(); q.ssq_ld = ssq_ld; q.nw = L.ln_in; q.eps = f.rms_norm_eps; q.H = H;
     q.Y = c->qkv; q.ldy = c->qkv_dim(); q.bias = L.bqkv;
-    int rc = run_gemm(c, CFG_QKV, q, 1, st);
+    rc = run_gemm(c, CFG_QKV, q, 1, st);
     if (rc) return rc;
 
-    rc = run_attention(c, rows, pos_dev, kc, vc, write_start, attend_len, mask, bias, bias_ld, st);
+    rc = run_attention(c, rows, kc, vc, write_start, attend_len, mask, bias, bias_ld, st);
     if (rc) return rc;
 
     GemmP o = gemm_args(L.po, o_tiles(c), H, c->q_dim(), c->attn, c->q_dim(), rows);
@@ -354,6 +367,12 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
     return fail(FDLLM_EHIP, "workspace allocation failed: %s", hipGetErrorString(e));
   }
   c->zero_i32 = (int32_t*)(c->counters + c->n_counters);
+  e = hipHostMalloc((void**)&c->host_err, 64, hipHostMallocMapped);
+  if (e != hipSuccess) {
+    fdllm_destroy(c);
+    return fail(FDLLM_EHIP, "pinned status word allocation failed: %s", hipGetErrorString(e));
+  }
+  *c->host_err = 0;
   int rc = ensure_rows(c, std::max(1, f.max_rows));
   if (rc == FDLLM_OK) rc = ensure_stats(c, std::max(32, f.max_rows));
   if (rc == FDLLM_OK) {
@@ -371,9 +390,21 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
 void fdllm_destroy(fdllm_ctx* c) {
   if (!c) return;
   (void)hipDeviceSynchronize();
-  for (void* p : {c->ws, (void*)c->gpart, (void*)c->apart, c->stats, (void*)c->counters, (void*)c->packed})
+  for (void* p : {c->ws, (void*)c->gpart, (void*)c->apart, c->stats, (void*)c->counters, (void*)c->packed,
+                  (void*)c->rope})
     if (p) (void)hipFree(p);
+  if (c->host_err) (void)hipHostFree(c->host_err);
   delete c;
+}
+
+int fdllm_device_status(fdllm_ctx* c) {
+  if (!c) return fail(FDLLM_EINVAL, "null context");
+  if (c->host_err && *(volatile unsigned*)c->host_err) {
+    *(volatile unsigned*)c->host_err = 0;
+    return fail(FDLLM_EHIP, "a device-side group wait gave up (workgroups were not co-resident); outputs since the "
+                            "last check are invalid");
+  }
+  return FDLLM_OK;
 }
 
 int fdllm_num_params(const fdllm_ctx* c) { return c ? (int)c->names.size() : 0; }
@@ -536,8 +567,10 @@ int fdllm_bench_op(fdllm_ctx* c, int op, int rows, int layer, int iters, void* k
       }
       case FDLLM_OP_ATTENTION:
         // the block's rows sit at the end of the attended range, as in a full cached step
-        rc = run_attention(c, rows, c->zero_i32, (uint16_t*)k + li * stride, (uint16_t*)v + li * stride,
-                           attend_len - rows, attend_len, 0, nullptr, 0, st);
+        if (it == 0) rc = rope_table(c, rows, c->zero_i32, st);
+        if (rc == FDLLM_OK)
+          rc = run_attention(c, rows, (uint16_t*)k + li * stride, (uint16_t*)v + li * stride, attend_len - rows,
+                             attend_len, 0, nullptr, 0, st);
         break;
       case FDLLM_OP_LM_HEAD_CONFIDENCE: {
         rc = run_lm_head(c, c->h, rows, nullptr, true, st);

@@ -58,6 +58,22 @@ template <int DT> __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x
 }
 
 // ---- wave reductions ------------------------------------------------------------------------
+// Sum / max over the four 16-lane rows of a wave (lanes l, l ^ 16, l ^ 32, l ^ 48), with the gfx950
+// row-swap permutes (no LDS crossbar): permlane16_swap(x, x) yields the even and odd row of each row
+// pair, permlane32_swap(x, x) the lower and upper half.
+__device__ __forceinline__ float rows_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+__device__ __forceinline__ float rows_max(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
   for (int k = 32; k >= 1; k >>= 1) v += __shfl_xor(v, k, WAVE);
   return v;

@@ -55,6 +55,8 @@ hipError_t launch_embed(const int32_t* ids, int n, const uint16_t* table, int vo
 hipError_t launch_load_rows(int dt, const uint16_t* x, int rows, int hidden, uint16_t* h, float* ssq, int ssq_ld,
                             hipStream_t st);
 // y = RMSNorm(h) from the sums of squares the producer left (final norm)
+hipError_t launch_rope_table(int dt, const int32_t* pos_offset, int rows, float neg_log_theta, float* tab,
+                             hipStream_t st);
 hipError_t launch_norm_rows(int dt, const uint16_t* h, int rows, int hidden, const float* ssq, int ssq_ld,
                             const uint16_t* w, float eps, uint16_t* y, hipStream_t st);
 
@@ -62,8 +64,7 @@ hipError_t launch_norm_rows(int dt, const uint16_t* h, int rows, int hidden, con
 struct AttnP {
   const uint16_t* qkv; int ldq;       // [rows][ldq]: q | k | v, bias added, before RoPE
   int rows, nq, nkv;
-  const int32_t* pos_offset;          // device int32: RoPE position of row 0
-  float neg_log_theta;                // (float)(-ln(theta))
+  const float* rope;                  // [rows][64][2] RoPE (cos, sin) of row r (position pos_offset + r), model-dtype values
   uint16_t* kc; uint16_t* vc;         // this layer's cache [cap][nkv][128]
   int ws;                             // rows [ws, ws + rows) are this call's: taken from qkv, written to the cache
   int Lk;                             // attended keys [0, Lk)
@@ -73,7 +74,8 @@ struct AttnP {
   const float* bias; long long bias_ld;
   int S, chunk;                       // key splits (gridDim.z), keys per split (multiple of 32)
   int target_wgs;                     // workgroups the plan aims for (attn_plan)
-  float* part; unsigned* counters;    // split partials / arrival counters
+  float* part; unsigned* counters;    // split partials / arrival counters (two per workgroup group)
+  unsigned* err;                      // set to 1 if a group wait gave up (workgroups not co-resident)
   uint16_t* out;                      // [rows][nq * 128]
 };
 struct AttnPlan { int chunked; int q_tiles_per_wg; int key_groups; int qg; int S; int chunk; };

@@ -62,6 +62,18 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(const u16* h, int hidden
   for (int c = threadIdx.x; c < hidden; c += 256) yr[c] = from_f32<DT>(to_f32<DT>(w[c]) * rnd<DT>(to_f32<DT>(hr[c]) * inv));
 }
 
+// RoPE tables of one call (cuda.py:288-299): position pos_offset + r, inv_freq = exp(-ln(theta) * i / 64),
+// angle = pos * inv_freq in fp32, cos / sin in fp32 rounded to the model dtype (emb = [f, f], so one
+// entry serves dims i and i + 64).  Shared by every layer's attention.
+template <int DT>
+__global__ __launch_bounds__(64) void rope_table_kernel(const int32_t* pos_offset, float nlt, float* tab) {
+  const int r = blockIdx.x, i = threadIdx.x;
+  const float pos = (float)(*pos_offset + r);
+  const float fr = pos * expf((nlt * (float)i) / 64.0f);
+  tab[((size_t)r * 64 + i) * 2] = rnd<DT>(cosf(fr));
+  tab[((size_t)r * 64 + i) * 2 + 1] = rnd<DT>(sinf(fr));
+}
+
 hipError_t launch_embed(const int32_t* ids, int n, const uint16_t* table, int vocab, int hidden, uint16_t* out,
                         hipStream_t st) {
   hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, st, ids, table, vocab, hidden, out);
@@ -74,6 +86,15 @@ hipError_t launch_load_rows(int dt, const uint16_t* x, int rows, int hidden, uin
     hipLaunchKernelGGL(load_rows_kernel<DT_BF16>, dim3(rows), dim3(256), 0, st, x, hidden, h, ssq, ssq_ld);
   else
     hipLaunchKernelGGL(load_rows_kernel<DT_F16>, dim3(rows), dim3(256), 0, st, x, hidden, h, ssq, ssq_ld);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_table(int dt, const int32_t* pos_offset, int rows, float neg_log_theta, float* tab,
+                             hipStream_t st) {
+  if (dt == DT_BF16)
+    hipLaunchKernelGGL(rope_table_kernel<DT_BF16>, dim3(rows), dim3(64), 0, st, pos_offset, neg_log_theta, tab);
+  else
+    hipLaunchKernelGGL(rope_table_kernel<DT_F16>, dim3(rows), dim3(64), 0, st, pos_offset, neg_log_theta, tab);
   return hipGetLastError();
 }
 

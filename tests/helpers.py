@@ -27,6 +27,7 @@ def make_pair(kw: dict, seed: int, dtype: str = "bfloat16", embed_std=None, max_
     return ref, vm
 
 
+
 def to_np(t) -> np.ndarray:
     return t.float().cpu().numpy()
 
