@@ -151,14 +151,12 @@ int run_gemm(fdllm_ctx* c, int cfg, GemmP a, int ksplit, hipStream_t st) {
   const fdllm_config& f = c->cfg;
   if (ksplit < 1 || a.KS % ksplit) return fail(FDLLM_EINVAL, "k split %d does not divide %d k steps", ksplit, a.KS);
   a.kps = a.KS / ksplit;
-  const GemmShape sh = gemm_shape(cfg);
-  const int groups = (a.ntiles + sh.tiles_per_wg - 1) / sh.tiles_per_wg;
-  const int mchunks = (a.M + 31) / 32;
+  const GemmPlan pl = gemm_plan(cfg, a, ksplit);
   if (ksplit > 1) {
-    size_t need = (size_t)groups * mchunks * ksplit * sh.tiles_per_wg * 2 * 64 * 4;
-    int rc = ensure_floats(&c->gpart, &c->gpart_floats, need);
+    int rc = ensure_floats(&c->gpart, &c->gpart_floats, pl.part_floats);
     if (rc) return rc;
-    if (groups * mchunks > c->n_counters) return fail(FDLLM_EINVAL, "too many GEMM workgroup groups (%d)", groups * mchunks);
+    if (pl.groups * pl.mchunks > c->n_counters)
+      return fail(FDLLM_EINVAL, "too many GEMM workgroup groups (%d)", pl.groups * pl.mchunks);
     a.part = c->gpart;
     a.counters = c->counters;
   }

@@ -20,6 +20,8 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <algorithm>
+
 namespace fdllm {
 
 __device__ __forceinline__ const u32x4* wblock(const u16* W, int KS, int t, int s) {
@@ -332,6 +334,225 @@ __global__ __launch_bounds__(64 * TW * KW) void gemm_pk_kernel(GemmP a) {
   }
 }
 
+// ---- one-shot skinny GEMM (M <= 32 rows per m-chunk) --------------------------------------------
+// A workgroup of NW = 8 waves owns NT consecutive 16-row weight tiles and the k steps of one
+// cross-workgroup split (gridDim.y).  Every wave requests all of its packed weight blocks at once (its
+// share of the split's k steps for all NT tiles, at most KPW steps), so the workgroup's whole weight
+// slice is in flight together.  The activation rows of the split are loaded once per workgroup,
+// normalised (XF_RMS) and kept in LDS in MFMA fragment order.  The waves' partial sums are added in
+// LDS in wave order, one (tile or pair, 16-row block) per wave; split partials are added in split
+// order by the workgroup that arrives last.  Results are deterministic.
+template <int DT, int EPI, int XF, int MT, int NT, int KPW>
+__global__ __launch_bounds__(512) void gemm_os_kernel(GemmP a) {
+  constexpr int NW = 8;
+  constexpr int UNITS = (EPI == EPI_SILU_PAIR ? NT / 2 : NT) * MT;
+  static_assert(UNITS <= NW, "one epilogue unit per wave");
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ float inv_s[32];
+  __shared__ int flag_s;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int m0 = blockIdx.z * 32, mlast = a.M - 1;
+  const int t0 = blockIdx.x * NT;
+  const int kb = blockIdx.y * a.kps;  // first k step of the split
+  const int kq = a.kps / NW, kr = a.kps % NW;
+  const int ws = kq * w + min(w, kr), wn = kq + (w < kr ? 1 : 0);  // this wave's k steps [ws, ws + wn)
+  u32x4* xl = reinterpret_cast<u32x4*>(smem);                      // [kps][MT][64] fragments
+
+  // 1. inputs of the activation staging first (their waits then do not cover the weight loads)
+  float ssv[16];
+  if constexpr (XF == XF_RMS) {
+    if (threadIdx.x < 256) {
+      const int m = m0 + (threadIdx.x >> 3), pp = threadIdx.x & 7;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int t = pp + 8 * q;
+        ssv[q] = (m < a.M && t < a.ssq_tiles) ? a.ssq[(size_t)t * a.ssq_ld + m] : 0.f;
+      }
+    }
+  }
+  // the split's norm weights go to LDS behind the fragments (one 16-byte chunk per thread)
+  u32x4* nwl = xl + (size_t)a.kps * MT * 64;  // [kps * 4] chunks of 8 weights
+  u32x4 nwv = {0u, 0u, 0u, 0u};
+  if constexpr (XF == XF_RMS) {
+    if ((int)threadIdx.x < a.kps * 4) nwv = *reinterpret_cast<const u32x4*>(a.nw + 32 * kb + 8 * threadIdx.x);
+  }
+  // activation fragments per thread: F1 requested before the weights, the rest (F2) after them, so
+  // that the registers of both are never live at once (kps * MT * 64 <= 512 * (F1 + F2))
+  constexpr int F1 = 6, F2 = 6;
+  const int nfrag = a.kps * MT * 64;
+  auto xload = [&](int f) {
+    f = min(f, nfrag - 1);
+    const int sl = f / (MT * 64), rem = f - sl * (MT * 64), mt = rem >> 6, l = rem & 63;
+    const int m = min(m0 + 16 * mt + (l & 15), mlast);
+    const int k = 32 * (kb + sl) + 8 * (l >> 4);
+    return *reinterpret_cast<const u32x4*>(a.X + (size_t)m * a.ldx + k);
+  };
+  u32x4 xv[F1];
+#pragma unroll
+  for (int i = 0; i < F1; ++i) xv[i] = xload(threadIdx.x + 512 * i);
+  // 2. the weight slice: KPW k steps x NT tiles per wave, all requested now (steps past wn re-read
+  //    the wave's first step and are not multiplied)
+  u32x4 A[KPW][NT];
+#pragma unroll
+  for (int s = 0; s < KPW; ++s)
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+      A[s][j] = __builtin_nontemporal_load(wblock(a.W, a.KS, t0 + j, kb + (s < wn ? ws + s : min(ws, a.kps - 1))));
+
+  // 3. 1 / rms of the chunk's rows, then the normalised fragments into LDS
+  if constexpr (XF == XF_RMS) {
+    if (threadIdx.x < 256) {
+      float ss = 0.f;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) ss += ssv[q];
+      const int m = m0 + (threadIdx.x >> 3), pp = threadIdx.x & 7;
+      for (int q = 16; pp + 8 * q < a.ssq_tiles; ++q) ss += (m < a.M) ? a.ssq[(size_t)(pp + 8 * q) * a.ssq_ld + m] : 0.f;
+      ss += __shfl_xor(ss, 1, WAVE);
+      ss += __shfl_xor(ss, 2, WAVE);
+      ss += __shfl_xor(ss, 4, WAVE);
+      if (pp == 0) inv_s[threadIdx.x >> 3] = 1.0f / sqrtf(ss / (float)a.H + a.eps);
+    }
+    if ((int)threadIdx.x < a.kps * 4) nwl[threadIdx.x] = nwv;
+    __syncthreads();
+  }
+  auto xstore = [&](int f, u32x4 x) {
+    if (f < nfrag) {
+      if constexpr (XF == XF_RMS) {
+        const int sl = f / (MT * 64), rem = f - sl * (MT * 64), mt = rem >> 6, l = rem & 63;
+        xl[f] = xform<DT, XF>(x, nwl[sl * 4 + (l >> 4)], inv_s[16 * mt + (l & 15)]);
+      } else {
+        xl[f] = x;
+      }
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < F1; ++i) xstore(threadIdx.x + 512 * i, xv[i]);
+  if (nfrag > 512 * F1) {
+    u32x4 xw[F2];
+#pragma unroll
+    for (int i = 0; i < F2; ++i) xw[i] = xload(threadIdx.x + 512 * (F1 + i));
+#pragma unroll
+    for (int i = 0; i < F2; ++i) xstore(threadIdx.x + 512 * (F1 + i), xw[i]);
+  }
+  __syncthreads();
+
+  // 4. multiply: fragment (kstep s, block mt) read from LDS once per step for all NT tiles
+  f32x4 acc[NT][MT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[j][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < KPW; ++s) {
+    if (s < wn) {
+      u32x4 b[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) b[mt] = xl[((ws + s) * MT + mt) * 64 + lane];
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[j][mt] = mfma16<DT>(A[s][j], b[mt], acc[j][mt]);
+    }
+  }
+
+  // 5. the waves' partials into LDS (the activation region is free now), summed per unit in wave order
+  __syncthreads();
+  f32x4* red = reinterpret_cast<f32x4*>(smem);  // [NW][NT][MT][64]
+#pragma unroll
+  for (int j = 0; j < NT; ++j)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) red[((w * NT + j) * MT + mt) * 64 + lane] = acc[j][mt];
+  __syncthreads();
+  constexpr int TPU = EPI == EPI_SILU_PAIR ? 2 : 1;  // tiles per unit
+  f32x4 v[TPU] = {};
+  const int u = w;
+  const bool has_unit = u < UNITS;
+  const int ut = (u / MT) * TPU, umt = u % MT;  // unit's first tile (within the workgroup) and row block
+  if (has_unit) {
+#pragma unroll
+    for (int q = 0; q < TPU; ++q) {
+      f32x4 sum = red[((0 * NT + ut + q) * MT + umt) * 64 + lane];
+      for (int ww = 1; ww < NW; ++ww) sum += red[((ww * NT + ut + q) * MT + umt) * 64 + lane];
+      v[q] = sum;
+    }
+  }
+
+  // 6. cross-workgroup k splits: partials with agent-scope stores, the last arriver adds them in order
+  if (gridDim.y > 1) {
+    const size_t grp = (size_t)blockIdx.z * gridDim.x + blockIdx.x;
+    constexpr int per = NT * MT * 64;  // f32x4 per split partial
+    f32x4* part = reinterpret_cast<f32x4*>(a.part) + grp * gridDim.y * per;
+    if (has_unit) {
+#pragma unroll
+      for (int q = 0; q < TPU; ++q) st_agent4(part + blockIdx.y * per + ((ut + q) * MT + umt) * 64 + lane, v[q]);
+    }
+    if (!arrive_last(a.counters + grp, gridDim.y, &flag_s)) return;
+    if (has_unit) {
+#pragma unroll
+      for (int q = 0; q < TPU; ++q) {
+        const size_t o = ((ut + q) * MT + umt) * 64 + lane;
+        f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+        constexpr int SB = 16;
+        for (int y0 = 0; y0 < (int)gridDim.y; y0 += SB) {
+          f32x4 pv[SB];
+#pragma unroll
+          for (int y = 0; y < SB; ++y) pv[y] = ld_agent4(part + (size_t)min(y0 + y, (int)gridDim.y - 1) * per + o);
+#pragma unroll
+          for (int y = 0; y < SB; ++y)
+            if (y0 + y < (int)gridDim.y) sum = (y0 + y == 0) ? pv[y] : sum + pv[y];
+        }
+        v[q] = sum;
+      }
+    }
+  }
+  if (!has_unit) return;
+
+  // 7. epilogue of the unit: lane holds rows m0 + 16 umt + lr, columns 16 t + 4 lg .. + 3
+  const int m = m0 + 16 * umt + lr;
+  const int t = t0 + ut;
+  if constexpr (EPI == EPI_SILU_PAIR) {
+    const int n = 16 * (t / 2) + 4 * lg;
+    if (m < a.M && n < a.N) {
+      u16 out[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float gt = rnd<DT>(v[0][i]);
+        const float up = rnd<DT>(v[1][i]);
+        const float sl = rnd<DT>(gt * (1.0f / (1.0f + expf(-gt))));
+        out[i] = from_f32<DT>(sl * up);
+      }
+      *reinterpret_cast<u32x2*>(a.Y + (size_t)m * a.ldy + n) = u32x2{pack2(out[0], out[1]), pack2(out[2], out[3])};
+    }
+  } else {
+    const int n = 16 * t + 4 * lg;
+    const bool ok = m < a.M && n < a.N;
+    u16 out[4];
+    float ss = 0.f;
+    if (ok) {
+      if constexpr (EPI == EPI_BIAS) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) out[i] = from_f32<DT>(v[0][i] + to_f32<DT>(a.bias[n + i]));
+      } else {
+        const u32x2 hv = *reinterpret_cast<const u32x2*>(a.Y + (size_t)m * a.ldy + n);
+        const float hf[4] = {lo_f32<DT>(hv[0]), hi_f32<DT>(hv[0]), lo_f32<DT>(hv[1]), hi_f32<DT>(hv[1])};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          out[i] = from_f32<DT>(hf[i] + rnd<DT>(v[0][i]));
+          const float y = to_f32<DT>(out[i]);
+          ss += y * y;
+        }
+      }
+      *reinterpret_cast<u32x2*>(a.Y + (size_t)m * a.ldy + n) = u32x2{pack2(out[0], out[1]), pack2(out[2], out[3])};
+    }
+    if constexpr (EPI == EPI_RESID) {
+      ss += __shfl_xor(ss, 16, WAVE);
+      ss += __shfl_xor(ss, 32, WAVE);
+      if (lg == 0 && m < a.M && 16 * t < a.N) a.ssq_out[(size_t)t * a.ssq_ld + m] = ss;
+    }
+  }
+}
+
 // One wave per row: combine the tile statistics into (argmax, maxp) in the fixed lane order.
 __global__ __launch_bounds__(64) void confidence_combine_kernel(const float* stat_m, const int32_t* stat_a,
                                                                 const float* stat_s, int tiles, int rows,
@@ -431,58 +652,131 @@ template <int EPI, int XF, int TPW, int TW, int KW, int U>
 struct Cfg {
   static constexpr int epi = EPI, xf = XF, tpw = TPW, tw = TW, kw = KW, u = U;
 };
+// streaming kernel (any M: prefill chunks, the lm_head)
 using CfgQkv = Cfg<EPI_BIAS, XF_RMS, 1, 1, 8, 3>;
 using CfgOproj = Cfg<EPI_RESID, XF_NONE, 1, 1, 8, 3>;
 using CfgGateUp = Cfg<EPI_SILU_PAIR, XF_RMS, 2, 2, 2, 4>;
 using CfgDown = Cfg<EPI_RESID, XF_NONE, 1, 4, 2, 4>;
 using CfgLmHead = Cfg<EPI_LOGITS, XF_NONE, 4, 4, 1, 2>;
+// one-shot kernel (M <= 32): tiles per workgroup, max k steps per wave
+template <int EPI, int XF, int NT, int KPW>
+struct OsCfg {
+  static constexpr int epi = EPI, xf = XF, nt = NT, kpw = KPW;
+};
+using OsQkv = OsCfg<EPI_BIAS, XF_RMS, 1, 6>;
+using OsOproj = OsCfg<EPI_RESID, XF_NONE, 1, 6>;
+using OsGateUp = OsCfg<EPI_SILU_PAIR, XF_RMS, 6, 6>;
+using OsDown = OsCfg<EPI_RESID, XF_NONE, 4, 5>;
 
-template <class C> constexpr GemmShape shape_of() { return GemmShape{C::tpw * C::tw, C::tw * C::kw}; }
+template <class C> constexpr int tiles_of() { return C::tpw * C::tw; }
 
-GemmShape gemm_shape(int cfg) {
+static int streaming_tiles(int cfg) {
   switch (cfg) {
-    case CFG_QKV: return shape_of<CfgQkv>();
-    case CFG_OPROJ: return shape_of<CfgOproj>();
-    case CFG_GATE_UP: return shape_of<CfgGateUp>();
-    case CFG_DOWN: return shape_of<CfgDown>();
-    default: return shape_of<CfgLmHead>();
+    case CFG_QKV: return tiles_of<CfgQkv>();
+    case CFG_OPROJ: return tiles_of<CfgOproj>();
+    case CFG_GATE_UP: return tiles_of<CfgGateUp>();
+    case CFG_DOWN: return tiles_of<CfgDown>();
+    default: return tiles_of<CfgLmHead>();
+  }
+}
+static int os_tiles(int cfg) {
+  switch (cfg) {
+    case CFG_QKV: return OsQkv::nt;
+    case CFG_OPROJ: return OsOproj::nt;
+    case CFG_GATE_UP: return OsGateUp::nt;
+    case CFG_DOWN: return OsDown::nt;
+    default: return 0;
+  }
+}
+static int os_kpw(int cfg) {
+  switch (cfg) {
+    case CFG_QKV: return OsQkv::kpw;
+    case CFG_OPROJ: return OsOproj::kpw;
+    case CFG_GATE_UP: return OsGateUp::kpw;
+    case CFG_DOWN: return OsDown::kpw;
+    default: return 0;
   }
 }
 
+GemmShape gemm_shape(int cfg) {
+  const int a = streaming_tiles(cfg), b = os_tiles(cfg);
+  int l = a;
+  if (b > 0) {
+    l = a * b;
+    for (int x = a, y = b; y != 0;) { const int r = x % y; x = y; y = r; if (y == 0) l /= x; }
+  }
+  return GemmShape{l, 0};
+}
+
+GemmPlan gemm_plan(int cfg, const GemmP& a, int ksplit) {
+  GemmPlan p{};
+  p.mchunks = (a.M + 31) / 32;
+  const int nt = os_tiles(cfg);
+  const int mt = a.M <= 16 ? 1 : 2;
+  p.one_shot = nt > 0 && a.M <= 32 && a.kps <= 8 * os_kpw(cfg) && a.kps * mt <= 96 && a.ntiles % nt == 0;  // 96 = 512 * (F1 + F2) / 64
+  const int tiles = p.one_shot ? nt : streaming_tiles(cfg);
+  p.tiles_per_wg = tiles;
+  p.groups = (a.ntiles + tiles - 1) / tiles;
+  p.part_floats = ksplit > 1 ? (size_t)p.groups * p.mchunks * ksplit * tiles * 2 * 64 * 4 : 0;
+  return p;
+}
+
 template <int DT, class C, int MT>
-static hipError_t launch_cfg(const GemmP& a, int ksplit, hipStream_t st) {
-  constexpr int tiles = C::tpw * C::tw;
-  const int groups = (a.ntiles + tiles - 1) / tiles;
-  const int mchunks = (a.M + 31) / 32;
+static hipError_t launch_cfg(const GemmP& a, const GemmPlan& p, int ksplit, hipStream_t st) {
   size_t lds = 0;
   if (C::kw > 1) lds = (size_t)(C::kw - 1) * C::tw * C::tpw * MT * 64 * 16;
   if (C::epi == EPI_LOGITS) lds = (size_t)32 * 256 * 4;
   auto kern = gemm_pk_kernel<DT, C::epi, C::xf, MT, C::tpw, C::tw, C::kw, C::u>;
-  hipLaunchKernelGGL(kern, dim3(groups, ksplit, mchunks), dim3(64 * C::tw * C::kw), lds, st, a);
+  hipLaunchKernelGGL(kern, dim3(p.groups, ksplit, p.mchunks), dim3(64 * C::tw * C::kw), lds, st, a);
   return hipGetLastError();
 }
 
-template <int DT, class C>
-static hipError_t launch_mt(const GemmP& a, int ksplit, hipStream_t st) {
-  if (a.M <= 16) return launch_cfg<DT, C, 1>(a, ksplit, st);
-  return launch_cfg<DT, C, 2>(a, ksplit, st);
+template <int DT, class C, int MT>
+static hipError_t launch_os(const GemmP& a, const GemmPlan& p, int ksplit, hipStream_t st) {
+  const size_t lds = std::max((size_t)a.kps * MT * 1024 + (size_t)a.kps * 64, (size_t)8 * C::nt * MT * 1024);
+  auto kern = gemm_os_kernel<DT, C::epi, C::xf, MT, C::nt, C::kpw>;
+  static size_t attr_lds = 0;  // per instantiation
+  if (lds > 64 * 1024 && lds > attr_lds) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) ==
+        hipSuccess)
+      attr_lds = lds;
+    else
+      (void)hipGetLastError();
+  }
+  hipLaunchKernelGGL(kern, dim3(p.groups, ksplit, p.mchunks), dim3(512), lds, st, a);
+  return hipGetLastError();
 }
 
+template <int DT, class C, class O>
+static hipError_t launch_mt(const GemmP& a, const GemmPlan& p, int ksplit, hipStream_t st) {
+  if constexpr (O::nt > 0) {
+    if (p.one_shot) {
+      if (a.M <= 16) return launch_os<DT, O, 1>(a, p, ksplit, st);
+      return launch_os<DT, O, 2>(a, p, ksplit, st);
+    }
+  }
+  if (a.M <= 16) return launch_cfg<DT, C, 1>(a, p, ksplit, st);
+  return launch_cfg<DT, C, 2>(a, p, ksplit, st);
+}
+
+using OsNone = OsCfg<EPI_LOGITS, XF_NONE, 0, 0>;
+
 template <int DT>
-static hipError_t launch_dt(int cfg, const GemmP& a, int ksplit, hipStream_t st) {
+static hipError_t launch_dt(int cfg, const GemmP& a, const GemmPlan& p, int ksplit, hipStream_t st) {
   switch (cfg) {
-    case CFG_QKV: return launch_mt<DT, CfgQkv>(a, ksplit, st);
-    case CFG_OPROJ: return launch_mt<DT, CfgOproj>(a, ksplit, st);
-    case CFG_GATE_UP: return launch_mt<DT, CfgGateUp>(a, ksplit, st);
-    case CFG_DOWN: return launch_mt<DT, CfgDown>(a, ksplit, st);
-    case CFG_LM_HEAD: return launch_mt<DT, CfgLmHead>(a, ksplit, st);
+    case CFG_QKV: return launch_mt<DT, CfgQkv, OsQkv>(a, p, ksplit, st);
+    case CFG_OPROJ: return launch_mt<DT, CfgOproj, OsOproj>(a, p, ksplit, st);
+    case CFG_GATE_UP: return launch_mt<DT, CfgGateUp, OsGateUp>(a, p, ksplit, st);
+    case CFG_DOWN: return launch_mt<DT, CfgDown, OsDown>(a, p, ksplit, st);
+    case CFG_LM_HEAD: return launch_mt<DT, CfgLmHead, OsNone>(a, p, ksplit, st);
     default: return hipErrorInvalidValue;
   }
 }
 
 hipError_t launch_gemm(int dt, int cfg, const GemmP& a, int ksplit, hipStream_t st) {
-  if (dt == DT_BF16) return launch_dt<DT_BF16>(cfg, a, ksplit, st);
-  return launch_dt<DT_F16>(cfg, a, ksplit, st);
+  const GemmPlan p = gemm_plan(cfg, a, ksplit);
+  if (dt == DT_BF16) return launch_dt<DT_BF16>(cfg, a, p, ksplit, st);
+  return launch_dt<DT_F16>(cfg, a, p, ksplit, st);
 }
 
 hipError_t launch_pack(const uint16_t* src, int N, int K, int ntiles, int mode, uint16_t* dst, hipStream_t st) {

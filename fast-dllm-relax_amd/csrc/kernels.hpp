@@ -38,8 +38,12 @@ struct GemmP {
 
 // Launch configurations (see gemm.hip); the host picks one per projection.
 enum GemmCfg : int { CFG_QKV = 0, CFG_OPROJ = 1, CFG_GATE_UP = 2, CFG_DOWN = 3, CFG_LM_HEAD = 4 };
+// tiles_per_wg: the padding unit of the packed tile count (every kernel of the projection divides it)
 struct GemmShape { int tiles_per_wg; int waves; };
 GemmShape gemm_shape(int cfg);
+// The kernel and grid a launch uses: groups x ksplit x mchunks workgroups, part_floats of split partials.
+struct GemmPlan { int one_shot; int tiles_per_wg; int groups; int mchunks; size_t part_floats; };
+GemmPlan gemm_plan(int cfg, const GemmP& a, int ksplit);
 hipError_t launch_gemm(int dt, int cfg, const GemmP& a, int ksplit, hipStream_t st);
 
 // ---- confidence ---------------------------------------------------------------------------------
