@@ -21,7 +21,7 @@ EXPORTS = (
     "fdllm_embed", "fdllm_forward_hidden", "fdllm_get_logits", "fdllm_build_prefix_cache",
     "fdllm_forward_cached", "fdllm_forward_block_partial", "fdllm_forward_block_partial_rp0",
     "fdllm_forward_block_partial_rp8", "fdllm_forward_block_partial_rp16", "fdllm_forward_block_partial_rp24",
-    "fdllm_get_confidence", "fdllm_confidence_from_logits", "fdllm_bench_op", "fdllm_device_status", "fdllm_last_error",
+    "fdllm_get_confidence", "fdllm_confidence_from_logits", "fdllm_bench_op", "fdllm_last_error",
 )
 
 OP_QKV, OP_O_PROJ, OP_GATE_UP, OP_DOWN, OP_ATTENTION, OP_LM_HEAD_CONFIDENCE = range(6)
@@ -59,7 +59,6 @@ _SIGS = {
     "fdllm_get_confidence": ([_P, _P, _I, _P, _P, _P, _P], _I),
     "fdllm_confidence_from_logits": ([_P, _P, _I, _I, _I, _P, _P, _P], _I),
     "fdllm_bench_op": ([_P, _I, _I, _I, _I, _P, _P, _I, _I, _P], _I),
-    "fdllm_device_status": ([_P], _I),
     "fdllm_last_error": ([], ctypes.c_char_p),
 }
 

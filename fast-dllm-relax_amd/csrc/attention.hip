@@ -12,9 +12,10 @@
 // (the query rows of the grp heads sharing g are stacked: row qi = head_in_group * rows + r, 16 per
 // tile).  The workgroup's QPW x KSW waves are QPW query-tile slots times KSW key groups; key group kg
 // stages blocks of 32 keys (K row-major, V transposed four keys at a time) in its own LDS buffers and
-// its waves run the scores S^T = K . Q^T and O += P . V for their query tiles.  Key groups are merged
-// in LDS in fixed order; key splits (S > 1) leave agent-coherent partials and the workgroup that
-// arrives last merges them in split order, so results are deterministic.
+// its waves run the scores S^T = K . Q^T and O^T += V^T . P^T for their query tiles (a lane holds one
+// query, so its softmax statistics stay in-lane).  Key groups are merged in LDS in fixed order; key
+// splits (S > 1) leave partials that attn_merge_kernel combines in split order, so results are
+// deterministic.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -60,7 +61,6 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
   constexpr int NT = 64 * QPW;  // threads of one key group
   constexpr int KBUF = KB * KLD, VBUF = HD * VLD;
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ int flag_s;
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int qw = w % QPW, kg = w / QPW;
@@ -194,8 +194,7 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
         s[kt][i] = v;
         mx = fmaxf(mx, v);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+    mx = rows_max(mx);
     const float m_new = fmaxf(m_run, mx);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
     const float alpha = expf(m_run - m_use);
@@ -208,18 +207,11 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
         s[kt][i] = p;
         ps += p;
       }
-    ps += __shfl_xor(ps, 16, WAVE);
-    ps += __shfl_xor(ps, 32, WAVE);
+    ps = rows_sum(ps);
     l_run = l_run * alpha + ps;
     m_run = m_new;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float al = __shfl(alpha, 4 * lg + i, WAVE);
-#pragma unroll
-      for (int dt = 0; dt < HD / 16; ++dt) o[dt][i] *= al;
-    }
-    // P as the A operand: k slot 8 lg + e holds key 4 lg + e (e < 4) or 16 + 4 lg + e - 4 (e >= 4);
-    // the V fragment below reads the same keys, so the contraction is over the same 32 keys.
+    // P^T as the B operand: k slot 8 lg + e holds key 4 lg + e (e < 4) or 16 + 4 lg + e - 4 (e >= 4);
+    // the V^T fragment (A operand) reads the same keys; O^T accumulates with this lane's query lr
     const u32x4 pa = {pack2(from_f32<DT>(s[0][0]), from_f32<DT>(s[0][1])),
                       pack2(from_f32<DT>(s[0][2]), from_f32<DT>(s[0][3])),
                       pack2(from_f32<DT>(s[1][0]), from_f32<DT>(s[1][1])),
@@ -229,13 +221,12 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
       const u16* vrow = vbuf + (16 * dt + lr) * VLD + 4 * lg;
       const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
       const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 16);
-      o[dt] = mfma16<DT>(pa, u32x4{lo[0], lo[1], hi[0], hi[1]}, o[dt]);
+      o[dt] = mfma16<DT>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pa, o[dt] * alpha);
     }
   }
 
-  // ---- merge the key groups in LDS (fixed order kg = 0, 1, ...) ----
-  // lane holds O rows q = 4 lg + i (dims 16 dt + lr); m_run / l_run belong to query lr.
-  float Mq[4], Lq[4];
+  // ---- merge the key groups in LDS (fixed order kg = 0, 1, ...); lane holds O^T[dims][query lr] ----
+  float Mq, Lq;
   __syncthreads();
   {
     float* cm = reinterpret_cast<float*>(smem);
@@ -251,148 +242,43 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
     }
     __syncthreads();
     if (kg == 0) {
+      float M = -INFINITY;
+      for (int k2 = 0; k2 < KSW; ++k2) M = fmaxf(M, cm[(k2 * QPW + qw) * 16 + lr]);
+      const float Mu = M == -INFINITY ? 0.f : M;
+      float L = 0.f;
+      for (int k2 = 0; k2 < KSW; ++k2) L += cl[(k2 * QPW + qw) * 16 + lr] * expf(cm[(k2 * QPW + qw) * 16 + lr] - Mu);
+      const float f0 = expf(cm[qw * 16 + lr] - Mu);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int q = 4 * lg + i;
-        float M = -INFINITY;
-        for (int k = 0; k < KSW; ++k) M = fmaxf(M, cm[(k * QPW + qw) * 16 + q]);
-        const float Mu = M == -INFINITY ? 0.f : M;
-        float L = 0.f;
-        for (int k = 0; k < KSW; ++k) L += cl[(k * QPW + qw) * 16 + q] * expf(cm[(k * QPW + qw) * 16 + q] - Mu);
-        const float f0 = expf(cm[qw * 16 + q] - Mu);
+      for (int dt = 0; dt < HD / 16; ++dt) o[dt] *= f0;
+      for (int k2 = 1; k2 < KSW; ++k2) {
+        const float fk = expf(cm[(k2 * QPW + qw) * 16 + lr] - Mu);
 #pragma unroll
-        for (int dt = 0; dt < HD / 16; ++dt) o[dt][i] *= f0;
-        for (int k = 1; k < KSW; ++k) {
-          const float fk = expf(cm[(k * QPW + qw) * 16 + q] - Mu);
-#pragma unroll
-          for (int dt = 0; dt < HD / 16; ++dt) o[dt][i] += co[(((k - 1) * QPW + qw) * (HD / 16) + dt) * 64 + lane][i] * fk;
-        }
-        Mq[i] = M;
-        Lq[i] = L;
+        for (int dt = 0; dt < HD / 16; ++dt) o[dt] += co[(((k2 - 1) * QPW + qw) * (HD / 16) + dt) * 64 + lane] * fk;
       }
+      Mq = M;
+      Lq = L;
     }
   }
-
-  auto store_out = [&](int q, int dim, float v) {
-    const int row = qt * 16 + q;
-    if (row >= QR) return;
-    const int h2 = row / a.rows, r2 = row - h2 * a.rows;
-    a.out[(size_t)r2 * a.nq * HD + (g * grp + h2) * HD + dim] = from_f32<DT>(v);
-  };
-
+  if (kg != 0 || !tile_ok) return;
   if (a.S == 1) {
-    if (kg == 0 && tile_ok) {
+    if (qvalid) {
+      const float inv = 1.0f / Lq;
+      u16* dst = a.out + (size_t)r * a.nq * HD + (g * grp + hh) * HD + 4 * lg;
 #pragma unroll
       for (int dt = 0; dt < HD / 16; ++dt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) store_out(4 * lg + i, 16 * dt + lr, o[dt][i] / Lq[i]);
+        *reinterpret_cast<u32x2*>(dst + 16 * dt) =
+            u32x2{pack2(from_f32<DT>(o[dt][0] * inv), from_f32<DT>(o[dt][1] * inv)),
+                  pack2(from_f32<DT>(o[dt][2] * inv), from_f32<DT>(o[dt][3] * inv))};
     }
     return;
   }
-
-  // ---- key splits: agent-coherent partials, merged by the last workgroup in split order ----
-  if (kg == 0 && tile_ok) {
-    float* pp = a.part + ((size_t)(g * QT + qt) * a.S + c) * PSZ;
+  // key splits: the partial of (g, qt, c) in the layout attn_merge_kernel reads
+  float* pp = a.part + ((size_t)(g * QT + qt) * a.S + c) * PSZ;
 #pragma unroll
-    for (int dt = 0; dt < HD / 16; ++dt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) st_agent(pp + (dt * 4 + i) * 64 + lane, o[dt][i]);
-    if (lr == 0) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        st_agent(pp + 16 * HD + 4 * lg + i, Mq[i]);
-        st_agent(pp + 16 * HD + 16 + 4 * lg + i, Lq[i]);
-      }
-    }
-  }
-  if (!arrive_last(a.counters + g * gridDim.x + blockIdx.x, a.S, &flag_s)) return;
-  // the splits' m and l of this workgroup's query tiles, staged in LDS with all loads in flight at once
-  float* ml = reinterpret_cast<float*>(smem);  // [QPW][S][32]: m of rows 0..15, then l
-  const int nml = QPW * a.S * 32;
-  for (int idx = threadIdx.x; idx < nml; idx += blockDim.x) {
-    const int q = idx / (a.S * 32), rem = idx - q * (a.S * 32);
-    const int qt2 = blockIdx.x * QPW + q;
-    ml[idx] = qt2 < QT ? ld_agent(a.part + ((size_t)(g * QT + qt2) * a.S + (rem >> 5)) * PSZ + 16 * HD + (rem & 31))
-                       : 0.f;
-  }
-  __syncthreads();
-  if (!tile_ok) return;
-  // every wave of the last workgroup merges its query tile for dims [128 kg / KSW, 128 (kg + 1) / KSW)
-  const float* mlq = ml + qw * a.S * 32;
-  const float* pt = a.part + (size_t)(g * QT + qt) * a.S * PSZ;
-  constexpr int DPW = (HD / 16) / KSW;  // dim tiles per wave
-  float M[4], L[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int q = 4 * lg + i;
-    M[i] = -INFINITY;
-    for (int sp = 0; sp < a.S; ++sp) M[i] = fmaxf(M[i], mlq[sp * 32 + q]);
-    if (M[i] == -INFINITY) M[i] = 0.f;
-    L[i] = 0.f;
-    for (int sp = 0; sp < a.S; ++sp) L[i] += mlq[sp * 32 + 16 + q] * expf(mlq[sp * 32 + q] - M[i]);
-  }
-  float acc[DPW][4];
-#pragma unroll
-  for (int d = 0; d < DPW; ++d)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[d][i] = 0.f;
-  constexpr int SB = 8;  // splits whose partial O is requested before any is added
-  for (int s0 = 0; s0 < a.S; s0 += SB) {
-    float v[SB][DPW][4];
-#pragma unroll
-    for (int q = 0; q < SB; ++q)
-#pragma unroll
-      for (int d = 0; d < DPW; ++d)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          v[q][d][i] = s0 + q < a.S ? ld_agent(pt + (s0 + q) * PSZ + ((kg * DPW + d) * 4 + i) * 64 + lane) : 0.f;
-#pragma unroll
-    for (int q = 0; q < SB; ++q) {
-      if (s0 + q >= a.S) break;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float f = expf(mlq[(s0 + q) * 32 + 4 * lg + i] - M[i]);
-#pragma unroll
-        for (int d = 0; d < DPW; ++d) acc[d][i] += v[q][d][i] * f;
-      }
-    }
-  }
-#pragma unroll
-  for (int d = 0; d < DPW; ++d)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) store_out(4 * lg + i, 16 * (kg * DPW + d) + lr, acc[d][i] / L[i]);
-}
-
-// Waits until `expected` workgroups (this one included) have arrived at ctr[0].  Every store this
-// workgroup made before the call is complete and agent-visible first.  The wait is bounded: if the
-// group's workgroups are not all resident it gives up, sets *err and carries on (the results are then
-// wrong, and the host reports the flag), so a wave never spins forever.
-__device__ __forceinline__ void group_wait(unsigned* ctr, unsigned expected, unsigned* err) {
-  wait_memory();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    int spins = 0;
-    while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < expected) {
-      __builtin_amdgcn_s_sleep(2);
-      if (++spins > (1 << 22)) {
-        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-    }
-  }
-  __syncthreads();
-}
-
-// The group's last workgroup to leave returns both counters (ctr[0] arrivals, ctr[1] departures) to
-// zero; every workgroup has passed its wait by then, so the next launch starts from zero.
-__device__ __forceinline__ void group_leave(unsigned* ctr, unsigned expected) {
-  if (threadIdx.x == 0) {
-    const unsigned old = __hip_atomic_fetch_add(ctr + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old == expected - 1) {
-      __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(ctr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+  for (int dt = 0; dt < HD / 16; ++dt) reinterpret_cast<f32x4*>(pp)[dt * 64 + lane] = o[dt];
+  if (lg == 0) {
+    pp[16 * HD + lr] = Mq;
+    pp[16 * HD + 16 + lr] = Lq;
   }
 }
 
@@ -401,9 +287,8 @@ __device__ __forceinline__ void group_leave(unsigned* ctr, unsigned expected) {
 // once, so the chunk costs one memory latency instead of one per 32-key block.  Waves are QPW query
 // tiles times KH key parts.  The output is accumulated transposed, O^T = V^T P^T, so that a lane holds
 // one query (its softmax statistics stay in-lane) and the row reductions use row-swap permutes.  The
-// key parts are merged in LDS; key splits (gridDim.z) store their partials, wait for the rest of their
-// group and merge one (query tile, 16-dim slice) per wave, with the split weights computed once per
-// query.
+// key parts are merged in LDS; with key splits (gridDim.z > 1) each workgroup stores its partial and
+// attn_merge_kernel, launched next on the stream, combines them across many workgroups.
 template <int DT, int QPW, int KH, int CH>
 __global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP a) {
   constexpr int NT = 64 * QPW * KH;
@@ -639,66 +524,65 @@ __global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP a) {
     return;
   }
 
-  // ---- key splits: partials, a wait for the whole group, then a parallel merge ----
-  // partial of (g, qt, c): O^T as f32x4 [HD / 16][64 lanes], then m and l of the tile's 16 queries
+  // ---- key splits: the partial of (g, qt, c): O^T as f32x4 [HD / 16][64 lanes], then m and l of the
+  // tile's 16 queries; attn_merge_kernel combines them ----
   if (kh == 0 && tile_ok) {
     float* pp = a.part + ((size_t)(g * QT + qt) * a.S + c) * PSZ;
 #pragma unroll
-    for (int dt = 0; dt < DT16; ++dt) st_agent4(reinterpret_cast<f32x4*>(pp) + dt * 64 + lane, o[dt]);
+    for (int dt = 0; dt < DT16; ++dt) reinterpret_cast<f32x4*>(pp)[dt * 64 + lane] = o[dt];
     if (lg == 0) {
-      st_agent(pp + 16 * HD + lr, Mq);
-      st_agent(pp + 16 * HD + 16 + lr, Lq);
+      pp[16 * HD + lr] = Mq;
+      pp[16 * HD + 16 + lr] = Lq;
     }
   }
-  unsigned* grp_ctr = a.counters + 2 * ((size_t)g * gridDim.x + blockIdx.x);
-  group_wait(grp_ctr, (unsigned)a.S, a.err);
+}
 
-  // merge unit = (query tile of the group, 16-dim slice): one wave.  The split weights
-  // exp(m_c - M) depend only on the query, so each lane computes them once for its query lr.
-  constexpr int NW = QPW * KH, SB = 8;
-  for (int u = c * NW + w; u < QPW * DT16; u += a.S * NW) {
-    const int ql = u / DT16, dt = u - ql * DT16;
-    const int qt2 = blockIdx.x * QPW + ql;
-    if (qt2 >= QT) continue;
-    const float* pt = a.part + (size_t)(g * QT + qt2) * a.S * PSZ;
-    float M = -INFINITY;
-    for (int s0 = 0; s0 < a.S; s0 += SB) {
-      float mv[SB];
+// Merge of the key splits: one wave per (kv head g, query tile, 16-dim slice).  The split weights
+// exp(m_c - M) depend only on the query, so each lane computes them once for its query lr; the split
+// partials are added in split order.
+template <int DT>
+__global__ __launch_bounds__(64) void attn_merge_kernel(AttnP a) {
+  constexpr int DT16 = HD / 16, SB = 8;
+  const int lane = threadIdx.x, lr = lane & 15, lg = lane >> 4;
+  const int dt = blockIdx.x, qt = blockIdx.y, g = blockIdx.z;
+  const int grp = a.nq / a.nkv, QR = grp * a.rows, QT = (QR + 15) / 16;
+  const float* pt = a.part + (size_t)(g * QT + qt) * a.S * PSZ;
+  float M = -INFINITY;
+  for (int s0 = 0; s0 < a.S; s0 += SB) {
+    float mv[SB];
 #pragma unroll
-      for (int q = 0; q < SB; ++q) mv[q] = ld_agent(pt + (size_t)min(s0 + q, a.S - 1) * PSZ + 16 * HD + lr);
+    for (int q = 0; q < SB; ++q) mv[q] = pt[(size_t)min(s0 + q, a.S - 1) * PSZ + 16 * HD + lr];
 #pragma unroll
-      for (int q = 0; q < SB; ++q) M = fmaxf(M, mv[q]);
+    for (int q = 0; q < SB; ++q) M = fmaxf(M, mv[q]);
+  }
+  const float Mu = M == -INFINITY ? 0.f : M;
+  float L = 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < a.S; s0 += SB) {
+    f32x4 ov[SB];
+    float mv[SB], lv[SB];
+#pragma unroll
+    for (int q = 0; q < SB; ++q) {
+      const float* ps = pt + (size_t)min(s0 + q, a.S - 1) * PSZ;
+      ov[q] = reinterpret_cast<const f32x4*>(ps)[dt * 64 + lane];
+      mv[q] = ps[16 * HD + lr];
+      lv[q] = ps[16 * HD + 16 + lr];
     }
-    const float Mu = M == -INFINITY ? 0.f : M;
-    float L = 0.f;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < a.S; s0 += SB) {
-      f32x4 ov[SB];
-      float mv[SB], lv[SB];
 #pragma unroll
-      for (int q = 0; q < SB; ++q) {
-        const float* ps = pt + (size_t)min(s0 + q, a.S - 1) * PSZ;
-        ov[q] = ld_agent4(reinterpret_cast<const f32x4*>(ps) + dt * 64 + lane);
-        mv[q] = ld_agent(ps + 16 * HD + lr);
-        lv[q] = ld_agent(ps + 16 * HD + 16 + lr);
-      }
-#pragma unroll
-      for (int q = 0; q < SB; ++q) {
-        const float e = s0 + q < a.S ? expf(mv[q] - Mu) : 0.f;
-        L += lv[q] * e;
-        acc += ov[q] * e;
-      }
-    }
-    const int qi2 = qt2 * 16 + lr;
-    if (qi2 < QR) {
-      const int h2 = qi2 / a.rows, r2 = qi2 - h2 * a.rows;
-      const float inv = 1.0f / L;
-      u16* dst = a.out + (size_t)r2 * a.nq * HD + (g * grp + h2) * HD + 16 * dt + 4 * lg;
-      *reinterpret_cast<u32x2*>(dst) = u32x2{pack2(from_f32<DT>(acc[0] * inv), from_f32<DT>(acc[1] * inv)),
-                                             pack2(from_f32<DT>(acc[2] * inv), from_f32<DT>(acc[3] * inv))};
+    for (int q = 0; q < SB; ++q) {
+      const float e = s0 + q < a.S ? expf(mv[q] - Mu) : 0.f;
+      L += lv[q] * e;
+      acc += ov[q] * e;
     }
   }
-  group_leave(grp_ctr, (unsigned)a.S);
+  const int qi = qt * 16 + lr;
+  if (qi < QR) {
+    const int h = qi / a.rows, r = qi - h * a.rows;
+    const float inv = 1.0f / L;
+    u16* dst = a.out + (size_t)r * a.nq * HD + (g * grp + h) * HD + 16 * dt + 4 * lg;
+    *reinterpret_cast<u32x2*>(dst) = u32x2{pack2(from_f32<DT>(acc[0] * inv), from_f32<DT>(acc[1] * inv)),
+                                           pack2(from_f32<DT>(acc[2] * inv), from_f32<DT>(acc[3] * inv))};
+  }
 }
 
 // Launch plan: short row blocks (the cached decode step) use attn_chunk_kernel with one key chunk of
@@ -750,12 +634,15 @@ template <int DT, int QPW, int KSW>
 static hipError_t launch_loop(const AttnP& a, const AttnPlan& p, hipStream_t st) {
   const size_t loop_lds = (size_t)KSW * (KB * KLD + HD * VLD) * 2;
   const size_t merge_lds = (size_t)2 * KSW * QPW * 16 * 4 + (size_t)(KSW - 1) * QPW * (HD / 16) * 64 * 16;
-  const size_t split_lds = a.S > 1 ? (size_t)QPW * a.S * 32 * 4 : 0;
-  const size_t lds = std::max(loop_lds, std::max(merge_lds, split_lds));
+  const size_t lds = std::max(loop_lds, merge_lds);
   if (lds > 160 * 1024) return hipErrorInvalidValue;
   auto kern = attn_kernel<DT, QPW, KSW>;
   raise_lds(kern, lds);
   hipLaunchKernelGGL(kern, dim3(p.qg, a.nkv, a.S), dim3(64 * QPW * KSW), lds, st, a);
+  if (a.S > 1) {
+    const int QT = ((a.nq / a.nkv) * a.rows + 15) / 16;
+    hipLaunchKernelGGL(attn_merge_kernel<DT>, dim3(HD / 16, QT, a.nkv), dim3(64), 0, st, a);
+  }
   return hipGetLastError();
 }
 
@@ -769,6 +656,10 @@ static hipError_t launch_chunk(const AttnP& a, const AttnPlan& p, hipStream_t st
   auto kern = attn_chunk_kernel<DT, QPW, KH, CH>;
   raise_lds(kern, lds);
   hipLaunchKernelGGL(kern, dim3(p.qg, a.nkv, a.S), dim3(64 * QPW * KH), lds, st, a);
+  if (a.S > 1) {
+    const int QT = ((a.nq / a.nkv) * a.rows + 15) / 16;
+    hipLaunchKernelGGL(attn_merge_kernel<DT>, dim3(HD / 16, QT, a.nkv), dim3(64), 0, st, a);
+  }
   return hipGetLastError();
 }
 

@@ -71,7 +71,6 @@ struct fdllm_ctx {
   unsigned* counters = nullptr; int n_counters = 0;
   int32_t* zero_i32 = nullptr;
   float* rope = nullptr; size_t rope_floats = 0;  // RoPE (cos, sin) table of the current call's rows
-  unsigned* host_err = nullptr;                  // pinned, device-written: a bounded group wait gave up
   int attn_target = 64;   // attention workgroups aimed for when splitting the keys
   int down_split = 10;    // cross-workgroup k splits of the down projection (largest divisor of K/32 <= this)
 
@@ -199,18 +198,15 @@ int run_attention(fdllm_ctx* c, int rows, uint16_t* kc, uint16_t* vc, int ws, in
   const fdllm_config& f = c->cfg;
   AttnP a{};
   a.qkv = c->qkv; a.ldq = c->qkv_dim(); a.rows = rows; a.nq = f.num_attention_heads; a.nkv = f.num_key_value_heads;
-  a.rope = c->rope; a.err = c->host_err;
+  a.rope = c->rope;
   a.kc = kc; a.vc = vc; a.ws = ws; a.Lk = Lk; a.scale = 1.0f / std::sqrt((float)f.head_dim);
   a.mask = mask; a.q_pos0 = 0; a.block = f.bd_size; a.bias = bias; a.bias_ld = bias_ld;
   const AttnPlan pl = attn_plan(rows, a.nq, a.nkv, Lk, c->attn_target);
-  const int base = pl.qg * a.nkv;
   a.S = pl.S; a.chunk = pl.chunk; a.target_wgs = c->attn_target;
   if (a.S > 1) {
     int rc = ensure_floats(&c->apart, &c->apart_floats, attn_partial_floats(a));
     if (rc) return rc;
-    if (2 * base > c->n_counters) return fail(FDLLM_EINVAL, "too many attention workgroup groups (%d)", base);
     a.part = c->apart;
-    a.counters = c->counters;
   }
   a.out = c->attn;
   HIPCHK(launch_attention(f.dtype, a, st));
@@ -365,12 +361,6 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
     return fail(FDLLM_EHIP, "workspace allocation failed: %s", hipGetErrorString(e));
   }
   c->zero_i32 = (int32_t*)(c->counters + c->n_counters);
-  e = hipHostMalloc((void**)&c->host_err, 64, hipHostMallocMapped);
-  if (e != hipSuccess) {
-    fdllm_destroy(c);
-    return fail(FDLLM_EHIP, "pinned status word allocation failed: %s", hipGetErrorString(e));
-  }
-  *c->host_err = 0;
   int rc = ensure_rows(c, std::max(1, f.max_rows));
   if (rc == FDLLM_OK) rc = ensure_stats(c, std::max(32, f.max_rows));
   if (rc == FDLLM_OK) {
@@ -391,18 +381,7 @@ void fdllm_destroy(fdllm_ctx* c) {
   for (void* p : {c->ws, (void*)c->gpart, (void*)c->apart, c->stats, (void*)c->counters, (void*)c->packed,
                   (void*)c->rope})
     if (p) (void)hipFree(p);
-  if (c->host_err) (void)hipHostFree(c->host_err);
   delete c;
-}
-
-int fdllm_device_status(fdllm_ctx* c) {
-  if (!c) return fail(FDLLM_EINVAL, "null context");
-  if (c->host_err && *(volatile unsigned*)c->host_err) {
-    *(volatile unsigned*)c->host_err = 0;
-    return fail(FDLLM_EHIP, "a device-side group wait gave up (workgroups were not co-resident); outputs since the "
-                            "last check are invalid");
-  }
-  return FDLLM_OK;
 }
 
 int fdllm_num_params(const fdllm_ctx* c) { return c ? (int)c->names.size() : 0; }

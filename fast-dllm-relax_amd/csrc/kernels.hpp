@@ -78,8 +78,7 @@ struct AttnP {
   const float* bias; long long bias_ld;
   int S, chunk;                       // key splits (gridDim.z), keys per split (multiple of 32)
   int target_wgs;                     // workgroups the plan aims for (attn_plan)
-  float* part; unsigned* counters;    // split partials / arrival counters (two per workgroup group)
-  unsigned* err;                      // set to 1 if a group wait gave up (workgroups not co-resident)
+  float* part;                        // split partials (merged by attn_merge_kernel)
   uint16_t* out;                      // [rows][nq * 128]
 };
 struct AttnPlan { int chunked; int q_tiles_per_wg; int key_groups; int qg; int S; int chunk; };

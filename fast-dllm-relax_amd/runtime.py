@@ -143,7 +143,6 @@ def shifted_confidence(vm: HipVM, hidden: torch.Tensor) -> tuple[np.ndarray, np.
     2 x rows values come back."""
     ids_d, maxp_d = vm.get_confidence(hidden)
     both = torch.cat([ids_d.view(torch.float32), maxp_d], dim=1).cpu().numpy()[0]
-    vm.check_device()
     rows = ids_d.shape[1]
     ids = both[:rows].view(np.int32).astype(np.int64)
     maxp = both[rows:].astype(np.float32)
@@ -215,7 +214,6 @@ def score_sequence_block(vm: HipVM, sequence_ids, *, block_size: int):
                                                               block_size=block_size)).cuda()
     hidden = vm.forward_hidden(_embed(vm, prefix_ids + active), bias)
     logits = vm.get_logits(hidden).cpu().numpy()
-    vm.check_device()
     cur = logits[:, -len(active):, :]
     shifted = extract_shifted_block_logits(logits, prefix_len=len(prefix_ids), block_len=len(active))
     return cur, shifted

@@ -198,10 +198,6 @@ class HipVM:
                                                  _ptr(logits), _stream()))
         return ids, maxp
 
-    def check_device(self) -> None:
-        """Raise if a device-side group wait gave up since the last check (call after a sync)."""
-        _lib.check(self.lib.fdllm_device_status(self.ctx))
-
     def confidence_from_logits(self, logits: torch.Tensor):
         """Device confidence of given fp32 logits [1, rows, vocab] (runtime.py:176-181 restated)."""
         if logits.dim() != 3 or logits.shape[2] != self.cfg.vocab_size or logits.dtype != torch.float32:

@@ -135,13 +135,6 @@ int fdllm_confidence_from_logits(fdllm_ctx* ctx, const float* logits, int rows, 
 int fdllm_bench_op(fdllm_ctx* ctx, int op, int rows, int layer, int iters, void* k_cache, void* v_cache, int cap,
                    int attend_len, void* stream);
 
-/* Device status; it has no counterpart in the reference.  The split attention merge waits for the other
- * workgroups of its group with a bounded spin; if one gives up (its workgroups were not all resident),
- * it records that in a pinned host word instead of hanging.  Returns FDLLM_EHIP (and clears the word) if
- * that happened in work that has completed; call it after synchronising the stream.  Reads host memory
- * only: no device call. */
-int fdllm_device_status(fdllm_ctx* ctx);
-
 /* Message of this thread's last failure ("" if none). */
 const char* fdllm_last_error(void);
 

@@ -101,4 +101,3 @@ def test_hd128_fixture_hip():
     off8 = torch.tensor(P + 8, dtype=torch.int32, device="cuda")
     hp = vm.forward_block_partial_rp8(vm.embed(dev[P + 8:P + 16])[None], k, v, off8, P)
     bf16_parity("golden partial rp8", to_np(hp)[0], g["partial8_bf16"], g["partial8_f32"])
-    vm.check_device()

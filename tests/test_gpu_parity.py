@@ -30,10 +30,7 @@ def _off(v):
 @pytest.fixture(scope="module")
 def tiny():
     log("setup: tiny bf16 model seed 0")
-    pair = make_pair(TINY, 0)
-    yield pair
-    torch.cuda.synchronize()
-    pair[1].check_device()
+    return make_pair(TINY, 0)
 
 
 def test_embed_bit_exact(tiny):
@@ -157,10 +154,7 @@ def test_fused_confidence_equals_confidence_of_get_logits(tiny):
 @pytest.fixture(scope="module")
 def wide2():
     log("setup: 1.5B-shape 2-layer bf16 model seed 1")
-    pair = make_pair(WIDE2, 1)
-    yield pair
-    torch.cuda.synchronize()
-    pair[1].check_device()
+    return make_pair(WIDE2, 1)
 
 
 def test_wide_cached_step_and_logits(wide2):
