@@ -1,0 +1,604 @@
+// GQA attention of a block of rows against the in-place KV cache, with RoPE and the KV append fused in
+// (fast_dllm.attn_inplace, fast_dllm_relax/runtime.py:51-73; RoPE cuda.py:278-316; in-graph restatement
+// model/metal.py:255-302, 378-408).  Query head h uses kv head h / (nq / nkv); scores q.k * scale in
+// fp32, online softmax in fp32, P rounded to the model dtype for P.V on MFMA with fp32 accumulation
+// (the flash-attention precision the reference's callback uses), one rounding of the output.
+//
+// Rows [ws, ws + rows) of the cache belong to this call: their K (after RoPE) and V are taken straight
+// from this call's qkv projection, and workgroup column 0 writes them to the cache.  Every other key
+// row comes from the cache.  Queries are RoPE'd in registers at positions pos_offset + r.
+//
+// Work split: blockIdx.y = kv head g, blockIdx.z = key split c, blockIdx.x = group of QPW query tiles
+// (the query rows of the grp heads sharing g are stacked: row qi = head_in_group * rows + r, 16 per
+// tile).  The workgroup's QPW x KSW waves are QPW query-tile slots times KSW key groups; key group kg
+// stages blocks of 32 keys (K row-major, V transposed four keys at a time) in its own LDS buffers and
+// its waves run the scores S^T = K . Q^T and O^T += V^T . P^T for their query tiles (a lane holds one
+// query, so its softmax statistics stay in-lane).  Key groups are merged in LDS in fixed order; key
+// splits (S > 1) leave partials that attn_merge_kernel combines in split order, so results are
+// deterministic.
+#pragma once
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace fdllm {
+
+constexpr int HD = 128;
+constexpr int KB = 32;        // keys per block
+constexpr int KLD = HD + 8;   // u16 stride of a K row in LDS
+constexpr int VLD = KB + 8;   // u16 stride of a transposed V row (one head dimension)
+constexpr int PSZ = 16 * HD + 32;  // floats per split partial of one query tile: O, m, l
+
+template <int DT> __device__ __forceinline__ float elem(const u32x4& v, int e) {
+  return (e & 1) ? hi_f32<DT>(v[e >> 1]) : lo_f32<DT>(v[e >> 1]);
+}
+
+// RoPE of 8 rotation pairs: lo holds dims i0 .. i0 + 7 (< 64), hi the partner dims + 64; cs points at
+// the (cos, sin) entries i0 .. i0 + 7 of the position's table row (cuda.py:314-315 with _rotate_half
+// 207-209: q' = q cos + rot(q) sin, every product and sum rounded to the model dtype).
+template <int DT>
+__device__ __forceinline__ void rope_tab(u32x4& lo, u32x4& hi, const float* cs) {
+  f32x4 t[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) t[c] = *reinterpret_cast<const f32x4*>(cs + 4 * c);
+  u16 o1[8], o2[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float c = t[e >> 1][2 * (e & 1)], sn = t[e >> 1][2 * (e & 1) + 1];
+    const float x1 = elem<DT>(lo, e), x2 = elem<DT>(hi, e);
+    o1[e] = from_f32<DT>(rnd<DT>(x1 * c) + rnd<DT>(-x2 * sn));
+    o2[e] = from_f32<DT>(rnd<DT>(x2 * c) + rnd<DT>(x1 * sn));
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    lo[c] = pack2(o1[2 * c], o1[2 * c + 1]);
+    hi[c] = pack2(o2[2 * c], o2[2 * c + 1]);
+  }
+}
+
+template <int DT, int QPW, int KSW>
+__global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
+  constexpr int NT = 64 * QPW;  // threads of one key group
+  constexpr int KBUF = KB * KLD, VBUF = HD * VLD;
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int qw = w % QPW, kg = w / QPW;
+  const int tid = threadIdx.x - kg * NT;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int g = blockIdx.y, c = blockIdx.z;
+  const int grp = a.nq / a.nkv, QR = grp * a.rows, QT = (QR + 15) / 16;
+  const int qt = blockIdx.x * QPW + qw;
+  const bool tile_ok = qt < QT;
+  const size_t krow = (size_t)a.nkv * HD;
+  u16* kbuf = reinterpret_cast<u16*>(smem) + kg * KBUF;
+  u16* vbuf = reinterpret_cast<u16*>(smem) + KSW * KBUF + kg * VBUF;
+
+  // this lane's query row: qi = 16 qt + lr
+  const int qi = qt * 16 + lr;
+  const bool qvalid = tile_ok && qi < QR;
+  const int hh = qvalid ? qi / a.rows : 0;
+  const int r = qvalid ? qi - hh * a.rows : 0;
+  u32x4 qf[4];
+  {
+    const u16* qp = a.qkv + (size_t)r * a.ldq + (g * grp + hh) * HD + 8 * lg;
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds)
+      qf[ds] = qvalid ? *reinterpret_cast<const u32x4*>(qp + 32 * ds) : u32x4{0u, 0u, 0u, 0u};
+    const float* cs = a.rope + (size_t)r * 128;
+    rope_tab<DT>(qf[0], qf[2], cs + 16 * lg);
+    rope_tab<DT>(qf[1], qf[3], cs + 16 * lg + 64);
+  }
+  const int qpos_blk = a.mask == 1 ? (a.q_pos0 + r) / a.block : 0;
+  const float* brow = a.mask == 2 ? a.bias + (long long)r * a.bias_ld : nullptr;
+
+  const int kbeg = c * a.chunk;
+  const int kend = min(kbeg + a.chunk, a.Lk);
+  const int nblk = (kend - kbeg + KB - 1) / KB;
+  const int iters = (nblk + KSW - 1) / KSW;
+  const bool writer = blockIdx.x == 0;
+  const u16* kq_base = a.qkv + a.nq * HD + g * HD;
+  const u16* vq_base = a.qkv + (a.nq + a.nkv) * HD + g * HD;
+
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4 o[HD / 16];
+#pragma unroll
+  for (int dt = 0; dt < HD / 16; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int it = 0; it < iters; ++it) {
+    const int b = it * KSW + kg;
+    const int kb = kbeg + b * KB;
+    const bool bvalid = b < nblk;
+    __syncthreads();
+    if (bvalid) {
+      // K: 32 keys x 8 rotation-pair chunks
+      for (int item = tid; item < KB * 8; item += NT) {
+        const int j = item >> 3, p = item & 7;
+        const int key = kb + j;
+        u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
+        if (key < kend) {
+          if (key >= a.ws && key < a.ws + a.rows) {
+            const u16* src = kq_base + (size_t)(key - a.ws) * a.ldq;
+            lo = *reinterpret_cast<const u32x4*>(src + 8 * p);
+            hi = *reinterpret_cast<const u32x4*>(src + 64 + 8 * p);
+            rope_tab<DT>(lo, hi, a.rope + (size_t)(key - a.ws) * 128 + 16 * p);
+            if (writer) {
+              u16* dst = a.kc + key * krow + g * HD;
+              *reinterpret_cast<u32x4*>(dst + 8 * p) = lo;
+              *reinterpret_cast<u32x4*>(dst + 64 + 8 * p) = hi;
+            }
+          } else {
+            const u16* src = a.kc + key * krow + g * HD;
+            lo = *reinterpret_cast<const u32x4*>(src + 8 * p);
+            hi = *reinterpret_cast<const u32x4*>(src + 64 + 8 * p);
+          }
+        }
+        *reinterpret_cast<u32x4*>(kbuf + j * KLD + 8 * p) = lo;
+        *reinterpret_cast<u32x4*>(kbuf + j * KLD + 64 + 8 * p) = hi;
+      }
+      // V: 8 key quads x 16 dim chunks, stored transposed (vbuf[dim][key], four keys per 8-byte word)
+      for (int item = tid; item < 8 * 16; item += NT) {
+        const int kq = item >> 4, dc = item & 15;
+        u32x4 v[4];
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          const int key = kb + 4 * kq + qq;
+          v[qq] = u32x4{0u, 0u, 0u, 0u};
+          if (key < kend) {
+            if (key >= a.ws && key < a.ws + a.rows) {
+              v[qq] = *reinterpret_cast<const u32x4*>(vq_base + (size_t)(key - a.ws) * a.ldq + 8 * dc);
+              if (writer) *reinterpret_cast<u32x4*>(a.vc + key * krow + g * HD + 8 * dc) = v[qq];
+            } else {
+              v[qq] = *reinterpret_cast<const u32x4*>(a.vc + key * krow + g * HD + 8 * dc);
+            }
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int sh = 16 * (e & 1);
+          const unsigned long long wd =
+              (unsigned long long)((v[0][e >> 1] >> sh) & 0xffffu) |
+              ((unsigned long long)((v[1][e >> 1] >> sh) & 0xffffu) << 16) |
+              ((unsigned long long)((v[2][e >> 1] >> sh) & 0xffffu) << 32) |
+              ((unsigned long long)((v[3][e >> 1] >> sh) & 0xffffu) << 48);
+          *reinterpret_cast<unsigned long long*>(vbuf + (8 * dc + e) * VLD + 4 * kq) = wd;
+        }
+      }
+    }
+    __syncthreads();
+    if (!bvalid || !tile_ok) continue;
+
+    f32x4 s[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const u16* kp = kbuf + (16 * kt + lr) * KLD + 8 * lg;
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds) s[kt] = mfma16<DT>(*reinterpret_cast<const u32x4*>(kp + 32 * ds), qf[ds], s[kt]);
+    }
+    // lane holds S^T[key = kb + 16 kt + 4 lg + i][query lr]
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = kb + 16 * kt + 4 * lg + i;
+        float v = s[kt][i] * a.scale;
+        if (key >= kend) {
+          v = -INFINITY;
+        } else if (a.mask == 1) {
+          if (qpos_blk < key / a.block) v = -INFINITY;
+        } else if (a.mask == 2) {
+          v += brow[key];
+        }
+        s[kt][i] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = rows_max(mx);
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = expf(m_run - m_use);
+    float ps = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = expf(s[kt][i] - m_use);
+        s[kt][i] = p;
+        ps += p;
+      }
+    ps = rows_sum(ps);
+    l_run = l_run * alpha + ps;
+    m_run = m_new;
+    // P^T as the B operand: k slot 8 lg + e holds key 4 lg + e (e < 4) or 16 + 4 lg + e - 4 (e >= 4);
+    // the V^T fragment (A operand) reads the same keys; O^T accumulates with this lane's query lr
+    const u32x4 pa = {pack2(from_f32<DT>(s[0][0]), from_f32<DT>(s[0][1])),
+                      pack2(from_f32<DT>(s[0][2]), from_f32<DT>(s[0][3])),
+                      pack2(from_f32<DT>(s[1][0]), from_f32<DT>(s[1][1])),
+                      pack2(from_f32<DT>(s[1][2]), from_f32<DT>(s[1][3]))};
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; ++dt) {
+      const u16* vrow = vbuf + (16 * dt + lr) * VLD + 4 * lg;
+      const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
+      const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 16);
+      o[dt] = mfma16<DT>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pa, o[dt] * alpha);
+    }
+  }
+
+  // ---- merge the key groups in LDS (fixed order kg = 0, 1, ...); lane holds O^T[dims][query lr] ----
+  float Mq, Lq;
+  __syncthreads();
+  {
+    float* cm = reinterpret_cast<float*>(smem);
+    float* cl = cm + KSW * QPW * 16;
+    f32x4* co = reinterpret_cast<f32x4*>(cl + KSW * QPW * 16);
+    if (lg == 0) {
+      cm[(kg * QPW + qw) * 16 + lr] = m_run;
+      cl[(kg * QPW + qw) * 16 + lr] = l_run;
+    }
+    if (KSW > 1 && kg > 0) {
+#pragma unroll
+      for (int dt = 0; dt < HD / 16; ++dt) co[(((kg - 1) * QPW + qw) * (HD / 16) + dt) * 64 + lane] = o[dt];
+    }
+    __syncthreads();
+    if (kg == 0) {
+      float M = -INFINITY;
+      for (int k2 = 0; k2 < KSW; ++k2) M = fmaxf(M, cm[(k2 * QPW + qw) * 16 + lr]);
+      const float Mu = M == -INFINITY ? 0.f : M;
+      float L = 0.f;
+      for (int k2 = 0; k2 < KSW; ++k2) L += cl[(k2 * QPW + qw) * 16 + lr] * expf(cm[(k2 * QPW + qw) * 16 + lr] - Mu);
+      const float f0 = expf(cm[qw * 16 + lr] - Mu);
+#pragma unroll
+      for (int dt = 0; dt < HD / 16; ++dt) o[dt] *= f0;
+      for (int k2 = 1; k2 < KSW; ++k2) {
+        const float fk = expf(cm[(k2 * QPW + qw) * 16 + lr] - Mu);
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; ++dt) o[dt] += co[(((k2 - 1) * QPW + qw) * (HD / 16) + dt) * 64 + lane] * fk;
+      }
+      Mq = M;
+      Lq = L;
+    }
+  }
+  if (kg != 0 || !tile_ok) return;
+  if (a.S == 1) {
+    if (qvalid) {
+      const float inv = 1.0f / Lq;
+      u16* dst = a.out + (size_t)r * a.nq * HD + (g * grp + hh) * HD + 4 * lg;
+#pragma unroll
+      for (int dt = 0; dt < HD / 16; ++dt)
+        *reinterpret_cast<u32x2*>(dst + 16 * dt) =
+            u32x2{pack2(from_f32<DT>(o[dt][0] * inv), from_f32<DT>(o[dt][1] * inv)),
+                  pack2(from_f32<DT>(o[dt][2] * inv), from_f32<DT>(o[dt][3] * inv))};
+    }
+    return;
+  }
+  // key splits: the partial of (g, qt, c) in the layout attn_merge_kernel reads
+  float* pp = a.part + ((size_t)(g * QT + qt) * a.S + c) * PSZ;
+#pragma unroll
+  for (int dt = 0; dt < HD / 16; ++dt) reinterpret_cast<f32x4*>(pp)[dt * 64 + lane] = o[dt];
+  if (lg == 0) {
+    pp[16 * HD + lr] = Mq;
+    pp[16 * HD + 16 + lr] = Lq;
+  }
+}
+
+// ---- one-shot variant for short key chunks (the cached decode step) -------------------------------
+// Same arithmetic as attn_kernel, but a workgroup requests every K/V row of its chunk (CH keys) at
+// once, so the chunk costs one memory latency instead of one per 32-key block.  Waves are QPW query
+// tiles times KH key parts.  The output is accumulated transposed, O^T = V^T P^T, so that a lane holds
+// one query (its softmax statistics stay in-lane) and the row reductions use row-swap permutes.  The
+// key parts are merged in LDS; with key splits (gridDim.z > 1) each workgroup stores its partial and
+// attn_merge_kernel, launched next on the stream, combines them across many workgroups.
+// Body of one workgroup (query-tile group bx, kv head by, key chunk bz).  With COH the qkv loads and the
+// output stores are agent-scope, for a launch in which other workgroups produce the qkv rows; the
+// kernel below uses plain accesses.
+template <int DT, int QPW, int KH, int CH, bool COH>
+__device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, int bz, unsigned char* smem) {
+  constexpr int NT = 64 * QPW * KH;
+  constexpr int KIT = (CH * 8 + NT - 1) / NT;        // K items (rotation-pair chunks) per thread
+  constexpr int VIT = ((CH / 4) * 16 + NT - 1) / NT;  // V items (key quad x dim chunk) per thread
+  constexpr int VLDC = CH + 8;                        // u16 stride of a transposed V row
+  constexpr int DT16 = HD / 16;
+  u16* kbuf = reinterpret_cast<u16*>(smem);           // [CH][KLD]
+  u16* vbuf = kbuf + CH * KLD;                        // [HD][VLDC]
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int qw = w % QPW, kh = w / QPW;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int g = by, c = bz;
+  const int grp = a.nq / a.nkv, QR = grp * a.rows, QT = (QR + 15) / 16;
+  const int qt = bx * QPW + qw;
+  const bool tile_ok = qt < QT;
+  const size_t krow = (size_t)a.nkv * HD;
+  const int kbeg = c * a.chunk;
+  const int kend = min(kbeg + a.chunk, a.Lk);
+  const bool writer = bx == 0;
+  const u16* kq_base = a.qkv + a.nq * HD + g * HD;
+  const u16* vq_base = a.qkv + (a.nq + a.nkv) * HD + g * HD;
+
+  // ---- request the whole chunk (rows past kend read row kbeg and are masked or zeroed later) ----
+  u32x4 klo[KIT], khi[KIT], vv[VIT][4];
+#pragma unroll
+  for (int it = 0; it < KIT; ++it) {
+    const int item = threadIdx.x + it * NT;
+    const int j = min(item >> 3, CH - 1), p = item & 7;
+    int key = kbeg + j;
+    key = key < kend ? key : kbeg;
+    const bool win = key >= a.ws && key < a.ws + a.rows;
+    if (win) {
+      const u16* src = kq_base + (size_t)(key - a.ws) * a.ldq;
+      klo[it] = ld16<COH>(src + 8 * p);
+      khi[it] = ld16<COH>(src + 64 + 8 * p);
+    } else {
+      const u16* src = a.kc + key * krow + g * HD;
+      klo[it] = *reinterpret_cast<const u32x4*>(src + 8 * p);
+      khi[it] = *reinterpret_cast<const u32x4*>(src + 64 + 8 * p);
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < VIT; ++it) {
+    const int item = threadIdx.x + it * NT;
+    const int kq = min(item >> 4, CH / 4 - 1), dc = item & 15;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      int key = kbeg + 4 * kq + qq;
+      key = key < kend ? key : kbeg;
+      const bool win = key >= a.ws && key < a.ws + a.rows;
+      vv[it][qq] = win ? ld16<COH>(vq_base + (size_t)(key - a.ws) * a.ldq + 8 * dc)
+                       : *reinterpret_cast<const u32x4*>(a.vc + key * krow + g * HD + 8 * dc);
+    }
+  }
+
+  // this lane's query row (qi = 16 qt + lr), RoPE'd in registers while the chunk is in flight
+  const int qi = qt * 16 + lr;
+  const bool qvalid = tile_ok && qi < QR;
+  const int hh = qvalid ? qi / a.rows : 0;
+  const int r = qvalid ? qi - hh * a.rows : 0;
+  u32x4 qf[4];
+  {
+    const u16* qp = a.qkv + (size_t)r * a.ldq + (g * grp + hh) * HD + 8 * lg;
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) qf[ds] = ld16<COH>(qp + 32 * ds);
+    const float* cs = a.rope + (size_t)r * 128;
+    rope_tab<DT>(qf[0], qf[2], cs + 16 * lg);
+    rope_tab<DT>(qf[1], qf[3], cs + 16 * lg + 64);
+  }
+  const int qpos_blk = a.mask == 1 ? (a.q_pos0 + r) / a.block : 0;
+  const float* brow = a.mask == 2 ? a.bias + (long long)r * a.bias_ld : nullptr;
+
+  // ---- stage: K rows (window rows RoPE'd and appended to the cache), V transposed ----
+#pragma unroll
+  for (int it = 0; it < KIT; ++it) {
+    const int item = threadIdx.x + it * NT;
+    if (item >= CH * 8) break;
+    const int j = item >> 3, p = item & 7;
+    const int key = kbeg + j;
+    u32x4 lo = klo[it], hi = khi[it];
+    if (key >= kend) {
+      lo = hi = u32x4{0u, 0u, 0u, 0u};
+    } else if (key >= a.ws && key < a.ws + a.rows) {
+      rope_tab<DT>(lo, hi, a.rope + (size_t)(key - a.ws) * 128 + 16 * p);
+      if (writer) {
+        u16* dst = a.kc + key * krow + g * HD;
+        *reinterpret_cast<u32x4*>(dst + 8 * p) = lo;
+        *reinterpret_cast<u32x4*>(dst + 64 + 8 * p) = hi;
+      }
+    }
+    *reinterpret_cast<u32x4*>(kbuf + j * KLD + 8 * p) = lo;
+    *reinterpret_cast<u32x4*>(kbuf + j * KLD + 64 + 8 * p) = hi;
+  }
+#pragma unroll
+  for (int it = 0; it < VIT; ++it) {
+    const int item = threadIdx.x + it * NT;
+    if (item >= (CH / 4) * 16) break;
+    const int kq = item >> 4, dc = item & 15;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      const int key = kbeg + 4 * kq + qq;
+      if (key >= kend) {
+        vv[it][qq] = u32x4{0u, 0u, 0u, 0u};
+      } else if (writer && key >= a.ws && key < a.ws + a.rows) {
+        *reinterpret_cast<u32x4*>(a.vc + key * krow + g * HD + 8 * dc) = vv[it][qq];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int sh = 16 * (e & 1);
+      const unsigned long long wd = (unsigned long long)((vv[it][0][e >> 1] >> sh) & 0xffffu) |
+                                    ((unsigned long long)((vv[it][1][e >> 1] >> sh) & 0xffffu) << 16) |
+                                    ((unsigned long long)((vv[it][2][e >> 1] >> sh) & 0xffffu) << 32) |
+                                    ((unsigned long long)((vv[it][3][e >> 1] >> sh) & 0xffffu) << 48);
+      *reinterpret_cast<unsigned long long*>(vbuf + (8 * dc + e) * VLDC + 4 * kq) = wd;
+    }
+  }
+  __syncthreads();
+
+  // ---- scores and P.V over this wave's key part ----
+  // lane (lr, lg) holds S^T[key kb + 16 kt + 4 lg + i][query lr] and O^T[dim 16 dt + 4 lg + i][query lr]
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4 o[DT16];
+#pragma unroll
+  for (int dt = 0; dt < DT16; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  constexpr int KPW = CH / KH;  // keys per wave
+  if (tile_ok) {
+    for (int b = 0; b < KPW / 32; ++b) {
+      const int kl = kh * KPW + 32 * b;  // chunk-local first key of the block
+      const int kb = kbeg + kl;
+      if (kb >= kend) break;
+      f32x4 s[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const u16* kp = kbuf + (kl + 16 * kt + lr) * KLD + 8 * lg;
+#pragma unroll
+        for (int ds = 0; ds < 4; ++ds) s[kt] = mfma16<DT>(*reinterpret_cast<const u32x4*>(kp + 32 * ds), qf[ds], s[kt]);
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = kb + 16 * kt + 4 * lg + i;
+          float v = s[kt][i] * a.scale;
+          if (key >= kend) {
+            v = -INFINITY;
+          } else if (a.mask == 1) {
+            if (qpos_blk < key / a.block) v = -INFINITY;
+          } else if (a.mask == 2) {
+            v += brow[key];
+          }
+          s[kt][i] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = rows_max(mx);
+      const float m_new = fmaxf(m_run, mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = expf(m_run - m_use);
+      float ps = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float pe = expf(s[kt][i] - m_use);
+          s[kt][i] = pe;
+          ps += pe;
+        }
+      ps = rows_sum(ps);
+      l_run = l_run * alpha + ps;
+      m_run = m_new;
+      // P^T as the B operand: k slot 8 lg + e holds key 4 lg + e (e < 4) or 16 + 4 lg + e - 4; the V^T
+      // fragment (A operand) reads the same keys
+      const u32x4 pb = {pack2(from_f32<DT>(s[0][0]), from_f32<DT>(s[0][1])),
+                        pack2(from_f32<DT>(s[0][2]), from_f32<DT>(s[0][3])),
+                        pack2(from_f32<DT>(s[1][0]), from_f32<DT>(s[1][1])),
+                        pack2(from_f32<DT>(s[1][2]), from_f32<DT>(s[1][3]))};
+#pragma unroll
+      for (int dt = 0; dt < DT16; ++dt) {
+        const u16* vrow = vbuf + (16 * dt + lr) * VLDC + kl + 4 * lg;
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 16);
+        o[dt] = mfma16<DT>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb, o[dt] * alpha);
+      }
+    }
+  }
+
+  // ---- merge the key parts in LDS (fixed order kh = 0, 1, ...); wave kh = 0 keeps the result ----
+  __syncthreads();
+  float Mq, Lq;
+  {
+    float* cm = reinterpret_cast<float*>(smem);
+    float* cl = cm + KH * QPW * 16;
+    f32x4* co = reinterpret_cast<f32x4*>(cl + KH * QPW * 16);
+    if (lg == 0) {
+      cm[(kh * QPW + qw) * 16 + lr] = m_run;
+      cl[(kh * QPW + qw) * 16 + lr] = l_run;
+    }
+    if (KH > 1 && kh > 0) {
+#pragma unroll
+      for (int dt = 0; dt < DT16; ++dt) co[(((kh - 1) * QPW + qw) * DT16 + dt) * 64 + lane] = o[dt];
+    }
+    __syncthreads();
+    if (kh == 0) {
+      float M = -INFINITY;
+      for (int k = 0; k < KH; ++k) M = fmaxf(M, cm[(k * QPW + qw) * 16 + lr]);
+      const float Mu = M == -INFINITY ? 0.f : M;
+      float L = 0.f;
+      for (int k = 0; k < KH; ++k) L += cl[(k * QPW + qw) * 16 + lr] * expf(cm[(k * QPW + qw) * 16 + lr] - Mu);
+      const float f0 = expf(cm[qw * 16 + lr] - Mu);
+#pragma unroll
+      for (int dt = 0; dt < DT16; ++dt) o[dt] *= f0;
+      for (int k = 1; k < KH; ++k) {
+        const float fk = expf(cm[(k * QPW + qw) * 16 + lr] - Mu);
+#pragma unroll
+        for (int dt = 0; dt < DT16; ++dt) o[dt] += co[(((k - 1) * QPW + qw) * DT16 + dt) * 64 + lane] * fk;
+      }
+      Mq = M;
+      Lq = L;
+    }
+  }
+
+  // lane output: query row qi (head hh, row r), dims 16 dt + 4 lg .. + 3
+  auto store4 = [&](int dt, f32x4 v) {
+    u16* dst = a.out + (size_t)r * a.nq * HD + (g * grp + hh) * HD + 16 * dt + 4 * lg;
+    st8<COH>(dst, u32x2{pack2(from_f32<DT>(v[0]), from_f32<DT>(v[1])), pack2(from_f32<DT>(v[2]), from_f32<DT>(v[3]))});
+  };
+  if (a.S == 1) {
+    if (kh == 0 && qvalid) {
+      const float inv = 1.0f / Lq;
+#pragma unroll
+      for (int dt = 0; dt < DT16; ++dt) store4(dt, o[dt] * inv);
+    }
+    return;
+  }
+
+  // ---- key splits: the partial of (g, qt, c): O^T as f32x4 [HD / 16][64 lanes], then m and l of the
+  // tile's 16 queries; attn_merge_kernel combines them ----
+  if (kh == 0 && tile_ok) {
+    float* pp = a.part + ((size_t)(g * QT + qt) * a.S + c) * PSZ;
+#pragma unroll
+    for (int dt = 0; dt < DT16; ++dt) stf4<COH>(reinterpret_cast<f32x4*>(pp) + dt * 64 + lane, o[dt]);
+    if (lg == 0) {
+      stf<COH>(pp + 16 * HD + lr, Mq);
+      stf<COH>(pp + 16 * HD + 16 + lr, Lq);
+    }
+  }
+}
+
+template <int DT, int QPW, int KH, int CH>
+__global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  attn_chunk_body<DT, QPW, KH, CH, false>(a, blockIdx.x, blockIdx.y, blockIdx.z, smem);
+}
+
+// Merge of the key splits: one wave per (kv head g, query tile qt, 16-dim slice dt).  The split weights
+// exp(m_c - M) depend only on the query, so each lane computes them once for its query lr; the split
+// partials are added in split order.
+template <int DT, bool COH>
+__device__ __forceinline__ void attn_merge_wave(const AttnP& a, int dt, int qt, int g, int lane) {
+  constexpr int SB = 8;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int grp = a.nq / a.nkv, QR = grp * a.rows, QT = (QR + 15) / 16;
+  const float* pt = a.part + (size_t)(g * QT + qt) * a.S * PSZ;
+  float M = -INFINITY;
+  for (int s0 = 0; s0 < a.S; s0 += SB) {
+    float mv[SB];
+#pragma unroll
+    for (int q = 0; q < SB; ++q) mv[q] = ldf<COH>(pt + (size_t)min(s0 + q, a.S - 1) * PSZ + 16 * HD + lr);
+#pragma unroll
+    for (int q = 0; q < SB; ++q) M = fmaxf(M, mv[q]);
+  }
+  const float Mu = M == -INFINITY ? 0.f : M;
+  float L = 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < a.S; s0 += SB) {
+    f32x4 ov[SB];
+    float mv[SB], lv[SB];
+#pragma unroll
+    for (int q = 0; q < SB; ++q) {
+      const float* ps = pt + (size_t)min(s0 + q, a.S - 1) * PSZ;
+      ov[q] = ldf4<COH>(reinterpret_cast<const f32x4*>(ps) + dt * 64 + lane);
+      mv[q] = ldf<COH>(ps + 16 * HD + lr);
+      lv[q] = ldf<COH>(ps + 16 * HD + 16 + lr);
+    }
+#pragma unroll
+    for (int q = 0; q < SB; ++q) {
+      const float e = s0 + q < a.S ? expf(mv[q] - Mu) : 0.f;
+      L += lv[q] * e;
+      acc += ov[q] * e;
+    }
+  }
+  const int qi = qt * 16 + lr;
+  if (qi < QR) {
+    const int h = qi / a.rows, r = qi - h * a.rows;
+    const float inv = 1.0f / L;
+    u16* dst = a.out + (size_t)r * a.nq * HD + (g * grp + h) * HD + 16 * dt + 4 * lg;
+    st8<COH>(dst, u32x2{pack2(from_f32<DT>(acc[0] * inv), from_f32<DT>(acc[1] * inv)),
+                        pack2(from_f32<DT>(acc[2] * inv), from_f32<DT>(acc[3] * inv))});
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(64) void attn_merge_kernel(AttnP a) {
+  attn_merge_wave<DT, false>(a, blockIdx.x, blockIdx.y, blockIdx.z, threadIdx.x);
+}
+
+}  // namespace fdllm

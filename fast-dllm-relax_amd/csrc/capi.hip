@@ -146,12 +146,12 @@ int divisor_at_most(int n, int cap) {
   return 1;
 }
 
+// ksplit: the k split of the streaming kernel (prefill-sized M); the one-shot kernel picks its own.
 int run_gemm(fdllm_ctx* c, int cfg, GemmP a, int ksplit, hipStream_t st) {
   const fdllm_config& f = c->cfg;
   if (ksplit < 1 || a.KS % ksplit) return fail(FDLLM_EINVAL, "k split %d does not divide %d k steps", ksplit, a.KS);
-  a.kps = a.KS / ksplit;
   const GemmPlan pl = gemm_plan(cfg, a, ksplit);
-  if (ksplit > 1) {
+  if (pl.ksplit > 1) {
     int rc = ensure_floats(&c->gpart, &c->gpart_floats, pl.part_floats);
     if (rc) return rc;
     if (pl.groups * pl.mchunks > c->n_counters)
@@ -159,7 +159,7 @@ int run_gemm(fdllm_ctx* c, int cfg, GemmP a, int ksplit, hipStream_t st) {
     a.part = c->gpart;
     a.counters = c->counters;
   }
-  HIPCHK(launch_gemm(f.dtype, cfg, a, ksplit, st));
+  HIPCHK(launch_gemm(f.dtype, cfg, a, pl, st));
   return FDLLM_OK;
 }
 

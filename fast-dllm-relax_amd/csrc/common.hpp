@@ -145,6 +145,72 @@ __device__ __forceinline__ void wait_memory() {
 // Split fix-up: returns true in every thread of the workgroup that arrived last of `expected`.
 // Callers write their partials with st_agent* first; the last arriver reads them with ld_agent*.
 // The counter is returned to zero, so the next launch starts clean.
+// Loads and stores of data that other workgroups of the same launch write or read: with COH they are
+// agent-scope (sc1) accesses, which always see the latest agent-visible value (a plain load may hit a
+// stale line of this XCD's L2) and write through; without COH they are plain.
+template <bool COH>
+__device__ __forceinline__ u32x4 ld16(const void* p) {
+  if constexpr (COH) {
+    typedef unsigned long long u64;
+    const u64* q = reinterpret_cast<const u64*>(p);
+    const u64 a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const u64 b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return u32x4{(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32)};
+  } else {
+    return *reinterpret_cast<const u32x4*>(p);
+  }
+}
+template <bool COH>
+__device__ __forceinline__ void st16(void* p, u32x4 v) {
+  if constexpr (COH) {
+    typedef unsigned long long u64;
+    u64* q = reinterpret_cast<u64*>(p);
+    __hip_atomic_store(q, (u64)v[0] | ((u64)v[1] << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(q + 1, (u64)v[2] | ((u64)v[3] << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    *reinterpret_cast<u32x4*>(p) = v;
+  }
+}
+template <bool COH>
+__device__ __forceinline__ u32x2 ld8(const void* p) {
+  if constexpr (COH) {
+    typedef unsigned long long u64;
+    const u64 a = __hip_atomic_load(reinterpret_cast<const u64*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return u32x2{(uint32_t)a, (uint32_t)(a >> 32)};
+  } else {
+    return *reinterpret_cast<const u32x2*>(p);
+  }
+}
+template <bool COH>
+__device__ __forceinline__ void st8(void* p, u32x2 v) {
+  if constexpr (COH) {
+    typedef unsigned long long u64;
+    __hip_atomic_store(reinterpret_cast<u64*>(p), (u64)v[0] | ((u64)v[1] << 32), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    *reinterpret_cast<u32x2*>(p) = v;
+  }
+}
+template <bool COH>
+__device__ __forceinline__ float ldf(const float* p) {
+  if constexpr (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else return *p;
+}
+template <bool COH>
+__device__ __forceinline__ void stf(float* p, float v) {
+  if constexpr (COH) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else *p = v;
+}
+template <bool COH>
+__device__ __forceinline__ f32x4 ldf4(const f32x4* p) {
+  const u32x4 v = ld16<COH>(p);
+  return f32x4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
+}
+template <bool COH>
+__device__ __forceinline__ void stf4(f32x4* p, f32x4 v) {
+  st16<COH>(p, u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])});
+}
+
 __device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned expected, int* lds_flag) {
   wait_memory();
   __syncthreads();

@@ -34,6 +34,7 @@ struct GemmP {
   float* logits; int ldl;             // EPI_LOGITS (optional)
   float* stat_m; int32_t* stat_a; float* stat_s; int stat_tiles;  // EPI_LOGITS confidence statistics
   float* part; unsigned* counters;    // cross-workgroup split partials / arrival counters
+  int ngroups;                        // tile groups of the one-shot launch (its gridDim.x)
 };
 
 // Launch configurations (see gemm.hip); the host picks one per projection.
@@ -41,10 +42,12 @@ enum GemmCfg : int { CFG_QKV = 0, CFG_OPROJ = 1, CFG_GATE_UP = 2, CFG_DOWN = 3, 
 // tiles_per_wg: the padding unit of the packed tile count (every kernel of the projection divides it)
 struct GemmShape { int tiles_per_wg; int waves; };
 GemmShape gemm_shape(int cfg);
-// The kernel and grid a launch uses: groups x ksplit x mchunks workgroups, part_floats of split partials.
-struct GemmPlan { int one_shot; int tiles_per_wg; int groups; int mchunks; size_t part_floats; };
-GemmPlan gemm_plan(int cfg, const GemmP& a, int ksplit);
-hipError_t launch_gemm(int dt, int cfg, const GemmP& a, int ksplit, hipStream_t st);
+// The kernel and grid a launch uses: groups x ksplit x mchunks workgroups, part_floats of split
+// partials.  The one-shot kernel (M <= 32) picks its own k split; the streaming kernel takes
+// stream_split.  Sets a.kps.
+struct GemmPlan { int one_shot; int ksplit; int tiles_per_wg; int groups; int mchunks; size_t part_floats; };
+GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split);
+hipError_t launch_gemm(int dt, int cfg, const GemmP& a, const GemmPlan& p, hipStream_t st);
 
 // ---- confidence ---------------------------------------------------------------------------------
 hipError_t launch_confidence_combine(const float* sm, const int32_t* sa, const float* ss, int tiles, int rows,

@@ -192,3 +192,4 @@ def test_wide_cached_step_and_logits(wide2):
     wid, wp = oconf.confidence(lg[0])
     np.testing.assert_array_equal(ids_d.cpu().numpy()[0], wid)
     np.testing.assert_array_equal(maxp_d.cpu().numpy()[0].view(np.uint32), wp.view(np.uint32))
+
