@@ -72,6 +72,8 @@ def main() -> int:
     ap.add_argument("--prefix", type=int, default=PREFIX)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-iters", type=int, default=2)
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only launch the dominant kernel over the 28 layers and a plain 256 MiB copy (for rocprofv3 --pmc)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -104,6 +106,8 @@ def main() -> int:
     log("generating random weights on the GPU")
     params = random_params_torch(cfg, SEED, dtype="bfloat16", device="cuda", std=0.02, lm_head_std=0.5)
     vm = HipVM(cfg, params, dtype="bfloat16", max_rows=PREFIX)
+    if args.traffic_probe:
+        return traffic_probe(vm, cfg)
     rng = np.random.default_rng(SEED)
     prompt = rng.integers(0, 150000, args.prefix).tolist()
     P = args.prefix
@@ -160,6 +164,7 @@ def main() -> int:
     H, I = cfg.hidden_size, cfg.intermediate_size
     gu_bytes = 2 * I * H * 2 + 32 * H * 2 + 32 * I * 2  # weights + input rows + output rows
     gu_gbps = gu_bytes / (gu_ms * 1e-3) / 1e9
+    traffic = measured_traffic()
 
     # ---- CPU baseline: the oracle's refinement step on the host ------------------------------------
     cpu = None
@@ -194,14 +199,48 @@ def main() -> int:
             "partial_r8_ms": round(partial_ms, 4), "partial_r8_bytes": bytes_r8,
             "partial_r8_gbps": round(bytes_r8 / (partial_ms * 1e-3) / 1e9, 1),
         },
-        "roofline": {"kernel": "gemm_pk_kernel<bf16, EPI_SILU_PAIR> (gate_up + SiLU*up, 32 rows)", "bound": "hbm",
-                     "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+        "roofline": {"kernel": "gemm_os_kernel<bf16, EPI_SILU_PAIR, XF_RMS> (RMSNorm + gate_up + SiLU*up, 32 rows)",
+                     "bound": "hbm", "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "avg_launch_us": round(gu_ms * 1e3, 2), "bytes_per_launch": gu_bytes},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def traffic_probe(vm, cfg) -> int:
+    """One pass of the dominant kernel over the layers, then a plain copy of 256 MiB (the counter scale)."""
+    import torch
+
+    stream = torch.cuda.current_stream().cuda_stream
+    _lib = vm_lib()
+    _lib.check(vm.lib.fdllm_bench_op(vm.ctx, _lib.OP_GATE_UP, 32, 0, cfg.num_hidden_layers, None, None, 0, 0, stream))
+    src = torch.ones(128 << 20, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log("traffic probe done: 28 gate_up launches, 3 copies of 256 MiB")
+    return 0
+
+
+def vm_lib():
+    from fast_dllm_relax_amd import _lib
+
+    return _lib
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary
+    (profiles/gate_up_traffic.md, line 'traffic_bytes_per_launch: N'), or None."""
+    path = ROOT / "profiles" / "gate_up_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.strip().startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip().strip("`"))
+    return None
 
 
 def cpu_baseline(vm, params, cache, block, P, iters, tokens_per_call):

@@ -5,6 +5,9 @@
 
 namespace fdllm {
 
+// key parts per workgroup of the chunked kernel (waves = 4 query tiles x ATTN_KH)
+constexpr int ATTN_KH = 2;
+
 // Launch plan: short row blocks (the cached decode step) use attn_chunk_kernel with one key chunk of
 // CH keys per workgroup; long row blocks (prefill, stateless forward) use attn_kernel with few, long
 // key ranges per workgroup.
@@ -66,9 +69,9 @@ static hipError_t launch_loop(const AttnP& a, const AttnPlan& p, hipStream_t st)
   return hipGetLastError();
 }
 
-template <int DT, int CH>
-static hipError_t launch_chunk(const AttnP& a, const AttnPlan& p, hipStream_t st) {
-  constexpr int QPW = 4, KH = 2;
+template <int DT, int CH, int KH>
+static hipError_t launch_chunk_kh(const AttnP& a, const AttnPlan& p, hipStream_t st) {
+  constexpr int QPW = 4;
   const size_t loop_lds = (size_t)CH * KLD * 2 + (size_t)HD * (CH + 8) * 2;
   const size_t merge_lds = (size_t)2 * KH * QPW * 16 * 4 + (size_t)(KH - 1) * QPW * (HD / 16) * 64 * 16;
   const size_t lds = std::max(loop_lds, merge_lds);
@@ -88,8 +91,8 @@ static hipError_t launch_dt(const AttnP& a, hipStream_t st) {
   const AttnPlan p = attn_plan(a.rows, a.nq, a.nkv, a.Lk, a.target_wgs);
   if (p.S != a.S || p.chunk != a.chunk) return hipErrorInvalidValue;
   if (p.chunked) {
-    if (p.chunk == 128) return launch_chunk<DT, 128>(a, p, st);
-    return launch_chunk<DT, 64>(a, p, st);
+    if (p.chunk == 128) return launch_chunk_kh<DT, 128, ATTN_KH>(a, p, st);
+    return launch_chunk_kh<DT, 64, ATTN_KH>(a, p, st);
   }
   if (p.key_groups == 1) return launch_loop<DT, 4, 1>(a, p, st);
   return launch_loop<DT, 4, 2>(a, p, st);

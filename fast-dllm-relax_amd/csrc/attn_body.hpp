@@ -298,6 +298,7 @@ __device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, 
   constexpr int VIT = ((CH / 4) * 16 + NT - 1) / NT;  // V items (key quad x dim chunk) per thread
   constexpr int VLDC = CH + 8;                        // u16 stride of a transposed V row
   constexpr int DT16 = HD / 16;
+  static_assert(CH % (32 * KH) == 0, "each key part must be whole 32-key blocks");
   u16* kbuf = reinterpret_cast<u16*>(smem);           // [CH][KLD]
   u16* vbuf = kbuf + CH * KLD;                        // [HD][VLDC]
 
