@@ -67,7 +67,7 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
-    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--new-tokens", type=int, default=NEW_TOKENS)
     ap.add_argument("--prefix", type=int, default=PREFIX)
     ap.add_argument("--no-cpu-baseline", action="store_true")

@@ -1,6 +1,7 @@
 // Skinny GEMM launch planning and launchers, the confidence kernels and the weight repack; the GEMM
 // kernels and their bodies are in gemm_body.hpp.
 #include "gemm_body.hpp"
+#include "gemm_mm.hpp"
 
 #include <algorithm>
 
@@ -155,9 +156,54 @@ GemmShape gemm_shape(int cfg) {
   return GemmShape{l, 0};
 }
 
+// large-M kernel configurations (rows x columns per workgroup)
+using MmSmall = MmCfg<4, 2, 4, 2, 2>;  // 64 x 128, weights two stages ahead
+using MmWide = MmCfg<4, 4, 4, 2, 1>;   // 64 x 256
+using MmWideD = MmCfg<4, 4, 4, 2, 2>;  // 64 x 256, weights two stages ahead
+using MmBig = MmCfg<8, 2, 8, 2, 1>;    // 128 x 256, 8 waves
+enum MmId : int { MM_SMALL = 0, MM_WIDE = 1, MM_WIDE_D = 2, MM_BIG = 3 };
+struct MmInfo { int bm, bn_tiles, kss; };
+template <class M> constexpr MmInfo mm_info_of() { return MmInfo{M::bm, M::bn_tiles, M::kss}; }
+static MmInfo mm_info(int id) {
+  switch (id) {
+    case MM_WIDE: return mm_info_of<MmWide>();
+    case MM_WIDE_D: return mm_info_of<MmWideD>();
+    case MM_BIG: return mm_info_of<MmBig>();
+    default: return mm_info_of<MmSmall>();
+  }
+}
+static int mm_choice(int cfg, int M) {
+  switch (cfg) {
+    case CFG_GATE_UP: return M >= 1024 ? MM_BIG : MM_WIDE;
+    case CFG_DOWN: return M >= 1024 ? MM_WIDE_D : MM_SMALL;
+    default: return MM_SMALL;
+  }
+}
+
 GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split) {
   GemmPlan p{};
   p.mchunks = (a.M + 31) / 32;
+  if (cfg != CFG_LM_HEAD && a.M > 32) {
+    const int id = mm_choice(cfg, a.M);
+    const MmInfo mi = mm_info(id);
+    if (a.KS % mi.kss == 0) {
+      const int nst = a.KS / mi.kss;
+      p.kind = GK_MM;
+      p.mm_id = id;
+      p.nbm = (a.M + mi.bm - 1) / mi.bm;
+      p.nbn = (a.ntiles + mi.bn_tiles - 1) / mi.bn_tiles;
+      // k split: the smallest divisor of the stage count that brings the launch to 256 workgroups (at
+      // most 8 splits of at least 4 stages), else the largest such divisor
+      const int wgs = p.nbm * p.nbn;
+      int split = 1;
+      for (int d = 2; d <= 8 && wgs * split < 256; ++d)
+        if (nst % d == 0 && nst / d >= 4) split = d;
+      p.ksplit = split;
+      a.kps = a.KS / split;
+      p.part_floats = split > 1 ? (size_t)split * a.ntiles * ((a.M + 15) / 16) * 256 : 0;
+      return p;
+    }
+  }
   const OsInfo o = os_info(cfg);
   const int mt = a.M <= 16 ? 1 : 2;
   if (o.nt > 0 && a.M <= 32 && a.ntiles % o.nt == 0) {
@@ -169,13 +215,13 @@ GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split) {
       if (a.KS % d == 0) { split = d; break; }
     while (split > 0 && split <= a.KS && (a.KS % split != 0 || a.KS / split > 8 * o.kpw)) ++split;
     if (split > 0 && split <= a.KS && (a.KS / split) * mt <= 96) {
-      p.one_shot = 1;
+      p.kind = GK_ONESHOT;
       p.ksplit = split;
     }
   }
-  if (!p.one_shot) p.ksplit = stream_split;
+  if (p.kind != GK_ONESHOT) p.ksplit = stream_split;
   a.kps = a.KS / p.ksplit;
-  const int tiles = p.one_shot ? o.nt : streaming_tiles(cfg);
+  const int tiles = p.kind == GK_ONESHOT ? o.nt : streaming_tiles(cfg);
   p.tiles_per_wg = tiles;
   p.groups = (a.ntiles + tiles - 1) / tiles;
   p.part_floats = p.ksplit > 1 ? (size_t)p.groups * p.mchunks * p.ksplit * tiles * 2 * 64 * 4 : 0;
@@ -214,10 +260,39 @@ static hipError_t launch_os(const GemmP& a, const GemmPlan& p, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <int DT, class C, class O>
+template <int DT, int EPI, int XF, class M>
+static hipError_t launch_mm_cfg(const GemmP& a, const GemmPlan& p, hipStream_t st) {
+  auto kern = gemm_mm_kernel<DT, EPI, XF, M::mf, M::tpw, M::nw, M::kss, M::wd>;
+  const int total = p.nbm * p.nbn, per = (total + 7) / 8;
+  hipLaunchKernelGGL(kern, dim3(8 * per, p.ksplit), dim3(64 * M::nw), M::lds, st, a, p.nbm, p.nbn);
+  if (p.ksplit > 1) {
+    const int nblk = (a.M + 15) / 16;
+    hipLaunchKernelGGL((gemm_mm_split_epilogue_kernel<DT, EPI>), dim3((a.N + 15) / 16, (nblk + 3) / 4), dim3(256), 0,
+                       st, a, p.ksplit);
+  }
+  return hipGetLastError();
+}
+
+template <int DT, int CFG, class C>
+static hipError_t launch_mm(const GemmP& a, const GemmPlan& p, hipStream_t st) {
+  if constexpr (CFG == CFG_GATE_UP) {
+    if (p.mm_id == MM_BIG) return launch_mm_cfg<DT, C::epi, C::xf, MmBig>(a, p, st);
+    return launch_mm_cfg<DT, C::epi, C::xf, MmWide>(a, p, st);
+  } else if constexpr (CFG == CFG_DOWN) {
+    if (p.mm_id == MM_WIDE_D) return launch_mm_cfg<DT, C::epi, C::xf, MmWideD>(a, p, st);
+    return launch_mm_cfg<DT, C::epi, C::xf, MmSmall>(a, p, st);
+  } else if constexpr (CFG == CFG_QKV || CFG == CFG_OPROJ) {
+    return launch_mm_cfg<DT, C::epi, C::xf, MmSmall>(a, p, st);
+  } else {
+    return hipErrorInvalidValue;
+  }
+}
+
+template <int DT, int CFG, class C, class O>
 static hipError_t launch_mt(const GemmP& a, const GemmPlan& p, hipStream_t st) {
+  if (p.kind == GK_MM) return launch_mm<DT, CFG, C>(a, p, st);
   if constexpr (O::nt > 0) {
-    if (p.one_shot) {
+    if (p.kind == GK_ONESHOT) {
       if (a.M <= 16) return launch_os<DT, O, 1>(a, p, st);
       return launch_os<DT, O, 2>(a, p, st);
     }
@@ -229,11 +304,11 @@ static hipError_t launch_mt(const GemmP& a, const GemmPlan& p, hipStream_t st) {
 template <int DT>
 static hipError_t launch_dt(int cfg, const GemmP& a, const GemmPlan& p, hipStream_t st) {
   switch (cfg) {
-    case CFG_QKV: return launch_mt<DT, CfgQkv, OsQkv>(a, p, st);
-    case CFG_OPROJ: return launch_mt<DT, CfgOproj, OsOproj>(a, p, st);
-    case CFG_GATE_UP: return launch_mt<DT, CfgGateUp, OsGateUp>(a, p, st);
-    case CFG_DOWN: return launch_mt<DT, CfgDown, OsDown>(a, p, st);
-    case CFG_LM_HEAD: return launch_mt<DT, CfgLmHead, OsNone>(a, p, st);
+    case CFG_QKV: return launch_mt<DT, CFG_QKV, CfgQkv, OsQkv>(a, p, st);
+    case CFG_OPROJ: return launch_mt<DT, CFG_OPROJ, CfgOproj, OsOproj>(a, p, st);
+    case CFG_GATE_UP: return launch_mt<DT, CFG_GATE_UP, CfgGateUp, OsGateUp>(a, p, st);
+    case CFG_DOWN: return launch_mt<DT, CFG_DOWN, CfgDown, OsDown>(a, p, st);
+    case CFG_LM_HEAD: return launch_mt<DT, CFG_LM_HEAD, CfgLmHead, OsNone>(a, p, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -42,10 +42,15 @@ enum GemmCfg : int { CFG_QKV = 0, CFG_OPROJ = 1, CFG_GATE_UP = 2, CFG_DOWN = 3, 
 // tiles_per_wg: the padding unit of the packed tile count (every kernel of the projection divides it)
 struct GemmShape { int tiles_per_wg; int waves; };
 GemmShape gemm_shape(int cfg);
-// The kernel and grid a launch uses: groups x ksplit x mchunks workgroups, part_floats of split
-// partials.  The one-shot kernel (M <= 32) picks its own k split; the streaming kernel takes
-// stream_split.  Sets a.kps.
-struct GemmPlan { int one_shot; int ksplit; int tiles_per_wg; int groups; int mchunks; size_t part_floats; };
+// The kernel and grid a launch uses.  GK_ONESHOT (M <= 32) and GK_MM (larger M, not the lm_head) pick
+// their own k split; GK_STREAM (the lm_head, or shapes the others do not take) runs stream_split.
+// Streaming and one-shot launches have groups x ksplit x mchunks workgroups; the large-M kernel
+// covers nbm x nbn blocks of config mm_id.  part_floats: split partials.  Sets a.kps.
+enum GemmKind : int { GK_STREAM = 0, GK_ONESHOT = 1, GK_MM = 2 };
+struct GemmPlan {
+  int kind; int ksplit; int tiles_per_wg; int groups; int mchunks; size_t part_floats;
+  int mm_id; int nbm; int nbn;
+};
 GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split);
 hipError_t launch_gemm(int dt, int cfg, const GemmP& a, const GemmPlan& p, hipStream_t st);
 

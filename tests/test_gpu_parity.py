@@ -193,3 +193,22 @@ def test_wide_cached_step_and_logits(wide2):
     np.testing.assert_array_equal(ids_d.cpu().numpy()[0], wid)
     np.testing.assert_array_equal(maxp_d.cpu().numpy()[0].view(np.uint32), wp.view(np.uint32))
 
+
+
+def test_wide_forward_hidden_large_m(wide2):
+    """Large-M projections (the MFMA block kernel) at the 1.5B layer shapes: a stateless block-causal
+    forward over 160 rows (64-row blocks with k splits) and 1056 rows (128-row blocks, ragged last
+    block) vs the bf16 and fp32 oracles."""
+    from oracle.model import OracleModel
+
+    ref, vm = wide2
+    ref32 = OracleModel(ref.cfg, ref.p, "float32")
+    rng = np.random.default_rng(11)
+    for S in (160, 1056):
+        ids = _ids(rng, S, WIDE2["vocab_size"])
+        bias = build_prefix_block_attention_bias(0, S, block_size=32)
+        want = ref.forward_hidden(ref.embed(ids)[None], bias)
+        want32 = ref32.forward_hidden(ref32.embed(ids)[None], bias)
+        log(f"case: wide forward_hidden S={S} arithmetic block-causal")
+        got = to_np(vm.forward_hidden(vm.embed(_dev_ids(ids))[None], None))
+        bf16_parity(f"hidden S={S}", got, want, want32)
