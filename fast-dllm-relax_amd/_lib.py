@@ -21,6 +21,7 @@ EXPORTS = (
     "fdllm_embed", "fdllm_forward_hidden", "fdllm_get_logits", "fdllm_build_prefix_cache",
     "fdllm_forward_cached", "fdllm_forward_block_partial", "fdllm_forward_block_partial_rp0",
     "fdllm_forward_block_partial_rp8", "fdllm_forward_block_partial_rp16", "fdllm_forward_block_partial_rp24",
+    "fdllm_forward_cached_batch", "fdllm_forward_block_partial_batch", "fdllm_build_prefix_cache_seq",
     "fdllm_get_confidence", "fdllm_confidence_from_logits", "fdllm_bench_op", "fdllm_last_error",
 )
 
@@ -56,6 +57,9 @@ _SIGS = {
     "fdllm_forward_block_partial_rp8": ([_P, _P, _I, _P, _P, _I, _P, _I64, _P, _P], _I),
     "fdllm_forward_block_partial_rp16": ([_P, _P, _I, _P, _P, _I, _P, _I64, _P, _P], _I),
     "fdllm_forward_block_partial_rp24": ([_P, _P, _I, _P, _P, _I, _P, _I64, _P, _P], _I),
+    "fdllm_forward_cached_batch": ([_P, _P, _I, _I, _P, _P, _I, _P, ctypes.POINTER(_I64), _P, _P], _I),
+    "fdllm_forward_block_partial_batch": ([_P, _I, _P, _I, _I, _P, _P, _I, _P, ctypes.POINTER(_I64), _P, _P], _I),
+    "fdllm_build_prefix_cache_seq": ([_P, _P, _I, _P, _P, _P, _I, _I, _I, _P], _I),
     "fdllm_get_confidence": ([_P, _P, _I, _P, _P, _P, _P], _I),
     "fdllm_confidence_from_logits": ([_P, _P, _I, _I, _I, _P, _P, _P], _I),
     "fdllm_bench_op": ([_P, _I, _I, _I, _I, _P, _P, _I, _I, _P], _I),

@@ -40,7 +40,7 @@ AttnPlan attn_plan(int rows, int nq, int nkv, int Lk, int target_wgs) {
 
 size_t attn_partial_floats(const AttnP& a) {
   const int QT = ((a.nq / a.nkv) * a.rows + 15) / 16;
-  return (size_t)a.nkv * QT * a.S * PSZ;
+  return (size_t)std::max(a.nseq, 1) * a.nkv * QT * a.S * PSZ;
 }
 
 template <typename K>
@@ -78,10 +78,11 @@ static hipError_t launch_chunk_kh(const AttnP& a, const AttnPlan& p, hipStream_t
   if (lds > 160 * 1024) return hipErrorInvalidValue;
   auto kern = attn_chunk_kernel<DT, QPW, KH, CH>;
   raise_lds(kern, lds);
-  hipLaunchKernelGGL(kern, dim3(p.qg, a.nkv, a.S), dim3(64 * QPW * KH), lds, st, a);
+  const int nseq = std::max(a.nseq, 1);
+  hipLaunchKernelGGL(kern, dim3(p.qg * nseq, a.nkv, a.S), dim3(64 * QPW * KH), lds, st, a);
   if (a.S > 1) {
     const int QT = ((a.nq / a.nkv) * a.rows + 15) / 16;
-    hipLaunchKernelGGL(attn_merge_kernel<DT>, dim3(HD / 16, QT, a.nkv), dim3(64), 0, st, a);
+    hipLaunchKernelGGL(attn_merge_kernel<DT>, dim3(HD / 16, QT, a.nkv * nseq), dim3(64), 0, st, a);
   }
   return hipGetLastError();
 }
@@ -90,6 +91,7 @@ template <int DT>
 static hipError_t launch_dt(const AttnP& a, hipStream_t st) {
   const AttnPlan p = attn_plan(a.rows, a.nq, a.nkv, a.Lk, a.target_wgs);
   if (p.S != a.S || p.chunk != a.chunk) return hipErrorInvalidValue;
+  if (a.nseq > 1 && (!p.chunked || a.nseq > MAX_SEQS)) return hipErrorInvalidValue;
   if (p.chunked) {
     if (p.chunk == 128) return launch_chunk_kh<DT, 128, ATTN_KH>(a, p, st);
     return launch_chunk_kh<DT, 64, ATTN_KH>(a, p, st);

@@ -544,45 +544,68 @@ __device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, 
   }
 }
 
+// Batched call: the view of sequence b (its rows, cache, window and split partials).
+__device__ __forceinline__ void seq_view(AttnP& a, int b) {
+  const int QT = ((a.nq / a.nkv) * a.rows + 15) / 16;
+  a.qkv += (size_t)b * a.rows * a.ldq;
+  a.rope += (size_t)b * a.rows * 128;
+  a.out += (size_t)b * a.rows * a.nq * HD;
+  a.kc += b * a.seq_stride;
+  a.vc += b * a.seq_stride;
+  a.ws = a.seq_ws[b];
+  a.Lk = a.seq_lk[b];
+  a.part += (size_t)b * a.nkv * QT * a.S * PSZ;
+}
+
+// gridDim.x = query-tile groups x sequences (sequence-major)
 template <int DT, int QPW, int KH, int CH>
 __global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  attn_chunk_body<DT, QPW, KH, CH, false>(a, blockIdx.x, blockIdx.y, blockIdx.z, smem);
+  int bx = blockIdx.x;
+  if (a.nseq > 1) {
+    const int qg = (int)gridDim.x / a.nseq, b = bx / qg;
+    bx -= b * qg;
+    seq_view(a, b);
+    if ((int)blockIdx.z * a.chunk >= a.Lk) return;  // past this sequence's keys: the merge skips it
+  }
+  attn_chunk_body<DT, QPW, KH, CH, false>(a, bx, blockIdx.y, blockIdx.z, smem);
 }
 
 // Merge of the key splits: one wave per (kv head g, query tile qt, 16-dim slice dt).  The split weights
 // exp(m_c - M) depend only on the query, so each lane computes them once for its query lr; the split
 // partials are added in split order.
+// Splits at or past ceil(Lk / chunk) (a shorter sequence of a batched call) hold nothing and are skipped.
 template <int DT, bool COH>
 __device__ __forceinline__ void attn_merge_wave(const AttnP& a, int dt, int qt, int g, int lane) {
   constexpr int SB = 8;
   const int lr = lane & 15, lg = lane >> 4;
   const int grp = a.nq / a.nkv, QR = grp * a.rows, QT = (QR + 15) / 16;
+  const int S = min(a.S, (a.Lk + a.chunk - 1) / a.chunk);  // splits that hold keys
   const float* pt = a.part + (size_t)(g * QT + qt) * a.S * PSZ;
   float M = -INFINITY;
-  for (int s0 = 0; s0 < a.S; s0 += SB) {
+  for (int s0 = 0; s0 < S; s0 += SB) {
     float mv[SB];
 #pragma unroll
-    for (int q = 0; q < SB; ++q) mv[q] = ldf<COH>(pt + (size_t)min(s0 + q, a.S - 1) * PSZ + 16 * HD + lr);
+    for (int q = 0; q < SB; ++q) mv[q] = ldf<COH>(pt + (size_t)min(s0 + q, S - 1) * PSZ + 16 * HD + lr);
 #pragma unroll
     for (int q = 0; q < SB; ++q) M = fmaxf(M, mv[q]);
   }
   const float Mu = M == -INFINITY ? 0.f : M;
   float L = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = 0; s0 < a.S; s0 += SB) {
+  for (int s0 = 0; s0 < S; s0 += SB) {
     f32x4 ov[SB];
     float mv[SB], lv[SB];
 #pragma unroll
     for (int q = 0; q < SB; ++q) {
-      const float* ps = pt + (size_t)min(s0 + q, a.S - 1) * PSZ;
+      const float* ps = pt + (size_t)min(s0 + q, S - 1) * PSZ;
       ov[q] = ldf4<COH>(reinterpret_cast<const f32x4*>(ps) + dt * 64 + lane);
       mv[q] = ldf<COH>(ps + 16 * HD + lr);
       lv[q] = ldf<COH>(ps + 16 * HD + 16 + lr);
     }
 #pragma unroll
     for (int q = 0; q < SB; ++q) {
-      const float e = s0 + q < a.S ? expf(mv[q] - Mu) : 0.f;
+      const float e = s0 + q < S ? expf(mv[q] - Mu) : 0.f;
       L += lv[q] * e;
       acc += ov[q] * e;
     }
@@ -597,9 +620,16 @@ __device__ __forceinline__ void attn_merge_wave(const AttnP& a, int dt, int qt, 
   }
 }
 
+// gridDim.z = kv heads x sequences (sequence-major)
 template <int DT>
 __global__ __launch_bounds__(64) void attn_merge_kernel(AttnP a) {
-  attn_merge_wave<DT, false>(a, blockIdx.x, blockIdx.y, blockIdx.z, threadIdx.x);
+  int g = blockIdx.z;
+  if (a.nseq > 1) {
+    const int b = g / a.nkv;
+    g -= b * a.nkv;
+    seq_view(a, b);
+  }
+  attn_merge_wave<DT, false>(a, blockIdx.x, blockIdx.y, g, threadIdx.x);
 }
 
 }  // namespace fdllm

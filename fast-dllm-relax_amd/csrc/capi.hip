@@ -39,6 +39,13 @@ struct Layer {
   const uint16_t *pqkv, *po, *pgu, *pd;                           // packed copies (context-owned)
 };
 
+// A batched call: nseq sequences of `rows` active rows each; sequence b's cache sits seq_stride
+// elements after sequence b - 1's in every layer, its rows are written from ws[b] and it attends [0, lk[b]).
+struct SeqBatch {
+  int nseq; int rows; long long seq_stride;
+  int ws[MAX_SEQS]; int lk[MAX_SEQS];
+};
+
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 int round_up(int x, int a) { return (x + a - 1) / a * a; }
 
@@ -184,25 +191,41 @@ int run_lm_head(fdllm_ctx* c, const uint16_t* hidden, int rows, float* logits, b
   return run_gemm(c, CFG_LM_HEAD, a, 1, st);
 }
 
-// RoPE table of `rows` rows at positions *pos + r, shared by every layer of the call.
-int rope_table(fdllm_ctx* c, int rows, const int32_t* pos, hipStream_t st) {
+// RoPE table of `rows` rows, row r at position pos[r / rows_per_seq] + r % rows_per_seq, shared by every
+// layer of the call.
+int rope_table(fdllm_ctx* c, int rows, const int32_t* pos, int rows_per_seq, hipStream_t st) {
   int rc = ensure_floats(&c->rope, &c->rope_floats, (size_t)rows * 128);
   if (rc) return rc;
-  HIPCHK(launch_rope_table(c->cfg.dtype, pos, rows, (float)(-std::log((double)c->cfg.rope_theta)), c->rope, st));
+  HIPCHK(launch_rope_table(c->cfg.dtype, pos, rows, rows_per_seq, (float)(-std::log((double)c->cfg.rope_theta)),
+                           c->rope, st));
   return FDLLM_OK;
 }
 
-// Attention of the call's rows; the RoPE table (rope_table) must hold the call's positions.
+// Attention of the call's rows; the RoPE table (rope_table) must hold the call's positions.  With sb,
+// the rows are sb->nseq sequences of sb->rows (ws and Lk are then ignored).
 int run_attention(fdllm_ctx* c, int rows, uint16_t* kc, uint16_t* vc, int ws, int Lk, int mask,
-                  const float* bias, long long bias_ld, hipStream_t st) {
+                  const float* bias, long long bias_ld, hipStream_t st, const SeqBatch* sb = nullptr) {
   const fdllm_config& f = c->cfg;
   AttnP a{};
   a.qkv = c->qkv; a.ldq = c->qkv_dim(); a.rows = rows; a.nq = f.num_attention_heads; a.nkv = f.num_key_value_heads;
   a.rope = c->rope;
   a.kc = kc; a.vc = vc; a.ws = ws; a.Lk = Lk; a.scale = 1.0f / std::sqrt((float)f.head_dim);
   a.mask = mask; a.q_pos0 = 0; a.block = f.bd_size; a.bias = bias; a.bias_ld = bias_ld;
-  const AttnPlan pl = attn_plan(rows, a.nq, a.nkv, Lk, c->attn_target);
-  a.S = pl.S; a.chunk = pl.chunk; a.target_wgs = c->attn_target;
+  a.nseq = 1;
+  int target = c->attn_target;
+  if (sb != nullptr) {
+    a.nseq = sb->nseq; a.rows = sb->rows; a.seq_stride = sb->seq_stride;
+    a.ws = 0; a.Lk = 0;
+    for (int b = 0; b < sb->nseq; ++b) {
+      a.seq_ws[b] = sb->ws[b]; a.seq_lk[b] = sb->lk[b];
+      a.ws = std::max(a.ws, sb->ws[b]); a.Lk = std::max(a.Lk, sb->lk[b]);
+    }
+    target = std::max(1, target / sb->nseq);
+  }
+  const AttnPlan pl = attn_plan(a.rows, a.nq, a.nkv, a.Lk, target);
+  if (sb != nullptr && !pl.chunked)
+    return fail(FDLLM_EINVAL, "batched call of %d rows per sequence over %d keys is too long for one step", a.rows, a.Lk);
+  a.S = pl.S; a.chunk = pl.chunk; a.target_wgs = target;
   if (a.S > 1) {
     int rc = ensure_floats(&c->apart, &c->apart_floats, attn_partial_floats(a));
     if (rc) return rc;
@@ -218,14 +241,15 @@ int run_attention(fdllm_ctx* c, int rows, uint16_t* kc, uint16_t* vc, int ws, in
 //              -> gate_up (RMSNorm on load, SiLU * up) -> down + residual
 // kv: per-layer cache base pointers are k/v + layer * layer_stride (elements).  out == nullptr skips
 // the final norm (build_prefix_cache returns only the caches).
+// sb: a batched call (rows = sb->nseq x sb->rows; pos_dev holds one offset per sequence).
 int run_layers(fdllm_ctx* c, const void* x_in, int rows, uint16_t* kbase, uint16_t* vbase, size_t layer_stride,
                int write_start, const int32_t* pos_dev, int attend_len, int mask, const float* bias,
-               long long bias_ld, void* out, hipStream_t st) {
+               long long bias_ld, void* out, hipStream_t st, const SeqBatch* sb = nullptr) {
   const fdllm_config& f = c->cfg;
   const int H = f.hidden_size, I = f.intermediate_size;
   const int ssq_ld = c->ws_rows;
   HIPCHK(launch_load_rows(f.dtype, (const uint16_t*)x_in, rows, H, c->h, c->ssq, ssq_ld, st));
-  int rc = rope_table(c, rows, pos_dev, st);
+  int rc = rope_table(c, rows, pos_dev, sb ? sb->rows : rows, st);
   if (rc) return rc;
   const int dsplit = divisor_at_most(I / 32, c->down_split);
   for (int l = 0; l < f.num_hidden_layers; ++l) {
@@ -239,7 +263,7 @@ int run_layers(fdllm_ctx* c, const void* x_in, int rows, uint16_t* kbase, uint16
     rc = run_gemm(c, CFG_QKV, q, 1, st);
     if (rc) return rc;
 
-    rc = run_attention(c, rows, kc, vc, write_start, attend_len, mask, bias, bias_ld, st);
+    rc = run_attention(c, rows, kc, vc, write_start, attend_len, mask, bias, bias_ld, st, sb);
     if (rc) return rc;
 
     GemmP o = gemm_args(L.po, o_tiles(c), H, c->q_dim(), c->attn, c->q_dim(), rows);
@@ -292,6 +316,38 @@ int cached_step(fdllm_ctx* c, const void* x, int rows, void* k, void* v, int cap
   size_t stride = (size_t)cap * f.num_key_value_heads * f.head_dim;
   return run_layers(c, x, rows, (uint16_t*)k, (uint16_t*)v, stride, (int)write_start, off, (int)attend_len, 0,
                     nullptr, 0, out, (hipStream_t)stream);
+}
+
+// Batched cached step over nseq sequences sharing one cache tensor [L, nseq, cap, nkv, hd]: the checks
+// of cached_step per sequence, then one pass of the layers over nseq x rows rows.
+int cached_step_batch(fdllm_ctx* c, const void* x, int nseq, int rows, void* k, void* v, int cap, const int32_t* off,
+                      const int64_t* prefix_lens, int write_rel, int attend_rel, void* out, void* stream) {
+  int rc = check_ready(c);
+  if (rc) return rc;
+  if (!x || !k || !v || !off || !prefix_lens || !out) return fail(FDLLM_EINVAL, "null tensor argument");
+  if (nseq <= 0 || nseq > MAX_SEQS) return fail(FDLLM_EINVAL, "batch of %d sequences (1 .. %d supported)", nseq, MAX_SEQS);
+  if (rows <= 0) return fail(FDLLM_EINVAL, "active rows must be positive, got %d", rows);
+  const fdllm_config& f = c->cfg;
+  SeqBatch sb{};
+  sb.nseq = nseq; sb.rows = rows; sb.seq_stride = (long long)cap * f.num_key_value_heads * f.head_dim;
+  for (int b = 0; b < nseq; ++b) {
+    const int64_t ws = prefix_lens[b] + write_rel, lk = prefix_lens[b] + attend_rel;
+    if (ws + rows > lk)
+      return fail(FDLLM_EINVAL, "sequence %d: KV write [%lld, %lld) past the attended rows [0, %lld)", b, (long long)ws,
+                  (long long)(ws + rows), (long long)lk);
+    if (ws < 0 || ws + rows > cap)
+      return fail(FDLLM_EINVAL, "sequence %d: KV write [%lld, %lld) outside cache capacity %d", b, (long long)ws,
+                  (long long)(ws + rows), cap);
+    if (lk > cap) return fail(FDLLM_EINVAL, "sequence %d: cached call needs %lld rows; cache capacity is %d", b,
+                              (long long)lk, cap);
+    sb.ws[b] = (int)ws;
+    sb.lk[b] = (int)lk;
+  }
+  rc = ensure_rows(c, nseq * rows);
+  if (rc) return rc;
+  const size_t layer_stride = (size_t)nseq * sb.seq_stride;
+  return run_layers(c, x, nseq * rows, (uint16_t*)k, (uint16_t*)v, layer_stride, 0, off, 0, 0, nullptr, 0, out,
+                    (hipStream_t)stream, &sb);
 }
 
 int pack_all(fdllm_ctx* c) {
@@ -479,6 +535,39 @@ FD_PARTIAL(16)
 FD_PARTIAL(24)
 #undef FD_PARTIAL
 
+int fdllm_forward_cached_batch(fdllm_ctx* c, const void* x, int nseq, int rows, void* k, void* v, int cap,
+                               const int32_t* off, const int64_t* prefix_lens, void* out, void* stream) {
+  return cached_step_batch(c, x, nseq, rows, k, v, cap, off, prefix_lens, 0, rows, out, stream);
+}
+
+int fdllm_forward_block_partial_batch(fdllm_ctx* c, int rp, const void* x, int nseq, int rows, void* k, void* v,
+                                      int cap, const int32_t* off, const int64_t* prefix_lens, void* out,
+                                      void* stream) {
+  if (!c) return fail(FDLLM_EINVAL, "null context");
+  const int sbs = c->cfg.bd_size / 4;
+  if (rp < 0 || rp % sbs || rp >= c->cfg.bd_size)
+    return fail(FDLLM_EINVAL, "replace_position %d is not one of 0, %d, ..., %d", rp, sbs, c->cfg.bd_size - sbs);
+  if (rows != sbs) return fail(FDLLM_EINVAL, "partial step takes %d rows, got %d", sbs, rows);
+  return cached_step_batch(c, x, nseq, rows, k, v, cap, off, prefix_lens, rp, c->cfg.bd_size, out, stream);
+}
+
+int fdllm_build_prefix_cache_seq(fdllm_ctx* c, const void* x, int P, const float* bias, void* k, void* v, int cap,
+                                 int nseq, int seq, void* stream) {
+  int rc = check_ready(c);
+  if (rc) return rc;
+  if (P <= 0 || !x || !k || !v) return fail(FDLLM_EINVAL, "invalid build_prefix_cache arguments");
+  if (nseq <= 0 || seq < 0 || seq >= nseq) return fail(FDLLM_EINVAL, "sequence %d of a batch of %d", seq, nseq);
+  if (P > cap) return fail(FDLLM_EINVAL, "KV write [0, %d) outside cache capacity %d", P, cap);
+  rc = ensure_rows(c, P);
+  if (rc) return rc;
+  const fdllm_config& f = c->cfg;
+  const size_t seq_stride = (size_t)cap * f.num_key_value_heads * f.head_dim;
+  uint16_t* kb = (uint16_t*)k + (size_t)seq * seq_stride;
+  uint16_t* vb = (uint16_t*)v + (size_t)seq * seq_stride;
+  return run_layers(c, x, P, kb, vb, (size_t)nseq * seq_stride, 0, c->zero_i32, P, bias ? 2 : 1, bias, P, nullptr,
+                    (hipStream_t)stream);
+}
+
 int fdllm_get_confidence(fdllm_ctx* c, const void* hidden, int rows, int32_t* ids, float* maxp, float* logits,
                          void* stream) {
   int rc = check_ready(c);
@@ -544,7 +633,7 @@ int fdllm_bench_op(fdllm_ctx* c, int op, int rows, int layer, int iters, void* k
       }
       case FDLLM_OP_ATTENTION:
         // the block's rows sit at the end of the attended range, as in a full cached step
-        if (it == 0) rc = rope_table(c, rows, c->zero_i32, st);
+        if (it == 0) rc = rope_table(c, rows, c->zero_i32, rows, st);
         if (rc == FDLLM_OK)
           rc = run_attention(c, rows, (uint16_t*)k + li * stride, (uint16_t*)v + li * stride, attend_len - rows,
                              attend_len, 0, nullptr, 0, st);

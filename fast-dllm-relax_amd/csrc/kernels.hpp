@@ -67,12 +67,14 @@ hipError_t launch_embed(const int32_t* ids, int n, const uint16_t* table, int vo
 hipError_t launch_load_rows(int dt, const uint16_t* x, int rows, int hidden, uint16_t* h, float* ssq, int ssq_ld,
                             hipStream_t st);
 // y = RMSNorm(h) from the sums of squares the producer left (final norm)
-hipError_t launch_rope_table(int dt, const int32_t* pos_offset, int rows, float neg_log_theta, float* tab,
-                             hipStream_t st);
+// RoPE (cos, sin) table: row r sits at position pos_offset[r / rows_per_seq] + r % rows_per_seq
+hipError_t launch_rope_table(int dt, const int32_t* pos_offset, int rows, int rows_per_seq, float neg_log_theta,
+                             float* tab, hipStream_t st);
 hipError_t launch_norm_rows(int dt, const uint16_t* h, int rows, int hidden, const float* ssq, int ssq_ld,
                             const uint16_t* w, float eps, uint16_t* y, hipStream_t st);
 
 // ---- attention ----------------------------------------------------------------------------------
+constexpr int MAX_SEQS = 64;  // sequences of one batched call
 struct AttnP {
   const uint16_t* qkv; int ldq;       // [rows][ldq]: q | k | v, bias added, before RoPE
   int rows, nq, nkv;
@@ -88,6 +90,11 @@ struct AttnP {
   int target_wgs;                     // workgroups the plan aims for (attn_plan)
   float* part;                        // split partials (merged by attn_merge_kernel)
   uint16_t* out;                      // [rows][nq * 128]
+  // batched call (nseq > 1, chunked kernel only): sequence b owns rows [b rows, (b + 1) rows) of qkv,
+  // rope and out, the cache at kc / vc + b seq_stride, writes from seq_ws[b] and attends
+  // [0, seq_lk[b]); ws and Lk above then hold the largest window (S and chunk are planned for it)
+  int nseq; long long seq_stride;
+  int seq_ws[MAX_SEQS]; int seq_lk[MAX_SEQS];
 };
 struct AttnPlan { int chunked; int q_tiles_per_wg; int key_groups; int qg; int S; int chunk; };
 AttnPlan attn_plan(int rows, int nq, int nkv, int Lk, int target_wgs);

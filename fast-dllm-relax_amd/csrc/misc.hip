@@ -66,9 +66,11 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(const u16* h, int hidden
 // angle = pos * inv_freq in fp32, cos / sin in fp32 rounded to the model dtype (emb = [f, f], so one
 // entry serves dims i and i + 64).  Shared by every layer's attention.
 template <int DT>
-__global__ __launch_bounds__(64) void rope_table_kernel(const int32_t* pos_offset, float nlt, float* tab) {
+__global__ __launch_bounds__(64) void rope_table_kernel(const int32_t* pos_offset, int rows_per_seq, float nlt,
+                                                        float* tab) {
   const int r = blockIdx.x, i = threadIdx.x;
-  const float pos = (float)(*pos_offset + r);
+  const int b = r / rows_per_seq;
+  const float pos = (float)(pos_offset[b] + (r - b * rows_per_seq));
   const float fr = pos * expf((nlt * (float)i) / 64.0f);
   tab[((size_t)r * 64 + i) * 2] = rnd<DT>(cosf(fr));
   tab[((size_t)r * 64 + i) * 2 + 1] = rnd<DT>(sinf(fr));
@@ -89,12 +91,14 @@ hipError_t launch_load_rows(int dt, const uint16_t* x, int rows, int hidden, uin
   return hipGetLastError();
 }
 
-hipError_t launch_rope_table(int dt, const int32_t* pos_offset, int rows, float neg_log_theta, float* tab,
+hipError_t launch_rope_table(int dt, const int32_t* pos_offset, int rows, int rows_per_seq, float neg_log_theta, float* tab,
                              hipStream_t st) {
   if (dt == DT_BF16)
-    hipLaunchKernelGGL(rope_table_kernel<DT_BF16>, dim3(rows), dim3(64), 0, st, pos_offset, neg_log_theta, tab);
+    hipLaunchKernelGGL(rope_table_kernel<DT_BF16>, dim3(rows), dim3(64), 0, st, pos_offset, rows_per_seq, neg_log_theta,
+                       tab);
   else
-    hipLaunchKernelGGL(rope_table_kernel<DT_F16>, dim3(rows), dim3(64), 0, st, pos_offset, neg_log_theta, tab);
+    hipLaunchKernelGGL(rope_table_kernel<DT_F16>, dim3(rows), dim3(64), 0, st, pos_offset, rows_per_seq, neg_log_theta,
+                       tab);
   return hipGetLastError();
 }
 

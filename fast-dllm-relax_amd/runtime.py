@@ -404,3 +404,95 @@ def relax_greedy_generate(vm: HipVM, prompt_token_ids, *, max_new_tokens: int, b
             break
 
     return make_continuation(generated), stats()
+
+
+# ---- batched block refinement (a build extension; the reference is batch 1) --------------------------
+def batched_shifted_confidence(vm: HipVM, hidden: torch.Tensor) -> tuple[np.ndarray, np.ndarray]:
+    """shifted_confidence of each sequence of hidden [nseq, rows, H]: ids / probs [nseq, rows], the shift
+    of runtime.py:172-174 applied within each sequence (row 0 keeps its own prediction)."""
+    nseq, rows = int(hidden.shape[0]), int(hidden.shape[1])
+    ids_d, maxp_d = vm.get_confidence(hidden.view(1, nseq * rows, -1))
+    both = torch.cat([ids_d.view(torch.float32), maxp_d], dim=1).cpu().numpy()[0]
+    ids = both[:nseq * rows].view(np.int32).astype(np.int64).reshape(nseq, rows)
+    maxp = both[nseq * rows:].astype(np.float32).reshape(nseq, rows)
+    return (np.concatenate([ids[:, :1], ids[:, :-1]], axis=1), np.concatenate([maxp[:, :1], maxp[:, :-1]], axis=1))
+
+
+def relax_batched_block_refine(vm: HipVM, prompts, *, mask_id: int, block_size: int = 32,
+                               small_block_size: int = 8, threshold: float = 0.9, use_block_cache: bool = True,
+                               timing: dict | None = None):
+    """Refine one block of masks for every sequence of ``prompts`` together, as the batch-1 loop refines
+    one block (runtime.py:748-843), with each model call a batched step over all sequences.
+
+    Per sequence the block is laid out as in runtime.py:719-739: x_t = prompt + masks up to the next
+    multiple of block_size, prefix = x_t[:a0] with a0 = len(x_t) - block_size (the prompt must reach
+    a full block, a0 > 0), built with build_prefix_cache into that sequence's slice of one batched
+    cache.  Sub-blocks are refined in order; a step is a partial step at rp = s0 when the block KV is
+    valid and every sequence's row s0 is unmasked (the batch-1 condition, runtime.py:765, for all
+    sequences at once), else a full 32-row step.  Each sequence takes the threshold rule with the top-1
+    fallback (runtime.py:794-805) on its own rows; sequences whose sub-block is complete ride along
+    unchanged.  Returns (blocks [nseq][block_size] token ids, stats)."""
+    c = vm.cfg
+    nseq = len(prompts)
+    if nseq == 0:
+        raise ValueError("no sequences")
+    xs, a0s = [], []
+    for p in prompts:
+        x_t = [int(t) for t in p]
+        x_t += [mask_id] * (block_size - len(x_t) % block_size)
+        a0 = len(x_t) - block_size
+        if a0 <= 0:
+            raise ValueError("every prompt must fill at least one block (the batched path is cached only)")
+        xs.append(x_t)
+        a0s.append(a0)
+    dev = torch.device("cuda")
+    t0 = time.perf_counter()
+    cap = max(a0s) + block_size
+    shape = (c.num_hidden_layers, nseq, cap, c.num_key_value_heads, c.head_dim)
+    k = torch.zeros(shape, dtype=vm.torch_dtype, device=dev)
+    v = torch.zeros_like(k)
+    for b in range(nseq):
+        vm.build_prefix_cache_seq(_embed(vm, xs[b][:a0s[b]]), None, k, v, b)
+    off_full = torch.tensor(a0s, dtype=torch.int32, device=dev)
+    if timing is not None:
+        torch.cuda.synchronize()
+        timing["prefill_s"] = time.perf_counter() - t0
+    t1 = time.perf_counter()
+    steps = partial_steps = unmasked = 0
+    block_kv_valid = False
+    for s0 in range(0, block_size, small_block_size):
+        s1 = min(block_size, s0 + small_block_size)
+        while True:
+            local = [[i for i, t in enumerate(x[a0 + s0:a0 + s1]) if t == mask_id] for x, a0 in zip(xs, a0s)]
+            if not any(local):
+                break
+            use_partial = use_block_cache and block_kv_valid and all(x[a0 + s0] != mask_id for x, a0 in zip(xs, a0s))
+            if use_partial:
+                ids = [t for x, a0 in zip(xs, a0s) for t in x[a0 + s0:a0 + s1]]
+                emb = _embed(vm, ids).view(nseq, s1 - s0, -1)
+                off = torch.tensor([a0 + s0 for a0 in a0s], dtype=torch.int32, device=dev)
+                hidden = vm.forward_block_partial_batch(s0, emb, k, v, off, a0s)
+                partial_steps += 1
+            else:
+                ids = [t for x, a0 in zip(xs, a0s) for t in x[a0:a0 + block_size]]
+                emb = _embed(vm, ids).view(nseq, block_size, -1)
+                hidden = vm.forward_cached_batch(emb, k, v, off_full, a0s)
+                block_kv_valid = use_block_cache
+            steps += 1
+            sids, sprobs = batched_shifted_confidence(vm, hidden)
+            for b in range(nseq):
+                if not local[b]:
+                    continue
+                bids = sids[b] if use_partial else sids[b][s0:s1]
+                bp = sprobs[b] if use_partial else sprobs[b][s0:s1]
+                rows = [r for r in local[b] if bp[r] > threshold]
+                if not rows:
+                    rows = [local[b][int(np.argmax([bp[r] for r in local[b]]))]]
+                for r in rows:
+                    xs[b][a0s[b] + s0 + r] = int(bids[r])
+                    unmasked += 1
+    if timing is not None:
+        torch.cuda.synchronize()
+        timing["refine_s"] = time.perf_counter() - t1
+    stats = {"steps": steps, "partial_steps": partial_steps, "unmasked": unmasked, "nseq": nseq}
+    return [x[a0:a0 + block_size] for x, a0 in zip(xs, a0s)], stats

@@ -186,6 +186,73 @@ class HipVM:
     def forward_block_partial_rp24(self, active_embed, k_cache, v_cache, cache_offset, prefix_len):
         return self._partial(24, active_embed, k_cache, v_cache, cache_offset, prefix_len)
 
+    # ---- batched steps (no reference counterpart: the reference is batch 1, cuda.py:796-836) ----
+    def _check_batch_cache(self, k: torch.Tensor, v: torch.Tensor, nseq: int) -> int:
+        c = self.cfg
+        exp = (c.num_hidden_layers, nseq, k.shape[2] if k.dim() == 5 else -1, c.num_key_value_heads, c.head_dim)
+        for t in (k, v):
+            if tuple(t.shape) != exp or t.dtype != self.torch_dtype or not t.is_contiguous() or not t.is_cuda:
+                raise ValueError(f"batched KV cache must be a contiguous {self.torch_dtype} device tensor of shape {exp}")
+        return int(k.shape[2])
+
+    def _check_batch_rows(self, x: torch.Tensor) -> tuple[int, int]:
+        if x.dim() != 3 or x.shape[2] != self.cfg.hidden_size or x.dtype != self.torch_dtype or not x.is_contiguous():
+            raise ValueError(f"expected a contiguous [nseq, rows, {self.cfg.hidden_size}] {self.torch_dtype} tensor, "
+                             f"got {tuple(x.shape)} {x.dtype}")
+        return int(x.shape[0]), int(x.shape[1])
+
+    @staticmethod
+    def _batch_offsets(cache_offset: torch.Tensor, nseq: int) -> torch.Tensor:
+        if cache_offset.shape != (nseq,) or cache_offset.dtype != torch.int32 or not cache_offset.is_cuda:
+            raise ValueError(f"cache_offset must be an int32 device tensor of shape ({nseq},)")
+        return cache_offset.contiguous()
+
+    @staticmethod
+    def _prefix_lens(prefix_lens, nseq: int):
+        lens = [int(p) for p in prefix_lens]
+        if len(lens) != nseq:
+            raise ValueError(f"prefix_lens has {len(lens)} entries for {nseq} sequences")
+        return (ctypes.c_int64 * nseq)(*lens)
+
+    def forward_cached_batch(self, active_embed: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                             cache_offset: torch.Tensor, prefix_lens) -> torch.Tensor:
+        """forward_cached of nseq sequences at once: active_embed [nseq, rows, H], caches
+        [L, nseq, cap, nkv, hd], cache_offset int32 [nseq], prefix_lens nseq host ints."""
+        nseq, rows = self._check_batch_rows(active_embed)
+        cap = self._check_batch_cache(k_cache, v_cache, nseq)
+        off = self._batch_offsets(cache_offset, nseq)
+        out = torch.empty_like(active_embed)
+        _lib.check(self.lib.fdllm_forward_cached_batch(self.ctx, _ptr(active_embed), nseq, rows, _ptr(k_cache),
+                                                       _ptr(v_cache), cap, _ptr(off), self._prefix_lens(prefix_lens, nseq),
+                                                       _ptr(out), _stream()))
+        return out
+
+    def forward_block_partial_batch(self, replace_position: int, active_embed: torch.Tensor, k_cache: torch.Tensor,
+                                    v_cache: torch.Tensor, cache_offset: torch.Tensor, prefix_lens) -> torch.Tensor:
+        """forward_block_partial_rp{replace_position} of nseq sequences at once (shapes as forward_cached_batch)."""
+        nseq, rows = self._check_batch_rows(active_embed)
+        cap = self._check_batch_cache(k_cache, v_cache, nseq)
+        off = self._batch_offsets(cache_offset, nseq)
+        out = torch.empty_like(active_embed)
+        _lib.check(self.lib.fdllm_forward_block_partial_batch(
+            self.ctx, int(replace_position), _ptr(active_embed), nseq, rows, _ptr(k_cache), _ptr(v_cache), cap,
+            _ptr(off), self._prefix_lens(prefix_lens, nseq), _ptr(out), _stream()))
+        return out
+
+    def build_prefix_cache_seq(self, prefix_embed: torch.Tensor, prefix_bias: torch.Tensor | None,
+                               k_cache: torch.Tensor, v_cache: torch.Tensor, seq: int):
+        """build_prefix_cache of sequence `seq` into its slice of a batched cache [L, nseq, cap, nkv, hd]."""
+        p = self._check_rows(prefix_embed)
+        nseq = int(k_cache.shape[1]) if k_cache.dim() == 5 else -1
+        cap = self._check_batch_cache(k_cache, v_cache, nseq)
+        if prefix_bias is not None:
+            if tuple(prefix_bias.shape) != (1, 1, p, p) or prefix_bias.dtype != torch.float32:
+                raise ValueError(f"prefix_bias must be [1, 1, {p}, {p}] float32")
+            prefix_bias = prefix_bias.contiguous()
+        _lib.check(self.lib.fdllm_build_prefix_cache_seq(self.ctx, _ptr(prefix_embed), p, _ptr(prefix_bias),
+                                                         _ptr(k_cache), _ptr(v_cache), cap, nseq, int(seq), _stream()))
+        return k_cache, v_cache
+
     def get_confidence(self, hidden_states: torch.Tensor, logits: torch.Tensor | None = None):
         """(ids [1, rows] int32, maxp [1, rows] fp32), unshifted (metal.py:505-528)."""
         rows = self._check_rows(hidden_states)

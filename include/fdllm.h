@@ -109,6 +109,26 @@ int fdllm_forward_block_partial_rp24(fdllm_ctx* ctx, const void* active_embed, i
                                      void* v_cache, int cap, const int32_t* cache_offset, int64_t prefix_len,
                                      void* out, void* stream);
 
+/* Batched steps: no counterpart in the reference, whose entry points are batch 1
+ * (fast_dllm_relax/model/cuda.py:796-836); they serve callers that refine one block per sequence
+ * for many sequences at once.  nseq (<= 64) sequences share one cache tensor [L, nseq, cap, nkv, hd]
+ * (inplace_bsnh_v1, export_utils.py:21-34, with a batch dimension); active_embed is [nseq, rows, H]
+ * and out the same shape.  cache_offset is a device int32 [nseq] (row 0's RoPE position per
+ * sequence) and prefix_lens a host int64 [nseq].  Each sequence follows the batch-1 semantics
+ * exactly: fdllm_forward_cached_batch writes rows [P_b, P_b + rows) and attends [0, P_b + rows);
+ * fdllm_forward_block_partial_batch writes [P_b + rp, + bd_size/4) and attends [0, P_b + bd_size).
+ * Window errors name the sequence. */
+int fdllm_forward_cached_batch(fdllm_ctx* ctx, const void* active_embed, int nseq, int rows, void* k_cache,
+                               void* v_cache, int cap, const int32_t* cache_offset, const int64_t* prefix_lens,
+                               void* out, void* stream);
+int fdllm_forward_block_partial_batch(fdllm_ctx* ctx, int replace_position, const void* active_embed, int nseq,
+                                      int rows, void* k_cache, void* v_cache, int cap, const int32_t* cache_offset,
+                                      const int64_t* prefix_lens, void* out, void* stream);
+/* build_prefix_cache (cuda.py:610-637) of sequence `seq` into its slice of a batched cache
+ * [L, nseq, cap, nkv, hd]; the other sequences' rows are untouched. */
+int fdllm_build_prefix_cache_seq(fdllm_ctx* ctx, const void* prefix_embed, int prefix_len, const float* prefix_bias,
+                                 void* k_cache, void* v_cache, int cap, int nseq, int seq, void* stream);
+
 /* Fused lm_head + confidence: the device restatement of get_confidence_m{rows}
  * (fast_dllm_relax/model/metal.py:505-528, dispatch runtime.py:136-174).  ids [rows] int32 = first
  * argmax of each row's logits; maxp [rows] fp32 = 1 / sum exp(logit - max).  Unshifted; the caller

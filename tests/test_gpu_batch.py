@@ -1,0 +1,137 @@
+"""Batched cached steps (a build extension: the reference's entry points are batch 1, cuda.py:796-836).
+
+Each sequence of a batched call follows the batch-1 semantics exactly, so the oracle is the batch-1
+oracle run per sequence; calls go through the C ABI."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import TINY, WIDE2, bf16_parity, log, make_pair, to_np
+from oracle.model import build_prefix_block_attention_bias
+
+pytestmark = pytest.mark.gpu
+
+SENTINEL = 7.0
+
+
+def _dev_ids(ids):
+    return torch.tensor(np.asarray(ids), dtype=torch.int32, device="cuda")
+
+
+def _batched_case(ref, vm, kw, prefixes, seed, label):
+    rng = np.random.default_rng(seed)
+    L, nkv, hd = kw["num_hidden_layers"], kw["num_key_value_heads"], kw["head_dim"]
+    B, R = len(prefixes), 32
+    cap = max(prefixes) + 2 * R
+    ids = [rng.integers(0, kw["vocab_size"] - 1, P + R) for P in prefixes]
+
+    want_h, want_k, want_v = [], [], []
+    for b, P in enumerate(prefixes):
+        kc = np.zeros((L, 1, cap, nkv, hd), np.float32)
+        vc = kc.copy()
+        ref.build_prefix_cache(ref.embed(ids[b][:P])[None], build_prefix_block_attention_bias(0, P, block_size=32),
+                               kc, vc)
+        want_h.append(ref.forward_cached(ref.embed(ids[b][P:])[None], kc, vc, P, P)[0])
+        want_k.append(kc[:, 0])
+        want_v.append(vc[:, 0])
+
+    k = torch.full((L, B, cap, nkv, hd), SENTINEL, dtype=vm.torch_dtype, device="cuda")
+    v = torch.full_like(k, SENTINEL)
+    log(f"case: {label} build_prefix_cache_seq x {B} (prefixes {prefixes})")
+    for b, P in enumerate(prefixes):
+        vm.build_prefix_cache_seq(vm.embed(_dev_ids(ids[b][:P]))[None], None, k, v, b)
+    x = torch.stack([vm.embed(_dev_ids(ids[b][P:])) for b, P in enumerate(prefixes)])
+    off = torch.tensor(prefixes, dtype=torch.int32, device="cuda")
+    log(f"case: {label} forward_cached_batch nseq={B} rows={R}")
+    h = vm.forward_cached_batch(x, k, v, off, prefixes)
+    kn, vn = to_np(k), to_np(v)
+    for b, P in enumerate(prefixes):
+        bf16_parity(f"{label} seq {b} hidden", to_np(h[b]), want_h[b])
+        bf16_parity(f"{label} seq {b} K", kn[:, b, :P + R], want_k[b][:, :P + R])
+        bf16_parity(f"{label} seq {b} V", vn[:, b, :P + R], want_v[b][:, :P + R])
+        assert (kn[:, b, P + R:] == SENTINEL).all() and (vn[:, b, P + R:] == SENTINEL).all(), \
+            f"sequence {b}: rows past its window were written"
+
+    # the partial step reproduces the full step's rows for the same tokens (cuda.py:740-756)
+    rp = 8
+    xp = x[:, rp:rp + 8].contiguous()
+    offp = torch.tensor([P + rp for P in prefixes], dtype=torch.int32, device="cuda")
+    log(f"case: {label} forward_block_partial_batch rp={rp}")
+    hp = vm.forward_block_partial_batch(rp, xp, k, v, offp, prefixes)
+    # the two calls run their projections at different M (different k splits), so bf16 roundings
+    # can differ by an ulp: the bf16 criterion, not an element-wise bound
+    bf16_parity(f"{label} partial rows vs full-step rows", to_np(hp), to_np(h[:, rp:rp + 8]))
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    log("setup: tiny bf16 model seed 0")
+    return make_pair(TINY, 0)
+
+
+def test_batched_step_matches_oracle_per_sequence(tiny):
+    ref, vm = tiny
+    _batched_case(ref, vm, TINY, [32, 96, 64], 21, "tiny")
+
+
+def test_batched_window_errors(tiny):
+    _, vm = tiny
+    c = vm.cfg
+    k = torch.zeros((c.num_hidden_layers, 2, 96, c.num_key_value_heads, c.head_dim), dtype=vm.torch_dtype,
+                    device="cuda")
+    v = torch.zeros_like(k)
+    x = torch.zeros((2, 32, c.hidden_size), dtype=vm.torch_dtype, device="cuda")
+    off = torch.tensor([32, 80], dtype=torch.int32, device="cuda")
+    log("case: batched write past capacity names the sequence")
+    with pytest.raises(ValueError, match="sequence 1"):
+        vm.forward_cached_batch(x, k, v, off, [32, 80])
+    with pytest.raises(ValueError):
+        vm.forward_block_partial_batch(8, x, k, v, off, [32, 32])  # 32 rows where 8 are required
+    with pytest.raises(ValueError):
+        vm.forward_cached_batch(x, k, v, off, [32])  # one prefix length for two sequences
+
+
+def test_batched_loop_equals_batch1_loop(tiny):
+    """One sequence through the batched loop runs the batch-1 kernels, so its tokens equal the batch-1
+    loop's (relax_greedy_generate over the same block) exactly; several sequences unmask every row."""
+    from fast_dllm_relax_amd.runtime import relax_batched_block_refine, relax_greedy_generate
+
+    _, vm = tiny
+    rng = np.random.default_rng(5)
+    mask_id = TINY["vocab_size"] - 1
+    prompt = [int(t) for t in rng.integers(0, mask_id, 45)]
+    log("case: batched loop, one sequence vs relax_greedy_generate")
+    blocks, stats = relax_batched_block_refine(vm, [prompt], mask_id=mask_id)
+    n_new = 64 - len(prompt)
+    # the batch-1 loop counts masked rows as generated (runtime.py:841-843): ask for one more block so that
+    # the first block is refined to the end
+    cont, _ = relax_greedy_generate(vm, prompt, max_new_tokens=n_new + 32, mask_id=mask_id, stop_token=None)
+    got = [int(t) for t in blocks[0]]
+    assert got[:len(prompt) - 32] == prompt[32:]
+    want = [int(t) for t in cont]
+    assert got[len(prompt) - 32:] == want[:n_new], (got, want)
+    log("case: batched loop, three sequences")
+    prompts = [[int(t) for t in rng.integers(0, mask_id, n)] for n in (33, 64, 90)]
+    blocks, stats = relax_batched_block_refine(vm, prompts, mask_id=mask_id)
+    assert stats["steps"] >= 4
+    for p, blk in zip(prompts, blocks):
+        a0 = len(p) - len(p) % 32 if len(p) % 32 else len(p)
+        assert mask_id not in blk
+        assert blk[:len(p) - a0] == p[a0:]
+
+
+@pytest.fixture(scope="module")
+def wide2():
+    log("setup: 1.5B-shape 2-layer bf16 model seed 1")
+    return make_pair(WIDE2, 1)
+
+
+def test_wide_batched_step_16_sequences(wide2):
+    """16 sequences x 32 rows: the projections run at M = 512 (the MFMA block kernel, with k splits)."""
+    ref, vm = wide2
+    rng = np.random.default_rng(3)
+    prefixes = [int(p) for p in 32 * rng.integers(1, 5, 16)]
+    _batched_case(ref, vm, WIDE2, prefixes, 31, "wide")
