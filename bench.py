@@ -16,7 +16,11 @@ Beside it the JSON line carries:
                   HIP events over launches that walk the 28 layers;
   cpu_baseline    the CPU oracle's 32-row refinement step (numpy fp32 with the bf16 rounding points) at
                   the same prefix on the host's cores, scaled to tokens/s with the GPU loop's tokens per
-                  model call.
+                  model call;
+  batched         BASELINE config 4: the 1.5B architecture in fp16, seed 3, 16 sequences with prefix
+                  lengths drawn from U[128, 1024], one 32-token masked block each refined in sub-blocks
+                  of 8 (threshold 0.9) by batched steps over all 16 sequences (the projections at M = 512);
+                  aggregate tokens/s, the batched step times and their MFMA rate against the fp16 peak.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 """
@@ -71,6 +75,7 @@ def main() -> int:
     ap.add_argument("--new-tokens", type=int, default=NEW_TOKENS)
     ap.add_argument("--prefix", type=int, default=PREFIX)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-batched", action="store_true")
     ap.add_argument("--cpu-iters", type=int, default=2)
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the dominant kernel over the 28 layers and a plain 256 MiB copy (for rocprofv3 --pmc)")
@@ -171,6 +176,15 @@ def main() -> int:
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(vm, params, cache, block, P, args.cpu_iters, tokens_per_call)
 
+    # ---- config 4: batched steps -------------------------------------------------------------------
+    batched = None
+    if not args.no_batched:
+        del cache
+        vm.close()
+        del vm, params
+        torch.cuda.empty_cache()
+        batched = batched_bench(args)
+
     line = {
         "metric": "decode tokens/s (1.5B bf16, bs1); block-step ms + achieved HBM GB/s",
         "value": round(value, 2),
@@ -204,9 +218,107 @@ def main() -> int:
                      "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "avg_launch_us": round(gu_ms * 1e3, 2), "bytes_per_launch": gu_bytes},
         "cpu_baseline": cpu,
+        "batched": batched,
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16 / bf16
+BATCH_SEED = 3
+BATCH_SEQS = 16
+
+
+def batched_bench(args) -> dict:
+    """Config 4: 16 sequences of the 1.5B architecture in fp16 refined together.
+
+    Synthetic weights N(0, 0.02) from seed 3 with an untied lm_head N(0, 0.5) (as in config 3: with the
+    tied N(0, 0.02) head a masked row's strongest logit is its own mask token, and the loop would
+    never unmask it).  Prefix lengths are drawn from U[128, 1024] with seed 3; each sequence's prompt
+    is that many random ids, and its 32-token block starts at the prefix rounded down to 32 (the block
+    holds the prompt's tail and masks, runtime.py:719-739 per sequence)."""
+    import numpy as np
+    import torch
+
+    from fast_dllm_relax_amd.config import DEFAULT_MASK_ID, fast_dllm_v2_1p5b
+    from fast_dllm_relax_amd.params import random_params_torch
+    from fast_dllm_relax_amd.runtime import _embed, batched_shifted_confidence, relax_batched_block_refine
+    from fast_dllm_relax_amd.vm import HipVM
+
+    cfg = fast_dllm_v2_1p5b(tie_word_embeddings=False)
+    log("batched: generating fp16 weights (seed 3)")
+    params = random_params_torch(cfg, BATCH_SEED, dtype="float16", device="cuda", std=0.02, lm_head_std=0.5)
+    vm = HipVM(cfg, params, dtype="float16", max_rows=1024)
+    rng = np.random.default_rng(BATCH_SEED)
+    prefixes = [int(p) for p in rng.integers(128, 1025, BATCH_SEQS)]
+    prompts = [rng.integers(0, 150000, p).tolist() for p in prefixes]
+
+    def run():
+        timing: dict = {}
+        blocks, stats = relax_batched_block_refine(vm, prompts, mask_id=DEFAULT_MASK_ID, block_size=32,
+                                                   small_block_size=8, threshold=0.9, timing=timing)
+        return stats, timing
+
+    for i in range(args.warmup):
+        log(f"batched: warmup {i + 1}/{args.warmup}")
+        run()
+    unmasked, refine_s, prefill_s, steps, partial_steps = 0, 0.0, 0.0, 0, 0
+    for i in range(args.steps):
+        stats, timing = run()
+        unmasked += stats["unmasked"]
+        refine_s += timing["refine_s"]
+        prefill_s += timing["prefill_s"]
+        steps += stats["steps"]
+        partial_steps += stats["partial_steps"]
+        log(f"batched: run {i + 1}/{args.steps}: {stats['unmasked']} tokens in {stats['steps']} steps "
+            f"({stats['partial_steps']} partial), refine {timing['refine_s'] * 1e3:.1f} ms, "
+            f"prefill {timing['prefill_s'] * 1e3:.1f} ms")
+
+    # synced batched steps over a freshly built batched cache
+    a0s = [p - p % 32 for p in prefixes]  # the block start of relax_batched_block_refine
+    cap = max(a0s) + 32
+    shape = (cfg.num_hidden_layers, BATCH_SEQS, cap, cfg.num_key_value_heads, cfg.head_dim)
+    k = torch.zeros(shape, dtype=torch.float16, device="cuda")
+    v = torch.zeros_like(k)
+    for b in range(BATCH_SEQS):
+        vm.build_prefix_cache_seq(_embed(vm, prompts[b][:a0s[b]]), None, k, v, b)
+    ids = rng.integers(0, 150000, BATCH_SEQS * 32).tolist()
+    emb = _embed(vm, ids).view(BATCH_SEQS, 32, -1)
+    emb8 = emb[:, 8:16].contiguous()
+    off = torch.tensor(a0s, dtype=torch.int32, device="cuda")
+    off8 = off + 8
+    full_ms = event_ms(lambda: batched_shifted_confidence(vm, vm.forward_cached_batch(emb, k, v, off, a0s)), 10)
+    part_ms = event_ms(lambda: batched_shifted_confidence(
+        vm, vm.forward_block_partial_batch(8, emb8, k, v, off8, a0s)), 10)
+
+    H, I, V, L = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.num_hidden_layers
+    qkv = (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim
+    gemm_params = L * (qkv * H + H * cfg.num_attention_heads * cfg.head_dim + 2 * I * H + H * I) + V * H
+
+    def flops(rows, attend):
+        att = sum(L * 4 * cfg.num_attention_heads * rows * (a0 + attend) * cfg.head_dim for a0 in a0s)
+        return 2.0 * BATCH_SEQS * rows * gemm_params + att
+
+    f_full, f_part = flops(32, 32), flops(8, 32)
+    tf_full = f_full / (full_ms * 1e-3) / 1e12
+    tf_part = f_part / (part_ms * 1e-3) / 1e12
+    res = {
+        "workload": f"BASELINE config 4: 1.5B fp16, seed 3, {BATCH_SEQS} sequences, prefixes U[128, 1024], one "
+                    f"32-token masked block each, sub-blocks of 8, threshold 0.9, untied lm_head N(0, 0.5)",
+        "prefixes": prefixes,
+        "tokens_per_s": round(unmasked / refine_s, 2), "tokens": unmasked, "refine_s": round(refine_s, 4),
+        "steps": steps, "partial_steps": partial_steps,
+        "prefill_ms_mean": round(prefill_s / args.steps * 1e3, 2),
+        "step_full_ms": round(full_ms, 4), "step_full_rows": BATCH_SEQS * 32,
+        "step_full_tflops": round(tf_full, 1), "step_full_mfma_frac": round(tf_full / MFMA_F16_PEAK_TFLOPS, 4),
+        "step_partial_ms": round(part_ms, 4), "step_partial_rows": BATCH_SEQS * 8,
+        "step_partial_tflops": round(tf_part, 1),
+        "mfma_peak_tflops": MFMA_F16_PEAK_TFLOPS,
+    }
+    log(f"batched: {res['tokens_per_s']} tokens/s, full step {full_ms:.3f} ms = {tf_full:.1f} TFLOP/s, "
+        f"partial {part_ms:.3f} ms")
+    vm.close()
+    return res
 
 
 def traffic_probe(vm, cfg) -> int:

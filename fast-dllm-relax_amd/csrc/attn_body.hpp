@@ -544,31 +544,34 @@ __device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, 
   }
 }
 
-// Batched call: the view of sequence b (its rows, cache, window and split partials).
-__device__ __forceinline__ void seq_view(AttnP& a, int b) {
-  const int QT = ((a.nq / a.nkv) * a.rows + 15) / 16;
-  a.qkv += (size_t)b * a.rows * a.ldq;
-  a.rope += (size_t)b * a.rows * 128;
-  a.out += (size_t)b * a.rows * a.nq * HD;
-  a.kc += b * a.seq_stride;
-  a.vc += b * a.seq_stride;
-  a.ws = a.seq_ws[b];
-  a.Lk = a.seq_lk[b];
-  a.part += (size_t)b * a.nkv * QT * a.S * PSZ;
+// Batched call: the view of sequence b (its rows, cache, window and split partials) in a, a copy of the
+// kernel argument p.  The per-sequence tables are read from p itself: indexing them in the copy would
+// keep the whole copy in scratch memory.
+__device__ __forceinline__ void seq_view(AttnP& a, const AttnP& p, int b) {
+  const int QT = ((p.nq / p.nkv) * p.rows + 15) / 16;
+  a.qkv = p.qkv + (size_t)b * p.rows * p.ldq;
+  a.rope = p.rope + (size_t)b * p.rows * 128;
+  a.out = p.out + (size_t)b * p.rows * p.nq * HD;
+  a.kc = p.kc + b * p.seq_stride;
+  a.vc = p.vc + b * p.seq_stride;
+  a.ws = p.seq_ws[b];
+  a.Lk = p.seq_lk[b];
+  a.part = p.part + (size_t)b * p.nkv * QT * p.S * PSZ;
 }
 
 // gridDim.x = query-tile groups x sequences (sequence-major)
 template <int DT, int QPW, int KH, int CH>
-__global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP a) {
+__global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP p) {
   extern __shared__ __align__(16) unsigned char smem[];
-  int bx = blockIdx.x;
-  if (a.nseq > 1) {
-    const int qg = (int)gridDim.x / a.nseq, b = bx / qg;
-    bx -= b * qg;
-    seq_view(a, b);
-    if ((int)blockIdx.z * a.chunk >= a.Lk) return;  // past this sequence's keys: the merge skips it
+  if (p.nseq <= 1) {
+    attn_chunk_body<DT, QPW, KH, CH, false>(p, blockIdx.x, blockIdx.y, blockIdx.z, smem);
+    return;
   }
-  attn_chunk_body<DT, QPW, KH, CH, false>(a, bx, blockIdx.y, blockIdx.z, smem);
+  const int qg = (int)gridDim.x / p.nseq, b = (int)blockIdx.x / qg;
+  AttnP a = p;
+  seq_view(a, p, b);
+  if ((int)blockIdx.z * a.chunk >= a.Lk) return;  // past this sequence's keys: the merge skips it
+  attn_chunk_body<DT, QPW, KH, CH, false>(a, (int)blockIdx.x - b * qg, blockIdx.y, blockIdx.z, smem);
 }
 
 // Merge of the key splits: one wave per (kv head g, query tile qt, 16-dim slice dt).  The split weights
@@ -622,14 +625,15 @@ __device__ __forceinline__ void attn_merge_wave(const AttnP& a, int dt, int qt, 
 
 // gridDim.z = kv heads x sequences (sequence-major)
 template <int DT>
-__global__ __launch_bounds__(64) void attn_merge_kernel(AttnP a) {
-  int g = blockIdx.z;
-  if (a.nseq > 1) {
-    const int b = g / a.nkv;
-    g -= b * a.nkv;
-    seq_view(a, b);
+__global__ __launch_bounds__(64) void attn_merge_kernel(AttnP p) {
+  if (p.nseq <= 1) {
+    attn_merge_wave<DT, false>(p, blockIdx.x, blockIdx.y, blockIdx.z, threadIdx.x);
+    return;
   }
-  attn_merge_wave<DT, false>(a, blockIdx.x, blockIdx.y, g, threadIdx.x);
+  const int b = (int)blockIdx.z / p.nkv;
+  AttnP a = p;
+  seq_view(a, p, b);
+  attn_merge_wave<DT, false>(a, blockIdx.x, blockIdx.y, (int)blockIdx.z - b * p.nkv, threadIdx.x);
 }
 
 }  // namespace fdllm

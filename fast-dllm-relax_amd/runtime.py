@@ -491,6 +491,10 @@ def relax_batched_block_refine(vm: HipVM, prompts, *, mask_id: int, block_size: 
                 for r in rows:
                     xs[b][a0s[b] + s0 + r] = int(bids[r])
                     unmasked += 1
+            if steps > 4 * block_size:
+                # every step unmasks at least one row per unfinished sequence unless the model predicts
+                # the mask token itself
+                raise RuntimeError(f"no progress after {steps} steps: the model keeps predicting mask id {mask_id}")
     if timing is not None:
         torch.cuda.synchronize()
         timing["refine_s"] = time.perf_counter() - t1

@@ -41,3 +41,23 @@ def test_config_struct_layout_matches_header():
     # 13 four-byte fields, in header order
     assert ctypes.sizeof(lib.FdllmConfig) == 13 * 4
     assert [f[0] for f in lib.FdllmConfig._fields_][-2:] == ["dtype", "max_rows"]
+
+
+def test_no_kernel_uses_scratch_memory():
+    """The build keeps the compiler's per-kernel resource report beside the library: no kernel may spill
+    to scratch (a private copy of a kernel-argument struct, or spilled registers, costs every wave
+    global-memory round trips on the decode step's critical path)."""
+    import pytest
+
+    report = lib.LIB_PATH.parent / "kernel_resources.txt"
+    if not report.exists():
+        pytest.skip("no resource report (library built without the Makefile)")
+    kernels, current = {}, None
+    for line in report.read_text().splitlines():
+        line = line.strip()
+        if line.startswith("Function Name:"):
+            current = line.split(":", 1)[1].strip()
+        elif line.startswith("ScratchSize") and current is not None:
+            kernels[current] = int(line.rsplit(":", 1)[1])
+    assert kernels, "empty resource report"
+    assert {k: v for k, v in kernels.items() if v} == {}
