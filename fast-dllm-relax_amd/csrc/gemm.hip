@@ -174,6 +174,7 @@ static MmInfo mm_info(int id) {
 }
 static int mm_choice(int cfg, int M) {
   switch (cfg) {
+    case CFG_LM_HEAD: return MM_WIDE;  // one 256-column confidence tile per block column
     case CFG_GATE_UP: return M >= 1024 ? MM_BIG : MM_WIDE;
     case CFG_DOWN: return M >= 1024 ? MM_WIDE_D : MM_SMALL;
     default: return MM_SMALL;
@@ -183,7 +184,7 @@ static int mm_choice(int cfg, int M) {
 GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split) {
   GemmPlan p{};
   p.mchunks = (a.M + 31) / 32;
-  if (cfg != CFG_LM_HEAD && a.M > 32) {
+  if (a.M > 32) {
     const int id = mm_choice(cfg, a.M);
     const MmInfo mi = mm_info(id);
     if (a.KS % mi.kss == 0) {
@@ -196,7 +197,7 @@ GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split) {
       // most 8 splits of at least 4 stages), else the largest such divisor
       const int wgs = p.nbm * p.nbn;
       int split = 1;
-      for (int d = 2; d <= 8 && wgs * split < 256; ++d)
+      for (int d = 2; d <= 8 && wgs * split < 256 && cfg != CFG_LM_HEAD; ++d)
         if (nst % d == 0 && nst / d >= 4) split = d;
       p.ksplit = split;
       a.kps = a.KS / split;
@@ -264,7 +265,8 @@ template <int DT, int EPI, int XF, class M>
 static hipError_t launch_mm_cfg(const GemmP& a, const GemmPlan& p, hipStream_t st) {
   auto kern = gemm_mm_kernel<DT, EPI, XF, M::mf, M::tpw, M::nw, M::kss, M::wd>;
   const int total = p.nbm * p.nbn, per = (total + 7) / 8;
-  hipLaunchKernelGGL(kern, dim3(8 * per, p.ksplit), dim3(64 * M::nw), M::lds, st, a, p.nbm, p.nbn);
+  const size_t lds = EPI == EPI_LOGITS ? std::max(M::lds, M::lds_logits) : M::lds;
+  hipLaunchKernelGGL(kern, dim3(8 * per, p.ksplit), dim3(64 * M::nw), lds, st, a, p.nbm, p.nbn);
   if (p.ksplit > 1) {
     const int nblk = (a.M + 15) / 16;
     hipLaunchKernelGGL((gemm_mm_split_epilogue_kernel<DT, EPI>), dim3((a.N + 15) / 16, (nblk + 3) / 4), dim3(256), 0,
@@ -284,7 +286,7 @@ static hipError_t launch_mm(const GemmP& a, const GemmPlan& p, hipStream_t st) {
   } else if constexpr (CFG == CFG_QKV || CFG == CFG_OPROJ) {
     return launch_mm_cfg<DT, C::epi, C::xf, MmSmall>(a, p, st);
   } else {
-    return hipErrorInvalidValue;
+    return launch_mm_cfg<DT, C::epi, C::xf, MmWide>(a, p, st);  // the lm_head
   }
 }
 

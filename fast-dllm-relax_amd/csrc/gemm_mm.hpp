@@ -32,7 +32,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_mm_kernel(GemmP a, int nbm, int 
   static_assert(KSS * MF % NW == 0, "whole fragment blocks per wave");
   static_assert(NT % BM == 0 && BM <= NT, "threads per row for the norm prologue");
   static_assert(EPI != EPI_SILU_PAIR || TPW % 2 == 0, "gate/up pairs stay within a wave");
-  static_assert(EPI != EPI_LOGITS, "logits use the streaming kernel");
+  static_assert(EPI != EPI_LOGITS || TPW * NW == 16, "one 256-column confidence tile per block column");
   extern __shared__ __align__(16) unsigned char smem[];
   u32x4* xl = reinterpret_cast<u32x4*>(smem);  // [2][KSS][MF][64]
   __shared__ float inv_s[BM];
@@ -151,7 +151,73 @@ __global__ __launch_bounds__(64 * NW) void gemm_mm_kernel(GemmP a, int nbm, int 
   }
 
   // epilogue: one (tile or gate/up pair, 16-row block) unit at a time
-  if constexpr (EPI == EPI_SILU_PAIR) {
+  if constexpr (EPI == EPI_LOGITS) {
+    // the block's logits, rounded to the model dtype as get_logits does (cuda.py:708-711), go to LDS
+    // ([BM][256] model-dtype values; exact) and to the optional fp32 output; then one wave per row
+    // reduces the row's 256 columns to the confidence statistics with the same lane order and
+    // butterflies as the streaming kernel, so both give identical bits
+    u16* tile = reinterpret_cast<u16*>(smem);
+    const int n0 = nb * 256;
+#pragma unroll
+    for (int j = 0; j < TPW; ++j)
+#pragma unroll
+      for (int f = 0; f < MF; ++f) {
+        const int ml = 16 * f + lr, nl = 16 * (w * TPW + j) + 4 * lg, n = n0 + nl, m = m0 + ml;
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = rnd<DT>(acc[j][f][i]);
+        *reinterpret_cast<u32x2*>(tile + ml * 256 + nl) =
+            u32x2{pack2(from_f32<DT>(v[0]), from_f32<DT>(v[1])), pack2(from_f32<DT>(v[2]), from_f32<DT>(v[3]))};
+        if (a.logits != nullptr && m < a.M) {
+          float* dst = a.logits + (size_t)m * a.ldl + n;
+          if (n + 3 < a.N) {
+            *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (n + i < a.N) dst[i] = v[i];
+          }
+        }
+      }
+    if (a.stat_m == nullptr) return;
+    __syncthreads();
+    for (int ml = w; ml < BM; ml += NW) {
+      if (m0 + ml >= a.M) break;
+      const u16* row = tile + ml * 256;
+      float vmax = -INFINITY;
+      int amax = 0x7fffffff;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = lane + 64 * i;
+        if (n0 + c < a.N) {
+          const float x = to_f32<DT>(row[c]);
+          if (x > vmax) { vmax = x; amax = n0 + c; }
+        }
+      }
+      for (int k = 32; k >= 1; k >>= 1) {
+        const float ov = __shfl_xor(vmax, k, WAVE);
+        const int oa = __shfl_xor(amax, k, WAVE);
+        if (ov > vmax || (ov == vmax && oa < amax)) { vmax = ov; amax = oa; }
+      }
+      float sum;
+      {
+#pragma clang fp contract(off)
+        sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int c = lane + 64 * i;
+          if (n0 + c < a.N) sum = sum + fd_exp_neg(to_f32<DT>(row[c]) - vmax);
+        }
+        for (int k = 32; k >= 1; k >>= 1) sum = sum + __shfl_xor(sum, k, WAVE);
+      }
+      if (lane == 0) {
+        const size_t o = (size_t)(m0 + ml) * a.stat_tiles + nb;
+        a.stat_m[o] = vmax;
+        a.stat_a[o] = amax;
+        a.stat_s[o] = sum;
+      }
+    }
+  } else if constexpr (EPI == EPI_SILU_PAIR) {
 #pragma unroll
     for (int p = 0; p < TPW / 2; ++p)
 #pragma unroll
@@ -197,6 +263,7 @@ struct MmCfg {
   static constexpr int mf = MF, tpw = TPW, nw = NW, kss = KSS, wd = WD;
   static constexpr int bm = 16 * MF, bn_tiles = TPW * NW;
   static constexpr size_t lds = 2ull * KSS * MF * 64 * 16;
+  static constexpr size_t lds_logits = (size_t)16 * MF * 256 * 2;  // EPI_LOGITS tile [BM][256] u16
 };
 
 }  // namespace fdllm

@@ -64,6 +64,7 @@ def _batched_case(ref, vm, kw, prefixes, seed, label):
     # the two calls run their projections at different M (different k splits), so bf16 roundings
     # can differ by an ulp: the bf16 criterion, not an element-wise bound
     bf16_parity(f"{label} partial rows vs full-step rows", to_np(hp), to_np(h[:, rp:rp + 8]))
+    return h
 
 
 @pytest.fixture(scope="module")
@@ -134,4 +135,14 @@ def test_wide_batched_step_16_sequences(wide2):
     ref, vm = wide2
     rng = np.random.default_rng(3)
     prefixes = [int(p) for p in 32 * rng.integers(1, 5, 16)]
-    _batched_case(ref, vm, WIDE2, prefixes, 31, "wide")
+    h = _batched_case(ref, vm, WIDE2, prefixes, 31, "wide")
+    # the confidence of all 512 rows (the lm_head at M = 512) is bit-exact given its own logits
+    from oracle import confidence as oconf
+
+    rows = h.shape[0] * h.shape[1]
+    logits = torch.empty((1, rows, WIDE2["vocab_size"]), dtype=torch.float32, device="cuda")
+    log("case: wide fused lm_head + confidence, 512 rows")
+    ids, maxp = vm.get_confidence(h.view(1, rows, -1), logits=logits)
+    wid, wp = oconf.confidence(to_np(logits)[0])
+    np.testing.assert_array_equal(ids.cpu().numpy()[0], wid)
+    np.testing.assert_array_equal(maxp.cpu().numpy()[0].view(np.uint32), wp.view(np.uint32))

@@ -139,7 +139,7 @@ def test_confidence_bit_exact_given_logits(tiny):
 def test_fused_confidence_equals_confidence_of_get_logits(tiny):
     ref, vm = tiny
     rng = np.random.default_rng(6)
-    for rows in (32, 8):
+    for rows in (32, 8, 96, 130):  # 96 and 130 rows take the MFMA block kernel's logits epilogue
         log(f"case: fused lm_head+confidence rows={rows}")
         h = torch.from_numpy(ref.rnd(rng.standard_normal((1, rows, TINY["hidden_size"])).astype(np.float32)))
         h = h.to("cuda", torch.bfloat16)
