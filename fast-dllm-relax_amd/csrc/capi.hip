@@ -70,6 +70,7 @@ struct fdllm_ctx {
   void* ws = nullptr;
   uint16_t *h = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr;
   uint16_t *kscr = nullptr, *vscr = nullptr;  // K/V of a stateless forward (one layer at a time)
+  uint16_t* xn = nullptr;                     // RMS-normalised rows for the large-M projections
   float* ssq = nullptr;                       // [hidden / 16][ws_rows] row sums of squares per 16 columns
   // split partials / confidence statistics (grown on demand)
   float* gpart = nullptr; size_t gpart_floats = 0;
@@ -80,6 +81,8 @@ struct fdllm_ctx {
   float* rope = nullptr; size_t rope_floats = 0;  // RoPE (cos, sin) table of the current call's rows
   int attn_target = 64;   // attention workgroups aimed for when splitting the keys
   int down_split = 10;    // cross-workgroup k splits of the down projection (largest divisor of K/32 <= this)
+  int mm_target_wgs = 256;  // large-M GEMM: split k while the launch has fewer workgroups than this
+  int mm_min_stages = 8;    // ... into splits of at least this many stages
 
   int qkv_dim() const { return (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim; }
   int q_dim() const { return cfg.num_attention_heads * cfg.head_dim; }
@@ -97,7 +100,7 @@ int ensure_rows(fdllm_ctx* c, int rows) {
   size_t e_h = (size_t)R * f.hidden_size, e_qkv = (size_t)R * c->qkv_dim(), e_q = (size_t)R * c->q_dim();
   size_t e_act = (size_t)R * f.intermediate_size, e_kv = (size_t)R * c->kv_dim();
   size_t e_ssq = (size_t)c->ssq_tiles() * R * 2;  // floats as u16 pairs
-  size_t bytes = 2 * (align_up(e_h, 64) + align_up(e_qkv, 64) + align_up(e_q, 64) + align_up(e_act, 64) +
+  size_t bytes = 2 * (align_up(e_h, 64) * 2 + align_up(e_qkv, 64) + align_up(e_q, 64) + align_up(e_act, 64) +
                       align_up(e_kv, 64) * 2 + align_up(e_ssq, 64));
   if (c->ws) {
     HIPCHK(hipDeviceSynchronize());
@@ -108,7 +111,7 @@ int ensure_rows(fdllm_ctx* c, int rows) {
   uint16_t* p = (uint16_t*)c->ws;
   auto take = [&](size_t n) { uint16_t* r = p; p += align_up(n, 64); return r; };
   c->h = take(e_h); c->qkv = take(e_qkv); c->attn = take(e_q); c->act = take(e_act);
-  c->kscr = take(e_kv); c->vscr = take(e_kv); c->ssq = (float*)take(e_ssq);
+  c->kscr = take(e_kv); c->vscr = take(e_kv); c->ssq = (float*)take(e_ssq); c->xn = take(e_h);
   c->ws_rows = R;
   return FDLLM_OK;
 }
@@ -157,7 +160,14 @@ int divisor_at_most(int n, int cap) {
 int run_gemm(fdllm_ctx* c, int cfg, GemmP a, int ksplit, hipStream_t st) {
   const fdllm_config& f = c->cfg;
   if (ksplit < 1 || a.KS % ksplit) return fail(FDLLM_EINVAL, "k split %d does not divide %d k steps", ksplit, a.KS);
-  const GemmPlan pl = gemm_plan(cfg, a, ksplit);
+  const GemmPlan pl = gemm_plan(cfg, a, ksplit, c->mm_target_wgs, c->mm_min_stages);
+  if (pl.kind == GK_MM && a.nw != nullptr) {
+    // RMSNorm once for all column blocks (the large-M kernel takes normalised rows)
+    if (a.ldx != a.H || a.KS * 32 != a.H) return fail(FDLLM_EINVAL, "normalised projection input must be [rows, hidden]");
+    HIPCHK(launch_norm_rows(f.dtype, a.X, a.M, a.H, a.ssq, a.ssq_ld, a.nw, a.eps, c->xn, st));
+    a.X = c->xn;
+    a.nw = nullptr;
+  }
   if (pl.ksplit > 1) {
     int rc = ensure_floats(&c->gpart, &c->gpart_floats, pl.part_floats);
     if (rc) return rc;
@@ -399,6 +409,8 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   (void)hipGetDevice(&c->dev);
   if (const char* e = std::getenv("FDLLM_ATTN_TARGET")) c->attn_target = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_DOWN_SPLIT")) c->down_split = std::max(1, atoi(e));
+  if (const char* e = std::getenv("FDLLM_MM_TARGET_WGS")) c->mm_target_wgs = std::max(1, atoi(e));
+  if (const char* e = std::getenv("FDLLM_MM_MIN_STAGES")) c->mm_min_stages = std::max(1, atoi(e));
   c->names.push_back("model.embed_tokens.weight");
   for (int i = 0; i < f.num_hidden_layers; ++i) {
     std::string p = "model.layers." + std::to_string(i);

@@ -181,7 +181,7 @@ static int mm_choice(int cfg, int M) {
   }
 }
 
-GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split) {
+GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, int mm_target_wgs, int mm_min_stages) {
   GemmPlan p{};
   p.mchunks = (a.M + 31) / 32;
   if (a.M > 32) {
@@ -193,12 +193,12 @@ GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split) {
       p.mm_id = id;
       p.nbm = (a.M + mi.bm - 1) / mi.bm;
       p.nbn = (a.ntiles + mi.bn_tiles - 1) / mi.bn_tiles;
-      // k split: the smallest divisor of the stage count that brings the launch to 256 workgroups (at
-      // most 8 splits of at least 4 stages), else the largest such divisor
+      // k split: the smallest divisor of the stage count that brings the launch to mm_target_wgs
+      // workgroups (at most 8 splits of at least mm_min_stages stages), else the largest such divisor
       const int wgs = p.nbm * p.nbn;
       int split = 1;
-      for (int d = 2; d <= 8 && wgs * split < 256 && cfg != CFG_LM_HEAD; ++d)
-        if (nst % d == 0 && nst / d >= 4) split = d;
+      for (int d = 2; d <= 8 && wgs * split < mm_target_wgs && cfg != CFG_LM_HEAD; ++d)
+        if (nst % d == 0 && nst / d >= mm_min_stages) split = d;
       p.ksplit = split;
       a.kps = a.KS / split;
       p.part_floats = split > 1 ? (size_t)split * a.ntiles * ((a.M + 15) / 16) * 256 : 0;
@@ -275,18 +275,19 @@ static hipError_t launch_mm_cfg(const GemmP& a, const GemmPlan& p, hipStream_t s
   return hipGetLastError();
 }
 
+// GK_MM rows arrive normalised (see GemmKind), so every large-M launch runs without the norm transform.
 template <int DT, int CFG, class C>
 static hipError_t launch_mm(const GemmP& a, const GemmPlan& p, hipStream_t st) {
   if constexpr (CFG == CFG_GATE_UP) {
-    if (p.mm_id == MM_BIG) return launch_mm_cfg<DT, C::epi, C::xf, MmBig>(a, p, st);
-    return launch_mm_cfg<DT, C::epi, C::xf, MmWide>(a, p, st);
+    if (p.mm_id == MM_BIG) return launch_mm_cfg<DT, C::epi, XF_NONE, MmBig>(a, p, st);
+    return launch_mm_cfg<DT, C::epi, XF_NONE, MmWide>(a, p, st);
   } else if constexpr (CFG == CFG_DOWN) {
-    if (p.mm_id == MM_WIDE_D) return launch_mm_cfg<DT, C::epi, C::xf, MmWideD>(a, p, st);
-    return launch_mm_cfg<DT, C::epi, C::xf, MmSmall>(a, p, st);
+    if (p.mm_id == MM_WIDE_D) return launch_mm_cfg<DT, C::epi, XF_NONE, MmWideD>(a, p, st);
+    return launch_mm_cfg<DT, C::epi, XF_NONE, MmSmall>(a, p, st);
   } else if constexpr (CFG == CFG_QKV || CFG == CFG_OPROJ) {
-    return launch_mm_cfg<DT, C::epi, C::xf, MmSmall>(a, p, st);
+    return launch_mm_cfg<DT, C::epi, XF_NONE, MmSmall>(a, p, st);
   } else {
-    return launch_mm_cfg<DT, C::epi, C::xf, MmWide>(a, p, st);  // the lm_head
+    return launch_mm_cfg<DT, C::epi, XF_NONE, MmWide>(a, p, st);  // the lm_head
   }
 }
 

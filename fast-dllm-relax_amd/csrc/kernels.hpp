@@ -46,12 +46,17 @@ GemmShape gemm_shape(int cfg);
 // their own k split; GK_STREAM (the lm_head, or shapes the others do not take) runs stream_split.
 // Streaming and one-shot launches have groups x ksplit x mchunks workgroups; the large-M kernel
 // covers nbm x nbn blocks of config mm_id.  part_floats: split partials.  Sets a.kps.
+// GK_MM takes its activations already normalised (the caller runs norm_rows once instead of every
+// column block normalising its rows again): a launch with XF_RMS in its configuration must not pass
+// GK_MM rows that still need the norm.
 enum GemmKind : int { GK_STREAM = 0, GK_ONESHOT = 1, GK_MM = 2 };
 struct GemmPlan {
   int kind; int ksplit; int tiles_per_wg; int groups; int mchunks; size_t part_floats;
   int mm_id; int nbm; int nbn;
 };
-GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split);
+// mm_target_wgs / mm_min_stages: the large-M kernel splits k only while the launch has fewer than
+// mm_target_wgs workgroups, and only into splits of at least mm_min_stages stages.
+GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, int mm_target_wgs = 256, int mm_min_stages = 8);
 hipError_t launch_gemm(int dt, int cfg, const GemmP& a, const GemmPlan& p, hipStream_t st);
 
 // ---- confidence ---------------------------------------------------------------------------------
