@@ -69,14 +69,14 @@ static hipError_t launch_loop(const AttnP& a, const AttnPlan& p, hipStream_t st)
   return hipGetLastError();
 }
 
-template <int DT, int CH, int KH>
+template <int DT, int CH, int KH, int MASK>
 static hipError_t launch_chunk_kh(const AttnP& a, const AttnPlan& p, hipStream_t st) {
   constexpr int QPW = 4;
   const size_t loop_lds = (size_t)CH * KLD * 2 + (size_t)HD * (CH + 8) * 2;
   const size_t merge_lds = (size_t)2 * KH * QPW * 16 * 4 + (size_t)(KH - 1) * QPW * (HD / 16) * 64 * 16;
   const size_t lds = std::max(loop_lds, merge_lds);
   if (lds > 160 * 1024) return hipErrorInvalidValue;
-  auto kern = attn_chunk_kernel<DT, QPW, KH, CH>;
+  auto kern = attn_chunk_kernel<DT, QPW, KH, CH, MASK>;
   raise_lds(kern, lds);
   const int nseq = std::max(a.nseq, 1);
   hipLaunchKernelGGL(kern, dim3(p.qg * nseq, a.nkv, a.S), dim3(64 * QPW * KH), lds, st, a);
@@ -87,14 +87,23 @@ static hipError_t launch_chunk_kh(const AttnP& a, const AttnPlan& p, hipStream_t
   return hipGetLastError();
 }
 
+template <int DT, int CH>
+static hipError_t launch_chunk_mask(const AttnP& a, const AttnPlan& p, hipStream_t st) {
+  switch (a.mask) {
+    case 0: return launch_chunk_kh<DT, CH, ATTN_KH, 0>(a, p, st);
+    case 1: return launch_chunk_kh<DT, CH, ATTN_KH, 1>(a, p, st);
+    default: return launch_chunk_kh<DT, CH, ATTN_KH, 2>(a, p, st);
+  }
+}
+
 template <int DT>
 static hipError_t launch_dt(const AttnP& a, hipStream_t st) {
   const AttnPlan p = attn_plan(a.rows, a.nq, a.nkv, a.Lk, a.target_wgs);
   if (p.S != a.S || p.chunk != a.chunk) return hipErrorInvalidValue;
   if (a.nseq > 1 && (!p.chunked || a.nseq > MAX_SEQS)) return hipErrorInvalidValue;
   if (p.chunked) {
-    if (p.chunk == 128) return launch_chunk_kh<DT, 128, ATTN_KH>(a, p, st);
-    return launch_chunk_kh<DT, 64, ATTN_KH>(a, p, st);
+    if (p.chunk == 128) return launch_chunk_mask<DT, 128>(a, p, st);
+    return launch_chunk_mask<DT, 64>(a, p, st);
   }
   if (p.key_groups == 1) return launch_loop<DT, 4, 1>(a, p, st);
   return launch_loop<DT, 4, 2>(a, p, st);

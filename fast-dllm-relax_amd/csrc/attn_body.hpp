@@ -26,7 +26,7 @@ constexpr int HD = 128;
 constexpr int KB = 32;        // keys per block
 constexpr int KLD = HD + 8;   // u16 stride of a K row in LDS
 constexpr int VLD = KB + 8;   // u16 stride of a transposed V row (one head dimension)
-constexpr int PSZ = 16 * HD + 32;  // floats per split partial of one query tile: O, m, l
+constexpr int PSZ = 16 * HD + 32;  // floats per split partial of one query tile: O, then (m, l) per query
 
 template <int DT> __device__ __forceinline__ float elem(const u32x4& v, int e) {
   return (e & 1) ? hi_f32<DT>(v[e >> 1]) : lo_f32<DT>(v[e >> 1]);
@@ -275,10 +275,7 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
   float* pp = a.part + ((size_t)(g * QT + qt) * a.S + c) * PSZ;
 #pragma unroll
   for (int dt = 0; dt < HD / 16; ++dt) reinterpret_cast<f32x4*>(pp)[dt * 64 + lane] = o[dt];
-  if (lg == 0) {
-    pp[16 * HD + lr] = Mq;
-    pp[16 * HD + 16 + lr] = Lq;
-  }
+  if (lg == 0) *reinterpret_cast<f32x2_t*>(pp + 16 * HD + 2 * lr) = f32x2_t{Mq, Lq};
 }
 
 // ---- one-shot variant for short key chunks (the cached decode step) -------------------------------
@@ -291,7 +288,7 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
 // Body of one workgroup (query-tile group bx, kv head by, key chunk bz).  With COH the qkv loads and the
 // output stores are agent-scope, for a launch in which other workgroups produce the qkv rows; the
 // kernel below uses plain accesses.
-template <int DT, int QPW, int KH, int CH, bool COH>
+template <int DT, int QPW, int KH, int CH, int MASK, bool COH>
 __device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, int bz, unsigned char* smem) {
   constexpr int NT = 64 * QPW * KH;
   constexpr int KIT = (CH * 8 + NT - 1) / NT;        // K items (rotation-pair chunks) per thread
@@ -317,11 +314,14 @@ __device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, 
   const u16* vq_base = a.qkv + (a.nq + a.nkv) * HD + g * HD;
 
   // ---- request the whole chunk (rows past kend read row kbeg and are masked or zeroed later) ----
+  // Item -> (key, chunk) maps: 16 consecutive lanes take 16 keys of one K chunk, and 32 consecutive
+  // lanes take 16 key quads x 2 dim chunks of V, so the LDS stores below hit 64 distinct banks per
+  // pass (rows are 68 dwords apart, 4 banks on).
   u32x4 klo[KIT], khi[KIT], vv[VIT][4];
 #pragma unroll
   for (int it = 0; it < KIT; ++it) {
     const int item = threadIdx.x + it * NT;
-    const int j = min(item >> 3, CH - 1), p = item & 7;
+    const int j = min((item & 15) + 16 * (item >> 7), CH - 1), p = (item >> 4) & 7;
     int key = kbeg + j;
     key = key < kend ? key : kbeg;
     const bool win = key >= a.ws && key < a.ws + a.rows;
@@ -338,7 +338,7 @@ __device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, 
 #pragma unroll
   for (int it = 0; it < VIT; ++it) {
     const int item = threadIdx.x + it * NT;
-    const int kq = min(item >> 4, CH / 4 - 1), dc = item & 15;
+    const int kq = min((item & 15) + 16 * (item >> 8), CH / 4 - 1), dc = (item >> 4) & 15;
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
       int key = kbeg + 4 * kq + qq;
@@ -363,15 +363,15 @@ __device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, 
     rope_tab<DT>(qf[0], qf[2], cs + 16 * lg);
     rope_tab<DT>(qf[1], qf[3], cs + 16 * lg + 64);
   }
-  const int qpos_blk = a.mask == 1 ? (a.q_pos0 + r) / a.block : 0;
-  const float* brow = a.mask == 2 ? a.bias + (long long)r * a.bias_ld : nullptr;
+  const int qpos_blk = MASK == 1 ? (a.q_pos0 + r) / a.block : 0;
+  const float* brow = MASK == 2 ? a.bias + (long long)r * a.bias_ld : nullptr;
 
   // ---- stage: K rows (window rows RoPE'd and appended to the cache), V transposed ----
 #pragma unroll
   for (int it = 0; it < KIT; ++it) {
     const int item = threadIdx.x + it * NT;
     if (item >= CH * 8) break;
-    const int j = item >> 3, p = item & 7;
+    const int j = (item & 15) + 16 * (item >> 7), p = (item >> 4) & 7;
     const int key = kbeg + j;
     u32x4 lo = klo[it], hi = khi[it];
     if (key >= kend) {
@@ -391,7 +391,7 @@ __device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, 
   for (int it = 0; it < VIT; ++it) {
     const int item = threadIdx.x + it * NT;
     if (item >= (CH / 4) * 16) break;
-    const int kq = item >> 4, dc = item & 15;
+    const int kq = (item & 15) + 16 * (item >> 8), dc = (item >> 4) & 15;
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
       const int key = kbeg + 4 * kq + qq;
@@ -401,14 +401,14 @@ __device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, 
         *reinterpret_cast<u32x4*>(a.vc + key * krow + g * HD + 8 * dc) = vv[it][qq];
       }
     }
+    // dim 8 dc + e of the quad's four keys, packed key-major into one 8-byte word (byte permutes:
+    // low halves select bytes 0-1 of each word, high halves bytes 2-3)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int sh = 16 * (e & 1);
-      const unsigned long long wd = (unsigned long long)((vv[it][0][e >> 1] >> sh) & 0xffffu) |
-                                    ((unsigned long long)((vv[it][1][e >> 1] >> sh) & 0xffffu) << 16) |
-                                    ((unsigned long long)((vv[it][2][e >> 1] >> sh) & 0xffffu) << 32) |
-                                    ((unsigned long long)((vv[it][3][e >> 1] >> sh) & 0xffffu) << 48);
-      *reinterpret_cast<unsigned long long*>(vbuf + (8 * dc + e) * VLDC + 4 * kq) = wd;
+      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+      const uint32_t w01 = __builtin_amdgcn_perm(vv[it][1][e >> 1], vv[it][0][e >> 1], sel);
+      const uint32_t w23 = __builtin_amdgcn_perm(vv[it][3][e >> 1], vv[it][2][e >> 1], sel);
+      *reinterpret_cast<u32x2*>(vbuf + (8 * dc + e) * VLDC + 4 * kq) = u32x2{w01, w23};
     }
   }
   __syncthreads();
@@ -442,9 +442,9 @@ __device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, 
           float v = s[kt][i] * a.scale;
           if (key >= kend) {
             v = -INFINITY;
-          } else if (a.mask == 1) {
+          } else if constexpr (MASK == 1) {
             if (qpos_blk < key / a.block) v = -INFINITY;
-          } else if (a.mask == 2) {
+          } else if constexpr (MASK == 2) {
             v += brow[key];
           }
           s[kt][i] = v;
@@ -531,16 +531,13 @@ __device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, 
     return;
   }
 
-  // ---- key splits: the partial of (g, qt, c): O^T as f32x4 [HD / 16][64 lanes], then m and l of the
-  // tile's 16 queries; attn_merge_kernel combines them ----
+  // ---- key splits: the partial of (g, qt, c): O^T as f32x4 [HD / 16][64 lanes], then (m, l) of each of
+  // the tile's 16 queries; attn_merge_kernel combines them ----
   if (kh == 0 && tile_ok) {
     float* pp = a.part + ((size_t)(g * QT + qt) * a.S + c) * PSZ;
 #pragma unroll
     for (int dt = 0; dt < DT16; ++dt) stf4<COH>(reinterpret_cast<f32x4*>(pp) + dt * 64 + lane, o[dt]);
-    if (lg == 0) {
-      stf<COH>(pp + 16 * HD + lr, Mq);
-      stf<COH>(pp + 16 * HD + 16 + lr, Lq);
-    }
+    if (lg == 0) stf2<COH>(pp + 16 * HD + 2 * lr, f32x2_t{Mq, Lq});
   }
 }
 
@@ -559,19 +556,19 @@ __device__ __forceinline__ void seq_view(AttnP& a, const AttnP& p, int b) {
   a.part = p.part + (size_t)b * p.nkv * QT * p.S * PSZ;
 }
 
-// gridDim.x = query-tile groups x sequences (sequence-major)
-template <int DT, int QPW, int KH, int CH>
+// gridDim.x = query-tile groups x sequences (sequence-major); MASK is the launch's AttnP::mask
+template <int DT, int QPW, int KH, int CH, int MASK>
 __global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP p) {
   extern __shared__ __align__(16) unsigned char smem[];
   if (p.nseq <= 1) {
-    attn_chunk_body<DT, QPW, KH, CH, false>(p, blockIdx.x, blockIdx.y, blockIdx.z, smem);
+    attn_chunk_body<DT, QPW, KH, CH, MASK, false>(p, blockIdx.x, blockIdx.y, blockIdx.z, smem);
     return;
   }
   const int qg = (int)gridDim.x / p.nseq, b = (int)blockIdx.x / qg;
   AttnP a = p;
   seq_view(a, p, b);
   if ((int)blockIdx.z * a.chunk >= a.Lk) return;  // past this sequence's keys: the merge skips it
-  attn_chunk_body<DT, QPW, KH, CH, false>(a, (int)blockIdx.x - b * qg, blockIdx.y, blockIdx.z, smem);
+  attn_chunk_body<DT, QPW, KH, CH, MASK, false>(a, (int)blockIdx.x - b * qg, blockIdx.y, blockIdx.z, smem);
 }
 
 // Merge of the key splits: one wave per (kv head g, query tile qt, 16-dim slice dt).  The split weights
@@ -580,37 +577,59 @@ __global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP p) {
 // Splits at or past ceil(Lk / chunk) (a shorter sequence of a batched call) hold nothing and are skipped.
 template <int DT, bool COH>
 __device__ __forceinline__ void attn_merge_wave(const AttnP& a, int dt, int qt, int g, int lane) {
-  constexpr int SB = 8;
+  constexpr int SR = 24;  // splits held in registers at once (two loads each): up to SR costs one round trip
+  constexpr int SB = 8;   // batch of the two-pass loop for more splits
   const int lr = lane & 15, lg = lane >> 4;
   const int grp = a.nq / a.nkv, QR = grp * a.rows, QT = (QR + 15) / 16;
   const int S = min(a.S, (a.Lk + a.chunk - 1) / a.chunk);  // splits that hold keys
   const float* pt = a.part + (size_t)(g * QT + qt) * a.S * PSZ;
-  float M = -INFINITY;
-  for (int s0 = 0; s0 < S; s0 += SB) {
-    float mv[SB];
-#pragma unroll
-    for (int q = 0; q < SB; ++q) mv[q] = ldf<COH>(pt + (size_t)min(s0 + q, S - 1) * PSZ + 16 * HD + lr);
-#pragma unroll
-    for (int q = 0; q < SB; ++q) M = fmaxf(M, mv[q]);
-  }
-  const float Mu = M == -INFINITY ? 0.f : M;
-  float L = 0.f;
+  float M = -INFINITY, L = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = 0; s0 < S; s0 += SB) {
-    f32x4 ov[SB];
-    float mv[SB], lv[SB];
+  if (S <= SR) {
+    f32x4 ov[SR];
+    f32x2_t ml[SR];  // (m, l) of this lane's query
 #pragma unroll
-    for (int q = 0; q < SB; ++q) {
-      const float* ps = pt + (size_t)min(s0 + q, S - 1) * PSZ;
+    for (int q = 0; q < SR; ++q) {
+      const float* ps = pt + (size_t)min(q, S - 1) * PSZ;
       ov[q] = ldf4<COH>(reinterpret_cast<const f32x4*>(ps) + dt * 64 + lane);
-      mv[q] = ldf<COH>(ps + 16 * HD + lr);
-      lv[q] = ldf<COH>(ps + 16 * HD + 16 + lr);
+      ml[q] = ldf2<COH>(ps + 16 * HD + 2 * lr);
     }
+    // keep every load above issued before the first use (the scheduler would otherwise sink the O loads
+    // next to their uses and pay one round trip per pair)
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int q = 0; q < SB; ++q) {
-      const float e = s0 + q < S ? expf(mv[q] - Mu) : 0.f;
-      L += lv[q] * e;
+    for (int q = 0; q < SR; ++q) M = fmaxf(M, ml[q][0]);
+    const float Mu = M == -INFINITY ? 0.f : M;
+#pragma unroll
+    for (int q = 0; q < SR; ++q) {
+      const float e = q < S ? expf(ml[q][0] - Mu) : 0.f;
+      L += ml[q][1] * e;
       acc += ov[q] * e;
+    }
+  } else {
+    for (int s0 = 0; s0 < S; s0 += SB) {
+      f32x2_t mv[SB];
+#pragma unroll
+      for (int q = 0; q < SB; ++q) mv[q] = ldf2<COH>(pt + (size_t)min(s0 + q, S - 1) * PSZ + 16 * HD + 2 * lr);
+#pragma unroll
+      for (int q = 0; q < SB; ++q) M = fmaxf(M, mv[q][0]);
+    }
+    const float Mu = M == -INFINITY ? 0.f : M;
+    for (int s0 = 0; s0 < S; s0 += SB) {
+      f32x4 ov[SB];
+      f32x2_t mv[SB];
+#pragma unroll
+      for (int q = 0; q < SB; ++q) {
+        const float* ps = pt + (size_t)min(s0 + q, S - 1) * PSZ;
+        ov[q] = ldf4<COH>(reinterpret_cast<const f32x4*>(ps) + dt * 64 + lane);
+        mv[q] = ldf2<COH>(ps + 16 * HD + 2 * lr);
+      }
+#pragma unroll
+      for (int q = 0; q < SB; ++q) {
+        const float e = s0 + q < S ? expf(mv[q][0] - Mu) : 0.f;
+        L += mv[q][1] * e;
+        acc += ov[q] * e;
+      }
     }
   }
   const int qi = qt * 16 + lr;

@@ -207,6 +207,15 @@ __device__ __forceinline__ f32x4 ldf4(const f32x4* p) {
   return f32x4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
 }
 template <bool COH>
+__device__ __forceinline__ f32x2_t ldf2(const float* p) {
+  const u32x2 v = ld8<COH>(p);
+  return f32x2_t{__uint_as_float(v[0]), __uint_as_float(v[1])};
+}
+template <bool COH>
+__device__ __forceinline__ void stf2(float* p, f32x2_t v) {
+  st8<COH>(p, u32x2{__float_as_uint(v[0]), __float_as_uint(v[1])});
+}
+template <bool COH>
 __device__ __forceinline__ void stf4(f32x4* p, f32x4 v) {
   st16<COH>(p, u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])});
 }
