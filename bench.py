@@ -17,6 +17,12 @@ Beside it the JSON line carries:
   cpu_baseline    the CPU oracle's 32-row refinement step (numpy fp32 with the bf16 rounding points) at
                   the same prefix on the host's cores, scaled to tokens/s with the GPU loop's tokens per
                   model call;
+  prefix512       BASELINE config 2: the 1.5B architecture in bf16 (tied head), seed 1, a 512-row prefix;
+                  synced medians of forward_cached alone, of the full 32-row refinement step and of the
+                  four 8-row partial steps (rp 0, 8, 16, 24) over a block of masks;
+  long_context    BASELINE config 5: seed 4, an 8192-token prefix through build_prefix_cache (prefill
+                  tokens/s), then a 64-token continuation scored by score_masked_continuation with the
+                  per-token log-probabilities of the loglikelihood path (scoring ms);
   batched         BASELINE config 4: the 1.5B architecture in fp16, seed 3, 16 sequences with prefix
                   lengths drawn from U[128, 1024], one 32-token masked block each refined in sub-blocks
                   of 8 (threshold 0.9) by batched steps over all 16 sequences (the projections at M = 512);
@@ -76,6 +82,8 @@ def main() -> int:
     ap.add_argument("--prefix", type=int, default=PREFIX)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batched", action="store_true")
+    ap.add_argument("--no-prefix512", action="store_true")
+    ap.add_argument("--no-long-context", action="store_true")
     ap.add_argument("--cpu-iters", type=int, default=2)
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the dominant kernel over the 28 layers and a plain 256 MiB copy (for rocprofv3 --pmc)")
@@ -176,14 +184,16 @@ def main() -> int:
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(vm, params, cache, block, P, args.cpu_iters, tokens_per_call)
 
-    # ---- config 4: batched steps -------------------------------------------------------------------
-    batched = None
-    if not args.no_batched:
-        del cache
-        vm.close()
-        del vm, params
-        torch.cuda.empty_cache()
-        batched = batched_bench(args)
+    # ---- the other BASELINE configurations, one model at a time ------------------------------------
+    del cache
+    vm.close()
+    del vm, params
+    torch.cuda.empty_cache()
+    prefix512 = None if args.no_prefix512 else prefix512_bench()
+    torch.cuda.empty_cache()
+    long_context = None if args.no_long_context else long_context_bench()
+    torch.cuda.empty_cache()
+    batched = None if args.no_batched else batched_bench(args)
 
     line = {
         "metric": "decode tokens/s (1.5B bf16, bs1); block-step ms + achieved HBM GB/s",
@@ -218,10 +228,103 @@ def main() -> int:
                      "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "avg_launch_us": round(gu_ms * 1e3, 2), "bytes_per_launch": gu_bytes},
         "cpu_baseline": cpu,
+        "prefix512": prefix512,
+        "long_context": long_context,
         "batched": batched,
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def prefix512_bench() -> dict:
+    """Config 2: seed 1, tied lm_head N(0, 0.02), 512 random prefix ids; a block of 32 mask tokens."""
+    import numpy as np
+
+    from fast_dllm_relax_amd.config import DEFAULT_MASK_ID, fast_dllm_v2_1p5b
+    from fast_dllm_relax_amd.params import random_params_torch
+    from fast_dllm_relax_amd.runtime import (_embed, _offset_tensor, build_prefix_cache_from_ids,
+                                             score_active_block_partial_perlayer, score_active_block_refine)
+    from fast_dllm_relax_amd.vm import HipVM
+
+    P = 512
+    cfg = fast_dllm_v2_1p5b()
+    log("prefix512: generating bf16 weights (seed 1)")
+    params = random_params_torch(cfg, 1, dtype="bfloat16", device="cuda")
+    vm = HipVM(cfg, params, dtype="bfloat16", max_rows=P)
+    rng = np.random.default_rng(1)
+    cache = build_prefix_cache_from_ids(vm, rng.integers(0, 150000, P).tolist(), block_size=32, capacity=P + 32)
+    block = [DEFAULT_MASK_ID] * 32
+    emb = _embed(vm, block)
+    off = _offset_tensor(P)
+    layers_ms = event_ms(lambda: vm.forward_cached(emb, cache.k, cache.v, off, P), 20)
+    full_ms = event_ms(lambda: score_active_block_refine(vm, block, cache), 20)
+    part = {}
+    for rp in (0, 8, 16, 24):
+        part[f"rp{rp}"] = round(event_ms(lambda: score_active_block_partial_perlayer(
+            vm, block[rp:rp + 8], cache, rp, block_size=32), 20), 4)
+    b32, b8 = cfg.step_bytes(32, P), cfg.step_bytes(8, P)
+    res = {"workload": "BASELINE config 2: 1.5B bf16, seed 1, tied lm_head, prefix 512 via build_prefix_cache, "
+                       "a block of 32 mask tokens",
+           "forward_cached_ms": round(layers_ms, 4), "refine_r32_ms": round(full_ms, 4),
+           "refine_r32_gbps": round(b32 / (full_ms * 1e-3) / 1e9, 1), "partial_r8_ms": part,
+           "partial_r8_gbps": round(b8 / (part["rp8"] * 1e-3) / 1e9, 1)}
+    log(f"prefix512: forward_cached {layers_ms:.3f} ms, refine {full_ms:.3f} ms, partial {part}")
+    vm.close()
+    return res
+
+
+def long_context_bench() -> dict:
+    """Config 5: seed 4, 8192 random prefix ids through build_prefix_cache, then a 64-token random
+    continuation scored with score_masked_continuation and reduced to per-token log-probabilities."""
+    import numpy as np
+    import torch
+
+    from fast_dllm_relax_amd.config import DEFAULT_MASK_ID, fast_dllm_v2_1p5b
+    from fast_dllm_relax_amd.params import random_params_torch
+    from fast_dllm_relax_amd.runtime import build_prefix_cache_from_ids, score_masked_continuation
+    from fast_dllm_relax_amd.vm import HipVM
+
+    P, C = 8192, 64
+    cfg = fast_dllm_v2_1p5b()
+    log("long_context: generating bf16 weights (seed 4)")
+    params = random_params_torch(cfg, 4, dtype="bfloat16", device="cuda")
+    vm = HipVM(cfg, params, dtype="bfloat16", max_rows=P)
+    rng = np.random.default_rng(4)
+    prefix = rng.integers(0, 150000, P).tolist()
+    cont = rng.integers(0, 150000, C).tolist()
+
+    def prefill():
+        return build_prefix_cache_from_ids(vm, prefix, block_size=32, capacity=P + C)
+
+    def timed(fn, n):
+        out, ts = None, []
+        for _ in range(n):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out = fn()
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        return out, statistics.median(ts)
+
+    prefill()  # warm-up
+    cache, prefill_s = timed(prefill, 3)
+    log(f"long_context: prefill {P} rows {prefill_s * 1e3:.1f} ms")
+
+    def score():
+        logits, _ = score_masked_continuation(vm, prefix, cont, block_size=32, mask_id=DEFAULT_MASK_ID,
+                                              cached_prefix=(prefix, cache))
+        x = torch.from_numpy(logits).double()
+        return torch.log_softmax(x, dim=-1)[torch.arange(C), torch.tensor(cont)].numpy()
+
+    score()  # warm-up
+    logprobs, score_s = timed(score, 5)
+    res = {"workload": f"BASELINE config 5: 1.5B bf16, seed 4, prefix {P} via build_prefix_cache, {C}-token "
+                       "continuation scored by score_masked_continuation + log-softmax",
+           "prefill_ms": round(prefill_s * 1e3, 2), "prefill_tokens_per_s": round(P / prefill_s, 1),
+           "scoring_ms": round(score_s * 1e3, 3), "loglikelihood": round(float(logprobs.sum()), 4)}
+    log(f"long_context: scoring {score_s * 1e3:.2f} ms")
+    vm.close()
+    return res
 
 
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16 / bf16

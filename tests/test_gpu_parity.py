@@ -212,3 +212,32 @@ def test_wide_forward_hidden_large_m(wide2):
         log(f"case: wide forward_hidden S={S} arithmetic block-causal")
         got = to_np(vm.forward_hidden(vm.embed(_dev_ids(ids))[None], None))
         bf16_parity(f"hidden S={S}", got, want, want32)
+
+
+def _log_softmax(x: np.ndarray) -> np.ndarray:
+    x = x.astype(np.float64)
+    m = x.max(axis=-1, keepdims=True)
+    return x - m - np.log(np.exp(x - m).sum(axis=-1, keepdims=True))
+
+
+def test_score_masked_continuation_matches_oracle(tiny):
+    """Masked-continuation scoring (runtime.py:485-588) and the per-token log-probabilities the
+    loglikelihood path takes from it (runners.py:839-881) vs the oracle: a prefix shorter than a block
+    (the stateless path), a prefix with a partial last block, and a continuation longer than a block."""
+    from fast_dllm_relax_amd.runtime import score_masked_continuation
+    from oracle import runtime as ort
+
+    ref, vm = tiny
+    rng = np.random.default_rng(12)
+    mask_id = TINY["vocab_size"] - 1
+    for plen, clen in ((20, 5), (70, 9), (64, 40)):
+        prefix = [int(t) for t in rng.integers(0, mask_id, plen)]
+        cont = [int(t) for t in rng.integers(0, mask_id, clen)]
+        log(f"case: score_masked_continuation prefix={plen} continuation={clen}")
+        got, _ = score_masked_continuation(vm, prefix, cont, block_size=32, mask_id=mask_id)
+        want = ort.score_masked_continuation(ref, prefix, cont, block_size=32, mask_id=mask_id)
+        assert got.shape == want.shape == (clen, TINY["vocab_size"])
+        np.testing.assert_allclose(got, want, **TOL)
+        lp_got = _log_softmax(got)[np.arange(clen), cont]
+        lp_want = _log_softmax(want)[np.arange(clen), cont]
+        np.testing.assert_allclose(lp_got, lp_want, rtol=0, atol=2e-2)
