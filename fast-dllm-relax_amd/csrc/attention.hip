@@ -96,11 +96,47 @@ static hipError_t launch_chunk_mask(const AttnP& a, const AttnPlan& p, hipStream
   }
 }
 
+// Long row blocks: RoPE + KV append pass, then the flash-style kernel with the most query heads per
+// workgroup that still gives 256 workgroups.
+template <int DT, int MASK, int TQ, int NWQ>
+static hipError_t launch_prefill_cfg(const AttnP& a, int hpw, hipStream_t st) {
+  constexpr size_t lds = 2 * ((size_t)64 * (HD + 8) + (size_t)HD * (64 + 8)) * 2;
+  auto kern = attn_prefill_kernel<DT, MASK, TQ, NWQ>;
+  raise_lds(kern, lds);
+  const int nqb = (a.rows + 31) / 32, grp = a.nq / a.nkv;
+  hipLaunchKernelGGL(kern, dim3(nqb * (grp / hpw), a.nkv), dim3(64 * NWQ), lds, st, a, hpw);
+  return hipGetLastError();
+}
+
+template <int DT, int MASK>
+static hipError_t launch_prefill(const AttnP& a, hipStream_t st) {
+  hipLaunchKernelGGL(rope_kv_kernel<DT>, dim3(a.rows), dim3(128), 0, st, a);
+  const int nqb = (a.rows + 31) / 32, grp = a.nq / a.nkv;
+  int hpw = 1;
+  for (int h : {6, 3, 2})
+    if (grp % h == 0 && nqb * (grp / h) * a.nkv >= 256) { hpw = h; break; }
+  const int ph = a.prefill_hpw;
+  if ((ph == 1 || ph == 2 || ph == 3 || ph == 6) && grp % ph == 0) hpw = ph;
+  switch (hpw) {
+    case 6: return launch_prefill_cfg<DT, MASK, 3, 4>(a, 6, st);
+    case 3: return launch_prefill_cfg<DT, MASK, 3, 2>(a, 3, st);
+    case 2: return launch_prefill_cfg<DT, MASK, 2, 2>(a, 2, st);
+    default: return launch_prefill_cfg<DT, MASK, 1, 2>(a, 1, st);
+  }
+}
+
+// the prefill kernel takes row blocks of at least this many rows without an explicit bias
+constexpr int PREFILL_MIN_ROWS = 128;
+
 template <int DT>
 static hipError_t launch_dt(const AttnP& a, hipStream_t st) {
   const AttnPlan p = attn_plan(a.rows, a.nq, a.nkv, a.Lk, a.target_wgs);
   if (p.S != a.S || p.chunk != a.chunk) return hipErrorInvalidValue;
   if (a.nseq > 1 && (!p.chunked || a.nseq > MAX_SEQS)) return hipErrorInvalidValue;
+  if (!p.chunked && a.nseq <= 1 && a.rows >= PREFILL_MIN_ROWS && a.mask != 2) {
+    if (a.mask == 1) return launch_prefill<DT, 1>(a, st);
+    return launch_prefill<DT, 0>(a, st);
+  }
   if (p.chunked) {
     if (p.chunk == 128) return launch_chunk_mask<DT, 128>(a, p, st);
     return launch_chunk_mask<DT, 64>(a, p, st);

@@ -655,4 +655,240 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(AttnP p) {
   attn_merge_wave<DT, false>(a, blockIdx.x, blockIdx.y, (int)blockIdx.z - b * p.nkv, threadIdx.x);
 }
 
+
+// ---- long row blocks (prefill, stateless forward): RoPE + KV append pass, then a flash-style kernel --
+// rope_kv_kernel: one workgroup per row r.  q heads are RoPE'd into out (the attention output buffer,
+// [rows][nq * 128]: the prefill kernel reads each query from there before it writes that query's
+// output), k heads are RoPE'd and v copied into the cache rows ws + r (the KV append of
+// fast_dllm.attn_inplace, runtime.py:51-60).  Same RoPE arithmetic as the chunk kernels.
+template <int DT>
+__global__ __launch_bounds__(128) void rope_kv_kernel(AttnP a) {
+  const int r = blockIdx.x;
+  const u16* src = a.qkv + (size_t)r * a.ldq;
+  const float* cs = a.rope + (size_t)r * 128;
+  const size_t krow = (size_t)a.nkv * HD;
+  const int nrope = (a.nq + a.nkv) * 8;  // (head, rotation-pair chunk) items
+  for (int item = threadIdx.x; item < nrope + a.nkv * 16; item += 128) {
+    if (item < nrope) {
+      const int hd = item >> 3, p = item & 7;
+      const u16* hs = src + hd * HD;
+      u32x4 lo = *reinterpret_cast<const u32x4*>(hs + 8 * p);
+      u32x4 hi = *reinterpret_cast<const u32x4*>(hs + 64 + 8 * p);
+      rope_tab<DT>(lo, hi, cs + 16 * p);
+      u16* dst = hd < a.nq ? a.out + (size_t)r * a.nq * HD + hd * HD
+                           : a.kc + (size_t)(a.ws + r) * krow + (hd - a.nq) * HD;
+      *reinterpret_cast<u32x4*>(dst + 8 * p) = lo;
+      *reinterpret_cast<u32x4*>(dst + 64 + 8 * p) = hi;
+    } else {
+      const int it = item - nrope, g = it >> 4, c = it & 15;
+      *reinterpret_cast<u32x4*>(a.vc + (size_t)(a.ws + r) * krow + g * HD + 8 * c) =
+          *reinterpret_cast<const u32x4*>(src + (a.nq + a.nkv + g) * HD + 8 * c);
+    }
+  }
+}
+
+// attn_prefill_kernel: workgroup (query block of 32 rows, head subset hg of kv head g) with NWQ waves x
+// TQ query tiles (2 tiles per head: rows q0 .. q0 + 15 and q0 + 16 .. q0 + 31 of head hh).  The kv head's
+// keys stream through LDS in blocks of 64 (K row-major, V transposed), double-buffered: the next block
+// is loaded into registers while this one is multiplied, so every K/V row is read once per workgroup
+// for all of its query tiles.  Scores in fp32 on MFMA, online softmax in base 2 with the scale folded
+// in (p = 2^(s * scale * log2 e - m)), P rounded to the model dtype for P.V, fp32 accumulation; the
+// precision order of the chunk kernels.  MASK 1 (block-causal, cuda.py:148-177) reduces to a key
+// bound per query: keys below ((q_pos0 + r) / block + 1) * block.  Query blocks are dealt heaviest
+// (latest) first.  Queries come from out (rope_kv_kernel) and results go back to the same places.
+template <int DT, int MASK, int TQ, int NWQ>
+__global__ __launch_bounds__(64 * NWQ) void attn_prefill_kernel(AttnP a, int hpw) {
+  constexpr int KBP = 64;          // keys per block
+  constexpr int KLDP = HD + 8;     // u16 stride of a K row
+  constexpr int VLDP = KBP + 8;    // u16 stride of a V^T row
+  constexpr int NT = 64 * NWQ;
+  constexpr int KIT = KBP * 16 / NT;       // 16-byte K chunks per thread per block
+  constexpr int VIT = (KBP / 4) * 16 / NT; // (key quad, dim chunk) V items per thread per block
+  static_assert(KIT * NT == KBP * 16 && VIT * NT == (KBP / 4) * 16, "whole staging rounds");
+  static_assert(MASK == 0 || MASK == 1, "explicit biases take attn_kernel");
+  constexpr int DT16 = HD / 16;
+  extern __shared__ __align__(16) unsigned char smem[];
+  u16* kb_[2];
+  u16* vb_[2];
+  kb_[0] = reinterpret_cast<u16*>(smem);
+  vb_[0] = kb_[0] + KBP * KLDP;
+  kb_[1] = vb_[0] + HD * VLDP;
+  vb_[1] = kb_[1] + KBP * KLDP;
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int grp = a.nq / a.nkv, nhg = grp / hpw;
+  const int nqb = (a.rows + 31) / 32;
+  const int qb = nqb - 1 - (int)blockIdx.x / nhg, hg = (int)blockIdx.x % nhg;
+  const int g = blockIdx.y;
+  const int q0 = qb * 32, rlast = a.rows - 1;
+  const size_t krow = (size_t)a.nkv * HD;
+  const u16* kc = a.kc + g * HD;
+  const u16* vc = a.vc + g * HD;
+  const float c2 = a.scale * 1.4426950408889634f;  // scale * log2(e)
+
+  // the keys this workgroup needs: up to its last query's bound
+  auto kend_of = [&](int r) {
+    if constexpr (MASK == 1) return min(a.Lk, ((a.q_pos0 + r) / a.block + 1) * a.block);
+    return a.Lk;
+  };
+  const int kend_wg = kend_of(min(q0 + 31, rlast));
+  const int nkb = (kend_wg + KBP - 1) / KBP;
+
+  // this wave's query tiles: tile t = w TQ + i -> head hg hpw + t / 2, rows q0 + 16 (t % 2) + lr
+  u32x4 qf[TQ][4];
+  int kend_q[TQ];
+  bool tvalid[TQ];
+  const u16* qsrc = a.out;
+#pragma unroll
+  for (int i = 0; i < TQ; ++i) {
+    const int t = w * TQ + i;
+    tvalid[i] = t < 2 * hpw && q0 + 16 * (t % 2) <= rlast;
+    const int hh = hg * hpw + min(t, 2 * hpw - 1) / 2;
+    const int r = min(q0 + 16 * (t % 2) + lr, rlast);
+    kend_q[i] = kend_of(r);
+    const u16* qp = qsrc + (size_t)r * a.nq * HD + (g * grp + hh) * HD + 8 * lg;
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) qf[i][ds] = *reinterpret_cast<const u32x4*>(qp + 32 * ds);
+  }
+
+  // staging maps (conflict-free LDS stores): K item -> key j, 16-byte chunk c; V item -> key quad kq, dim chunk dc
+  u32x4 kr[KIT], vr[VIT][4];
+  auto load = [&](int kb) {
+    const int k0 = kb * KBP;
+#pragma unroll
+    for (int it = 0; it < KIT; ++it) {
+      const int item = threadIdx.x + it * NT;
+      const int j = (item & 15) + 16 * (item >> 8), c = (item >> 4) & 15;
+      const int key = min(k0 + j, kend_wg - 1);
+      kr[it] = *reinterpret_cast<const u32x4*>(kc + (size_t)key * krow + 8 * c);
+    }
+#pragma unroll
+    for (int it = 0; it < VIT; ++it) {
+      const int item = threadIdx.x + it * NT;
+      const int kq = item & 15, dc = item >> 4;
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const int key = min(k0 + 4 * kq + qq, kend_wg - 1);
+        vr[it][qq] = *reinterpret_cast<const u32x4*>(vc + (size_t)key * krow + 8 * dc);
+      }
+    }
+  };
+  auto stage = [&](int buf) {
+#pragma unroll
+    for (int it = 0; it < KIT; ++it) {
+      const int item = threadIdx.x + it * NT;
+      const int j = (item & 15) + 16 * (item >> 8), c = (item >> 4) & 15;
+      *reinterpret_cast<u32x4*>(kb_[buf] + j * KLDP + 8 * c) = kr[it];
+    }
+#pragma unroll
+    for (int it = 0; it < VIT; ++it) {
+      const int item = threadIdx.x + it * NT;
+      const int kq = item & 15, dc = item >> 4;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+        const uint32_t w01 = __builtin_amdgcn_perm(vr[it][1][e >> 1], vr[it][0][e >> 1], sel);
+        const uint32_t w23 = __builtin_amdgcn_perm(vr[it][3][e >> 1], vr[it][2][e >> 1], sel);
+        *reinterpret_cast<u32x2*>(vb_[buf] + (8 * dc + e) * VLDP + 4 * kq) = u32x2{w01, w23};
+      }
+    }
+  };
+
+  float m_run[TQ], l_run[TQ];
+  f32x4 o[TQ][DT16];
+#pragma unroll
+  for (int i = 0; i < TQ; ++i) {
+    m_run[i] = -INFINITY;
+    l_run[i] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT16; ++dt) o[i][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  load(0);
+  stage(0);
+  __syncthreads();
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int buf = kb & 1;
+    load(min(kb + 1, nkb - 1));
+    const u16* kbuf = kb_[buf];
+    const u16* vbuf = vb_[buf];
+    const int k0 = kb * KBP;
+#pragma unroll
+    for (int i = 0; i < TQ; ++i) {
+      if (!tvalid[i]) continue;
+      // S^T = K Q^T: lane holds S^T[key k0 + 16 kt + 4 lg + e][query lr]
+      f32x4 s[4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const u16* kp = kbuf + (16 * kt + lr) * KLDP + 8 * lg;
+#pragma unroll
+        for (int ds = 0; ds < 4; ++ds) s[kt] = mfma16<DT>(*reinterpret_cast<const u32x4*>(kp + 32 * ds), qf[i][ds], s[kt]);
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int key = k0 + 16 * kt + 4 * lg + e;
+          const float v = key < kend_q[i] ? s[kt][e] * c2 : -INFINITY;
+          s[kt][e] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = rows_max(mx);
+      const float m_new = fmaxf(m_run[i], mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run[i] - m_use);
+      float ps = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float pe = __builtin_amdgcn_exp2f(s[kt][e] - m_use);
+          s[kt][e] = pe;
+          ps += pe;
+        }
+      ps = rows_sum(ps);
+      l_run[i] = l_run[i] * alpha + ps;
+      m_run[i] = m_new;
+#pragma unroll
+      for (int dt = 0; dt < DT16; ++dt) o[i][dt] *= alpha;
+      // O^T += V^T P^T over the block's two 32-key k steps (k slot 8 lg + e: key 4 lg + e, then 16 + 4 lg + e - 4)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const u32x4 pb = {pack2(from_f32<DT>(s[2 * ks][0]), from_f32<DT>(s[2 * ks][1])),
+                          pack2(from_f32<DT>(s[2 * ks][2]), from_f32<DT>(s[2 * ks][3])),
+                          pack2(from_f32<DT>(s[2 * ks + 1][0]), from_f32<DT>(s[2 * ks + 1][1])),
+                          pack2(from_f32<DT>(s[2 * ks + 1][2]), from_f32<DT>(s[2 * ks + 1][3]))};
+#pragma unroll
+        for (int dt = 0; dt < DT16; ++dt) {
+          const u16* vrow = vbuf + (16 * dt + lr) * VLDP + 32 * ks + 4 * lg;
+          const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
+          const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 16);
+          o[i][dt] = mfma16<DT>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb, o[i][dt]);
+        }
+      }
+    }
+    stage(buf ^ 1);
+    __syncthreads();
+  }
+
+  // lane output: query row r of tile i, dims 16 dt + 4 lg .. + 3
+#pragma unroll
+  for (int i = 0; i < TQ; ++i) {
+    const int t = w * TQ + i;
+    const int r = q0 + 16 * (t % 2) + lr;
+    if (!tvalid[i] || r > rlast) continue;
+    const int hh = hg * hpw + t / 2;
+    const float inv = 1.0f / l_run[i];
+    u16* dst = a.out + (size_t)r * a.nq * HD + (g * grp + hh) * HD + 4 * lg;
+#pragma unroll
+    for (int dt = 0; dt < DT16; ++dt)
+      *reinterpret_cast<u32x2*>(dst + 16 * dt) =
+          u32x2{pack2(from_f32<DT>(o[i][dt][0] * inv), from_f32<DT>(o[i][dt][1] * inv)),
+                pack2(from_f32<DT>(o[i][dt][2] * inv), from_f32<DT>(o[i][dt][3] * inv))};
+  }
+}
+
 }  // namespace fdllm

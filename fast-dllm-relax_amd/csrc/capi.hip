@@ -80,6 +80,7 @@ struct fdllm_ctx {
   int32_t* zero_i32 = nullptr;
   float* rope = nullptr; size_t rope_floats = 0;  // RoPE (cos, sin) table of the current call's rows
   int attn_target = 64;   // attention workgroups aimed for when splitting the keys
+  int prefill_hpw = 0;    // query heads per prefill-attention workgroup (0: chosen per launch)
   int down_split = 10;    // cross-workgroup k splits of the down projection (largest divisor of K/32 <= this)
   int mm_target_wgs = 256;  // large-M GEMM: split k while the launch has fewer workgroups than this
   int mm_min_stages = 8;    // ... into splits of at least this many stages
@@ -235,7 +236,7 @@ int run_attention(fdllm_ctx* c, int rows, uint16_t* kc, uint16_t* vc, int ws, in
   const AttnPlan pl = attn_plan(a.rows, a.nq, a.nkv, a.Lk, target);
   if (sb != nullptr && !pl.chunked)
     return fail(FDLLM_EINVAL, "batched call of %d rows per sequence over %d keys is too long for one step", a.rows, a.Lk);
-  a.S = pl.S; a.chunk = pl.chunk; a.target_wgs = target;
+  a.S = pl.S; a.chunk = pl.chunk; a.target_wgs = target; a.prefill_hpw = c->prefill_hpw;
   if (a.S > 1) {
     int rc = ensure_floats(&c->apart, &c->apart_floats, attn_partial_floats(a));
     if (rc) return rc;
@@ -408,6 +409,7 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   c->cfg = f;
   (void)hipGetDevice(&c->dev);
   if (const char* e = std::getenv("FDLLM_ATTN_TARGET")) c->attn_target = std::max(1, atoi(e));
+  if (const char* e = std::getenv("FDLLM_PREFILL_HPW")) c->prefill_hpw = std::max(0, atoi(e));
   if (const char* e = std::getenv("FDLLM_DOWN_SPLIT")) c->down_split = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_MM_TARGET_WGS")) c->mm_target_wgs = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_MM_MIN_STAGES")) c->mm_min_stages = std::max(1, atoi(e));

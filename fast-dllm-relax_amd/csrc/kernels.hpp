@@ -93,6 +93,7 @@ struct AttnP {
   const float* bias; long long bias_ld;
   int S, chunk;                       // key splits (gridDim.z), keys per split (multiple of 32)
   int target_wgs;                     // workgroups the plan aims for (attn_plan)
+  int prefill_hpw;                    // query heads per workgroup of the prefill kernel (0: chosen per launch)
   float* part;                        // split partials (merged by attn_merge_kernel)
   uint16_t* out;                      // [rows][nq * 128]
   // batched call (nseq > 1, chunked kernel only): sequence b owns rows [b rows, (b + 1) rows) of qkv,

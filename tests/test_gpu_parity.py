@@ -204,7 +204,7 @@ def test_wide_forward_hidden_large_m(wide2):
     ref, vm = wide2
     ref32 = OracleModel(ref.cfg, ref.p, "float32")
     rng = np.random.default_rng(11)
-    for S in (160, 1056):
+    for S in (160, 1056, 2080):
         ids = _ids(rng, S, WIDE2["vocab_size"])
         bias = build_prefix_block_attention_bias(0, S, block_size=32)
         want = ref.forward_hidden(ref.embed(ids)[None], bias)
@@ -241,3 +241,27 @@ def test_score_masked_continuation_matches_oracle(tiny):
         lp_got = _log_softmax(got)[np.arange(clen), cont]
         lp_want = _log_softmax(want)[np.arange(clen), cont]
         np.testing.assert_allclose(lp_got, lp_want, rtol=0, atol=2e-2)
+
+
+def test_prefill_attention_configs_agree(wide2, monkeypatch):
+    """The prefill attention kernel gives every query the same arithmetic whatever the number of query
+    heads per workgroup (1, 2, 3 or 6 of a kv head's 6), so all four give bit-identical outputs."""
+    from fast_dllm_relax_amd.config import FastDLLMConfig
+    from fast_dllm_relax_amd.params import from_numpy
+    from fast_dllm_relax_amd.vm import HipVM
+
+    ref, vm0 = wide2
+    rng = np.random.default_rng(13)
+    S = 352
+    ids = _ids(rng, S, WIDE2["vocab_size"])
+    x = vm0.embed(_dev_ids(ids))[None]
+    outs = {}
+    for hpw in (1, 2, 3, 6):
+        monkeypatch.setenv("FDLLM_PREFILL_HPW", str(hpw))
+        cfg = FastDLLMConfig(**WIDE2)
+        vm = HipVM(cfg, from_numpy(ref.p, cfg, dtype="bfloat16"), dtype="bfloat16", max_rows=S)
+        log(f"case: prefill attention, {hpw} query heads per workgroup, S={S}")
+        outs[hpw] = to_np(vm.forward_hidden(x, None))
+        vm.close()
+    for hpw in (2, 3, 6):
+        np.testing.assert_array_equal(outs[hpw], outs[1])
