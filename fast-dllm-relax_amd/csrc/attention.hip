@@ -97,7 +97,8 @@ static hipError_t launch_chunk_mask(const AttnP& a, const AttnPlan& p, hipStream
 }
 
 // Long row blocks: RoPE + KV append pass, then the flash-style kernel with the most query heads per
-// workgroup that still gives 256 workgroups.
+// workgroup that still gives 1024 workgroups (measured at 512 / 2048 / 8192 rows: more workgroups win
+// over fewer K/V re-reads until about that many).
 template <int DT, int MASK, int TQ, int NWQ>
 static hipError_t launch_prefill_cfg(const AttnP& a, int hpw, hipStream_t st) {
   constexpr size_t lds = 2 * ((size_t)64 * (HD + 8) + (size_t)HD * (64 + 8)) * 2;
@@ -114,7 +115,7 @@ static hipError_t launch_prefill(const AttnP& a, hipStream_t st) {
   const int nqb = (a.rows + 31) / 32, grp = a.nq / a.nkv;
   int hpw = 1;
   for (int h : {6, 3, 2})
-    if (grp % h == 0 && nqb * (grp / h) * a.nkv >= 256) { hpw = h; break; }
+    if (grp % h == 0 && nqb * (grp / h) * a.nkv >= 1024) { hpw = h; break; }
   const int ph = a.prefill_hpw;
   if ((ph == 1 || ph == 2 || ph == 3 || ph == 6) && grp % ph == 0) hpw = ph;
   switch (hpw) {
