@@ -85,35 +85,114 @@ def from_numpy(arrays: dict[str, np.ndarray], cfg: FastDLLMConfig, *, dtype: str
             for n in param_names(cfg)]
 
 
-def load_artifact(artifact_dir, cfg: FastDLLMConfig, *, device: str = "cuda") -> tuple[list[torch.Tensor], str]:
-    """Load a reference artifact directory: fast_dllm_relax_nn_params.npz, _param_names.txt, _dtype.txt
-    and the KV-cache manifest (export_cuda.py:143-168).  Returns (packed params, dtype)."""
+# Artifact file names (export_cuda.py:9-11, 162-168; export_utils.py:22).
+PARAMS_NPZ = "fast_dllm_relax_nn_params.npz"
+PARAM_NAMES_TXT = "fast_dllm_relax_nn_param_names.txt"
+DTYPE_TXT = "fast_dllm_relax_nn_dtype.txt"
+KV_CACHE_MANIFEST = "fast_dllm_relax_nn_kv_cache.json"
+
+
+def save_artifact(artifact_dir, cfg: FastDLLMConfig, params: list[torch.Tensor], dtype: str) -> pathlib.Path:
+    """Write the weight files of a reference artifact: the packed params as positional npz arrays arr_i in
+    param_names order (bf16 as its uint16 bits, export_utils.py:56-66), the names one per line, the
+    dtype sidecar and the KV-cache manifest (export_cuda.py:162-168, export_utils.py:25-34).  The Relax
+    executable itself (fast_dllm_relax_nn.so) is not written: this build's kernels replace it."""
+    if dtype not in TORCH_DTYPES:
+        raise ValueError(f"dtype {dtype!r} is not supported (bfloat16, float16)")
+    names = param_names(cfg)
+    if len(params) != len(names):
+        raise ValueError(f"{len(params)} tensors for {len(names)} parameter names")
     d = pathlib.Path(artifact_dir)
-    dtype = (d / "fast_dllm_relax_nn_dtype.txt").read_text().strip()
+    d.mkdir(parents=True, exist_ok=True)
+    arrays = []
+    for t in params:
+        t = t.detach().to(TORCH_DTYPES[dtype]).contiguous().cpu()
+        arrays.append(t.view(torch.int16).numpy().view(np.uint16) if dtype == "bfloat16" else t.numpy())
+    np.savez(d / PARAMS_NPZ, *arrays)
+    (d / PARAM_NAMES_TXT).write_text("\n".join(names) + "\n", encoding="utf-8")
+    (d / DTYPE_TXT).write_text(dtype + "\n", encoding="utf-8")
+    manifest = {"kv_cache": KV_CACHE_CONTRACT, "num_layers": cfg.num_hidden_layers,
+                "num_kv_heads": cfg.num_key_value_heads, "head_dim": cfg.head_dim, "dtype": dtype}
+    (d / KV_CACHE_MANIFEST).write_text(json.dumps(manifest, indent=2) + "\n", encoding="utf-8")
+    return d
+
+
+def _artifact_checks(d: pathlib.Path) -> dict:
+    """The reference runner's checks at load (runners.py:597-603, 819-831): the weight files exist and
+    the KV-cache manifest names the in-place contract."""
+    missing = [p for p in (d / PARAMS_NPZ, d / PARAM_NAMES_TXT) if not p.exists()]
+    if missing:
+        formatted = "\n".join(f"- {p}" for p in missing)
+        raise FileNotFoundError(f"Missing Relax artifact file(s):\n{formatted}")
+    manifest_path = d / KV_CACHE_MANIFEST
+    manifest = json.loads(manifest_path.read_text(encoding="utf-8")) if manifest_path.exists() else {}
+    if manifest.get("kv_cache") != KV_CACHE_CONTRACT:
+        raise RuntimeError(f"Relax artifact {d} does not use the in-place KV cache (no {KV_CACHE_MANIFEST} with "
+                           f"kv_cache={KV_CACHE_CONTRACT!r}).")
+    return manifest
+
+
+def artifact_dtype(artifact_dir) -> str:
+    """The artifact's semantic dtype; float16 when dtype.txt is absent (runners.py:947-949)."""
+    path = pathlib.Path(artifact_dir) / DTYPE_TXT
+    return path.read_text().strip() if path.exists() else "float16"
+
+
+def config_from_artifact(artifact_dir, **overrides) -> FastDLLMConfig:
+    """Model dimensions read from an artifact: layers, kv heads and head dim from the KV-cache manifest,
+    the rest from the parameter shapes (embedding [V, H], gate_up [2I, H], qkv [(nq + 2 nkv) hd, H]) and
+    whether lm_head.weight is listed.  rms_norm_eps, rope_theta and the block size are not stored in
+    the weight files: the defaults (the 1.5B model's) apply unless given in ``overrides``."""
+    d = pathlib.Path(artifact_dir)
+    manifest = _artifact_checks(d)
+    names = (d / PARAM_NAMES_TXT).read_text(encoding="utf-8").splitlines()
+    index = {n: i for i, n in enumerate(names)}
+    with np.load(d / PARAMS_NPZ, allow_pickle=False) as z:
+        def shape(name):
+            if name not in index:
+                raise ValueError(f"artifact has no parameter {name}")
+            return tuple(z[f"arr_{index[name]}"].shape)
+        vocab, hidden = shape("model.embed_tokens.weight")
+        inter = shape("model.layers.0.mlp.gate_up_proj.weight")[0] // 2
+        qkv = shape("model.layers.0.self_attn.qkv_proj.weight")[0]
+    nkv, hd = int(manifest["num_kv_heads"]), int(manifest["head_dim"])
+    base = dict(vocab_size=vocab, hidden_size=hidden, intermediate_size=inter,
+                num_hidden_layers=int(manifest["num_layers"]), num_attention_heads=qkv // hd - 2 * nkv,
+                num_key_value_heads=nkv, head_dim=hd, tie_word_embeddings="lm_head.weight" not in index)
+    base.update(overrides)
+    return FastDLLMConfig(**base)
+
+
+def load_artifact(artifact_dir, cfg: FastDLLMConfig | None = None, *,
+                  device: str = "cuda") -> tuple[list[torch.Tensor], str]:
+    """Load a reference artifact's weights (runners.py:938-968): the packed param list in param_names
+    order on ``device`` and the artifact dtype.  With ``cfg`` the names and shapes are checked against it;
+    without, the configuration is config_from_artifact's."""
+    d = pathlib.Path(artifact_dir)
+    _artifact_checks(d)
+    dtype = artifact_dtype(d)
     if dtype not in TORCH_DTYPES:
         raise ValueError(f"artifact dtype {dtype!r} is not supported (bfloat16, float16)")
-    manifest = d / "fast_dllm_relax_nn_kv_cache.json"
-    if manifest.exists():
-        info = json.loads(manifest.read_text())
-        if info.get("kv_cache") != KV_CACHE_CONTRACT:
-            raise ValueError(f"artifact KV-cache contract {info.get('kv_cache')!r} != {KV_CACHE_CONTRACT!r}")
-    names = (d / "fast_dllm_relax_nn_param_names.txt").read_text().split()
+    if cfg is None:
+        cfg = config_from_artifact(d)
+    names = (d / PARAM_NAMES_TXT).read_text(encoding="utf-8").splitlines()
     if names != param_names(cfg):
         raise ValueError("artifact parameter names do not match the configuration's packed order")
     shapes = param_shapes(cfg)
     td = TORCH_DTYPES[dtype]
     out = []
-    with np.load(d / "fast_dllm_relax_nn_params.npz", allow_pickle=False) as z:
+    with np.load(d / PARAMS_NPZ, allow_pickle=False) as z:
         missing = [f"arr_{i}" for i in range(len(names)) if f"arr_{i}" not in z.files]
-        if missing:  # runners.py:953-963
-            raise ValueError(f"Parameter archive is missing expected arrays: {', '.join(missing[:10])}")
+        if missing:  # runners.py:953-960
+            suffix = "..." if len(missing) > 10 else ""
+            raise ValueError(f"Parameter archive is missing expected arrays: {', '.join(missing[:10])}{suffix}")
         for i, name in enumerate(names):
             arr = z[f"arr_{i}"]
             if tuple(arr.shape) != shapes[name]:
                 raise ValueError(f"{name}: shape {arr.shape} != {shapes[name]}")
             if dtype == "bfloat16":
-                t = torch.from_numpy(arr.view(np.int16).copy()).view(torch.bfloat16)
+                t = torch.from_numpy(np.ascontiguousarray(arr).view(np.int16).copy()).view(torch.bfloat16)
             else:
-                t = torch.from_numpy(arr.astype(np.float16))
+                t = torch.from_numpy(np.ascontiguousarray(arr).astype(np.float16))
             out.append(t.to(device=device, dtype=td))
     return out, dtype

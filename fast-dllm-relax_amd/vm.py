@@ -54,6 +54,16 @@ class HipVM:
             raise RuntimeError("libfdllm parameter order differs from params.param_names")
         self.bind(params)
 
+    @classmethod
+    def from_artifact(cls, artifact_dir, *, max_rows: int = 64, device: str = "cuda", **config_overrides) -> "HipVM":
+        """A function table over the weights of a reference artifact directory (the params npz, names,
+        dtype and KV-cache manifest of scripts/export_cuda.py; runners.py:597-639 loads the same files)."""
+        from .params import config_from_artifact, load_artifact
+
+        cfg = config_from_artifact(artifact_dir, **config_overrides)
+        params, dtype = load_artifact(artifact_dir, cfg, device=device)
+        return cls(cfg, params, dtype=dtype, max_rows=max_rows)
+
     def bind(self, params: list[torch.Tensor]) -> None:
         names = param_names(self.cfg)
         if len(params) != len(names):

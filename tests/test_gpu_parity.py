@@ -265,3 +265,23 @@ def test_prefill_attention_configs_agree(wide2, monkeypatch):
         vm.close()
     for hpw in (2, 3, 6):
         np.testing.assert_array_equal(outs[hpw], outs[1])
+
+
+def test_vm_from_artifact_equals_vm_from_tensors(tiny, tmp_path):
+    """HipVM.from_artifact (the reference artifact's weight files) binds exactly the weights it was
+    written from: a stateless forward is bit-identical."""
+    from fast_dllm_relax_amd import params as P
+    from fast_dllm_relax_amd.config import FastDLLMConfig
+    from fast_dllm_relax_amd.vm import HipVM
+
+    ref, vm = tiny
+    cfg = FastDLLMConfig(**TINY)
+    tensors = P.from_numpy(ref.p, cfg, dtype="bfloat16")
+    P.save_artifact(tmp_path, cfg, tensors, "bfloat16")
+    log("case: HipVM.from_artifact vs HipVM(tensors)")
+    vm2 = HipVM.from_artifact(tmp_path, max_rows=64)
+    ids = _dev_ids(np.random.default_rng(14).integers(0, TINY["vocab_size"] - 1, 64))
+    a = to_np(vm.forward_hidden(vm.embed(ids)[None], None))
+    b = to_np(vm2.forward_hidden(vm2.embed(ids)[None], None))
+    vm2.close()
+    np.testing.assert_array_equal(a, b)
