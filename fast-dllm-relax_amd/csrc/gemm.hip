@@ -157,10 +157,10 @@ GemmShape gemm_shape(int cfg) {
 }
 
 // large-M kernel configurations (rows x columns per workgroup)
-using MmSmall = MmCfg<4, 2, 4, 2, 2>;  // 64 x 128, weights two stages ahead
-using MmWide = MmCfg<4, 4, 4, 2, 1>;   // 64 x 256
-using MmWideD = MmCfg<4, 4, 4, 2, 2>;  // 64 x 256, weights two stages ahead
-using MmBig = MmCfg<8, 2, 8, 2, 1>;    // 128 x 256, 8 waves
+using MmSmall = MmCfg<4, 2, 1, 4, 2, 2>;  // 64 x 128, weights two stages ahead
+using MmWide = MmCfg<4, 4, 1, 4, 2, 1>;   // 64 x 256
+using MmWideD = MmCfg<4, 4, 1, 4, 2, 2>;  // 64 x 256, weights two stages ahead
+using MmBig = MmCfg<8, 2, 1, 8, 2, 1>;    // 128 x 256, 8 waves
 enum MmId : int { MM_SMALL = 0, MM_WIDE = 1, MM_WIDE_D = 2, MM_BIG = 3 };
 struct MmInfo { int bm, bn_tiles, kss; };
 template <class M> constexpr MmInfo mm_info_of() { return MmInfo{M::bm, M::bn_tiles, M::kss}; }
@@ -263,7 +263,7 @@ static hipError_t launch_os(const GemmP& a, const GemmPlan& p, hipStream_t st) {
 
 template <int DT, int EPI, int XF, class M>
 static hipError_t launch_mm_cfg(const GemmP& a, const GemmPlan& p, hipStream_t st) {
-  auto kern = gemm_mm_kernel<DT, EPI, XF, M::mf, M::tpw, M::nw, M::kss, M::wd>;
+  auto kern = gemm_mm_kernel<DT, EPI, XF, M::mf, M::tpw, M::nwm, M::nwn, M::kss, M::wd>;
   const int total = p.nbm * p.nbn, per = (total + 7) / 8;
   const size_t lds = EPI == EPI_LOGITS ? std::max(M::lds, M::lds_logits) : M::lds;
   hipLaunchKernelGGL(kern, dim3(8 * per, p.ksplit), dim3(64 * M::nw), lds, st, a, p.nbm, p.nbn);

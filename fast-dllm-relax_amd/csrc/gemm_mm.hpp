@@ -1,10 +1,11 @@
 // Large-M GEMM over packed weights (prefill, stateless forward, batched steps): Y[M, N] = X[M, K] . W[N, K]^T
 // on MFMA 16x16x32 with fp32 accumulation, same epilogues and rounding points as the skinny kernels.
 //
-// A workgroup computes a block of BM = 16 MF rows by BN = 16 TPW NW columns with NW waves side by side
-// along n: wave w owns TPW consecutive 16-row weight tiles and every row block of the workgroup, so each
-// packed weight block is read once per workgroup, straight from global memory into registers (it is
-// already in operand order), and each activation fragment is read from LDS by all NW waves.
+// A workgroup computes a block of BM = 16 MF NWM rows by BN = 16 TPW NWN columns with NWM x NWN waves:
+// wave (wm, wn) owns TPW consecutive 16-row weight tiles and MF row blocks.  Weight blocks go straight
+// from global memory into registers (they are already in operand order); with NWM = 2 two waves load
+// each (the second mostly from L1), in exchange for each wave reading only its own MF activation
+// fragments from LDS instead of all of them.
 //
 // The k loop runs in stages of KSS k steps.  Activations pass through two LDS buffers in MFMA fragment
 // order: while stage s is multiplied out of one buffer, stage s + 1 is loaded into registers and then
@@ -24,17 +25,19 @@
 
 namespace fdllm {
 
-template <int DT, int EPI, int XF, int MF, int TPW, int NW, int KSS, int WD>
-__global__ __launch_bounds__(64 * NW) void gemm_mm_kernel(GemmP a, int nbm, int nbn) {
-  constexpr int BM = 16 * MF;
+template <int DT, int EPI, int XF, int MF, int TPW, int NWM, int NWN, int KSS, int WD>
+__global__ __launch_bounds__(64 * NWM * NWN) void gemm_mm_kernel(GemmP a, int nbm, int nbn) {
+  constexpr int NW = NWM * NWN;
+  constexpr int MFT = MF * NWM;                // row blocks of the workgroup
+  constexpr int BM = 16 * MFT;
   constexpr int NT = 64 * NW;                  // threads
-  constexpr int XCH = KSS * MF * 64 / NT;      // activation chunks (16 bytes) per thread per stage
-  static_assert(KSS * MF % NW == 0, "whole fragment blocks per wave");
+  constexpr int XCH = KSS * MFT * 64 / NT;     // activation chunks (16 bytes) per thread per stage
+  static_assert(KSS * MFT % NW == 0, "whole fragment blocks per wave");
   static_assert(NT % BM == 0 && BM <= NT, "threads per row for the norm prologue");
   static_assert(EPI != EPI_SILU_PAIR || TPW % 2 == 0, "gate/up pairs stay within a wave");
-  static_assert(EPI != EPI_LOGITS || TPW * NW == 16, "one 256-column confidence tile per block column");
+  static_assert(EPI != EPI_LOGITS || TPW * NWN == 16, "one 256-column confidence tile per block column");
   extern __shared__ __align__(16) unsigned char smem[];
-  u32x4* xl = reinterpret_cast<u32x4*>(smem);  // [2][KSS][MF][64]
+  u32x4* xl = reinterpret_cast<u32x4*>(smem);  // [2][KSS][MFT][64]
   __shared__ float inv_s[BM];
 
   const int total = nbm * nbn;
@@ -44,9 +47,11 @@ __global__ __launch_bounds__(64 * NW) void gemm_mm_kernel(GemmP a, int nbm, int 
   const int nb = logical / nbm, mb = logical - nb * nbm;
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wm = w / NWN, wn = w - wm * NWN;
   const int lr = lane & 15, lg = lane >> 4;
   const int m0 = mb * BM, mlast = a.M - 1;
-  const int t0 = (nb * NW + w) * TPW;
+  const int f0 = wm * MF;                      // this wave's first row block
+  const int t0 = (nb * NWN + wn) * TPW;
   const int nst = a.KS / KSS / (int)gridDim.y;  // stages of this k split
   const int kb = (int)blockIdx.y * nst * KSS;   // its first k step
 
@@ -69,7 +74,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_mm_kernel(GemmP a, int nbm, int 
   auto xload = [&](int st) {
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
-      const int blk = w + NW * i, ks = blk / MF, f = blk - ks * MF;
+      const int blk = w + NW * i, ks = blk / MFT, f = blk - ks * MFT;
       const int m = min(m0 + 16 * f + lr, mlast);
       const int k = 32 * (kb + st * KSS + ks) + 8 * lg;
       xr[i] = *reinterpret_cast<const u32x4*>(a.X + (size_t)m * a.ldx + k);
@@ -78,13 +83,13 @@ __global__ __launch_bounds__(64 * NW) void gemm_mm_kernel(GemmP a, int nbm, int 
   auto xstore = [&](int buf, int st) {
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
-      const int blk = w + NW * i, ks = blk / MF, f = blk - ks * MF;
+      const int blk = w + NW * i, ks = blk / MFT, f = blk - ks * MFT;
       u32x4 v = xr[i];
       if constexpr (XF == XF_RMS) {
         const int k = 32 * (kb + st * KSS + ks) + 8 * lg;
         v = xform<DT, XF>(v, *reinterpret_cast<const u32x4*>(a.nw + k), inv_s[16 * f + lr]);
       }
-      xl[((buf * KSS + ks) * MF + f) * 64 + lane] = v;
+      xl[((buf * KSS + ks) * MFT + f) * 64 + lane] = v;
     }
   };
   // weight blocks: WD + 1 register buffers, stage s + WD requested while stage s is multiplied
@@ -108,7 +113,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_mm_kernel(GemmP a, int nbm, int 
     for (int ks = 0; ks < KSS; ++ks) {
       u32x4 b[MF];
 #pragma unroll
-      for (int f = 0; f < MF; ++f) b[f] = xl[((buf * KSS + ks) * MF + f) * 64 + lane];
+      for (int f = 0; f < MF; ++f) b[f] = xl[((buf * KSS + ks) * MFT + f0 + f) * 64 + lane];
 #pragma unroll
       for (int j = 0; j < TPW; ++j)
 #pragma unroll
@@ -144,7 +149,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_mm_kernel(GemmP a, int nbm, int 
     for (int j = 0; j < TPW; ++j)
 #pragma unroll
       for (int f = 0; f < MF; ++f) {
-        const int t = t0 + j, b = mb * MF + f;
+        const int t = t0 + j, b = mb * MFT + f0 + f;
         if (t < a.ntiles && b < nblk) part[(((size_t)blockIdx.y * a.ntiles + t) * nblk + b) * 64 + lane] = acc[j][f];
       }
     return;
@@ -162,7 +167,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_mm_kernel(GemmP a, int nbm, int 
     for (int j = 0; j < TPW; ++j)
 #pragma unroll
       for (int f = 0; f < MF; ++f) {
-        const int ml = 16 * f + lr, nl = 16 * (w * TPW + j) + 4 * lg, n = n0 + nl, m = m0 + ml;
+        const int ml = 16 * (f0 + f) + lr, nl = 16 * (wn * TPW + j) + 4 * lg, n = n0 + nl, m = m0 + ml;
         float v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = rnd<DT>(acc[j][f][i]);
@@ -223,7 +228,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_mm_kernel(GemmP a, int nbm, int 
 #pragma unroll
       for (int f = 0; f < MF; ++f) {
         const f32x4 v[2] = {acc[2 * p][f], acc[2 * p + 1][f]};
-        os_epilogue<DT, EPI, 2, false>(a, v, m0 + 16 * f + lr, t0 + 2 * p, lg);
+        os_epilogue<DT, EPI, 2, false>(a, v, m0 + 16 * (f0 + f) + lr, t0 + 2 * p, lg);
       }
   } else {
 #pragma unroll
@@ -231,7 +236,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_mm_kernel(GemmP a, int nbm, int 
 #pragma unroll
       for (int f = 0; f < MF; ++f) {
         const f32x4 v[1] = {acc[j][f]};
-        os_epilogue<DT, EPI, 1, false>(a, v, m0 + 16 * f + lr, t0 + j, lg);
+        os_epilogue<DT, EPI, 1, false>(a, v, m0 + 16 * (f0 + f) + lr, t0 + j, lg);
       }
   }
 }
@@ -258,12 +263,12 @@ __global__ __launch_bounds__(256) void gemm_mm_split_epilogue_kernel(GemmP a, in
   os_epilogue<DT, EPI, TPU, false>(a, v, 16 * b + lr, t, lg);
 }
 
-template <int MF, int TPW, int NW, int KSS, int WD>
+template <int MF, int TPW, int NWM, int NWN, int KSS, int WD>
 struct MmCfg {
-  static constexpr int mf = MF, tpw = TPW, nw = NW, kss = KSS, wd = WD;
-  static constexpr int bm = 16 * MF, bn_tiles = TPW * NW;
-  static constexpr size_t lds = 2ull * KSS * MF * 64 * 16;
-  static constexpr size_t lds_logits = (size_t)16 * MF * 256 * 2;  // EPI_LOGITS tile [BM][256] u16
+  static constexpr int mf = MF, tpw = TPW, nwm = NWM, nwn = NWN, nw = NWM * NWN, kss = KSS, wd = WD;
+  static constexpr int bm = 16 * MF * NWM, bn_tiles = TPW * NWN;
+  static constexpr size_t lds = 2ull * KSS * MF * NWM * 64 * 16;
+  static constexpr size_t lds_logits = (size_t)16 * MF * NWM * 256 * 2;  // EPI_LOGITS tile [BM][256] u16
 };
 
 }  // namespace fdllm
