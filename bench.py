@@ -85,6 +85,9 @@ def main() -> int:
     ap.add_argument("--no-prefix512", action="store_true")
     ap.add_argument("--no-long-context", action="store_true")
     ap.add_argument("--cpu-iters", type=int, default=2)
+    ap.add_argument("--profile-target", choices=("batched", "prefill8192"),
+                    help="only run a short workload for rocprofv3: 'batched' = config 4's 512-row and 128-row "
+                         "batched steps (5 each), 'prefill8192' = two 8192-row prefills")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the dominant kernel over the 28 layers and a plain 256 MiB copy (for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -100,6 +103,8 @@ def main() -> int:
     import __graft_entry__
 
     __graft_entry__.load_package()
+    if args.profile_target is not None:
+        return profile_target(args.profile_target)
     from fast_dllm_relax_amd import _lib
     from fast_dllm_relax_amd.config import DEFAULT_MASK_ID, fast_dllm_v2_1p5b
     from fast_dllm_relax_amd.params import random_params_torch
@@ -422,6 +427,49 @@ def batched_bench(args) -> dict:
         f"partial {part_ms:.3f} ms")
     vm.close()
     return res
+
+
+def profile_target(which: str) -> int:
+    """Short workloads for rocprofv3 (the commands in profiles/ name them)."""
+    import numpy as np
+    import torch
+
+    from fast_dllm_relax_amd.config import fast_dllm_v2_1p5b
+    from fast_dllm_relax_amd.params import random_params_torch
+    from fast_dllm_relax_amd.runtime import _embed, batched_shifted_confidence, build_prefix_cache_from_ids
+    from fast_dllm_relax_amd.vm import HipVM
+
+    if which == "prefill8192":
+        cfg = fast_dllm_v2_1p5b()
+        vm = HipVM(cfg, random_params_torch(cfg, 4, dtype="bfloat16", device="cuda"), dtype="bfloat16", max_rows=8192)
+        ids = np.random.default_rng(4).integers(0, 150000, 8192).tolist()
+        for i in range(2):
+            build_prefix_cache_from_ids(vm, ids, block_size=32, capacity=8192 + 64)
+            torch.cuda.synchronize()
+            log(f"profile target: prefill {i + 1}/2 done")
+        return 0
+    # config 4's batched steps over the config's prefixes (fp16, seed 3)
+    cfg = fast_dllm_v2_1p5b(tie_word_embeddings=False)
+    vm = HipVM(cfg, random_params_torch(cfg, BATCH_SEED, dtype="float16", device="cuda", lm_head_std=0.5),
+               dtype="float16", max_rows=1024)
+    rng = np.random.default_rng(BATCH_SEED)
+    prefixes = [int(p) for p in rng.integers(128, 1025, BATCH_SEQS)]
+    a0s = [p - p % 32 for p in prefixes]
+    shape = (cfg.num_hidden_layers, BATCH_SEQS, max(a0s) + 32, cfg.num_key_value_heads, cfg.head_dim)
+    k = torch.zeros(shape, dtype=torch.float16, device="cuda")
+    v = torch.zeros_like(k)
+    for b in range(BATCH_SEQS):
+        vm.build_prefix_cache_seq(_embed(vm, rng.integers(0, 150000, a0s[b]).tolist()), None, k, v, b)
+    emb = _embed(vm, rng.integers(0, 150000, BATCH_SEQS * 32).tolist()).view(BATCH_SEQS, 32, -1)
+    emb8 = emb[:, 8:16].contiguous()
+    off = torch.tensor(a0s, dtype=torch.int32, device="cuda")
+    for _ in range(5):
+        batched_shifted_confidence(vm, vm.forward_cached_batch(emb, k, v, off, a0s))
+    for _ in range(5):
+        batched_shifted_confidence(vm, vm.forward_block_partial_batch(8, emb8, k, v, off + 8, a0s))
+    torch.cuda.synchronize()
+    log("profile target: 5 full + 5 partial batched steps done")
+    return 0
 
 
 def traffic_probe(vm, cfg) -> int:
