@@ -285,3 +285,32 @@ def test_vm_from_artifact_equals_vm_from_tensors(tiny, tmp_path):
     b = to_np(vm2.forward_hidden(vm2.embed(ids)[None], None))
     vm2.close()
     np.testing.assert_array_equal(a, b)
+
+
+def test_long_context_prefill_and_cached_step(tiny):
+    """A prefix past 64 key chunks of 128 (P = 8200, ragged): the prefill kernel over 8200 rows, then a
+    32-row cached step whose attention takes the split loop kernel (more than 64 chunks), vs the oracle."""
+    ref, vm = tiny
+    from oracle.model import OracleModel
+
+    ref32 = OracleModel(ref.cfg, ref.p, "float32")
+    rng = np.random.default_rng(15)
+    P, R = 8200, 32
+    cap = P + 64
+    ids = _ids(rng, P + R, TINY["vocab_size"])
+    L, nkv, hd = TINY["num_hidden_layers"], TINY["num_key_value_heads"], TINY["head_dim"]
+    outs = {}
+    for name, model in (("bf16", ref), ("f32", ref32)):
+        kc = np.zeros((L, 1, cap, nkv, hd), np.float32)
+        vc = kc.copy()
+        model.build_prefix_cache(model.embed(ids[:P])[None], build_prefix_block_attention_bias(0, P, block_size=32),
+                                 kc, vc)
+        outs[name] = (model.forward_cached(model.embed(ids[P:])[None], kc, vc, P, P), kc)
+    k = torch.zeros((L, 1, cap, nkv, hd), dtype=torch.bfloat16, device="cuda")
+    v = torch.zeros_like(k)
+    log(f"case: build_prefix_cache P={P}")
+    vm.build_prefix_cache(vm.embed(_dev_ids(ids[:P]))[None], None, k, v)
+    bf16_parity("long prefix K", to_np(k)[:, :, :P], outs["bf16"][1][:, :, :P], outs["f32"][1][:, :, :P])
+    log(f"case: forward_cached R={R} over {P + R} keys")
+    h = vm.forward_cached(vm.embed(_dev_ids(ids[P:]))[None], k, v, _off(P), P)
+    bf16_parity("long-context hidden", to_np(h), outs["bf16"][0], outs["f32"][0])
