@@ -22,7 +22,8 @@ EXPORTS = (
     "fdllm_forward_cached", "fdllm_forward_block_partial", "fdllm_forward_block_partial_rp0",
     "fdllm_forward_block_partial_rp8", "fdllm_forward_block_partial_rp16", "fdllm_forward_block_partial_rp24",
     "fdllm_forward_cached_batch", "fdllm_forward_block_partial_batch", "fdllm_build_prefix_cache_seq",
-    "fdllm_get_confidence", "fdllm_confidence_from_logits", "fdllm_bench_op", "fdllm_last_error",
+    "fdllm_get_confidence", "fdllm_confidence_from_logits", "fdllm_bench_op", "fdllm_persistent_steps",
+    "fdllm_last_error",
 )
 
 OP_QKV, OP_O_PROJ, OP_GATE_UP, OP_DOWN, OP_ATTENTION, OP_LM_HEAD_CONFIDENCE = range(6)
@@ -63,6 +64,7 @@ _SIGS = {
     "fdllm_get_confidence": ([_P, _P, _I, _P, _P, _P, _P], _I),
     "fdllm_confidence_from_logits": ([_P, _P, _I, _I, _I, _P, _P, _P], _I),
     "fdllm_bench_op": ([_P, _I, _I, _I, _I, _P, _P, _I, _I, _P], _I),
+    "fdllm_persistent_steps": ([_P], ctypes.c_longlong),
     "fdllm_last_error": ([], ctypes.c_char_p),
 }
 

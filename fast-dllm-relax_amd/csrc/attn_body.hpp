@@ -285,21 +285,89 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
 // one query (its softmax statistics stay in-lane) and the row reductions use row-swap permutes.  The
 // key parts are merged in LDS; with key splits (gridDim.z > 1) each workgroup stores its partial and
 // attn_merge_kernel, launched next on the stream, combines them across many workgroups.
-// Body of one workgroup (query-tile group bx, kv head by, key chunk bz).  With COH the qkv loads and the
-// output stores are agent-scope, for a launch in which other workgroups produce the qkv rows; the
-// kernel below uses plain accesses.
+// Body of one workgroup (query-tile group bx, kv head by, key chunk bz; tid = threadIdx.x), in two phases:
+// attn_chunk_load requests the chunk's K/V rows into registers (AttnChunkRegs) and attn_chunk_compute
+// does the rest.  PART selects which rows a load call requests: CHUNK_ALL every row, CHUNK_CACHE only
+// rows read from the cache (they do not depend on this call's qkv projection, so a persistent launch
+// requests them before it waits for the projection) and CHUNK_WINDOW only this call's own rows (from
+// qkv).  With COH the qkv loads and the output stores are agent-scope, for a launch in which other
+// workgroups produce the qkv rows; the kernel below uses plain accesses.
+enum ChunkPart : int { CHUNK_ALL = 0, CHUNK_CACHE = 1, CHUNK_WINDOW = 2 };
+
+template <int QPW, int KH, int CH>
+struct AttnChunkRegs {
+  static constexpr int NT = 64 * QPW * KH;
+  static constexpr int KIT = (CH * 8 + NT - 1) / NT;        // K items (rotation-pair chunks) per thread
+  static constexpr int VIT = ((CH / 4) * 16 + NT - 1) / NT;  // V items (key quad x dim chunk) per thread
+  u32x4 klo[KIT], khi[KIT], vv[VIT][4];
+};
+
+// Item -> (key, chunk) maps: 16 consecutive lanes take 16 keys of one K chunk, and 32 consecutive lanes
+// take 16 key quads x 2 dim chunks of V, so the LDS stores of attn_chunk_compute hit 64 distinct banks
+// per pass (rows are 68 dwords apart, 4 banks on).  Rows past kend read row kbeg and are masked or
+// zeroed later.
+template <int QPW, int KH, int CH, bool COH, int PART>
+__device__ __forceinline__ void attn_chunk_load(const AttnP& a, int by, int bz, AttnChunkRegs<QPW, KH, CH>& R, int tid) {
+  typedef AttnChunkRegs<QPW, KH, CH> Regs;
+  constexpr int NT = Regs::NT, KIT = Regs::KIT, VIT = Regs::VIT;
+  const int g = by;
+  const size_t krow = (size_t)a.nkv * HD;
+  const int kbeg = bz * a.chunk;
+  const int kend = min(kbeg + a.chunk, a.Lk);
+  const u16* kq_base = a.qkv + a.nq * HD + g * HD;
+  const u16* vq_base = a.qkv + (a.nq + a.nkv) * HD + g * HD;
+#pragma unroll
+  for (int it = 0; it < KIT; ++it) {
+    const int item = tid + it * NT;
+    const int j = min((item & 15) + 16 * (item >> 7), CH - 1), p = (item >> 4) & 7;
+    int key = kbeg + j;
+    key = key < kend ? key : kbeg;
+    const bool win = key >= a.ws && key < a.ws + a.rows;
+    if (win) {
+      if (PART != CHUNK_CACHE) {
+        const u16* src = kq_base + (size_t)(key - a.ws) * a.ldq;
+        R.klo[it] = ld16<COH>(src + 8 * p);
+        R.khi[it] = ld16<COH>(src + 64 + 8 * p);
+      }
+    } else if (PART != CHUNK_WINDOW) {
+      const u16* src = a.kc + key * krow + g * HD;
+      R.klo[it] = *reinterpret_cast<const u32x4*>(src + 8 * p);
+      R.khi[it] = *reinterpret_cast<const u32x4*>(src + 64 + 8 * p);
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < VIT; ++it) {
+    const int item = tid + it * NT;
+    const int kq = min((item & 15) + 16 * (item >> 8), CH / 4 - 1), dc = (item >> 4) & 15;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      int key = kbeg + 4 * kq + qq;
+      key = key < kend ? key : kbeg;
+      const bool win = key >= a.ws && key < a.ws + a.rows;
+      if (win) {
+        if (PART != CHUNK_CACHE) R.vv[it][qq] = ld16<COH>(vq_base + (size_t)(key - a.ws) * a.ldq + 8 * dc);
+      } else if (PART != CHUNK_WINDOW) {
+        R.vv[it][qq] = *reinterpret_cast<const u32x4*>(a.vc + key * krow + g * HD + 8 * dc);
+      }
+    }
+  }
+}
+
 template <int DT, int QPW, int KH, int CH, int MASK, bool COH>
-__device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, int bz, unsigned char* smem) {
-  constexpr int NT = 64 * QPW * KH;
-  constexpr int KIT = (CH * 8 + NT - 1) / NT;        // K items (rotation-pair chunks) per thread
-  constexpr int VIT = ((CH / 4) * 16 + NT - 1) / NT;  // V items (key quad x dim chunk) per thread
+__device__ __forceinline__ void attn_chunk_compute(const AttnP& a, int bx, int by, int bz, unsigned char* smem,
+                                                   AttnChunkRegs<QPW, KH, CH>& R, int tid) {
+  typedef AttnChunkRegs<QPW, KH, CH> Regs;
+  constexpr int NT = Regs::NT, KIT = Regs::KIT, VIT = Regs::VIT;
   constexpr int VLDC = CH + 8;                        // u16 stride of a transposed V row
   constexpr int DT16 = HD / 16;
   static_assert(CH % (32 * KH) == 0, "each key part must be whole 32-key blocks");
   u16* kbuf = reinterpret_cast<u16*>(smem);           // [CH][KLD]
   u16* vbuf = kbuf + CH * KLD;                        // [HD][VLDC]
+  u32x4 (&klo)[KIT] = R.klo;
+  u32x4 (&khi)[KIT] = R.khi;
+  u32x4 (&vv)[VIT][4] = R.vv;
 
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = tid & 63, w = tid >> 6;
   const int qw = w % QPW, kh = w / QPW;
   const int lr = lane & 15, lg = lane >> 4;
   const int g = by, c = bz;
@@ -310,44 +378,6 @@ __device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, 
   const int kbeg = c * a.chunk;
   const int kend = min(kbeg + a.chunk, a.Lk);
   const bool writer = bx == 0;
-  const u16* kq_base = a.qkv + a.nq * HD + g * HD;
-  const u16* vq_base = a.qkv + (a.nq + a.nkv) * HD + g * HD;
-
-  // ---- request the whole chunk (rows past kend read row kbeg and are masked or zeroed later) ----
-  // Item -> (key, chunk) maps: 16 consecutive lanes take 16 keys of one K chunk, and 32 consecutive
-  // lanes take 16 key quads x 2 dim chunks of V, so the LDS stores below hit 64 distinct banks per
-  // pass (rows are 68 dwords apart, 4 banks on).
-  u32x4 klo[KIT], khi[KIT], vv[VIT][4];
-#pragma unroll
-  for (int it = 0; it < KIT; ++it) {
-    const int item = threadIdx.x + it * NT;
-    const int j = min((item & 15) + 16 * (item >> 7), CH - 1), p = (item >> 4) & 7;
-    int key = kbeg + j;
-    key = key < kend ? key : kbeg;
-    const bool win = key >= a.ws && key < a.ws + a.rows;
-    if (win) {
-      const u16* src = kq_base + (size_t)(key - a.ws) * a.ldq;
-      klo[it] = ld16<COH>(src + 8 * p);
-      khi[it] = ld16<COH>(src + 64 + 8 * p);
-    } else {
-      const u16* src = a.kc + key * krow + g * HD;
-      klo[it] = *reinterpret_cast<const u32x4*>(src + 8 * p);
-      khi[it] = *reinterpret_cast<const u32x4*>(src + 64 + 8 * p);
-    }
-  }
-#pragma unroll
-  for (int it = 0; it < VIT; ++it) {
-    const int item = threadIdx.x + it * NT;
-    const int kq = min((item & 15) + 16 * (item >> 8), CH / 4 - 1), dc = (item >> 4) & 15;
-#pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
-      int key = kbeg + 4 * kq + qq;
-      key = key < kend ? key : kbeg;
-      const bool win = key >= a.ws && key < a.ws + a.rows;
-      vv[it][qq] = win ? ld16<COH>(vq_base + (size_t)(key - a.ws) * a.ldq + 8 * dc)
-                       : *reinterpret_cast<const u32x4*>(a.vc + key * krow + g * HD + 8 * dc);
-    }
-  }
 
   // this lane's query row (qi = 16 qt + lr), RoPE'd in registers while the chunk is in flight
   const int qi = qt * 16 + lr;
@@ -369,7 +399,7 @@ __device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, 
   // ---- stage: K rows (window rows RoPE'd and appended to the cache), V transposed ----
 #pragma unroll
   for (int it = 0; it < KIT; ++it) {
-    const int item = threadIdx.x + it * NT;
+    const int item = tid + it * NT;
     if (item >= CH * 8) break;
     const int j = (item & 15) + 16 * (item >> 7), p = (item >> 4) & 7;
     const int key = kbeg + j;
@@ -389,7 +419,7 @@ __device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, 
   }
 #pragma unroll
   for (int it = 0; it < VIT; ++it) {
-    const int item = threadIdx.x + it * NT;
+    const int item = tid + it * NT;
     if (item >= (CH / 4) * 16) break;
     const int kq = (item & 15) + 16 * (item >> 8), dc = (item >> 4) & 15;
 #pragma unroll
@@ -539,6 +569,13 @@ __device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, 
     for (int dt = 0; dt < DT16; ++dt) stf4<COH>(reinterpret_cast<f32x4*>(pp) + dt * 64 + lane, o[dt]);
     if (lg == 0) stf2<COH>(pp + 16 * HD + 2 * lr, f32x2_t{Mq, Lq});
   }
+}
+
+template <int DT, int QPW, int KH, int CH, int MASK, bool COH>
+__device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, int bz, unsigned char* smem) {
+  AttnChunkRegs<QPW, KH, CH> R;
+  attn_chunk_load<QPW, KH, CH, COH, CHUNK_ALL>(a, by, bz, R, threadIdx.x);
+  attn_chunk_compute<DT, QPW, KH, CH, MASK, COH>(a, bx, by, bz, smem, R, threadIdx.x);
 }
 
 // Batched call: the view of sequence b (its rows, cache, window and split partials) in a, a copy of the

@@ -84,6 +84,20 @@ struct fdllm_ctx {
   int down_split = 10;    // cross-workgroup k splits of the down projection (largest divisor of K/32 <= this)
   int mm_target_wgs = 256;  // large-M GEMM: split k while the launch has fewer workgroups than this
   int mm_min_stages = 8;    // ... into splits of at least this many stages
+  // the persistent cached step (step_body.hpp)
+  bool step_on = false;                // FDLLM_PERSISTENT=1 turns it on (measured slower than the kernels)
+  bool step_check = false;             // FDLLM_STEP_CHECK=1: wait for every launch and check its status
+  int step_attn_target = 0;            // attention workgroups aimed for (0: attn_target)
+  int step_grid = 0;                   // workgroups of the launch (compute units, at most 256)
+  long long step_limit = 0;            // wall-clock ticks a barrier wait may take
+  StepLayerW* step_layers = nullptr;   // device table of the layers' weights
+  unsigned* step_sync = nullptr;       // barrier / arrival counters, abort flag
+  size_t step_sync_words = 0;
+  unsigned* step_status = nullptr;     // host-visible (pinned, mapped) abort word
+  unsigned* step_status_dev = nullptr;
+  long long step_launches = 0;         // persistent steps run (fdllm_persistent_steps)
+  std::string step_trace_path;         // FDLLM_STEP_TRACE: write each launch's barrier timeline there
+  unsigned long long* step_trace = nullptr;
 
   int qkv_dim() const { return (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim; }
   int q_dim() const { return cfg.num_attention_heads * cfg.head_dim; }
@@ -247,6 +261,85 @@ int run_attention(fdllm_ctx* c, int rows, uint16_t* kc, uint16_t* vc, int ws, in
   return FDLLM_OK;
 }
 
+// The layers of a one-sequence cached step (at most 32 rows, no mask) as one persistent cooperative launch
+// (step_body.hpp), when the model and the call fit its plan.  *done tells whether it ran; when it did
+// not, the caller runs the per-operator kernels.  h / ssq and the RoPE table must hold the call's rows.
+int try_step(fdllm_ctx* c, int rows, uint16_t* kbase, uint16_t* vbase, size_t layer_stride, int write_start,
+             int attend_len, hipStream_t st, bool* done) {
+  *done = false;
+  if (!c->step_on || rows > 32) return FDLLM_OK;
+  const fdllm_config& f = c->cfg;
+  StepP p{};
+  p.layers = c->step_layers; p.L = f.num_hidden_layers;
+  p.H = f.hidden_size; p.I = f.intermediate_size; p.nq = f.num_attention_heads; p.nkv = f.num_key_value_heads;
+  p.qkv_dim = c->qkv_dim(); p.q_dim = c->q_dim(); p.eps = f.rms_norm_eps; p.M = rows;
+  p.h = c->h; p.ssq = c->ssq; p.ssq_ld = c->ws_rows; p.qkv = c->qkv; p.attn = c->attn; p.act = c->act;
+  AttnP& a = p.at;
+  a.qkv = c->qkv; a.ldq = c->qkv_dim(); a.rows = rows; a.nq = p.nq; a.nkv = p.nkv; a.rope = c->rope;
+  a.ws = write_start; a.Lk = attend_len; a.scale = 1.0f / std::sqrt((float)f.head_dim); a.mask = 0; a.nseq = 1;
+  a.block = f.bd_size;
+  a.target_wgs = c->step_attn_target > 0 ? c->step_attn_target : c->attn_target;
+  const AttnPlan pl = attn_plan(rows, p.nq, p.nkv, attend_len, a.target_wgs);
+  if (!pl.chunked || pl.q_tiles_per_wg != 4 || pl.key_groups != 2) return FDLLM_OK;
+  a.S = pl.S; a.chunk = pl.chunk; a.out = c->attn;
+  p.qg = pl.qg;
+  p.kbase = kbase; p.vbase = vbase; p.layer_stride = (long long)layer_stride;
+  p.nt_q = c->qkv_dim() / 16; p.nt_o = f.hidden_size / 16; p.np_u = f.intermediate_size / 16;
+  // down: the one-shot kernel's tile groups and k split
+  GemmP dp = gemm_args(nullptr, d_tiles(c), f.hidden_size, f.intermediate_size, nullptr, f.intermediate_size, rows);
+  const GemmPlan dpl = gemm_plan(CFG_DOWN, dp, 1, c->mm_target_wgs, c->mm_min_stages);
+  if (dpl.kind != GK_ONESHOT || dpl.tiles_per_wg != STEP_DNT) return FDLLM_OK;
+  p.d_groups = dpl.groups; p.d_splits = dpl.ksplit;
+  p.sync.ctr = c->step_sync;
+  p.sync.la = c->step_sync + BAR_CTRS * BAR_STRIDE;
+  p.sync.abort_f = p.sync.la + 256 * BAR_STRIDE;
+  p.sync.status = c->step_status_dev;
+  p.sync.limit = c->step_limit;
+  const StepPlan sp = step_plan(p, c->step_grid);
+  if (!sp.ok || p.d_groups > 256) return FDLLM_OK;
+  if (a.S > 1) {
+    const int rc = ensure_floats(&c->apart, &c->apart_floats, attn_partial_floats(a));
+    if (rc) return rc;
+    a.part = c->apart;
+  }
+  {
+    const int rc = ensure_floats(&c->gpart, &c->gpart_floats, (size_t)p.d_groups * p.d_splits * STEP_DNT * 2 * 64 * 4);
+    if (rc) return rc;
+    p.dpart = c->gpart;
+  }
+  constexpr int kTraceBars = 256;
+  if (!c->step_trace_path.empty()) {
+    if (c->step_trace == nullptr) HIPCHK(hipMalloc((void**)&c->step_trace, (size_t)256 * kTraceBars * 16));
+    HIPCHK(launch_fill_u32((unsigned*)c->step_trace, (size_t)256 * kTraceBars * 4, 0u, st));
+    p.sync.trace = c->step_trace;
+    p.sync.trace_bars = kTraceBars;
+  }
+  HIPCHK(launch_fill_u32(c->step_sync, c->step_sync_words, 0u, st));
+  HIPCHK(launch_step(f.dtype, p, c->step_grid, sp.lds, st));
+  if (c->step_trace != nullptr && !c->step_trace_path.empty()) {
+    // timeline of this launch: header (grid, barriers per row, layers, merge stage), then the rows
+    std::vector<unsigned long long> tr((size_t)c->step_grid * kTraceBars * 2);
+    HIPCHK(hipMemcpyAsync(tr.data(), c->step_trace, tr.size() * 8, hipMemcpyDeviceToHost, st));
+    HIPCHK(hipStreamSynchronize(st));
+    if (FILE* fp = std::fopen(c->step_trace_path.c_str(), "wb")) {
+      const long long hdr[4] = {c->step_grid, kTraceBars, f.num_hidden_layers, a.S > 1 ? 1 : 0};
+      std::fwrite(hdr, sizeof(hdr), 1, fp);
+      std::fwrite(tr.data(), 8, tr.size(), fp);
+      std::fclose(fp);
+    }
+  }
+  if (c->step_check) {
+    HIPCHK(hipStreamSynchronize(st));
+    if (*(volatile unsigned*)c->step_status != 0u) {
+      *c->step_status = 0u;
+      return fail(FDLLM_EHIP, "persistent step aborted: a grid barrier wait timed out");
+    }
+  }
+  ++c->step_launches;
+  *done = true;
+  return FDLLM_OK;
+}
+
 // The decoder-layer loop (cuda.py:561-579 per layer, 639-666 for the model).
 //   per layer: qkv (RMSNorm on load, + bias) -> attention (RoPE, KV append, GQA) -> o_proj + residual
 //              -> gate_up (RMSNorm on load, SiLU * up) -> down + residual
@@ -262,6 +355,16 @@ int run_layers(fdllm_ctx* c, const void* x_in, int rows, uint16_t* kbase, uint16
   HIPCHK(launch_load_rows(f.dtype, (const uint16_t*)x_in, rows, H, c->h, c->ssq, ssq_ld, st));
   int rc = rope_table(c, rows, pos_dev, sb ? sb->rows : rows, st);
   if (rc) return rc;
+  if (sb == nullptr && mask == 0 && bias == nullptr) {
+    bool done = false;
+    rc = try_step(c, rows, kbase, vbase, layer_stride, write_start, attend_len, st, &done);
+    if (rc) return rc;
+    if (done) {
+      if (out != nullptr)
+        HIPCHK(launch_norm_rows(f.dtype, c->h, rows, H, c->ssq, ssq_ld, c->final_norm, f.rms_norm_eps, (uint16_t*)out, st));
+      return FDLLM_OK;
+    }
+  }
   const int dsplit = divisor_at_most(I / 32, c->down_split);
   for (int l = 0; l < f.num_hidden_layers; ++l) {
     const Layer& L = c->layers[l];
@@ -308,6 +411,13 @@ int cached_step(fdllm_ctx* c, const void* x, int rows, void* k, void* v, int cap
                 int64_t prefix_len, int write_rel, int attend_rel, void* out, void* stream) {
   int rc = check_ready(c);
   if (rc) return rc;
+  if (c->step_status != nullptr && *(volatile unsigned*)c->step_status != 0u) {
+    // an earlier persistent launch timed out at a barrier (its outputs are wrong): report it once and
+    // run the per-operator kernels from now on
+    *c->step_status = 0u;
+    c->step_on = false;
+    return fail(FDLLM_EHIP, "an earlier persistent step aborted (grid barrier timeout); its results are invalid");
+  }
   if (!x || !k || !v || !off || !out) return fail(FDLLM_EINVAL, "null tensor argument");
   if (rows <= 0) return fail(FDLLM_EINVAL, "active rows must be positive, got %d", rows);
   int64_t write_start = prefix_len + write_rel, attend_len = prefix_len + attend_rel;
@@ -413,6 +523,10 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   if (const char* e = std::getenv("FDLLM_DOWN_SPLIT")) c->down_split = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_MM_TARGET_WGS")) c->mm_target_wgs = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_MM_MIN_STAGES")) c->mm_min_stages = std::max(1, atoi(e));
+  if (const char* e = std::getenv("FDLLM_PERSISTENT")) c->step_on = atoi(e) != 0;
+  if (const char* e = std::getenv("FDLLM_STEP_CHECK")) c->step_check = atoi(e) != 0;
+  if (const char* e = std::getenv("FDLLM_STEP_ATTN_TARGET")) c->step_attn_target = std::max(0, atoi(e));
+  if (const char* e = std::getenv("FDLLM_STEP_TRACE")) c->step_trace_path = e;
   c->names.push_back("model.embed_tokens.weight");
   for (int i = 0; i < f.num_hidden_layers; ++i) {
     std::string p = "model.layers." + std::to_string(i);
@@ -431,6 +545,25 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
     return fail(FDLLM_EHIP, "workspace allocation failed: %s", hipGetErrorString(e));
   }
   c->zero_i32 = (int32_t*)(c->counters + c->n_counters);
+  if (c->step_on) {
+    // the persistent step needs a cooperative launch of one workgroup per compute unit
+    int coop = 0, cus = 0, khz = 0;
+    (void)hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, c->dev);
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->dev);
+    (void)hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, c->dev);
+    c->step_grid = std::min(cus, 256);
+    c->step_limit = (long long)std::max(khz, 1000) * 200;  // 0.2 s
+    c->step_sync_words = (size_t)BAR_CTRS * BAR_STRIDE + 256 * BAR_STRIDE + BAR_STRIDE;
+    if (!coop || c->step_grid < 64 ||
+        hipMalloc((void**)&c->step_sync, c->step_sync_words * 4) != hipSuccess ||
+        hipHostMalloc((void**)&c->step_status, 64, hipHostMallocMapped) != hipSuccess ||
+        hipHostGetDevicePointer((void**)&c->step_status_dev, c->step_status, 0) != hipSuccess) {
+      (void)hipGetLastError();
+      c->step_on = false;
+    } else {
+      *c->step_status = 0u;
+    }
+  }
   int rc = ensure_rows(c, std::max(1, f.max_rows));
   if (rc == FDLLM_OK) rc = ensure_stats(c, std::max(32, f.max_rows));
   if (rc == FDLLM_OK) {
@@ -449,8 +582,9 @@ void fdllm_destroy(fdllm_ctx* c) {
   if (!c) return;
   (void)hipDeviceSynchronize();
   for (void* p : {c->ws, (void*)c->gpart, (void*)c->apart, c->stats, (void*)c->counters, (void*)c->packed,
-                  (void*)c->rope})
+                  (void*)c->rope, (void*)c->step_layers, (void*)c->step_sync, (void*)c->step_trace})
     if (p) (void)hipFree(p);
+  if (c->step_status) (void)hipHostFree(c->step_status);
   delete c;
 }
 
@@ -478,6 +612,15 @@ int fdllm_bind_weights(fdllm_ctx* c, const void* const* ptrs, int n) {
   c->bound = false;
   int rc = pack_all(c);
   if (rc) return rc;
+  if (c->step_on) {
+    std::vector<StepLayerW> tab(c->cfg.num_hidden_layers);
+    for (int i = 0; i < c->cfg.num_hidden_layers; ++i) {
+      const Layer& L = c->layers[i];
+      tab[i] = StepLayerW{L.pqkv, L.bqkv, L.po, L.pgu, L.pd, L.ln_in, L.ln_post};
+    }
+    if (c->step_layers == nullptr) HIPCHK(hipMalloc((void**)&c->step_layers, tab.size() * sizeof(StepLayerW)));
+    HIPCHK(hipMemcpy(c->step_layers, tab.data(), tab.size() * sizeof(StepLayerW), hipMemcpyHostToDevice));
+  }
   c->bound = true;
   return FDLLM_OK;
 }
@@ -598,6 +741,8 @@ int fdllm_get_confidence(fdllm_ctx* c, const void* hidden, int rows, int32_t* id
                                    (float*)(base + c->stats_rows * T * 8), T, rows, ids, maxp, st));
   return FDLLM_OK;
 }
+
+long long fdllm_persistent_steps(const fdllm_ctx* c) { return c ? c->step_launches : 0; }
 
 int fdllm_bench_op(fdllm_ctx* c, int op, int rows, int layer, int iters, void* k, void* v, int cap, int attend_len,
                    void* stream) {

@@ -554,12 +554,12 @@ __global__ __launch_bounds__(512) void gemm_os_kernel(GemmP a) {
 }
 
 // Sum of the k-split partials of one unit per wave, in split order, then the epilogue (workgroup =
-// tile group bx of m-chunk bz).
+// tile group bx of m-chunk bz; tid = threadIdx.x).
 template <int DT, int EPI, int MT, int NT, bool COH>
-__device__ __forceinline__ void gemm_os_epilogue_body(const GemmP& a, int splits, int bx, int bz) {
+__device__ __forceinline__ void gemm_os_epilogue_body(const GemmP& a, int splits, int bx, int bz, int tid) {
   constexpr int TPU = EPI == EPI_SILU_PAIR ? 2 : 1;
   constexpr int UNITS = NT / TPU * MT;
-  const int lane = threadIdx.x & 63, u = threadIdx.x >> 6;
+  const int lane = tid & 63, u = tid >> 6;
   if (u >= UNITS) return;
   const int lr = lane & 15, lg = lane >> 4;
   const int ut = (u / MT) * TPU, umt = u % MT;
@@ -587,7 +587,7 @@ __device__ __forceinline__ void gemm_os_epilogue_body(const GemmP& a, int splits
 
 template <int DT, int EPI, int MT, int NT>
 __global__ __launch_bounds__(512) void gemm_os_epilogue_kernel(GemmP a, int splits) {
-  gemm_os_epilogue_body<DT, EPI, MT, NT, false>(a, splits, blockIdx.x, blockIdx.z);
+  gemm_os_epilogue_body<DT, EPI, MT, NT, false>(a, splits, blockIdx.x, blockIdx.z, threadIdx.x);
 }
 
 }  // namespace fdllm

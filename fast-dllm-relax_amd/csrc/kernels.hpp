@@ -107,4 +107,51 @@ AttnPlan attn_plan(int rows, int nq, int nkv, int Lk, int target_wgs);
 hipError_t launch_attention(int dt, const AttnP& a, hipStream_t st);
 size_t attn_partial_floats(const AttnP& a);
 
+// ---- the cached step as one persistent launch (step_body.hpp) -------------------------------------
+struct StepSync {
+  unsigned* ctr;      // 32 barrier counters, 32 words apart; zero at launch
+  unsigned* la;       // down tile-group arrival counters, 32 words apart; zero at launch
+  unsigned* abort_f;  // nonzero: some wait timed out; every workgroup leaves at its next wait
+  unsigned* status;   // host-visible word: set to 1 when the launch aborted
+  long long limit;    // wall-clock ticks a wait may take
+  unsigned long long* trace;  // optional: per workgroup and barrier n, the wall clock at arrival and release
+  int trace_bars;             // barriers per workgroup row of trace (slot 0: kernel start / end)
+};
+constexpr int BAR_CTRS = 32;
+constexpr int BAR_STRIDE = 32;  // words between counters (128 B)
+
+struct StepLayerW {
+  const uint16_t *pqkv, *bqkv, *po, *pgu, *pd, *ln_in, *ln_post;  // packed weights, bias, norm weights
+};
+
+// Upper bounds of the register-resident weight slices (step_plan checks a model fits them).
+constexpr int STEP_KPW = 6;    // k steps per wave of qkv / o_proj / gate_up (K <= 8 x 6 x 32 = 1536)
+constexpr int STEP_PAIRS = 3;  // gate_up tile pairs per workgroup
+constexpr int STEP_DNT = 4;    // down tiles per group (the one-shot kernel's grouping)
+constexpr int STEP_DKPW = 4;   // down k steps per wave (splits of at most 32 k steps)
+
+struct StepP {
+  const StepLayerW* layers; int L;
+  int H, I, nq, nkv, qkv_dim, q_dim;
+  float eps;
+  int M;                      // active rows (<= 32)
+  uint16_t* h; float* ssq; int ssq_ld;
+  uint16_t* qkv; uint16_t* attn; uint16_t* act;
+  float* dpart;               // down split partials
+  AttnP at;                   // attention of the call (kc / vc set per layer from the bases below)
+  uint16_t* kbase; uint16_t* vbase; long long layer_stride;
+  int qg;                     // query-tile groups of the attention (4 tiles each)
+  int nt_q, nt_o, np_u;       // qkv tiles, o_proj tiles, gate_up pairs
+  int d_groups, d_splits;     // down: tile groups of STEP_DNT tiles, k splits
+  StepSync sync;
+};
+// Whether the launch fits G co-resident workgroups and the kernel's register slices; the LDS it needs.
+// why: the reason when it does not.
+struct StepPlan { bool ok; const char* why; size_t lds; };
+StepPlan step_plan(const StepP& p, int G);
+size_t step_sync_words(const StepP& p);  // words of the sync area (barrier + arrival counters, abort)
+// A cooperative launch of G workgroups (all co-resident, or the launch fails).
+hipError_t launch_step(int dt, const StepP& p, int G, size_t lds, hipStream_t st);
+hipError_t launch_fill_u32(unsigned* p, size_t n, unsigned v, hipStream_t st);
+
 }  // namespace fdllm

@@ -155,6 +155,12 @@ int fdllm_confidence_from_logits(fdllm_ctx* ctx, const float* logits, int rows, 
 int fdllm_bench_op(fdllm_ctx* ctx, int op, int rows, int layer, int iters, void* k_cache, void* v_cache, int cap,
                    int attend_len, void* stream);
 
+/* Diagnostic; it has no counterpart in the reference.  Number of cached steps this context has run as one
+ * persistent launch (all layers in one cooperative kernel).  That path is off unless the environment
+ * variable FDLLM_PERSISTENT=1 is set when the context is created; otherwise every step runs the
+ * per-operator kernels. */
+long long fdllm_persistent_steps(const fdllm_ctx* ctx);
+
 /* Message of this thread's last failure ("" if none). */
 const char* fdllm_last_error(void);
 
