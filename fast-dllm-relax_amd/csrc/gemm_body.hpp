@@ -547,10 +547,145 @@ __device__ __forceinline__ void gemm_os_body(const GemmP& a, int bx, int by, int
   if (has_unit) os_epilogue<DT, EPI, TPU, COH>(a, v, m0 + 16 * umt + lr, t0 + ut, lg);
 }
 
+// The same one-shot GEMM with the activations loaded straight into registers: a wave multiplies only
+// its own k steps, so it loads only its own slice of the rows (MT 16-row blocks x its k steps, one
+// 16-byte load per fragment), all at once and before its weight slice, and RMS-normalises them in
+// registers.  Nothing goes through LDS but the 32 inverse RMS values and the wave sums, so the chain
+// from launch to the first MFMA is one memory round trip.  Same k partition, same per-wave MFMA order,
+// same wave-order sums and epilogues as gemm_os_body: the results are bit-identical.
+template <int DT, int EPI, int XF, int MT, int NT, int KPW>
+__device__ __forceinline__ void gemm_os_direct_body(const GemmP& a, int bx, int by, int bz, int gy, unsigned char* smem) {
+  constexpr int NW = 8;
+  constexpr int UNITS = (EPI == EPI_SILU_PAIR ? NT / 2 : NT) * MT;
+  static_assert(UNITS <= NW, "one epilogue unit per wave");
+  __shared__ float inv_s[32];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
+  const int m0 = bz * 32, mlast = a.M - 1;
+  const int t0 = bx * NT;
+  const int kb = by * a.kps;  // first k step of the split
+  const int kq = a.kps / NW, kr = a.kps % NW;
+  const int ws = kq * w + min(w, kr), wn = kq + (w < kr ? 1 : 0);  // this wave's k steps [ws, ws + wn)
+
+  // 1. the activation path first (its waits then do not cover the weight loads): the wave's fragments,
+  //    the rows' sums of squares and the norm weights of its k steps
+  u32x4 X[KPW][MT];
+#pragma unroll
+  for (int s = 0; s < KPW; ++s)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = min(m0 + 16 * mt + lr, mlast);
+      const int k = 32 * (kb + ws + min(s, max(wn, 1) - 1)) + 8 * lg;
+      X[s][mt] = *reinterpret_cast<const u32x4*>(a.X + (size_t)m * a.ldx + k);
+    }
+  float ssv[16];
+  if constexpr (XF == XF_RMS) {
+    if (threadIdx.x < 256) {
+      const int m = m0 + (threadIdx.x >> 3), pp = threadIdx.x & 7;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int t = pp + 8 * q;
+        ssv[q] = (m < a.M && t < a.ssq_tiles) ? a.ssq[(size_t)t * a.ssq_ld + m] : 0.f;
+      }
+    }
+  }
+  u32x4 NWv[XF == XF_RMS ? KPW : 1];
+  if constexpr (XF == XF_RMS) {
+#pragma unroll
+    for (int s = 0; s < KPW; ++s)
+      NWv[s] = *reinterpret_cast<const u32x4*>(a.nw + 32 * (kb + ws + min(s, max(wn, 1) - 1)) + 8 * lg);
+  }
+  // 2. the weight slice: KPW k steps x NT tiles per wave, all requested now
+  u32x4 A[KPW][NT];
+#pragma unroll
+  for (int s = 0; s < KPW; ++s)
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+      A[s][j] = __builtin_nontemporal_load(wblock(a.W, a.KS, t0 + j, kb + ws + min(s, max(wn, 1) - 1)));
+
+  // 3. 1 / rms of the chunk's rows (gemm_os_body's order), then the transform in registers
+  if constexpr (XF == XF_RMS) {
+    if (threadIdx.x < 256) {
+      float ss = 0.f;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) ss += ssv[q];
+      const int m = m0 + (threadIdx.x >> 3), pp = threadIdx.x & 7;
+      for (int q = 16; pp + 8 * q < a.ssq_tiles; ++q) ss += (m < a.M) ? a.ssq[(size_t)(pp + 8 * q) * a.ssq_ld + m] : 0.f;
+      ss += __shfl_xor(ss, 1, WAVE);
+      ss += __shfl_xor(ss, 2, WAVE);
+      ss += __shfl_xor(ss, 4, WAVE);
+      if (pp == 0) inv_s[threadIdx.x >> 3] = 1.0f / sqrtf(ss / (float)a.H + a.eps);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const float inv = inv_s[16 * mt + lr];
+#pragma unroll
+      for (int s = 0; s < KPW; ++s) X[s][mt] = xform<DT, XF>(X[s][mt], NWv[s], inv);
+    }
+  }
+
+  // 4. multiply
+  f32x4 acc[NT][MT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[j][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < KPW; ++s) {
+    if (s < wn) {
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[j][mt] = mfma16<DT>(A[s][j], X[s][mt], acc[j][mt]);
+    }
+  }
+
+  // 5. the waves' partials, summed per unit in wave order
+  f32x4* red = reinterpret_cast<f32x4*>(smem);  // [NW][NT][MT][64]
+#pragma unroll
+  for (int j = 0; j < NT; ++j)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) red[((w * NT + j) * MT + mt) * 64 + lane] = acc[j][mt];
+  __syncthreads();
+  constexpr int TPU = EPI == EPI_SILU_PAIR ? 2 : 1;  // tiles per unit
+  f32x4 v[TPU] = {};
+  const int u = w;
+  const bool has_unit = u < UNITS;
+  const int ut = (u / MT) * TPU, umt = u % MT;
+  if (has_unit) {
+#pragma unroll
+    for (int q = 0; q < TPU; ++q) {
+      f32x4 sum = red[((0 * NT + ut + q) * MT + umt) * 64 + lane];
+      for (int ww = 1; ww < NW; ++ww) sum += red[((ww * NT + ut + q) * MT + umt) * 64 + lane];
+      v[q] = sum;
+    }
+  }
+
+  // 6. cross-workgroup k splits: the unit's partial, summed by the epilogue body
+  if (gy > 1) {
+    if (has_unit) {
+      const size_t grp = (size_t)bz * a.ngroups + bx;
+      constexpr int per = NT * MT * 64;
+      f32x4* part = reinterpret_cast<f32x4*>(a.part) + (grp * gy + by) * per;
+#pragma unroll
+      for (int q = 0; q < TPU; ++q) part[((ut + q) * MT + umt) * 64 + lane] = v[q];
+    }
+    return;
+  }
+  if (has_unit) os_epilogue<DT, EPI, TPU, false>(a, v, m0 + 16 * umt + lr, t0 + ut, lg);
+}
+
 template <int DT, int EPI, int XF, int MT, int NT, int KPW>
 __global__ __launch_bounds__(512) void gemm_os_kernel(GemmP a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  gemm_os_body<DT, EPI, XF, MT, NT, KPW, false>(a, blockIdx.x, blockIdx.y, blockIdx.z, gridDim.y, smem);
+  // gate_up's six tiles keep the LDS-staged activations (their register slice would not fit beside
+  // the weights); the narrower projections load their fragments directly
+  if constexpr (NT <= 4) {
+    gemm_os_direct_body<DT, EPI, XF, MT, NT, KPW>(a, blockIdx.x, blockIdx.y, blockIdx.z, gridDim.y, smem);
+  } else {
+    gemm_os_body<DT, EPI, XF, MT, NT, KPW, false>(a, blockIdx.x, blockIdx.y, blockIdx.z, gridDim.y, smem);
+  }
 }
 
 // Sum of the k-split partials of one unit per wave, in split order, then the epilogue (workgroup =
