@@ -23,6 +23,12 @@
 
 namespace fdllm {
 
+#ifdef FD_WLOAD_PLAIN
+#define FD_WLOAD(p) (*(p))
+#else
+#define FD_WLOAD(p) __builtin_nontemporal_load(p)
+#endif
+
 __device__ __forceinline__ const u32x4* wblock(const u16* W, int KS, int t, int s) {
   return reinterpret_cast<const u32x4*>(W + ((size_t)t * KS + s) * 512) + (threadIdx.x & 63);
 }
@@ -453,7 +459,7 @@ __device__ __forceinline__ void gemm_os_body(const GemmP& a, int bx, int by, int
   for (int s = 0; s < KPW; ++s)
 #pragma unroll
     for (int j = 0; j < NT; ++j)
-      A[s][j] = __builtin_nontemporal_load(wblock(a.W, a.KS, t0 + j, kb + (s < wn ? ws + s : min(ws, a.kps - 1))));
+      A[s][j] = FD_WLOAD(wblock(a.W, a.KS, t0 + j, kb + (s < wn ? ws + s : min(ws, a.kps - 1))));
 
   // 3. 1 / rms of the chunk's rows, then the normalised fragments into LDS
   if constexpr (XF == XF_RMS) {
@@ -567,8 +573,23 @@ __device__ __forceinline__ void gemm_os_direct_body(const GemmP& a, int bx, int 
   const int kq = a.kps / NW, kr = a.kps % NW;
   const int ws = kq * w + min(w, kr), wn = kq + (w < kr ? 1 : 0);  // this wave's k steps [ws, ws + wn)
 
-  // 1. the activation path first (its waits then do not cover the weight loads): the wave's fragments,
-  //    the rows' sums of squares and the norm weights of its k steps
+  // A wave may have at most 63 loads outstanding, and a load waits for every older one.  A narrow slice
+  // (qkv, o_proj, down) goes after the activation path, whose waits then do not cover it; a wide one
+  // (gate_up's 36 blocks per wave, which with the activation path would pass 63 and stall the weight
+  // requests behind the activation round trip) goes first: the weights are the long pole, and the
+  // activations arrive while they stream.
+  constexpr bool W_FIRST = NT * KPW > 16;
+  u32x4 A[KPW][NT];
+  auto issue_w = [&]() {
+#pragma unroll
+    for (int s = 0; s < KPW; ++s)
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+        A[s][j] = FD_WLOAD(wblock(a.W, a.KS, t0 + j, kb + ws + min(s, max(wn, 1) - 1)));
+  };
+  if constexpr (W_FIRST) issue_w();
+  // 1. the activation path: the wave's fragments, the rows' sums of squares and the norm weights of
+  //    its k steps
   u32x4 X[KPW][MT];
 #pragma unroll
   for (int s = 0; s < KPW; ++s)
@@ -595,13 +616,8 @@ __device__ __forceinline__ void gemm_os_direct_body(const GemmP& a, int bx, int 
     for (int s = 0; s < KPW; ++s)
       NWv[s] = *reinterpret_cast<const u32x4*>(a.nw + 32 * (kb + ws + min(s, max(wn, 1) - 1)) + 8 * lg);
   }
-  // 2. the weight slice: KPW k steps x NT tiles per wave, all requested now
-  u32x4 A[KPW][NT];
-#pragma unroll
-  for (int s = 0; s < KPW; ++s)
-#pragma unroll
-    for (int j = 0; j < NT; ++j)
-      A[s][j] = __builtin_nontemporal_load(wblock(a.W, a.KS, t0 + j, kb + ws + min(s, max(wn, 1) - 1)));
+  // 2. the weight slice: KPW k steps x NT tiles per wave, all requested at once
+  if constexpr (!W_FIRST) issue_w();
 
   // 3. 1 / rms of the chunk's rows (gemm_os_body's order), then the transform in registers
   if constexpr (XF == XF_RMS) {
@@ -623,6 +639,44 @@ __device__ __forceinline__ void gemm_os_direct_body(const GemmP& a, int bx, int 
 #pragma unroll
       for (int s = 0; s < KPW; ++s) X[s][mt] = xform<DT, XF>(X[s][mt], NWv[s], inv);
     }
+  }
+
+  if constexpr (EPI == EPI_SILU_PAIR && NT > 2) {
+    // gate_up: one tile pair at a time (two tiles' accumulators live), each pair's wave sums through
+    // LDS, then its row blocks' SiLU * up by waves 0 .. MT - 1
+    f32x4* red = reinterpret_cast<f32x4*>(smem);  // [NW][2][MT][64]
+#pragma unroll
+    for (int pr = 0; pr < NT / 2; ++pr) {
+      f32x4 acc[2][MT];
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[q][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KPW; ++s)
+        if (s < wn)
+#pragma unroll
+          for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[q][mt] = mfma16<DT>(A[s][2 * pr + q], X[s][mt], acc[q][mt]);
+      if (pr > 0) __syncthreads();  // the previous pair's sums have been read
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) red[((w * 2 + q) * MT + mt) * 64 + lane] = acc[q][mt];
+      __syncthreads();
+      if (w < MT) {
+        f32x4 v[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          f32x4 sum = red[((0 * 2 + q) * MT + w) * 64 + lane];
+          for (int ww = 1; ww < NW; ++ww) sum += red[((ww * 2 + q) * MT + w) * 64 + lane];
+          v[q] = sum;
+        }
+        os_epilogue<DT, EPI, 2, false>(a, v, m0 + 16 * w + lr, t0 + 2 * pr, lg);
+      }
+    }
+    return;
   }
 
   // 4. multiply
@@ -679,10 +733,15 @@ __device__ __forceinline__ void gemm_os_direct_body(const GemmP& a, int bx, int 
 template <int DT, int EPI, int XF, int MT, int NT, int KPW>
 __global__ __launch_bounds__(512) void gemm_os_kernel(GemmP a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  // gate_up's six tiles keep the LDS-staged activations (their register slice would not fit beside
-  // the weights); the narrower projections load their fragments directly
   if constexpr (NT <= 4) {
     gemm_os_direct_body<DT, EPI, XF, MT, NT, KPW>(a, blockIdx.x, blockIdx.y, blockIdx.z, gridDim.y, smem);
+  } else if constexpr (EPI == EPI_SILU_PAIR) {
+    // gate_up: pair by pair with the fragments in registers (no k split at the 1.5B shape); a k split
+    // takes the LDS-staged body
+    if (gridDim.y == 1)
+      gemm_os_direct_body<DT, EPI, XF, MT, NT, KPW>(a, blockIdx.x, 0, blockIdx.z, 1, smem);
+    else
+      gemm_os_body<DT, EPI, XF, MT, NT, KPW, false>(a, blockIdx.x, blockIdx.y, blockIdx.z, gridDim.y, smem);
   } else {
     gemm_os_body<DT, EPI, XF, MT, NT, KPW, false>(a, blockIdx.x, blockIdx.y, blockIdx.z, gridDim.y, smem);
   }
