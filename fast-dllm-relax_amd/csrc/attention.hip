@@ -43,6 +43,12 @@ size_t attn_partial_floats(const AttnP& a) {
   return (size_t)std::max(a.nseq, 1) * a.nkv * QT * a.S * PSZ;
 }
 
+// the merge kernel whose register path covers S splits in one round trip where it can
+template <int DT>
+static auto merge_kernel_for(int S) {
+  return S > 24 ? attn_merge_kernel<DT, 40> : attn_merge_kernel<DT, 24>;
+}
+
 template <typename K>
 static void raise_lds(K kern, size_t lds) {
   // a runtime that needs no attribute for LDS up to the device limit may reject it: clear that error
@@ -64,7 +70,7 @@ static hipError_t launch_loop(const AttnP& a, const AttnPlan& p, hipStream_t st)
   hipLaunchKernelGGL(kern, dim3(p.qg, a.nkv, a.S), dim3(64 * QPW * KSW), lds, st, a);
   if (a.S > 1) {
     const int QT = ((a.nq / a.nkv) * a.rows + 15) / 16;
-    hipLaunchKernelGGL(attn_merge_kernel<DT>, dim3(HD / 16, QT, a.nkv), dim3(64), 0, st, a);
+    hipLaunchKernelGGL(merge_kernel_for<DT>(a.S), dim3(HD / 16, QT, a.nkv), dim3(64), 0, st, a);
   }
   return hipGetLastError();
 }
@@ -82,7 +88,7 @@ static hipError_t launch_chunk_kh(const AttnP& a, const AttnPlan& p, hipStream_t
   hipLaunchKernelGGL(kern, dim3(p.qg * nseq, a.nkv, a.S), dim3(64 * QPW * KH), lds, st, a);
   if (a.S > 1) {
     const int QT = ((a.nq / a.nkv) * a.rows + 15) / 16;
-    hipLaunchKernelGGL(attn_merge_kernel<DT>, dim3(HD / 16, QT, a.nkv * nseq), dim3(64), 0, st, a);
+    hipLaunchKernelGGL(merge_kernel_for<DT>(a.S), dim3(HD / 16, QT, a.nkv * nseq), dim3(64), 0, st, a);
   }
   return hipGetLastError();
 }

@@ -612,9 +612,9 @@ __global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP p) {
 // exp(m_c - M) depend only on the query, so each lane computes them once for its query lr; the split
 // partials are added in split order.
 // Splits at or past ceil(Lk / chunk) (a shorter sequence of a batched call) hold nothing and are skipped.
-template <int DT, bool COH>
+// SR: splits held in registers at once (two loads each), so that up to SR splits cost one round trip.
+template <int DT, bool COH, int SR = 24>
 __device__ __forceinline__ void attn_merge_wave(const AttnP& a, int dt, int qt, int g, int lane) {
-  constexpr int SR = 24;  // splits held in registers at once (two loads each): up to SR costs one round trip
   constexpr int SB = 8;   // batch of the two-pass loop for more splits
   const int lr = lane & 15, lg = lane >> 4;
   const int grp = a.nq / a.nkv, QR = grp * a.rows, QT = (QR + 15) / 16;
@@ -679,17 +679,18 @@ __device__ __forceinline__ void attn_merge_wave(const AttnP& a, int dt, int qt, 
   }
 }
 
-// gridDim.z = kv heads x sequences (sequence-major)
-template <int DT>
+// gridDim.z = kv heads x sequences (sequence-major).  SR: the splits one round trip covers (the launcher
+// picks 24 or, for more splits, 40; a one-wave workgroup can spend the registers).
+template <int DT, int SR>
 __global__ __launch_bounds__(64) void attn_merge_kernel(AttnP p) {
   if (p.nseq <= 1) {
-    attn_merge_wave<DT, false>(p, blockIdx.x, blockIdx.y, blockIdx.z, threadIdx.x);
+    attn_merge_wave<DT, false, SR>(p, blockIdx.x, blockIdx.y, blockIdx.z, threadIdx.x);
     return;
   }
   const int b = (int)blockIdx.z / p.nkv;
   AttnP a = p;
   seq_view(a, p, b);
-  attn_merge_wave<DT, false>(a, blockIdx.x, blockIdx.y, (int)blockIdx.z - b * p.nkv, threadIdx.x);
+  attn_merge_wave<DT, false, SR>(a, blockIdx.x, blockIdx.y, (int)blockIdx.z - b * p.nkv, threadIdx.x);
 }
 
 
