@@ -556,8 +556,8 @@ __device__ __forceinline__ void gemm_os_body(const GemmP& a, int bx, int by, int
 // The same one-shot GEMM with the activations loaded straight into registers: a wave multiplies only
 // its own k steps, so it loads only its own slice of the rows (MT 16-row blocks x its k steps, one
 // 16-byte load per fragment), all at once and before its weight slice, and RMS-normalises them in
-// registers.  Nothing goes through LDS but the 32 inverse RMS values and the wave sums, so the chain
-// from launch to the first MFMA is one memory round trip.  Same k partition, same per-wave MFMA order,
+// registers.  Nothing goes through LDS but the norm weights, the 32 inverse RMS values and the wave
+// sums, so the chain from launch to the first MFMA is one memory round trip.  Same k partition, same per-wave MFMA order,
 // same wave-order sums and epilogues as gemm_os_body: the results are bit-identical.
 template <int DT, int EPI, int XF, int MT, int NT, int KPW>
 __device__ __forceinline__ void gemm_os_direct_body(const GemmP& a, int bx, int by, int bz, int gy, unsigned char* smem) {
@@ -573,12 +573,12 @@ __device__ __forceinline__ void gemm_os_direct_body(const GemmP& a, int bx, int 
   const int kq = a.kps / NW, kr = a.kps % NW;
   const int ws = kq * w + min(w, kr), wn = kq + (w < kr ? 1 : 0);  // this wave's k steps [ws, ws + wn)
 
-  // A wave may have at most 63 loads outstanding, and a load waits for every older one.  A narrow slice
-  // (qkv, o_proj, down) goes after the activation path, whose waits then do not cover it; a wide one
-  // (gate_up's 36 blocks per wave, which with the activation path would pass 63 and stall the weight
-  // requests behind the activation round trip) goes first: the weights are the long pole, and the
-  // activations arrive while they stream.
-  constexpr bool W_FIRST = NT * KPW > 16;
+  // A wave may have at most 63 loads outstanding, and a load waits for every older one.  With the norm
+  // transform the activation path (KPW x MT fragments, 12 sums-of-squares loads, one norm-weight chunk)
+  // goes first: it is short enough that the weight slice (gate_up's 36 blocks per wave) still fits
+  // behind it, and the norm is done while the weights stream.  Without it, a wide slice (down's 20
+  // blocks) goes first and the fragments arrive while it streams.
+  constexpr bool W_FIRST = XF != XF_RMS && NT * KPW > 16;
   u32x4 A[KPW][NT];
   auto issue_w = [&]() {
 #pragma unroll
@@ -588,8 +588,8 @@ __device__ __forceinline__ void gemm_os_direct_body(const GemmP& a, int bx, int 
         A[s][j] = FD_WLOAD(wblock(a.W, a.KS, t0 + j, kb + ws + min(s, max(wn, 1) - 1)));
   };
   if constexpr (W_FIRST) issue_w();
-  // 1. the activation path: the wave's fragments, the rows' sums of squares and the norm weights of
-  //    its k steps
+  // 1. the activation path: the wave's fragments, the rows' sums of squares (threads 0 .. 255: row
+  //    tid / 8, tiles tid % 8 + 8q) and the split's norm weights (one 16-byte chunk per thread)
   u32x4 X[KPW][MT];
 #pragma unroll
   for (int s = 0; s < KPW; ++s)
@@ -599,34 +599,34 @@ __device__ __forceinline__ void gemm_os_direct_body(const GemmP& a, int bx, int 
       const int k = 32 * (kb + ws + min(s, max(wn, 1) - 1)) + 8 * lg;
       X[s][mt] = *reinterpret_cast<const u32x4*>(a.X + (size_t)m * a.ldx + k);
     }
-  float ssv[16];
+  constexpr int SQ = 12;  // unrolled sums-of-squares loads (96 tiles: hidden 1536); the rest in a loop
+  __shared__ u32x4 nw_s[XF == XF_RMS ? 8 * KPW * 4 : 1];
+  float ssv[SQ];
+  u32x4 nwv = {0u, 0u, 0u, 0u};
+  const bool nw_ld = XF == XF_RMS && (int)threadIdx.x < a.kps * 4;  // kps <= 8 KPW (the plan's bound)
   if constexpr (XF == XF_RMS) {
     if (threadIdx.x < 256) {
       const int m = m0 + (threadIdx.x >> 3), pp = threadIdx.x & 7;
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
+      for (int q = 0; q < SQ; ++q) {
         const int t = pp + 8 * q;
         ssv[q] = (m < a.M && t < a.ssq_tiles) ? a.ssq[(size_t)t * a.ssq_ld + m] : 0.f;
       }
     }
-  }
-  u32x4 NWv[XF == XF_RMS ? KPW : 1];
-  if constexpr (XF == XF_RMS) {
-#pragma unroll
-    for (int s = 0; s < KPW; ++s)
-      NWv[s] = *reinterpret_cast<const u32x4*>(a.nw + 32 * (kb + ws + min(s, max(wn, 1) - 1)) + 8 * lg);
+    if (nw_ld) nwv = *reinterpret_cast<const u32x4*>(a.nw + 32 * kb + 8 * threadIdx.x);
   }
   // 2. the weight slice: KPW k steps x NT tiles per wave, all requested at once
   if constexpr (!W_FIRST) issue_w();
 
   // 3. 1 / rms of the chunk's rows (gemm_os_body's order), then the transform in registers
   if constexpr (XF == XF_RMS) {
+    if (nw_ld) nw_s[threadIdx.x] = nwv;
     if (threadIdx.x < 256) {
       float ss = 0.f;
 #pragma unroll
-      for (int q = 0; q < 16; ++q) ss += ssv[q];
+      for (int q = 0; q < SQ; ++q) ss += ssv[q];
       const int m = m0 + (threadIdx.x >> 3), pp = threadIdx.x & 7;
-      for (int q = 16; pp + 8 * q < a.ssq_tiles; ++q) ss += (m < a.M) ? a.ssq[(size_t)(pp + 8 * q) * a.ssq_ld + m] : 0.f;
+      for (int q = SQ; pp + 8 * q < a.ssq_tiles; ++q) ss += (m < a.M) ? a.ssq[(size_t)(pp + 8 * q) * a.ssq_ld + m] : 0.f;
       ss += __shfl_xor(ss, 1, WAVE);
       ss += __shfl_xor(ss, 2, WAVE);
       ss += __shfl_xor(ss, 4, WAVE);
@@ -637,46 +637,8 @@ __device__ __forceinline__ void gemm_os_direct_body(const GemmP& a, int bx, int 
     for (int mt = 0; mt < MT; ++mt) {
       const float inv = inv_s[16 * mt + lr];
 #pragma unroll
-      for (int s = 0; s < KPW; ++s) X[s][mt] = xform<DT, XF>(X[s][mt], NWv[s], inv);
+      for (int s = 0; s < KPW; ++s) X[s][mt] = xform<DT, XF>(X[s][mt], nw_s[(ws + min(s, max(wn, 1) - 1)) * 4 + lg], inv);
     }
-  }
-
-  if constexpr (EPI == EPI_SILU_PAIR && NT > 2) {
-    // gate_up: one tile pair at a time (two tiles' accumulators live), each pair's wave sums through
-    // LDS, then its row blocks' SiLU * up by waves 0 .. MT - 1
-    f32x4* red = reinterpret_cast<f32x4*>(smem);  // [NW][2][MT][64]
-#pragma unroll
-    for (int pr = 0; pr < NT / 2; ++pr) {
-      f32x4 acc[2][MT];
-#pragma unroll
-      for (int q = 0; q < 2; ++q)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[q][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < KPW; ++s)
-        if (s < wn)
-#pragma unroll
-          for (int q = 0; q < 2; ++q)
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) acc[q][mt] = mfma16<DT>(A[s][2 * pr + q], X[s][mt], acc[q][mt]);
-      if (pr > 0) __syncthreads();  // the previous pair's sums have been read
-#pragma unroll
-      for (int q = 0; q < 2; ++q)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) red[((w * 2 + q) * MT + mt) * 64 + lane] = acc[q][mt];
-      __syncthreads();
-      if (w < MT) {
-        f32x4 v[2];
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          f32x4 sum = red[((0 * 2 + q) * MT + w) * 64 + lane];
-          for (int ww = 1; ww < NW; ++ww) sum += red[((ww * 2 + q) * MT + w) * 64 + lane];
-          v[q] = sum;
-        }
-        os_epilogue<DT, EPI, 2, false>(a, v, m0 + 16 * w + lr, t0 + 2 * pr, lg);
-      }
-    }
-    return;
   }
 
   // 4. multiply
@@ -736,8 +698,9 @@ __global__ __launch_bounds__(512) void gemm_os_kernel(GemmP a) {
   if constexpr (NT <= 4) {
     gemm_os_direct_body<DT, EPI, XF, MT, NT, KPW>(a, blockIdx.x, blockIdx.y, blockIdx.z, gridDim.y, smem);
   } else if constexpr (EPI == EPI_SILU_PAIR) {
-    // gate_up: pair by pair with the fragments in registers (no k split at the 1.5B shape); a k split
-    // takes the LDS-staged body
+    // gate_up: every pair's MFMAs with the fragments in registers, then one pass of wave sums through LDS
+    // and the pairs' SiLU * up by waves 0 .. NT / 2 x MT - 1 in parallel (no k split at the 1.5B shape);
+    // a k split takes the LDS-staged body
     if (gridDim.y == 1)
       gemm_os_direct_body<DT, EPI, XF, MT, NT, KPW>(a, blockIdx.x, 0, blockIdx.z, 1, smem);
     else
