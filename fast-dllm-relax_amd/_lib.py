@@ -23,6 +23,7 @@ EXPORTS = (
     "fdllm_forward_block_partial_rp8", "fdllm_forward_block_partial_rp16", "fdllm_forward_block_partial_rp24",
     "fdllm_forward_cached_batch", "fdllm_forward_block_partial_batch", "fdllm_build_prefix_cache_seq",
     "fdllm_get_confidence", "fdllm_confidence_from_logits", "fdllm_bench_op", "fdllm_persistent_steps",
+    "fdllm_frag_calls",
     "fdllm_last_error",
 )
 
@@ -65,6 +66,7 @@ _SIGS = {
     "fdllm_confidence_from_logits": ([_P, _P, _I, _I, _I, _P, _P, _P], _I),
     "fdllm_bench_op": ([_P, _I, _I, _I, _I, _P, _P, _I, _I, _P], _I),
     "fdllm_persistent_steps": ([_P], ctypes.c_longlong),
+    "fdllm_frag_calls": ([_P], ctypes.c_longlong),
     "fdllm_last_error": ([], ctypes.c_char_p),
 }
 

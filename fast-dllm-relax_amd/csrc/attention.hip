@@ -140,6 +140,7 @@ static hipError_t launch_dt(const AttnP& a, hipStream_t st) {
   const AttnPlan p = attn_plan(a.rows, a.nq, a.nkv, a.Lk, a.target_wgs);
   if (p.S != a.S || p.chunk != a.chunk) return hipErrorInvalidValue;
   if (a.nseq > 1 && (!p.chunked || a.nseq > MAX_SEQS)) return hipErrorInvalidValue;
+  if (a.ofrag && (a.nseq > 1 || a.rows > 32)) return hipErrorInvalidValue;
   if (!p.chunked && a.nseq <= 1 && a.rows >= PREFILL_MIN_ROWS && a.mask != 2) {
     if (a.mask == 1) return launch_prefill<DT, 1>(a, st);
     return launch_prefill<DT, 0>(a, st);

@@ -55,6 +55,12 @@ __device__ __forceinline__ void rope_tab(u32x4& lo, u32x4& hi, const float* cs) 
   }
 }
 
+// Output element (row r, column c = head x 128 + dim): row-major [rows][nq x 128], or MFMA-fragment
+// order (frag_off) when the next projection is a one-shot chain's (at most 32 rows, one sequence).
+__device__ __forceinline__ u16* out_at(const AttnP& a, int r, int c) {
+  return a.out + (a.ofrag ? frag_off(r, c) : (size_t)r * a.nq * HD + c);
+}
+
 template <int DT, int QPW, int KSW>
 __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
   constexpr int NT = 64 * QPW;  // threads of one key group
@@ -262,10 +268,9 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
   if (a.S == 1) {
     if (qvalid) {
       const float inv = 1.0f / Lq;
-      u16* dst = a.out + (size_t)r * a.nq * HD + (g * grp + hh) * HD + 4 * lg;
 #pragma unroll
       for (int dt = 0; dt < HD / 16; ++dt)
-        *reinterpret_cast<u32x2*>(dst + 16 * dt) =
+        *reinterpret_cast<u32x2*>(out_at(a, r, (g * grp + hh) * HD + 16 * dt + 4 * lg)) =
             u32x2{pack2(from_f32<DT>(o[dt][0] * inv), from_f32<DT>(o[dt][1] * inv)),
                   pack2(from_f32<DT>(o[dt][2] * inv), from_f32<DT>(o[dt][3] * inv))};
     }
@@ -549,7 +554,7 @@ __device__ __forceinline__ void attn_chunk_compute(const AttnP& a, int bx, int b
 
   // lane output: query row qi (head hh, row r), dims 16 dt + 4 lg .. + 3
   auto store4 = [&](int dt, f32x4 v) {
-    u16* dst = a.out + (size_t)r * a.nq * HD + (g * grp + hh) * HD + 16 * dt + 4 * lg;
+    u16* dst = out_at(a, r, (g * grp + hh) * HD + 16 * dt + 4 * lg);
     st8<COH>(dst, u32x2{pack2(from_f32<DT>(v[0]), from_f32<DT>(v[1])), pack2(from_f32<DT>(v[2]), from_f32<DT>(v[3]))});
   };
   if (a.S == 1) {
@@ -673,7 +678,7 @@ __device__ __forceinline__ void attn_merge_wave(const AttnP& a, int dt, int qt, 
   if (qi < QR) {
     const int h = qi / a.rows, r = qi - h * a.rows;
     const float inv = 1.0f / L;
-    u16* dst = a.out + (size_t)r * a.nq * HD + (g * grp + h) * HD + 16 * dt + 4 * lg;
+    u16* dst = out_at(a, r, (g * grp + h) * HD + 16 * dt + 4 * lg);
     st8<COH>(dst, u32x2{pack2(from_f32<DT>(acc[0] * inv), from_f32<DT>(acc[1] * inv)),
                         pack2(from_f32<DT>(acc[2] * inv), from_f32<DT>(acc[3] * inv))});
   }

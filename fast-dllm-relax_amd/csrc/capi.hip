@@ -84,6 +84,7 @@ struct fdllm_ctx {
   int down_split = 10;    // cross-workgroup k splits of the down projection (largest divisor of K/32 <= this)
   int mm_target_wgs = 256;  // large-M GEMM: split k while the launch has fewer workgroups than this
   int mm_min_stages = 8;    // ... into splits of at least this many stages
+  bool frag_on = true;      // one-shot chains keep activations in MFMA-fragment order (FDLLM_XFRAG=0: row-major)
   // the persistent cached step (step_body.hpp)
   bool step_on = false;                // FDLLM_PERSISTENT=1 turns it on (measured slower than the kernels)
   bool step_check = false;             // FDLLM_STEP_CHECK=1: wait for every launch and check its status
@@ -96,6 +97,7 @@ struct fdllm_ctx {
   unsigned* step_status = nullptr;     // host-visible (pinned, mapped) abort word
   unsigned* step_status_dev = nullptr;
   long long step_launches = 0;         // persistent steps run (fdllm_persistent_steps)
+  long long frag_calls = 0;            // layer loops run in MFMA-fragment order (fdllm_frag_calls)
   std::string step_trace_path;         // FDLLM_STEP_TRACE: write each launch's barrier timeline there
   unsigned long long* step_trace = nullptr;
 
@@ -229,7 +231,7 @@ int rope_table(fdllm_ctx* c, int rows, const int32_t* pos, int rows_per_seq, hip
 // Attention of the call's rows; the RoPE table (rope_table) must hold the call's positions.  With sb,
 // the rows are sb->nseq sequences of sb->rows (ws and Lk are then ignored).
 int run_attention(fdllm_ctx* c, int rows, uint16_t* kc, uint16_t* vc, int ws, int Lk, int mask,
-                  const float* bias, long long bias_ld, hipStream_t st, const SeqBatch* sb = nullptr) {
+                  const float* bias, long long bias_ld, hipStream_t st, const SeqBatch* sb = nullptr, bool frag = false) {
   const fdllm_config& f = c->cfg;
   AttnP a{};
   a.qkv = c->qkv; a.ldq = c->qkv_dim(); a.rows = rows; a.nq = f.num_attention_heads; a.nkv = f.num_key_value_heads;
@@ -257,6 +259,7 @@ int run_attention(fdllm_ctx* c, int rows, uint16_t* kc, uint16_t* vc, int ws, in
     a.part = c->apart;
   }
   a.out = c->attn;
+  a.ofrag = frag;
   HIPCHK(launch_attention(f.dtype, a, st));
   return FDLLM_OK;
 }
@@ -340,6 +343,45 @@ int try_step(fdllm_ctx* c, int rows, uint16_t* kbase, uint16_t* vbase, size_t la
   return FDLLM_OK;
 }
 
+// The four projections of layer L at `rows` rows, as the layer loop launches them.  frag: the one-shot
+// chain's activations (h, the attention output, SiLU * up) are in MFMA-fragment order.
+struct LayerGemms { GemmP q, o, gu, d; int dsplit; };
+LayerGemms layer_gemms(const fdllm_ctx* c, const Layer& L, int rows, bool frag) {
+  const fdllm_config& f = c->cfg;
+  const int H = f.hidden_size, I = f.intermediate_size, ssq_ld = c->ws_rows;
+  LayerGemms g;
+  g.q = gemm_args(L.pqkv, qkv_tiles(c), c->qkv_dim(), H, c->h, H, rows);
+  g.q.ssq = c->ssq; g.q.ssq_tiles = c->ssq_tiles(); g.q.ssq_ld = ssq_ld; g.q.nw = L.ln_in; g.q.eps = f.rms_norm_eps;
+  g.q.H = H; g.q.Y = c->qkv; g.q.ldy = c->qkv_dim(); g.q.bias = L.bqkv;
+  g.q.xfrag = frag;
+  g.o = gemm_args(L.po, o_tiles(c), H, c->q_dim(), c->attn, c->q_dim(), rows);
+  g.o.Y = c->h; g.o.ldy = H; g.o.ssq_out = c->ssq; g.o.ssq_ld = ssq_ld;
+  g.o.xfrag = g.o.yfrag = frag;
+  g.gu = gemm_args(L.pgu, gu_tiles(c), I, H, c->h, H, rows);
+  g.gu.ssq = c->ssq; g.gu.ssq_tiles = c->ssq_tiles(); g.gu.ssq_ld = ssq_ld; g.gu.nw = L.ln_post;
+  g.gu.eps = f.rms_norm_eps; g.gu.H = H; g.gu.Y = c->act; g.gu.ldy = I;
+  g.gu.xfrag = g.gu.yfrag = frag;
+  g.d = gemm_args(L.pd, d_tiles(c), H, I, c->act, I, rows);
+  g.d.Y = c->h; g.d.ldy = H; g.d.ssq_out = c->ssq; g.d.ssq_ld = ssq_ld;
+  g.d.xfrag = g.d.yfrag = frag;
+  g.dsplit = divisor_at_most(I / 32, c->down_split);
+  return g;
+}
+
+// Whether a call of `rows` rows runs every projection in the one-shot register-fragment body, so that its
+// activations can stay in MFMA-fragment order from load_rows to the final norm.
+bool frag_chain(const fdllm_ctx* c, int rows) {
+  if (!c->frag_on || rows > 32) return false;
+  LayerGemms g = layer_gemms(c, c->layers[0], rows, false);
+  const std::pair<int, GemmP*> all[] = {{CFG_QKV, &g.q}, {CFG_OPROJ, &g.o}, {CFG_GATE_UP, &g.gu}, {CFG_DOWN, &g.d}};
+  for (const auto& [cfg, a] : all) {
+    GemmP t = *a;
+    const GemmPlan pl = gemm_plan(cfg, t, cfg == CFG_DOWN ? g.dsplit : 1, c->mm_target_wgs, c->mm_min_stages);
+    if (!gemm_takes_frag(cfg, pl)) return false;
+  }
+  return true;
+}
+
 // The decoder-layer loop (cuda.py:561-579 per layer, 639-666 for the model).
 //   per layer: qkv (RMSNorm on load, + bias) -> attention (RoPE, KV append, GQA) -> o_proj + residual
 //              -> gate_up (RMSNorm on load, SiLU * up) -> down + residual
@@ -350,12 +392,15 @@ int run_layers(fdllm_ctx* c, const void* x_in, int rows, uint16_t* kbase, uint16
                int write_start, const int32_t* pos_dev, int attend_len, int mask, const float* bias,
                long long bias_ld, void* out, hipStream_t st, const SeqBatch* sb = nullptr) {
   const fdllm_config& f = c->cfg;
-  const int H = f.hidden_size, I = f.intermediate_size;
+  const int H = f.hidden_size;
   const int ssq_ld = c->ws_rows;
-  HIPCHK(launch_load_rows(f.dtype, (const uint16_t*)x_in, rows, H, c->h, c->ssq, ssq_ld, st));
+  // the persistent step (when it may run) and batched calls keep the activations row-major
+  const bool step_may = sb == nullptr && mask == 0 && bias == nullptr && c->step_on;
+  const bool frag = sb == nullptr && !step_may && frag_chain(c, rows);
+  HIPCHK(launch_load_rows(f.dtype, (const uint16_t*)x_in, rows, H, c->h, c->ssq, ssq_ld, st, frag));
   int rc = rope_table(c, rows, pos_dev, sb ? sb->rows : rows, st);
   if (rc) return rc;
-  if (sb == nullptr && mask == 0 && bias == nullptr) {
+  if (step_may) {
     bool done = false;
     rc = try_step(c, rows, kbase, vbase, layer_stride, write_start, attend_len, st, &done);
     if (rc) return rc;
@@ -365,39 +410,25 @@ int run_layers(fdllm_ctx* c, const void* x_in, int rows, uint16_t* kbase, uint16
       return FDLLM_OK;
     }
   }
-  const int dsplit = divisor_at_most(I / 32, c->down_split);
+  if (frag) ++c->frag_calls;
   for (int l = 0; l < f.num_hidden_layers; ++l) {
     const Layer& L = c->layers[l];
     uint16_t* kc = kbase + (size_t)l * layer_stride;
     uint16_t* vc = vbase + (size_t)l * layer_stride;
-
-    GemmP q = gemm_args(L.pqkv, qkv_tiles(c), c->qkv_dim(), H, c->h, H, rows);
-    q.ssq = c->ssq; q.ssq_tiles = c->ssq_tiles(); q.ssq_ld = ssq_ld; q.nw = L.ln_in; q.eps = f.rms_norm_eps; q.H = H;
-    q.Y = c->qkv; q.ldy = c->qkv_dim(); q.bias = L.bqkv;
-    rc = run_gemm(c, CFG_QKV, q, 1, st);
+    LayerGemms g = layer_gemms(c, L, rows, frag);
+    rc = run_gemm(c, CFG_QKV, g.q, 1, st);
     if (rc) return rc;
-
-    rc = run_attention(c, rows, kc, vc, write_start, attend_len, mask, bias, bias_ld, st, sb);
+    rc = run_attention(c, rows, kc, vc, write_start, attend_len, mask, bias, bias_ld, st, sb, frag);
     if (rc) return rc;
-
-    GemmP o = gemm_args(L.po, o_tiles(c), H, c->q_dim(), c->attn, c->q_dim(), rows);
-    o.Y = c->h; o.ldy = H; o.ssq_out = c->ssq; o.ssq_ld = ssq_ld;
-    rc = run_gemm(c, CFG_OPROJ, o, 1, st);
+    rc = run_gemm(c, CFG_OPROJ, g.o, 1, st);
     if (rc) return rc;
-
-    GemmP gu = gemm_args(L.pgu, gu_tiles(c), I, H, c->h, H, rows);
-    gu.ssq = c->ssq; gu.ssq_tiles = c->ssq_tiles(); gu.ssq_ld = ssq_ld; gu.nw = L.ln_post; gu.eps = f.rms_norm_eps;
-    gu.H = H; gu.Y = c->act; gu.ldy = I;
-    rc = run_gemm(c, CFG_GATE_UP, gu, 1, st);
+    rc = run_gemm(c, CFG_GATE_UP, g.gu, 1, st);
     if (rc) return rc;
-
-    GemmP d = gemm_args(L.pd, d_tiles(c), H, I, c->act, I, rows);
-    d.Y = c->h; d.ldy = H; d.ssq_out = c->ssq; d.ssq_ld = ssq_ld;
-    rc = run_gemm(c, CFG_DOWN, d, dsplit, st);
+    rc = run_gemm(c, CFG_DOWN, g.d, g.dsplit, st);
     if (rc) return rc;
   }
   if (out != nullptr)
-    HIPCHK(launch_norm_rows(f.dtype, c->h, rows, H, c->ssq, ssq_ld, c->final_norm, f.rms_norm_eps, (uint16_t*)out, st));
+    HIPCHK(launch_norm_rows(f.dtype, c->h, rows, H, c->ssq, ssq_ld, c->final_norm, f.rms_norm_eps, (uint16_t*)out, st, frag));
   return FDLLM_OK;
 }
 
@@ -524,6 +555,7 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   if (const char* e = std::getenv("FDLLM_MM_TARGET_WGS")) c->mm_target_wgs = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_MM_MIN_STAGES")) c->mm_min_stages = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_PERSISTENT")) c->step_on = atoi(e) != 0;
+  if (const char* e = std::getenv("FDLLM_XFRAG")) c->frag_on = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_STEP_CHECK")) c->step_check = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_STEP_ATTN_TARGET")) c->step_attn_target = std::max(0, atoi(e));
   if (const char* e = std::getenv("FDLLM_STEP_TRACE")) c->step_trace_path = e;
@@ -744,6 +776,8 @@ int fdllm_get_confidence(fdllm_ctx* c, const void* hidden, int rows, int32_t* id
 
 long long fdllm_persistent_steps(const fdllm_ctx* c) { return c ? c->step_launches : 0; }
 
+long long fdllm_frag_calls(const fdllm_ctx* c) { return c ? c->frag_calls : 0; }
+
 int fdllm_bench_op(fdllm_ctx* c, int op, int rows, int layer, int iters, void* k, void* v, int cap, int attend_len,
                    void* stream) {
   int rc = check_ready(c);
@@ -757,45 +791,24 @@ int fdllm_bench_op(fdllm_ctx* c, int op, int rows, int layer, int iters, void* k
   if (rc == FDLLM_OK) rc = ensure_stats(c, rows);
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
-  const int H = f.hidden_size, I = f.intermediate_size, ssq_ld = c->ws_rows;
   const size_t stride = (size_t)cap * f.num_key_value_heads * f.head_dim;
+  // the launches a cached step of `rows` rows makes (layout included), on whatever the buffers hold
+  const bool frag = !c->step_on && frag_chain(c, rows);
   for (int it = 0; it < iters && rc == FDLLM_OK; ++it) {
     // consecutive launches walk the layers, as a step does, so no weight is re-read from cache
     const int li = (layer + it) % f.num_hidden_layers;
-    const Layer& L = c->layers[li];
+    LayerGemms g = layer_gemms(c, c->layers[li], rows, frag);
     switch (op) {
-      case FDLLM_OP_QKV: {
-        GemmP q = gemm_args(L.pqkv, qkv_tiles(c), c->qkv_dim(), H, c->h, H, rows);
-        q.ssq = c->ssq; q.ssq_tiles = c->ssq_tiles(); q.ssq_ld = ssq_ld; q.nw = L.ln_in; q.eps = f.rms_norm_eps;
-        q.H = H; q.Y = c->qkv; q.ldy = c->qkv_dim(); q.bias = L.bqkv;
-        rc = run_gemm(c, CFG_QKV, q, 1, st);
-        break;
-      }
-      case FDLLM_OP_O_PROJ: {
-        GemmP o = gemm_args(L.po, o_tiles(c), H, c->q_dim(), c->attn, c->q_dim(), rows);
-        o.Y = c->h; o.ldy = H; o.ssq_out = c->ssq; o.ssq_ld = ssq_ld;
-        rc = run_gemm(c, CFG_OPROJ, o, 1, st);
-        break;
-      }
-      case FDLLM_OP_GATE_UP: {
-        GemmP gu = gemm_args(L.pgu, gu_tiles(c), I, H, c->h, H, rows);
-        gu.ssq = c->ssq; gu.ssq_tiles = c->ssq_tiles(); gu.ssq_ld = ssq_ld; gu.nw = L.ln_post;
-        gu.eps = f.rms_norm_eps; gu.H = H; gu.Y = c->act; gu.ldy = I;
-        rc = run_gemm(c, CFG_GATE_UP, gu, 1, st);
-        break;
-      }
-      case FDLLM_OP_DOWN: {
-        GemmP d = gemm_args(L.pd, d_tiles(c), H, I, c->act, I, rows);
-        d.Y = c->h; d.ldy = H; d.ssq_out = c->ssq; d.ssq_ld = ssq_ld;
-        rc = run_gemm(c, CFG_DOWN, d, divisor_at_most(I / 32, c->down_split), st);
-        break;
-      }
+      case FDLLM_OP_QKV: rc = run_gemm(c, CFG_QKV, g.q, 1, st); break;
+      case FDLLM_OP_O_PROJ: rc = run_gemm(c, CFG_OPROJ, g.o, 1, st); break;
+      case FDLLM_OP_GATE_UP: rc = run_gemm(c, CFG_GATE_UP, g.gu, 1, st); break;
+      case FDLLM_OP_DOWN: rc = run_gemm(c, CFG_DOWN, g.d, g.dsplit, st); break;
       case FDLLM_OP_ATTENTION:
         // the block's rows sit at the end of the attended range, as in a full cached step
         if (it == 0) rc = rope_table(c, rows, c->zero_i32, rows, st);
         if (rc == FDLLM_OK)
           rc = run_attention(c, rows, (uint16_t*)k + li * stride, (uint16_t*)v + li * stride, attend_len - rows,
-                             attend_len, 0, nullptr, 0, st);
+                             attend_len, 0, nullptr, 0, st, nullptr, frag);
         break;
       case FDLLM_OP_LM_HEAD_CONFIDENCE: {
         rc = run_lm_head(c, c->h, rows, nullptr, true, st);

@@ -233,6 +233,16 @@ __device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned expected
   return *lds_flag != 0;
 }
 
+// ---- activations in MFMA-fragment order ---------------------------------------------------------
+// A one-shot projection chain (at most 32 rows) keeps its activations (the residual stream, the
+// attention output, SiLU * up) in the order its GEMMs load them: k step s (columns 32 s .. 32 s + 31)
+// and row tile t (rows 16 t .. 16 t + 15) form one 1 KB block at element (2 s + t) x 512, whose 16 bytes
+// at lane l = r % 16 + 16 g hold row 16 t + r % 16, columns 32 s + 8 g .. + 7 -- one MFMA operand
+// fragment per block, so a wave's fragment load is one coalesced 1 KB read.  Element (r, c), r < 32:
+__device__ __forceinline__ size_t frag_off(int r, int c) {
+  return (size_t)((c >> 5) * 2 + (r >> 4)) * 512 + (size_t)((r & 15) + 16 * ((c >> 3) & 3)) * 8 + (c & 7);
+}
+
 // ---- bf16/fp16 pairs packed in 32-bit words ---------------------------------------------------
 template <int DT> __device__ __forceinline__ float lo_f32(uint32_t w) { return to_f32<DT>((u16)(w & 0xffffu)); }
 template <int DT> __device__ __forceinline__ float hi_f32(uint32_t w) { return to_f32<DT>((u16)(w >> 16)); }

@@ -316,7 +316,15 @@ static hipError_t launch_dt(int cfg, const GemmP& a, const GemmPlan& p, hipStrea
   }
 }
 
+// gemm_os_kernel's dispatch: up to 4 tiles per workgroup, or gate_up without a k split, take the
+// register-fragment body
+bool gemm_takes_frag(int cfg, const GemmPlan& p) {
+  const int nt = os_info(cfg).nt;
+  return p.kind == GK_ONESHOT && p.mchunks == 1 && nt > 0 && (nt <= 4 || (cfg == CFG_GATE_UP && p.ksplit == 1));
+}
+
 hipError_t launch_gemm(int dt, int cfg, const GemmP& a, const GemmPlan& p, hipStream_t st) {
+  if ((a.xfrag || a.yfrag) && !gemm_takes_frag(cfg, p)) return hipErrorInvalidValue;
   if (dt == DT_BF16) return launch_dt<DT_BF16>(cfg, a, p, st);
   return launch_dt<DT_F16>(cfg, a, p, st);
 }

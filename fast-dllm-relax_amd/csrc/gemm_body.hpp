@@ -354,11 +354,12 @@ __device__ __forceinline__ void os_epilogue(const GemmP& a, const f32x4 (&v)[TPU
         const float sl = rnd<DT>(gt * (1.0f / (1.0f + expf(-gt))));
         out[i] = from_f32<DT>(sl * up);
       }
-      st8<COH>(a.Y + (size_t)m * a.ldy + n, u32x2{pack2(out[0], out[1]), pack2(out[2], out[3])});
+      st8<COH>(a.Y + (a.yfrag ? frag_off(m, n) : (size_t)m * a.ldy + n), u32x2{pack2(out[0], out[1]), pack2(out[2], out[3])});
     }
   } else {
     const int n = 16 * t + 4 * lg;
     const bool ok = m < a.M && n < a.N;
+    u16* y = a.Y + (EPI == EPI_RESID && a.yfrag ? frag_off(m, n) : (size_t)m * a.ldy + n);
     u16 out[4];
     float ss = 0.f;
     if (ok) {
@@ -366,7 +367,7 @@ __device__ __forceinline__ void os_epilogue(const GemmP& a, const f32x4 (&v)[TPU
 #pragma unroll
         for (int i = 0; i < 4; ++i) out[i] = from_f32<DT>(v[0][i] + to_f32<DT>(a.bias[n + i]));
       } else {
-        const u32x2 hv = ld8<COH>(a.Y + (size_t)m * a.ldy + n);
+        const u32x2 hv = ld8<COH>(y);
         const float hf[4] = {lo_f32<DT>(hv[0]), hi_f32<DT>(hv[0]), lo_f32<DT>(hv[1]), hi_f32<DT>(hv[1])};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -375,7 +376,7 @@ __device__ __forceinline__ void os_epilogue(const GemmP& a, const f32x4 (&v)[TPU
           ss += y * y;
         }
       }
-      st8<COH>(a.Y + (size_t)m * a.ldy + n, u32x2{pack2(out[0], out[1]), pack2(out[2], out[3])});
+      st8<COH>(y, u32x2{pack2(out[0], out[1]), pack2(out[2], out[3])});
     }
     if constexpr (EPI == EPI_RESID) {
       ss += __shfl_xor(ss, 16, WAVE);
@@ -595,9 +596,11 @@ __device__ __forceinline__ void gemm_os_direct_body(const GemmP& a, int bx, int 
   for (int s = 0; s < KPW; ++s)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const int m = min(m0 + 16 * mt + lr, mlast);
-      const int k = 32 * (kb + ws + min(s, max(wn, 1) - 1)) + 8 * lg;
-      X[s][mt] = *reinterpret_cast<const u32x4*>(a.X + (size_t)m * a.ldx + k);
+      // row-major: the row (clamped to the last; rows past it are never stored); fragment order: the
+      // whole 1 KB block (m0 = 0)
+      const int m = min(m0 + 16 * mt + lr, mlast), ks = kb + ws + min(s, max(wn, 1) - 1);
+      const size_t off = a.xfrag ? (size_t)((2 * ks + mt) * 64 + lane) * 8 : (size_t)m * a.ldx + 32 * ks + 8 * lg;
+      X[s][mt] = *reinterpret_cast<const u32x4*>(a.X + off);
     }
   constexpr int SQ = 12;  // unrolled sums-of-squares loads (96 tiles: hidden 1536); the rest in a loop
   __shared__ u32x4 nw_s[XF == XF_RMS ? 8 * KPW * 4 : 1];

@@ -35,6 +35,9 @@ struct GemmP {
   float* stat_m; int32_t* stat_a; float* stat_s; int stat_tiles;  // EPI_LOGITS confidence statistics
   float* part; unsigned* counters;    // cross-workgroup split partials / arrival counters
   int ngroups;                        // tile groups of the one-shot launch (its gridDim.x)
+  // one-shot chains (M <= 32, the register-fragment body only): X, and Y of EPI_RESID / EPI_SILU_PAIR,
+  // in MFMA-fragment order (frag_off) instead of row-major
+  int xfrag, yfrag;
 };
 
 // Launch configurations (see gemm.hip); the host picks one per projection.
@@ -57,6 +60,8 @@ struct GemmPlan {
 // mm_target_wgs / mm_min_stages: the large-M kernel splits k only while the launch has fewer than
 // mm_target_wgs workgroups, and only into splits of at least mm_min_stages stages.
 GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, int mm_target_wgs = 256, int mm_min_stages = 8);
+// whether the plan runs the one-shot register-fragment body, the only one that takes xfrag / yfrag
+bool gemm_takes_frag(int cfg, const GemmPlan& p);
 hipError_t launch_gemm(int dt, int cfg, const GemmP& a, const GemmPlan& p, hipStream_t st);
 
 // ---- confidence ---------------------------------------------------------------------------------
@@ -68,15 +73,16 @@ hipError_t launch_confidence_tiles(const float* logits, int ld, int vocab, int r
 // ---- row kernels --------------------------------------------------------------------------------
 hipError_t launch_embed(const int32_t* ids, int n, const uint16_t* table, int vocab, int hidden, uint16_t* out,
                         hipStream_t st);
-// copy the input rows into the residual stream and emit their per-16-column sums of squares
+// copy the input rows into the residual stream and emit their per-16-column sums of squares; hfrag: h
+// in MFMA-fragment order (rows <= 32)
 hipError_t launch_load_rows(int dt, const uint16_t* x, int rows, int hidden, uint16_t* h, float* ssq, int ssq_ld,
-                            hipStream_t st);
-// y = RMSNorm(h) from the sums of squares the producer left (final norm)
+                            hipStream_t st, int hfrag = 0);
 // RoPE (cos, sin) table: row r sits at position pos_offset[r / rows_per_seq] + r % rows_per_seq
 hipError_t launch_rope_table(int dt, const int32_t* pos_offset, int rows, int rows_per_seq, float neg_log_theta,
                              float* tab, hipStream_t st);
+// y = RMSNorm(h) from the sums of squares the producer left (final norm); hfrag: h in MFMA-fragment order
 hipError_t launch_norm_rows(int dt, const uint16_t* h, int rows, int hidden, const float* ssq, int ssq_ld,
-                            const uint16_t* w, float eps, uint16_t* y, hipStream_t st);
+                            const uint16_t* w, float eps, uint16_t* y, hipStream_t st, int hfrag = 0);
 
 // ---- attention ----------------------------------------------------------------------------------
 constexpr int MAX_SEQS = 64;  // sequences of one batched call
@@ -96,6 +102,7 @@ struct AttnP {
   int prefill_hpw;                    // query heads per workgroup of the prefill kernel (0: chosen per launch)
   float* part;                        // split partials (merged by attn_merge_kernel)
   uint16_t* out;                      // [rows][nq * 128]
+  int ofrag;                          // out in MFMA-fragment order (frag_off; rows <= 32, nseq 1)
   // batched call (nseq > 1, chunked kernel only): sequence b owns rows [b rows, (b + 1) rows) of qkv,
   // rope and out, the cache at kc / vc + b seq_stride, writes from seq_ws[b] and attends
   // [0, seq_lk[b]); ws and Lk above then hold the largest window (S and chunk are planned for it)

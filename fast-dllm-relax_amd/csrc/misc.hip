@@ -20,11 +20,12 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t* ids, const u1
 // leaves the sum of squares of one 16-column tile of its row for the first layer's RMSNorm (the
 // layers' own residual epilogues leave the same statistics for the next norm).
 template <int DT>
-__global__ __launch_bounds__(256) void load_rows_kernel(const u16* x, int hidden, u16* h, float* ssq, int ssq_ld) {
+__global__ __launch_bounds__(256) void load_rows_kernel(const u16* x, int hidden, u16* h, float* ssq, int ssq_ld,
+                                                        int hfrag) {
   const int r = blockIdx.x;
   const u32x4* src = reinterpret_cast<const u32x4*>(x + (size_t)r * hidden);
-  u32x4* dst = reinterpret_cast<u32x4*>(h + (size_t)r * hidden);
-  for (int c = threadIdx.x; c < hidden / 8; c += blockDim.x) dst[c] = src[c];
+  for (int c = threadIdx.x; c < hidden / 8; c += blockDim.x)
+    *reinterpret_cast<u32x4*>(h + (hfrag ? frag_off(r, 8 * c) : (size_t)r * hidden + 8 * c)) = src[c];
   for (int t = threadIdx.x; t < hidden / 16; t += blockDim.x) {
     const u32x4 a = src[2 * t], b = src[2 * t + 1];
     float ss = 0.f;
@@ -48,7 +49,7 @@ __global__ __launch_bounds__(256) void load_rows_kernel(const u16* x, int hidden
 // x * 1/sqrt(var + eps) cast to the model dtype, then the weight multiply in the model dtype.
 template <int DT>
 __global__ __launch_bounds__(256) void norm_rows_kernel(const u16* h, int hidden, const float* ssq, int ssq_ld,
-                                                        const u16* w, float eps, u16* y) {
+                                                        const u16* w, float eps, u16* y, int hfrag) {
   __shared__ float part_s[4];
   const int r = blockIdx.x;
   float ss = 0.f;
@@ -57,9 +58,11 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(const u16* h, int hidden
   if ((threadIdx.x & 63) == 0) part_s[threadIdx.x >> 6] = ss;
   __syncthreads();
   const float inv = 1.0f / sqrtf(((part_s[0] + part_s[1]) + (part_s[2] + part_s[3])) / (float)hidden + eps);
-  const u16* hr = h + (size_t)r * hidden;
   u16* yr = y + (size_t)r * hidden;
-  for (int c = threadIdx.x; c < hidden; c += 256) yr[c] = from_f32<DT>(to_f32<DT>(w[c]) * rnd<DT>(to_f32<DT>(hr[c]) * inv));
+  for (int c = threadIdx.x; c < hidden; c += 256) {
+    const u16 hv = h[hfrag ? frag_off(r, c) : (size_t)r * hidden + c];
+    yr[c] = from_f32<DT>(to_f32<DT>(w[c]) * rnd<DT>(to_f32<DT>(hv) * inv));
+  }
 }
 
 // RoPE tables of one call (cuda.py:288-299): position pos_offset + r, inv_freq = exp(-ln(theta) * i / 64),
@@ -83,11 +86,12 @@ hipError_t launch_embed(const int32_t* ids, int n, const uint16_t* table, int vo
 }
 
 hipError_t launch_load_rows(int dt, const uint16_t* x, int rows, int hidden, uint16_t* h, float* ssq, int ssq_ld,
-                            hipStream_t st) {
+                            hipStream_t st, int hfrag) {
+  if (hfrag && rows > 32) return hipErrorInvalidValue;
   if (dt == DT_BF16)
-    hipLaunchKernelGGL(load_rows_kernel<DT_BF16>, dim3(rows), dim3(256), 0, st, x, hidden, h, ssq, ssq_ld);
+    hipLaunchKernelGGL(load_rows_kernel<DT_BF16>, dim3(rows), dim3(256), 0, st, x, hidden, h, ssq, ssq_ld, hfrag);
   else
-    hipLaunchKernelGGL(load_rows_kernel<DT_F16>, dim3(rows), dim3(256), 0, st, x, hidden, h, ssq, ssq_ld);
+    hipLaunchKernelGGL(load_rows_kernel<DT_F16>, dim3(rows), dim3(256), 0, st, x, hidden, h, ssq, ssq_ld, hfrag);
   return hipGetLastError();
 }
 
@@ -103,11 +107,12 @@ hipError_t launch_rope_table(int dt, const int32_t* pos_offset, int rows, int ro
 }
 
 hipError_t launch_norm_rows(int dt, const uint16_t* h, int rows, int hidden, const float* ssq, int ssq_ld,
-                            const uint16_t* w, float eps, uint16_t* y, hipStream_t st) {
+                            const uint16_t* w, float eps, uint16_t* y, hipStream_t st, int hfrag) {
+  if (hfrag && rows > 32) return hipErrorInvalidValue;
   if (dt == DT_BF16)
-    hipLaunchKernelGGL(norm_rows_kernel<DT_BF16>, dim3(rows), dim3(256), 0, st, h, hidden, ssq, ssq_ld, w, eps, y);
+    hipLaunchKernelGGL(norm_rows_kernel<DT_BF16>, dim3(rows), dim3(256), 0, st, h, hidden, ssq, ssq_ld, w, eps, y, hfrag);
   else
-    hipLaunchKernelGGL(norm_rows_kernel<DT_F16>, dim3(rows), dim3(256), 0, st, h, hidden, ssq, ssq_ld, w, eps, y);
+    hipLaunchKernelGGL(norm_rows_kernel<DT_F16>, dim3(rows), dim3(256), 0, st, h, hidden, ssq, ssq_ld, w, eps, y, hfrag);
   return hipGetLastError();
 }
 

@@ -320,6 +320,7 @@ __device__ __forceinline__ void step_attn_view(const Src& s, AttnP& a) {
   a.q_pos0 = s.q_pos0; a.block = s.block; a.bias = s.bias; a.bias_ld = s.bias_ld; a.S = s.S; a.chunk = s.chunk;
   a.target_wgs = s.target_wgs; a.prefill_hpw = s.prefill_hpw; a.part = gp(s.part); a.out = gp(s.out); a.nseq = 1;
   a.seq_stride = 0;
+  a.ofrag = 0;  // the persistent step keeps its activations row-major
 }
 
 // The launch's parameters are read through a constant-address-space pointer (scalar loads into scalar

@@ -161,6 +161,12 @@ int fdllm_bench_op(fdllm_ctx* ctx, int op, int rows, int layer, int iters, void*
  * per-operator kernels. */
 long long fdllm_persistent_steps(const fdllm_ctx* ctx);
 
+/* Diagnostic; it has no counterpart in the reference.  Number of layer-loop calls (cached steps, short
+ * stateless forwards) this context has run with the activations in MFMA-fragment order: calls of at
+ * most 32 rows whose four projections all take the one-shot GEMM, unless FDLLM_XFRAG=0 was set when
+ * the context was created.  Results are the same bit for bit either way. */
+long long fdllm_frag_calls(const fdllm_ctx* ctx);
+
 /* Message of this thread's last failure ("" if none). */
 const char* fdllm_last_error(void);
 
