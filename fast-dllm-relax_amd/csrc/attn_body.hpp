@@ -1,8 +1,10 @@
 // GQA attention of a block of rows against the in-place KV cache, with RoPE and the KV append fused in
 // (fast_dllm.attn_inplace, fast_dllm_relax/runtime.py:51-73; RoPE cuda.py:278-316; in-graph restatement
 // model/metal.py:255-302, 378-408).  Query head h uses kv head h / (nq / nkv); scores q.k * scale in
-// fp32, online softmax in fp32, P rounded to the model dtype for P.V on MFMA with fp32 accumulation
-// (the flash-attention precision the reference's callback uses), one rounding of the output.
+// fp32, online softmax in fp32 (in base 2: scores scaled by scale x log2(e), exponentials by the
+// hardware exp2), P rounded to the model dtype for P.V on MFMA with fp32 accumulation (the
+// flash-attention precision the reference's callback uses), one rounding of the output.  Split partials
+// carry their running maxima in the same base-2 units.
 //
 // Rows [ws, ws + rows) of the cache belong to this call: their K (after RoPE) and V are taken straight
 // from this call's qkv projection, and workgroup column 0 writes them to the cache.  Every other key
@@ -27,6 +29,7 @@ constexpr int KB = 32;        // keys per block
 constexpr int KLD = HD + 8;   // u16 stride of a K row in LDS
 constexpr int VLD = KB + 8;   // u16 stride of a transposed V row (one head dimension)
 constexpr int PSZ = 16 * HD + 32;  // floats per split partial of one query tile: O, then (m, l) per query
+constexpr float LOG2E = 1.4426950408889634f;
 
 template <int DT> __device__ __forceinline__ float elem(const u32x4& v, int e) {
   return (e & 1) ? hi_f32<DT>(v[e >> 1]) : lo_f32<DT>(v[e >> 1]);
@@ -96,6 +99,7 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
   }
   const int qpos_blk = a.mask == 1 ? (a.q_pos0 + r) / a.block : 0;
   const float* brow = a.mask == 2 ? a.bias + (long long)r * a.bias_ld : nullptr;
+  const float c2 = a.scale * LOG2E;
 
   const int kbeg = c * a.chunk;
   const int kend = min(kbeg + a.chunk, a.Lk);
@@ -188,13 +192,13 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int key = kb + 16 * kt + 4 * lg + i;
-        float v = s[kt][i] * a.scale;
+        float v = s[kt][i] * c2;
         if (key >= kend) {
           v = -INFINITY;
         } else if (a.mask == 1) {
           if (qpos_blk < key / a.block) v = -INFINITY;
         } else if (a.mask == 2) {
-          v += brow[key];
+          v += brow[key] * LOG2E;
         }
         s[kt][i] = v;
         mx = fmaxf(mx, v);
@@ -202,13 +206,13 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
     mx = rows_max(mx);
     const float m_new = fmaxf(m_run, mx);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = expf(m_run - m_use);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
     float ps = 0.f;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = expf(s[kt][i] - m_use);
+        const float p = __builtin_amdgcn_exp2f(s[kt][i] - m_use);
         s[kt][i] = p;
         ps += p;
       }
@@ -251,12 +255,12 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
       for (int k2 = 0; k2 < KSW; ++k2) M = fmaxf(M, cm[(k2 * QPW + qw) * 16 + lr]);
       const float Mu = M == -INFINITY ? 0.f : M;
       float L = 0.f;
-      for (int k2 = 0; k2 < KSW; ++k2) L += cl[(k2 * QPW + qw) * 16 + lr] * expf(cm[(k2 * QPW + qw) * 16 + lr] - Mu);
-      const float f0 = expf(cm[qw * 16 + lr] - Mu);
+      for (int k2 = 0; k2 < KSW; ++k2) L += cl[(k2 * QPW + qw) * 16 + lr] * __builtin_amdgcn_exp2f(cm[(k2 * QPW + qw) * 16 + lr] - Mu);
+      const float f0 = __builtin_amdgcn_exp2f(cm[qw * 16 + lr] - Mu);
 #pragma unroll
       for (int dt = 0; dt < HD / 16; ++dt) o[dt] *= f0;
       for (int k2 = 1; k2 < KSW; ++k2) {
-        const float fk = expf(cm[(k2 * QPW + qw) * 16 + lr] - Mu);
+        const float fk = __builtin_amdgcn_exp2f(cm[(k2 * QPW + qw) * 16 + lr] - Mu);
 #pragma unroll
         for (int dt = 0; dt < HD / 16; ++dt) o[dt] += co[(((k2 - 1) * QPW + qw) * (HD / 16) + dt) * 64 + lane] * fk;
       }
@@ -400,6 +404,7 @@ __device__ __forceinline__ void attn_chunk_compute(const AttnP& a, int bx, int b
   }
   const int qpos_blk = MASK == 1 ? (a.q_pos0 + r) / a.block : 0;
   const float* brow = MASK == 2 ? a.bias + (long long)r * a.bias_ld : nullptr;
+  const float c2 = a.scale * LOG2E;
 
   // ---- stage: K rows (window rows RoPE'd and appended to the cache), V transposed ----
 #pragma unroll
@@ -469,32 +474,42 @@ __device__ __forceinline__ void attn_chunk_compute(const AttnP& a, int bx, int b
         for (int ds = 0; ds < 4; ++ds) s[kt] = mfma16<DT>(*reinterpret_cast<const u32x4*>(kp + 32 * ds), qf[ds], s[kt]);
       }
       float mx = -INFINITY;
+      if (MASK == 0 && kb + 32 <= kend) {  // a whole block of keys: no per-key test
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+        for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = kb + 16 * kt + 4 * lg + i;
-          float v = s[kt][i] * a.scale;
-          if (key >= kend) {
-            v = -INFINITY;
-          } else if constexpr (MASK == 1) {
-            if (qpos_blk < key / a.block) v = -INFINITY;
-          } else if constexpr (MASK == 2) {
-            v += brow[key];
+          for (int i = 0; i < 4; ++i) {
+            s[kt][i] *= c2;
+            mx = fmaxf(mx, s[kt][i]);
           }
-          s[kt][i] = v;
-          mx = fmaxf(mx, v);
-        }
+      } else {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = kb + 16 * kt + 4 * lg + i;
+            float v = s[kt][i] * c2;
+            if (key >= kend) {
+              v = -INFINITY;
+            } else if constexpr (MASK == 1) {
+              if (qpos_blk < key / a.block) v = -INFINITY;
+            } else if constexpr (MASK == 2) {
+              v += brow[key] * LOG2E;
+            }
+            s[kt][i] = v;
+            mx = fmaxf(mx, v);
+          }
+      }
       mx = rows_max(mx);
       const float m_new = fmaxf(m_run, mx);
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = expf(m_run - m_use);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
       float ps = 0.f;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float pe = expf(s[kt][i] - m_use);
+          const float pe = __builtin_amdgcn_exp2f(s[kt][i] - m_use);
           s[kt][i] = pe;
           ps += pe;
         }
@@ -538,12 +553,12 @@ __device__ __forceinline__ void attn_chunk_compute(const AttnP& a, int bx, int b
       for (int k = 0; k < KH; ++k) M = fmaxf(M, cm[(k * QPW + qw) * 16 + lr]);
       const float Mu = M == -INFINITY ? 0.f : M;
       float L = 0.f;
-      for (int k = 0; k < KH; ++k) L += cl[(k * QPW + qw) * 16 + lr] * expf(cm[(k * QPW + qw) * 16 + lr] - Mu);
-      const float f0 = expf(cm[qw * 16 + lr] - Mu);
+      for (int k = 0; k < KH; ++k) L += cl[(k * QPW + qw) * 16 + lr] * __builtin_amdgcn_exp2f(cm[(k * QPW + qw) * 16 + lr] - Mu);
+      const float f0 = __builtin_amdgcn_exp2f(cm[qw * 16 + lr] - Mu);
 #pragma unroll
       for (int dt = 0; dt < DT16; ++dt) o[dt] *= f0;
       for (int k = 1; k < KH; ++k) {
-        const float fk = expf(cm[(k * QPW + qw) * 16 + lr] - Mu);
+        const float fk = __builtin_amdgcn_exp2f(cm[(k * QPW + qw) * 16 + lr] - Mu);
 #pragma unroll
         for (int dt = 0; dt < DT16; ++dt) o[dt] += co[(((k - 1) * QPW + qw) * DT16 + dt) * 64 + lane] * fk;
       }
@@ -644,7 +659,7 @@ __device__ __forceinline__ void attn_merge_wave(const AttnP& a, int dt, int qt, 
     const float Mu = M == -INFINITY ? 0.f : M;
 #pragma unroll
     for (int q = 0; q < SR; ++q) {
-      const float e = q < S ? expf(ml[q][0] - Mu) : 0.f;
+      const float e = q < S ? __builtin_amdgcn_exp2f(ml[q][0] - Mu) : 0.f;
       L += ml[q][1] * e;
       acc += ov[q] * e;
     }
@@ -668,7 +683,7 @@ __device__ __forceinline__ void attn_merge_wave(const AttnP& a, int dt, int qt, 
       }
 #pragma unroll
       for (int q = 0; q < SB; ++q) {
-        const float e = s0 + q < S ? expf(mv[q][0] - Mu) : 0.f;
+        const float e = s0 + q < S ? __builtin_amdgcn_exp2f(mv[q][0] - Mu) : 0.f;
         L += mv[q][1] * e;
         acc += ov[q] * e;
       }
@@ -768,7 +783,7 @@ __global__ __launch_bounds__(64 * NWQ) void attn_prefill_kernel(AttnP a, int hpw
   const size_t krow = (size_t)a.nkv * HD;
   const u16* kc = a.kc + g * HD;
   const u16* vc = a.vc + g * HD;
-  const float c2 = a.scale * 1.4426950408889634f;  // scale * log2(e)
+  const float c2 = a.scale * LOG2E;
 
   // the keys this workgroup needs: up to its last query's bound
   auto kend_of = [&](int r) {
