@@ -388,19 +388,25 @@ __device__ __forceinline__ void attn_chunk_compute(const AttnP& a, int bx, int b
   const int kend = min(kbeg + a.chunk, a.Lk);
   const bool writer = bx == 0;
 
-  // this lane's query row (qi = 16 qt + lr), RoPE'd in registers while the chunk is in flight
+  // this lane's query row (qi = 16 qt + lr), RoPE'd in registers while the chunk is in flight by the
+  // first key part's wave of the tile, which leaves the fragments in LDS for the other key parts
   const int qi = qt * 16 + lr;
   const bool qvalid = tile_ok && qi < QR;
   const int hh = qvalid ? qi / a.rows : 0;
   const int r = qvalid ? qi - hh * a.rows : 0;
   u32x4 qf[4];
-  {
+  u32x4* qbuf = reinterpret_cast<u32x4*>(vbuf + HD * VLDC);  // [QPW][4][64] (KH > 1)
+  if (KH == 1 || kh == 0) {
     const u16* qp = a.qkv + (size_t)r * a.ldq + (g * grp + hh) * HD + 8 * lg;
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) qf[ds] = ld16<COH>(qp + 32 * ds);
     const float* cs = a.rope + (size_t)r * 128;
     rope_tab<DT>(qf[0], qf[2], cs + 16 * lg);
     rope_tab<DT>(qf[1], qf[3], cs + 16 * lg + 64);
+    if (KH > 1) {
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds) qbuf[(qw * 4 + ds) * 64 + lane] = qf[ds];
+    }
   }
   const int qpos_blk = MASK == 1 ? (a.q_pos0 + r) / a.block : 0;
   const float* brow = MASK == 2 ? a.bias + (long long)r * a.bias_ld : nullptr;
@@ -452,6 +458,10 @@ __device__ __forceinline__ void attn_chunk_compute(const AttnP& a, int bx, int b
     }
   }
   __syncthreads();
+  if (KH > 1 && kh > 0) {
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) qf[ds] = qbuf[(qw * 4 + ds) * 64 + lane];
+  }
 
   // ---- scores and P.V over this wave's key part ----
   // lane (lr, lg) holds S^T[key kb + 16 kt + 4 lg + i][query lr] and O^T[dim 16 dt + 4 lg + i][query lr]

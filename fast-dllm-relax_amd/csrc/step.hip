@@ -19,9 +19,10 @@ size_t step_sync_words(const StepP& p) {
   return (size_t)BAR_CTRS * BAR_STRIDE + (size_t)std::max(p.d_groups, 1) * BAR_STRIDE + BAR_STRIDE;
 }
 
-// LDS of the attention chunk body (attn_chunk_compute with 4 query tiles x 2 key parts)
+// LDS of the attention chunk body (attn_chunk_compute with 4 query tiles x 2 key parts: K, V^T and the
+// query fragments)
 static size_t chunk_lds(int ch) {
-  const size_t loop = (size_t)ch * KLD * 2 + (size_t)HD * (ch + 8) * 2;
+  const size_t loop = (size_t)ch * KLD * 2 + (size_t)HD * (ch + 8) * 2 + (size_t)4 * 4 * 64 * 16;
   const size_t merge = (size_t)2 * 2 * 4 * 16 * 4 + (size_t)1 * 4 * (HD / 16) * 64 * 16;
   return std::max(loop, merge);
 }
