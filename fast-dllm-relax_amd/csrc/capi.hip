@@ -179,11 +179,14 @@ int run_gemm(fdllm_ctx* c, int cfg, GemmP a, int ksplit, hipStream_t st) {
   if (ksplit < 1 || a.KS % ksplit) return fail(FDLLM_EINVAL, "k split %d does not divide %d k steps", ksplit, a.KS);
   const GemmPlan pl = gemm_plan(cfg, a, ksplit, c->mm_target_wgs, c->mm_min_stages);
   if (pl.kind == GK_MM && a.nw != nullptr) {
-    // RMSNorm once for all column blocks (the large-M kernel takes normalised rows)
+    // RMSNorm once for all column blocks (the large-M kernel takes normalised rows; the LDS-staged one
+    // in its fragment blocks)
     if (a.ldx != a.H || a.KS * 32 != a.H) return fail(FDLLM_EINVAL, "normalised projection input must be [rows, hidden]");
-    HIPCHK(launch_norm_rows(f.dtype, a.X, a.M, a.H, a.ssq, a.ssq_ld, a.nw, a.eps, c->xn, st));
+    const int blocks = gemm_takes_blocks(pl) ? 1 : 0;
+    HIPCHK(launch_norm_rows(f.dtype, a.X, a.M, a.H, a.ssq, a.ssq_ld, a.nw, a.eps, c->xn, st, 0, blocks));
     a.X = c->xn;
     a.nw = nullptr;
+    a.xfrag = blocks ? 2 : 0;
   }
   if (pl.ksplit > 1) {
     int rc = ensure_floats(&c->gpart, &c->gpart_floats, pl.part_floats);

@@ -243,6 +243,13 @@ __device__ __forceinline__ size_t frag_off(int r, int c) {
   return (size_t)((c >> 5) * 2 + (r >> 4)) * 512 + (size_t)((r & 15) + 16 * ((c >> 3) & 3)) * 8 + (c & 7);
 }
 
+// The large-M LDS-staged GEMM takes its (normalised) activations in the same 1 KB fragment blocks,
+// ordered row block by row block: block (row block b, k step s) at element (b KS + s) x 512, KS k steps
+// per row.  Element (r, c):
+__device__ __forceinline__ size_t frag_blk_off(int r, int c, int KS) {
+  return ((size_t)(r >> 4) * KS + (c >> 5)) * 512 + (size_t)((r & 15) + 16 * ((c >> 3) & 3)) * 8 + (c & 7);
+}
+
 // ---- bf16/fp16 pairs packed in 32-bit words ---------------------------------------------------
 template <int DT> __device__ __forceinline__ float lo_f32(uint32_t w) { return to_f32<DT>((u16)(w & 0xffffu)); }
 template <int DT> __device__ __forceinline__ float hi_f32(uint32_t w) { return to_f32<DT>((u16)(w >> 16)); }

@@ -2,6 +2,7 @@
 // kernels and their bodies are in gemm_body.hpp.
 #include "gemm_body.hpp"
 #include "gemm_mm.hpp"
+#include "gemm_wt.hpp"
 
 #include <algorithm>
 
@@ -161,7 +162,16 @@ using MmSmall = MmCfg<4, 2, 1, 4, 2, 2>;  // 64 x 128, weights two stages ahead
 using MmWide = MmCfg<4, 4, 1, 4, 2, 1>;   // 64 x 256
 using MmWideD = MmCfg<4, 4, 1, 4, 2, 2>;  // 64 x 256, weights two stages ahead
 using MmBig = MmCfg<8, 2, 1, 8, 2, 1>;    // 128 x 256, 8 waves
-enum MmId : int { MM_SMALL = 0, MM_WIDE = 1, MM_WIDE_D = 2, MM_BIG = 3 };
+// LDS-staged kernel (gemm_wt.hpp): 2 x 2 waves of 64 x 96, a 128 x 192 block, four stage buffers of
+// 20 KB (two workgroups per compute unit)
+template <int MF, int TPW, int WM, int WN, int NBUF>
+struct WtCfg {
+  static constexpr int mf = MF, tpw = TPW, wm = WM, wn = WN, nw = WM * WN, nbuf = NBUF;
+  static constexpr int bm = 16 * MF * WM, bn_tiles = TPW * WN, kss = 1;
+  static constexpr size_t lds = (size_t)NBUF * (MF * WM + TPW * WN) * 1024;
+};
+using WtBig = WtCfg<4, 6, 2, 2, 4>;
+enum MmId : int { MM_SMALL = 0, MM_WIDE = 1, MM_WIDE_D = 2, MM_BIG = 3, MM_WT = 4 };
 struct MmInfo { int bm, bn_tiles, kss; };
 template <class M> constexpr MmInfo mm_info_of() { return MmInfo{M::bm, M::bn_tiles, M::kss}; }
 static MmInfo mm_info(int id) {
@@ -169,13 +179,16 @@ static MmInfo mm_info(int id) {
     case MM_WIDE: return mm_info_of<MmWide>();
     case MM_WIDE_D: return mm_info_of<MmWideD>();
     case MM_BIG: return mm_info_of<MmBig>();
+    case MM_WT: return mm_info_of<WtBig>();
     default: return mm_info_of<MmSmall>();
   }
 }
-static int mm_choice(int cfg, int M) {
+static int mm_choice(int cfg, int M, int ntiles) {
   switch (cfg) {
     case CFG_LM_HEAD: return MM_WIDE;  // one 256-column confidence tile per block column
-    case CFG_GATE_UP: return M >= 1024 ? MM_BIG : MM_WIDE;
+    case CFG_GATE_UP:
+      if (M >= 256 && ntiles % WtBig::bn_tiles == 0) return MM_WT;
+      return M >= 1024 ? MM_BIG : MM_WIDE;
     case CFG_DOWN: return M >= 1024 ? MM_WIDE_D : MM_SMALL;
     default: return MM_SMALL;
   }
@@ -185,7 +198,7 @@ GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, int mm_target_wgs, int m
   GemmPlan p{};
   p.mchunks = (a.M + 31) / 32;
   if (a.M > 32) {
-    const int id = mm_choice(cfg, a.M);
+    const int id = mm_choice(cfg, a.M, a.ntiles);
     const MmInfo mi = mm_info(id);
     if (a.KS % mi.kss == 0) {
       const int nst = a.KS / mi.kss;
@@ -196,8 +209,11 @@ GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, int mm_target_wgs, int m
       // k split: the smallest divisor of the stage count that brings the launch to mm_target_wgs
       // workgroups (at most 8 splits of at least mm_min_stages stages), else the largest such divisor
       const int wgs = p.nbm * p.nbn;
+      // (the LDS-staged kernel's blocks are four times the work of the others': it splits only below
+      // half of mm_target_wgs)
+      const int target = id == MM_WT ? mm_target_wgs / 2 : mm_target_wgs;
       int split = 1;
-      for (int d = 2; d <= 8 && wgs * split < mm_target_wgs && cfg != CFG_LM_HEAD; ++d)
+      for (int d = 2; d <= 8 && wgs * split < target && cfg != CFG_LM_HEAD; ++d)
         if (nst % d == 0 && nst / d >= mm_min_stages) split = d;
       p.ksplit = split;
       a.kps = a.KS / split;
@@ -275,10 +291,31 @@ static hipError_t launch_mm_cfg(const GemmP& a, const GemmPlan& p, hipStream_t s
   return hipGetLastError();
 }
 
+template <int DT, int EPI, class W>
+static hipError_t launch_wt_cfg(const GemmP& a, const GemmPlan& p, hipStream_t st) {
+  auto kern = gemm_wt_kernel<DT, EPI, W::mf, W::tpw, W::wm, W::wn, W::nbuf>;
+  static bool attr = false;  // per instantiation
+  if (!attr) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)W::lds) !=
+        hipSuccess)
+      (void)hipGetLastError();
+    attr = true;
+  }
+  const int total = p.nbm * p.nbn, per = (total + 7) / 8;
+  hipLaunchKernelGGL(kern, dim3(8 * per, p.ksplit), dim3(64 * W::nw), W::lds, st, a, p.nbm, p.nbn);
+  if (p.ksplit > 1) {
+    const int nblk = (a.M + 15) / 16;
+    hipLaunchKernelGGL((gemm_mm_split_epilogue_kernel<DT, EPI>), dim3((a.N + 15) / 16, (nblk + 3) / 4), dim3(256), 0,
+                       st, a, p.ksplit);
+  }
+  return hipGetLastError();
+}
+
 // GK_MM rows arrive normalised (see GemmKind), so every large-M launch runs without the norm transform.
 template <int DT, int CFG, class C>
 static hipError_t launch_mm(const GemmP& a, const GemmPlan& p, hipStream_t st) {
   if constexpr (CFG == CFG_GATE_UP) {
+    if (p.mm_id == MM_WT) return launch_wt_cfg<DT, C::epi, WtBig>(a, p, st);
     if (p.mm_id == MM_BIG) return launch_mm_cfg<DT, C::epi, XF_NONE, MmBig>(a, p, st);
     return launch_mm_cfg<DT, C::epi, XF_NONE, MmWide>(a, p, st);
   } else if constexpr (CFG == CFG_DOWN) {
@@ -323,8 +360,11 @@ bool gemm_takes_frag(int cfg, const GemmPlan& p) {
   return p.kind == GK_ONESHOT && p.mchunks == 1 && nt > 0 && (nt <= 4 || (cfg == CFG_GATE_UP && p.ksplit == 1));
 }
 
+bool gemm_takes_blocks(const GemmPlan& p) { return p.kind == GK_MM && p.mm_id == MM_WT; }
+
 hipError_t launch_gemm(int dt, int cfg, const GemmP& a, const GemmPlan& p, hipStream_t st) {
-  if ((a.xfrag || a.yfrag) && !gemm_takes_frag(cfg, p)) return hipErrorInvalidValue;
+  if (a.xfrag == 2 ? (a.yfrag || !gemm_takes_blocks(p)) : ((a.xfrag || a.yfrag) && !gemm_takes_frag(cfg, p)))
+    return hipErrorInvalidValue;
   if (dt == DT_BF16) return launch_dt<DT_BF16>(cfg, a, p, st);
   return launch_dt<DT_F16>(cfg, a, p, st);
 }

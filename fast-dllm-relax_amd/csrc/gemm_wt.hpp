@@ -1,0 +1,165 @@
+// Large-M GEMM with both operands staged through LDS by the gfx950 global-to-LDS copy (prefill, stateless
+// forward, batched steps): Y[M, N] = X[M, K] . W[N, K]^T on MFMA 16x16x32, fp32 accumulation, the
+// skinny kernels' epilogues and rounding points.
+//
+// A workgroup of WM x WN waves computes BM = 16 MF WM rows by BNT = TPW WN weight tiles (16 columns
+// each).  Wave (wm, wn) owns an MF x TPW block of 16 x 16 accumulators (128 x 96 at MF 8, TPW 6, kept
+// in the accumulation registers), so each 1 KB operand fragment it reads from LDS feeds TPW or MF
+// MFMAs.  The k loop runs one k step (32 columns) per stage.  A stage is BMB = MF WM activation
+// fragment blocks and BNT packed weight blocks, 1 KB each, copied global -> LDS without passing through
+// registers (one block per wave instruction: lane l's 16 bytes land at byte 16 l, which is MFMA
+// fragment order for both: the packed weights already are, and lane l of an activation block reads row
+// l % 16, columns 8 (l / 16) .. + 7).  NBUF stage buffers rotate: a wave waits for its own copies of the
+// stage (memory counter), one barrier makes every wave's copies visible and frees the buffer multiplied
+// one stage earlier, which then receives the copies NBUF - 1 stages ahead.  Every copy is unconditional
+// (stages past the last re-read the last; rows past M re-read row M - 1), so every wave issues the same
+// number per stage and the counter waits are exact.
+//
+// K splits (gridDim.y > 1) store fp32 sums per (tile, 16-row block) exactly as gemm_mm_kernel does, and
+// gemm_mm_split_epilogue_kernel adds them in split order.  Per output element the k steps are
+// accumulated in order by one MFMA chain, as in the other kernels, so for the same split the results are
+// the same bits as gemm_mm_kernel's.  Rows arrive normalised (the large-M path runs norm_rows once).
+#pragma once
+#include "gemm_mm.hpp"
+
+namespace fdllm {
+
+typedef __attribute__((address_space(3))) void lds_raw;
+
+// One 16-byte global -> LDS copy per lane (a wave: 1 KB at the wave-uniform LDS address, lane l at byte
+// 16 l).  Kept out of the kernel body: the builtin written in a kernel template's own body stops the
+// host pass from emitting the kernel's launch stub.
+__device__ __forceinline__ void lds_copy16(const u16* g, unsigned char* l) {
+  __builtin_amdgcn_global_load_lds(g, (lds_raw*)l, 16, 0, 0);
+}
+
+// s_waitcnt with the vector-memory count N (gfx9 encoding: vmcnt bits [3:0] and [15:14]; export and LDS
+// counts left at their maxima, so only vector memory is waited for)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int DT, int EPI, int MF, int TPW, int WM, int WN, int NBUF>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_wt_kernel(GemmP a, int nbm, int nbn) {
+  constexpr int NW = WM * WN;
+  constexpr int BMB = MF * WM;        // activation blocks (16 rows) per stage
+  constexpr int BNT = TPW * WN;       // weight tiles per stage
+  constexpr int SB = BMB + BNT;       // 1 KB blocks per stage
+  constexpr int DPW = SB / NW;        // copies per wave per stage
+  static_assert(SB % NW == 0, "every wave copies the same number of blocks per stage");
+  static_assert(NBUF >= 2, "at least two stage buffers");
+  static_assert((NBUF - 2) * DPW < 64, "outstanding copies fit the memory counter");
+  static_assert(EPI != EPI_SILU_PAIR || TPW % 2 == 0, "gate/up pairs stay within a wave");
+  static_assert(EPI != EPI_LOGITS, "the lm_head takes the streaming kernel");
+  extern __shared__ __align__(16) unsigned char smem[];  // [NBUF][SB][1 KB]
+
+  const int total = nbm * nbn;
+  const int per = (total + 7) / 8;
+  // workgroups of one weight column block on one XCD (the hardware deals workgroups to the 8 XCDs
+  // round-robin), so the blocks that re-read those weights share its L2
+  const int logical = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if (logical >= total) return;
+  const int nb = logical / nbm, mb = logical - nb * nbm;
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wm = w / WN, wn = w - wm * WN;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int m0 = mb * 16 * BMB, mlast = a.M - 1;
+  const int t0 = nb * BNT, tlast = a.ntiles - 1;
+  const int nst = a.KS / (int)gridDim.y;        // k steps of this split
+  const int kb = (int)blockIdx.y * nst;         // its first k step
+
+  // this wave's copies: block i = w + NW q of every stage; the per-lane source of k step 0
+  const u16* src[DPW];
+  size_t sstep[DPW];  // elements per k step
+#pragma unroll
+  for (int q = 0; q < DPW; ++q) {
+    const int i = w + NW * q;
+    if (i < BMB && a.xfrag == 2) {
+      // fragment blocks: one 1 KB read per block (a block past the last row block re-reads the last)
+      const int b = min(m0 / 16 + i, mlast / 16);
+      src[q] = a.X + ((size_t)b * a.KS + kb) * 512 + 8 * lane;
+      sstep[q] = 512;
+    } else if (i < BMB) {
+      const int m = min(m0 + 16 * i + lr, mlast);
+      src[q] = a.X + (size_t)m * a.ldx + 32 * kb + 8 * lg;
+      sstep[q] = 32;
+    } else {
+      src[q] = a.W + ((size_t)min(t0 + i - BMB, tlast) * a.KS + kb) * 512 + 8 * lane;
+      sstep[q] = 512;
+    }
+  }
+  auto copy_stage = [&](int st, int buf) {
+    const int s = min(st, nst - 1);
+#pragma unroll
+    for (int q = 0; q < DPW; ++q)
+      lds_copy16(src[q] + (size_t)s * sstep[q], smem + ((size_t)buf * SB + w + NW * q) * 1024);
+  };
+
+  f32x4 acc[TPW][MF];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j)
+#pragma unroll
+    for (int f = 0; f < MF; ++f) acc[j][f] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int st = 0; st < NBUF - 1; ++st) copy_stage(st, st);
+
+  // one stage per iteration, buffers indexed at run time: an unrolled rotation makes the register
+  // allocator shuffle the accumulators between copies of the loop body
+  const u32x4* lds = reinterpret_cast<const u32x4*>(smem);
+  int q = 0;  // buffer of stage st
+#pragma nounroll
+  for (int st = 0; st < nst; ++st) {
+    wait_vmcnt<(NBUF - 2) * DPW>();  // this wave's copies of stage st have landed
+    __builtin_amdgcn_s_barrier();    // everyone's have; buffer (st - 1) % NBUF is free
+    copy_stage(st + NBUF - 1, q == 0 ? NBUF - 1 : q - 1);
+    const u32x4* blk = lds + (size_t)q * SB * 64;
+    u32x4 xf[MF];
+#pragma unroll
+    for (int f = 0; f < MF; ++f) xf[f] = blk[(wm * MF + f) * 64 + lane];
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+      const u32x4 wf = blk[(BMB + wn * TPW + j) * 64 + lane];
+#pragma unroll
+      for (int f = 0; f < MF; ++f) acc[j][f] = mfma16<DT>(wf, xf[f], acc[j][f]);
+    }
+    q = q == NBUF - 1 ? 0 : q + 1;
+  }
+  wait_vmcnt<0>();  // no copy may still be writing LDS when the workgroup ends
+
+  const int f0 = wm * MF, tw0 = t0 + wn * TPW;
+  if (gridDim.y > 1) {
+    const int nblk = (a.M + 15) / 16;
+    f32x4* part = reinterpret_cast<f32x4*>(a.part);
+#pragma unroll
+    for (int j = 0; j < TPW; ++j)
+#pragma unroll
+      for (int f = 0; f < MF; ++f) {
+        const int t = tw0 + j, b = mb * BMB + f0 + f;
+        if (t < a.ntiles && b < nblk) part[(((size_t)blockIdx.y * a.ntiles + t) * nblk + b) * 64 + lane] = acc[j][f];
+      }
+    return;
+  }
+  if constexpr (EPI == EPI_SILU_PAIR) {
+#pragma unroll
+    for (int p = 0; p < TPW / 2; ++p)
+#pragma unroll
+      for (int f = 0; f < MF; ++f) {
+        const f32x4 v[2] = {acc[2 * p][f], acc[2 * p + 1][f]};
+        os_epilogue<DT, EPI, 2, false>(a, v, m0 + 16 * (f0 + f) + lr, tw0 + 2 * p, lg);
+      }
+  } else {
+#pragma unroll
+    for (int j = 0; j < TPW; ++j)
+#pragma unroll
+      for (int f = 0; f < MF; ++f) {
+        const f32x4 v[1] = {acc[j][f]};
+        os_epilogue<DT, EPI, 1, false>(a, v, m0 + 16 * (f0 + f) + lr, tw0 + j, lg);
+      }
+  }
+}
+
+}  // namespace fdllm

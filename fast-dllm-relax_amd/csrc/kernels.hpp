@@ -36,7 +36,8 @@ struct GemmP {
   float* part; unsigned* counters;    // cross-workgroup split partials / arrival counters
   int ngroups;                        // tile groups of the one-shot launch (its gridDim.x)
   // one-shot chains (M <= 32, the register-fragment body only): X, and Y of EPI_RESID / EPI_SILU_PAIR,
-  // in MFMA-fragment order (frag_off) instead of row-major
+  // in MFMA-fragment order (frag_off) instead of row-major; xfrag 2: X in the large-M LDS-staged
+  // kernel's fragment blocks (frag_blk_off)
   int xfrag, yfrag;
 };
 
@@ -60,8 +61,10 @@ struct GemmPlan {
 // mm_target_wgs / mm_min_stages: the large-M kernel splits k only while the launch has fewer than
 // mm_target_wgs workgroups, and only into splits of at least mm_min_stages stages.
 GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, int mm_target_wgs = 256, int mm_min_stages = 8);
-// whether the plan runs the one-shot register-fragment body, the only one that takes xfrag / yfrag
+// whether the plan runs the one-shot register-fragment body, the only one that takes xfrag / yfrag 1
 bool gemm_takes_frag(int cfg, const GemmPlan& p);
+// whether the plan runs the large-M LDS-staged kernel, the only one that takes xfrag 2
+bool gemm_takes_blocks(const GemmPlan& p);
 hipError_t launch_gemm(int dt, int cfg, const GemmP& a, const GemmPlan& p, hipStream_t st);
 
 // ---- confidence ---------------------------------------------------------------------------------
@@ -80,9 +83,10 @@ hipError_t launch_load_rows(int dt, const uint16_t* x, int rows, int hidden, uin
 // RoPE (cos, sin) table: row r sits at position pos_offset[r / rows_per_seq] + r % rows_per_seq
 hipError_t launch_rope_table(int dt, const int32_t* pos_offset, int rows, int rows_per_seq, float neg_log_theta,
                              float* tab, hipStream_t st);
-// y = RMSNorm(h) from the sums of squares the producer left (final norm); hfrag: h in MFMA-fragment order
+// y = RMSNorm(h) from the sums of squares the producer left (final norm); hfrag: h in MFMA-fragment order;
+// yblk: y in the large-M kernel's fragment blocks (frag_blk_off) instead of row-major
 hipError_t launch_norm_rows(int dt, const uint16_t* h, int rows, int hidden, const float* ssq, int ssq_ld,
-                            const uint16_t* w, float eps, uint16_t* y, hipStream_t st, int hfrag = 0);
+                            const uint16_t* w, float eps, uint16_t* y, hipStream_t st, int hfrag = 0, int yblk = 0);
 
 // ---- attention ----------------------------------------------------------------------------------
 constexpr int MAX_SEQS = 64;  // sequences of one batched call

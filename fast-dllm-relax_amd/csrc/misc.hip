@@ -49,7 +49,7 @@ __global__ __launch_bounds__(256) void load_rows_kernel(const u16* x, int hidden
 // x * 1/sqrt(var + eps) cast to the model dtype, then the weight multiply in the model dtype.
 template <int DT>
 __global__ __launch_bounds__(256) void norm_rows_kernel(const u16* h, int hidden, const float* ssq, int ssq_ld,
-                                                        const u16* w, float eps, u16* y, int hfrag) {
+                                                        const u16* w, float eps, u16* y, int hfrag, int yblk) {
   __shared__ float part_s[4];
   const int r = blockIdx.x;
   float ss = 0.f;
@@ -58,10 +58,10 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(const u16* h, int hidden
   if ((threadIdx.x & 63) == 0) part_s[threadIdx.x >> 6] = ss;
   __syncthreads();
   const float inv = 1.0f / sqrtf(((part_s[0] + part_s[1]) + (part_s[2] + part_s[3])) / (float)hidden + eps);
-  u16* yr = y + (size_t)r * hidden;
   for (int c = threadIdx.x; c < hidden; c += 256) {
     const u16 hv = h[hfrag ? frag_off(r, c) : (size_t)r * hidden + c];
-    yr[c] = from_f32<DT>(to_f32<DT>(w[c]) * rnd<DT>(to_f32<DT>(hv) * inv));
+    y[yblk ? frag_blk_off(r, c, hidden / 32) : (size_t)r * hidden + c] =
+        from_f32<DT>(to_f32<DT>(w[c]) * rnd<DT>(to_f32<DT>(hv) * inv));
   }
 }
 
@@ -107,12 +107,14 @@ hipError_t launch_rope_table(int dt, const int32_t* pos_offset, int rows, int ro
 }
 
 hipError_t launch_norm_rows(int dt, const uint16_t* h, int rows, int hidden, const float* ssq, int ssq_ld,
-                            const uint16_t* w, float eps, uint16_t* y, hipStream_t st, int hfrag) {
-  if (hfrag && rows > 32) return hipErrorInvalidValue;
+                            const uint16_t* w, float eps, uint16_t* y, hipStream_t st, int hfrag, int yblk) {
+  if ((hfrag && rows > 32) || (yblk && hidden % 32)) return hipErrorInvalidValue;
   if (dt == DT_BF16)
-    hipLaunchKernelGGL(norm_rows_kernel<DT_BF16>, dim3(rows), dim3(256), 0, st, h, hidden, ssq, ssq_ld, w, eps, y, hfrag);
+    hipLaunchKernelGGL(norm_rows_kernel<DT_BF16>, dim3(rows), dim3(256), 0, st, h, hidden, ssq, ssq_ld, w, eps, y, hfrag,
+                       yblk);
   else
-    hipLaunchKernelGGL(norm_rows_kernel<DT_F16>, dim3(rows), dim3(256), 0, st, h, hidden, ssq, ssq_ld, w, eps, y, hfrag);
+    hipLaunchKernelGGL(norm_rows_kernel<DT_F16>, dim3(rows), dim3(256), 0, st, h, hidden, ssq, ssq_ld, w, eps, y, hfrag,
+                       yblk);
   return hipGetLastError();
 }
 
