@@ -368,6 +368,14 @@ LayerGemms layer_gemms(const fdllm_ctx* c, const Layer& L, int rows, bool frag) 
   g.d.Y = c->h; g.d.ldy = H; g.d.ssq_out = c->ssq; g.d.ssq_ld = ssq_ld;
   g.d.xfrag = g.d.yfrag = frag;
   g.dsplit = divisor_at_most(I / 32, c->down_split);
+  if (!frag && rows > 32) {
+    // large M: when gate_up and down both run the LDS-staged kernel, SiLU * up goes straight into the
+    // fragment blocks down copies
+    GemmP tg = g.gu, td = g.d;
+    const GemmPlan pg = gemm_plan(CFG_GATE_UP, tg, 1, c->mm_target_wgs, c->mm_min_stages);
+    const GemmPlan pd = gemm_plan(CFG_DOWN, td, g.dsplit, c->mm_target_wgs, c->mm_min_stages);
+    if (gemm_takes_blocks(pg) && gemm_takes_blocks(pd)) g.gu.yfrag = g.d.xfrag = 2;
+  }
   return g;
 }
 

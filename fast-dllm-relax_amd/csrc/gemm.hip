@@ -189,8 +189,11 @@ static int mm_choice(int cfg, int M, int ntiles) {
     case CFG_GATE_UP:
       if (M >= 256 && ntiles % WtBig::bn_tiles == 0) return MM_WT;
       return M >= 1024 ? MM_BIG : MM_WIDE;
-    case CFG_DOWN: return M >= 1024 ? MM_WIDE_D : MM_SMALL;
-    default: return MM_SMALL;
+    case CFG_DOWN:
+      if (M >= 256 && ntiles % WtBig::bn_tiles == 0) return MM_WT;
+      return M >= 1024 ? MM_WIDE_D : MM_SMALL;
+    default:  // qkv, o_proj: the LDS-staged kernel measured slower at their widths (2048 / 1536 columns)
+      return MM_SMALL;
   }
 }
 
@@ -209,11 +212,8 @@ GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, int mm_target_wgs, int m
       // k split: the smallest divisor of the stage count that brings the launch to mm_target_wgs
       // workgroups (at most 8 splits of at least mm_min_stages stages), else the largest such divisor
       const int wgs = p.nbm * p.nbn;
-      // (the LDS-staged kernel's blocks are four times the work of the others': it splits only below
-      // half of mm_target_wgs)
-      const int target = id == MM_WT ? mm_target_wgs / 2 : mm_target_wgs;
       int split = 1;
-      for (int d = 2; d <= 8 && wgs * split < target && cfg != CFG_LM_HEAD; ++d)
+      for (int d = 2; d <= 8 && wgs * split < mm_target_wgs && cfg != CFG_LM_HEAD; ++d)
         if (nst % d == 0 && nst / d >= mm_min_stages) split = d;
       p.ksplit = split;
       a.kps = a.KS / split;
@@ -319,6 +319,7 @@ static hipError_t launch_mm(const GemmP& a, const GemmPlan& p, hipStream_t st) {
     if (p.mm_id == MM_BIG) return launch_mm_cfg<DT, C::epi, XF_NONE, MmBig>(a, p, st);
     return launch_mm_cfg<DT, C::epi, XF_NONE, MmWide>(a, p, st);
   } else if constexpr (CFG == CFG_DOWN) {
+    if (p.mm_id == MM_WT) return launch_wt_cfg<DT, C::epi, WtBig>(a, p, st);
     if (p.mm_id == MM_WIDE_D) return launch_mm_cfg<DT, C::epi, XF_NONE, MmWideD>(a, p, st);
     return launch_mm_cfg<DT, C::epi, XF_NONE, MmSmall>(a, p, st);
   } else if constexpr (CFG == CFG_QKV || CFG == CFG_OPROJ) {
@@ -363,8 +364,9 @@ bool gemm_takes_frag(int cfg, const GemmPlan& p) {
 bool gemm_takes_blocks(const GemmPlan& p) { return p.kind == GK_MM && p.mm_id == MM_WT; }
 
 hipError_t launch_gemm(int dt, int cfg, const GemmP& a, const GemmPlan& p, hipStream_t st) {
-  if (a.xfrag == 2 ? (a.yfrag || !gemm_takes_blocks(p)) : ((a.xfrag || a.yfrag) && !gemm_takes_frag(cfg, p)))
-    return hipErrorInvalidValue;
+  if ((a.xfrag == 1 || a.yfrag == 1) && !gemm_takes_frag(cfg, p)) return hipErrorInvalidValue;
+  if ((a.xfrag == 2 || a.yfrag == 2) && !gemm_takes_blocks(p)) return hipErrorInvalidValue;
+  if (a.yfrag == 2 && cfg != CFG_GATE_UP) return hipErrorInvalidValue;
   if (dt == DT_BF16) return launch_dt<DT_BF16>(cfg, a, p, st);
   return launch_dt<DT_F16>(cfg, a, p, st);
 }

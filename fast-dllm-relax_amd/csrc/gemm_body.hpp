@@ -354,7 +354,8 @@ __device__ __forceinline__ void os_epilogue(const GemmP& a, const f32x4 (&v)[TPU
         const float sl = rnd<DT>(gt * (1.0f / (1.0f + expf(-gt))));
         out[i] = from_f32<DT>(sl * up);
       }
-      st8<COH>(a.Y + (a.yfrag ? frag_off(m, n) : (size_t)m * a.ldy + n), u32x2{pack2(out[0], out[1]), pack2(out[2], out[3])});
+      const size_t o = a.yfrag == 1 ? frag_off(m, n) : a.yfrag == 2 ? frag_blk_off(m, n, a.ldy >> 5) : (size_t)m * a.ldy + n;
+      st8<COH>(a.Y + o, u32x2{pack2(out[0], out[1]), pack2(out[2], out[3])});
     }
   } else {
     const int n = 16 * t + 4 * lg;

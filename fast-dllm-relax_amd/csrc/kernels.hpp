@@ -35,9 +35,9 @@ struct GemmP {
   float* stat_m; int32_t* stat_a; float* stat_s; int stat_tiles;  // EPI_LOGITS confidence statistics
   float* part; unsigned* counters;    // cross-workgroup split partials / arrival counters
   int ngroups;                        // tile groups of the one-shot launch (its gridDim.x)
-  // one-shot chains (M <= 32, the register-fragment body only): X, and Y of EPI_RESID / EPI_SILU_PAIR,
-  // in MFMA-fragment order (frag_off) instead of row-major; xfrag 2: X in the large-M LDS-staged
-  // kernel's fragment blocks (frag_blk_off)
+  // 1: one-shot chains (M <= 32, the register-fragment body only): X, and Y of EPI_RESID /
+  // EPI_SILU_PAIR, in MFMA-fragment order (frag_off) instead of row-major; 2: X, and the Y of
+  // EPI_SILU_PAIR, in the large-M LDS-staged kernel's fragment blocks (frag_blk_off)
   int xfrag, yfrag;
 };
 
