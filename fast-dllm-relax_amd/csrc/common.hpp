@@ -250,6 +250,25 @@ __device__ __forceinline__ size_t frag_blk_off(int r, int c, int KS) {
   return ((size_t)(r >> 4) * KS + (c >> 5)) * 512 + (size_t)((r & 15) + 16 * ((c >> 3) & 3)) * 8 + (c & 7);
 }
 
+// ---- LDS helpers ---------------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_raw;
+
+// One 16-byte global -> LDS copy per lane (gfx950 global_load_lds_dwordx4: a wave writes 1 KB at the
+// wave-uniform LDS address, lane l at byte 16 l).  Kept out of kernel
+// bodies: the builtin written in a kernel template's own body stops the host pass from emitting the
+// kernel's launch stub.
+__device__ __forceinline__ void lds_copy16(const u16* g, unsigned char* l) {
+  __builtin_amdgcn_global_load_lds(g, (lds_raw*)l, 16, 0, 0);
+}
+
+// s_waitcnt with the vector-memory count N (gfx9 encoding: vmcnt bits [3:0] and [15:14]; export and LDS
+// counts left at their maxima, so only vector memory is waited for)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // ---- bf16/fp16 pairs packed in 32-bit words ---------------------------------------------------
 template <int DT> __device__ __forceinline__ float lo_f32(uint32_t w) { return to_f32<DT>((u16)(w & 0xffffu)); }
 template <int DT> __device__ __forceinline__ float hi_f32(uint32_t w) { return to_f32<DT>((u16)(w >> 16)); }

@@ -24,23 +24,6 @@
 
 namespace fdllm {
 
-typedef __attribute__((address_space(3))) void lds_raw;
-
-// One 16-byte global -> LDS copy per lane (a wave: 1 KB at the wave-uniform LDS address, lane l at byte
-// 16 l).  Kept out of the kernel body: the builtin written in a kernel template's own body stops the
-// host pass from emitting the kernel's launch stub.
-__device__ __forceinline__ void lds_copy16(const u16* g, unsigned char* l) {
-  __builtin_amdgcn_global_load_lds(g, (lds_raw*)l, 16, 0, 0);
-}
-
-// s_waitcnt with the vector-memory count N (gfx9 encoding: vmcnt bits [3:0] and [15:14]; export and LDS
-// counts left at their maxima, so only vector memory is waited for)
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 template <int DT, int EPI, int MF, int TPW, int WM, int WN, int NBUF>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_wt_kernel(GemmP a, int nbm, int nbn) {
   constexpr int NW = WM * WN;
