@@ -776,12 +776,10 @@ __global__ __launch_bounds__(64 * NWQ) void attn_prefill_kernel(AttnP a, int hpw
   static_assert(MASK == 0 || MASK == 1, "explicit biases take attn_kernel");
   constexpr int DT16 = HD / 16;
   extern __shared__ __align__(16) unsigned char smem[];
-  u16* kb_[2];
-  u16* vb_[2];
-  kb_[0] = reinterpret_cast<u16*>(smem);
-  vb_[0] = kb_[0] + KBP * KLDP;
-  kb_[1] = vb_[0] + HD * VLDP;
-  vb_[1] = kb_[1] + KBP * KLDP;
+  // buffer b: K at element b * BUFE, V^T after it.  Offsets from the shared array itself (not pointers
+  // picked from a local array), so that every access stays a direct LDS access instead of a flat one.
+  constexpr int BUFE = KBP * KLDP + HD * VLDP;
+  u16* const lds16 = reinterpret_cast<u16*>(smem);
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int lr = lane & 15, lg = lane >> 4;
@@ -847,7 +845,7 @@ __global__ __launch_bounds__(64 * NWQ) void attn_prefill_kernel(AttnP a, int hpw
     for (int it = 0; it < KIT; ++it) {
       const int item = threadIdx.x + it * NT;
       const int j = (item & 15) + 16 * (item >> 8), c = (item >> 4) & 15;
-      *reinterpret_cast<u32x4*>(kb_[buf] + j * KLDP + 8 * c) = kr[it];
+      *reinterpret_cast<u32x4*>(lds16 + buf * BUFE + j * KLDP + 8 * c) = kr[it];
     }
 #pragma unroll
     for (int it = 0; it < VIT; ++it) {
@@ -858,7 +856,7 @@ __global__ __launch_bounds__(64 * NWQ) void attn_prefill_kernel(AttnP a, int hpw
         const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
         const uint32_t w01 = __builtin_amdgcn_perm(vr[it][1][e >> 1], vr[it][0][e >> 1], sel);
         const uint32_t w23 = __builtin_amdgcn_perm(vr[it][3][e >> 1], vr[it][2][e >> 1], sel);
-        *reinterpret_cast<u32x2*>(vb_[buf] + (8 * dc + e) * VLDP + 4 * kq) = u32x2{w01, w23};
+        *reinterpret_cast<u32x2*>(lds16 + buf * BUFE + KBP * KLDP + (8 * dc + e) * VLDP + 4 * kq) = u32x2{w01, w23};
       }
     }
   };
@@ -879,8 +877,8 @@ __global__ __launch_bounds__(64 * NWQ) void attn_prefill_kernel(AttnP a, int hpw
   for (int kb = 0; kb < nkb; ++kb) {
     const int buf = kb & 1;
     load(min(kb + 1, nkb - 1));
-    const u16* kbuf = kb_[buf];
-    const u16* vbuf = vb_[buf];
+    const u16* kbuf = lds16 + buf * BUFE;
+    const u16* vbuf = kbuf + KBP * KLDP;
     const int k0 = kb * KBP;
 #pragma unroll
     for (int i = 0; i < TQ; ++i) {
