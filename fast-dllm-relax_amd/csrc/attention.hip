@@ -102,9 +102,11 @@ static hipError_t launch_chunk_mask(const AttnP& a, const AttnPlan& p, hipStream
   }
 }
 
-// Long row blocks: RoPE + KV append pass, then the flash-style kernel with the most query heads per
-// workgroup that still gives 1024 workgroups (measured at 512 / 2048 / 8192 rows: more workgroups win
-// over fewer K/V re-reads until about that many).
+// Long row blocks: RoPE + KV append pass, then the flash-style kernel.  Two query heads per workgroup,
+// as four waves of one query tile each, once that still gives 1024 workgroups; else one head (more
+// workgroups win over fewer K/V re-reads below about that many).  Measured at 2048 and 8192 rows
+// against three heads as two waves of three tiles (one wave per SIMD either way): 38.7 against 41.4 ms
+// for the 8192-row prefill.  Three and six heads stay available through FDLLM_PREFILL_HPW.
 template <int DT, int MASK, int TQ, int NWQ>
 static hipError_t launch_prefill_cfg(const AttnP& a, int hpw, hipStream_t st) {
   constexpr size_t lds = 2 * ((size_t)64 * (HD + 8) + (size_t)HD * (64 + 8)) * 2;
@@ -119,15 +121,13 @@ template <int DT, int MASK>
 static hipError_t launch_prefill(const AttnP& a, hipStream_t st) {
   hipLaunchKernelGGL(rope_kv_kernel<DT>, dim3(a.rows), dim3(128), 0, st, a);
   const int nqb = (a.rows + 31) / 32, grp = a.nq / a.nkv;
-  int hpw = 1;
-  for (int h : {6, 3, 2})
-    if (grp % h == 0 && nqb * (grp / h) * a.nkv >= 1024) { hpw = h; break; }
+  int hpw = grp % 2 == 0 && nqb * (grp / 2) * a.nkv >= 1024 ? 2 : 1;
   const int ph = a.prefill_hpw;
   if ((ph == 1 || ph == 2 || ph == 3 || ph == 6) && grp % ph == 0) hpw = ph;
   switch (hpw) {
     case 6: return launch_prefill_cfg<DT, MASK, 3, 4>(a, 6, st);
     case 3: return launch_prefill_cfg<DT, MASK, 3, 2>(a, 3, st);
-    case 2: return launch_prefill_cfg<DT, MASK, 2, 2>(a, 2, st);
+    case 2: return launch_prefill_cfg<DT, MASK, 1, 4>(a, 2, st);
     default: return launch_prefill_cfg<DT, MASK, 1, 2>(a, 1, st);
   }
 }
