@@ -78,7 +78,9 @@ static hipError_t launch_loop(const AttnP& a, const AttnPlan& p, hipStream_t st)
 template <int DT, int CH, int KH, int MASK>
 static hipError_t launch_chunk_kh(const AttnP& a, const AttnPlan& p, hipStream_t st) {
   constexpr int QPW = 4;
-  const size_t loop_lds = (size_t)CH * KLD * 2 + (size_t)HD * (CH + 8) * 2 + (KH > 1 ? (size_t)QPW * 4 * 64 * 16 : 0);
+  // K and V^T of the chunk, then (one-sequence calls) the queries the first key part shares
+  const size_t loop_lds = (size_t)CH * KLD * 2 + (size_t)HD * (CH + 8) * 2 +
+                          (KH > 1 && a.nseq <= 1 ? (size_t)QPW * 4 * 64 * 16 : 0);
   const size_t merge_lds = (size_t)2 * KH * QPW * 16 * 4 + (size_t)(KH - 1) * QPW * (HD / 16) * 64 * 16;
   const size_t lds = std::max(loop_lds, merge_lds);
   if (lds > 160 * 1024) return hipErrorInvalidValue;

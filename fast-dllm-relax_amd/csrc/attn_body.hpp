@@ -394,16 +394,19 @@ __device__ __forceinline__ void attn_chunk_compute(const AttnP& a, int bx, int b
   const bool qvalid = tile_ok && qi < QR;
   const int hh = qvalid ? qi / a.rows : 0;
   const int r = qvalid ? qi - hh * a.rows : 0;
+  // (a batched call runs three or more workgroup rounds: it skips the sharing, whose 16 KB of LDS would
+  // keep a second workgroup off each compute unit, and every wave loads its queries itself)
   u32x4 qf[4];
   u32x4* qbuf = reinterpret_cast<u32x4*>(vbuf + HD * VLDC);  // [QPW][4][64] (KH > 1)
-  if (KH == 1 || kh == 0) {
+  const bool qshare = KH > 1 && a.nseq <= 1;
+  if (!qshare || kh == 0) {
     const u16* qp = a.qkv + (size_t)r * a.ldq + (g * grp + hh) * HD + 8 * lg;
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) qf[ds] = ld16<COH>(qp + 32 * ds);
     const float* cs = a.rope + (size_t)r * 128;
     rope_tab<DT>(qf[0], qf[2], cs + 16 * lg);
     rope_tab<DT>(qf[1], qf[3], cs + 16 * lg + 64);
-    if (KH > 1) {
+    if (qshare) {
 #pragma unroll
       for (int ds = 0; ds < 4; ++ds) qbuf[(qw * 4 + ds) * 64 + lane] = qf[ds];
     }
@@ -458,7 +461,7 @@ __device__ __forceinline__ void attn_chunk_compute(const AttnP& a, int bx, int b
     }
   }
   __syncthreads();
-  if (KH > 1 && kh > 0) {
+  if (qshare && kh > 0) {
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) qf[ds] = qbuf[(qw * 4 + ds) * 64 + lane];
   }
