@@ -141,9 +141,10 @@ def shifted_confidence(vm: HipVM, hidden: torch.Tensor) -> tuple[np.ndarray, np.
 
     Device path of runtime.py:168-174: the fused lm_head + confidence kernel reduces the logits, only
     2 x rows values come back."""
-    ids_d, maxp_d = vm.get_confidence(hidden)
-    both = torch.cat([ids_d.view(torch.float32), maxp_d], dim=1).cpu().numpy()[0]
-    rows = ids_d.shape[1]
+    rows = hidden.shape[1]
+    both_d = torch.empty((1, 2 * rows), dtype=torch.int32, device=hidden.device)
+    vm.get_confidence(hidden, out=both_d)
+    both = both_d.cpu().numpy()[0].view(np.float32)
     ids = both[:rows].view(np.int32).astype(np.int64)
     maxp = both[rows:].astype(np.float32)
     return np.concatenate([ids[:1], ids[:-1]]), np.concatenate([maxp[:1], maxp[:-1]]), int(ids[-1])
@@ -411,8 +412,9 @@ def batched_shifted_confidence(vm: HipVM, hidden: torch.Tensor) -> tuple[np.ndar
     """shifted_confidence of each sequence of hidden [nseq, rows, H]: ids / probs [nseq, rows], the shift
     of runtime.py:172-174 applied within each sequence (row 0 keeps its own prediction)."""
     nseq, rows = int(hidden.shape[0]), int(hidden.shape[1])
-    ids_d, maxp_d = vm.get_confidence(hidden.view(1, nseq * rows, -1))
-    both = torch.cat([ids_d.view(torch.float32), maxp_d], dim=1).cpu().numpy()[0]
+    both_d = torch.empty((1, 2 * nseq * rows), dtype=torch.int32, device=hidden.device)
+    vm.get_confidence(hidden.view(1, nseq * rows, -1), out=both_d)
+    both = both_d.cpu().numpy()[0].view(np.float32)
     ids = both[:nseq * rows].view(np.int32).astype(np.int64).reshape(nseq, rows)
     maxp = both[nseq * rows:].astype(np.float32).reshape(nseq, rows)
     return (np.concatenate([ids[:, :1], ids[:, :-1]], axis=1), np.concatenate([maxp[:, :1], maxp[:, :-1]], axis=1))

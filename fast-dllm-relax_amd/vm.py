@@ -263,11 +263,18 @@ class HipVM:
                                                          _ptr(k_cache), _ptr(v_cache), cap, nseq, int(seq), _stream()))
         return k_cache, v_cache
 
-    def get_confidence(self, hidden_states: torch.Tensor, logits: torch.Tensor | None = None):
-        """(ids [1, rows] int32, maxp [1, rows] fp32), unshifted (metal.py:505-528)."""
+    def get_confidence(self, hidden_states: torch.Tensor, logits: torch.Tensor | None = None, out=None):
+        """(ids [1, rows] int32, maxp [1, rows] fp32), unshifted (metal.py:505-528).  out: an optional
+        contiguous [1, 2 rows] int32 device tensor that receives ids then maxp (bit-cast), so that one
+        copy brings both back to the host."""
         rows = self._check_rows(hidden_states)
-        ids = torch.empty((1, rows), dtype=torch.int32, device=hidden_states.device)
-        maxp = torch.empty((1, rows), dtype=torch.float32, device=hidden_states.device)
+        if out is None:
+            ids = torch.empty((1, rows), dtype=torch.int32, device=hidden_states.device)
+            maxp = torch.empty((1, rows), dtype=torch.float32, device=hidden_states.device)
+        else:
+            if tuple(out.shape) != (1, 2 * rows) or out.dtype != torch.int32 or not out.is_contiguous():
+                raise ValueError(f"out must be a contiguous [1, {2 * rows}] int32 tensor")
+            ids, maxp = out[:, :rows], out[:, rows:].view(torch.float32)
         if logits is not None and (tuple(logits.shape) != (1, rows, self.cfg.vocab_size)
                                    or logits.dtype != torch.float32 or not logits.is_contiguous()):
             raise ValueError("logits must be a contiguous [1, rows, vocab] float32 tensor")
