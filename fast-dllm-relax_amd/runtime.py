@@ -9,8 +9,9 @@ contract, window checks and exceptions, so the reference's loop reads the same h
   score_active_block_cached_fast / _refine / _partial        runtime.py:346-436
   score_sequence_block / score_masked_continuation           runtime.py:439-588
   relax_greedy_generate                                      runtime.py:591-880
-Differences: prefill passes no host-built bias (the kernels apply the same block-causal rule
-arithmetically, build_prefix_block_attention_bias semantics, cuda.py:148-177); the cached-step
+Differences: prefill passes no host-built bias when block_size is the model's bd_size (the kernels
+apply the same block-causal rule arithmetically, build_prefix_block_attention_bias semantics,
+cuda.py:148-177); the cached-step
 confidence always runs on the device (fused lm_head + argmax + max-softmax), reading back 2 x rows values.
 """
 
@@ -113,20 +114,26 @@ def build_prefix_cache_from_ids(vm: HipVM, prefix_ids, *, block_size: int, cache
         if prefix_len % block_size != 0:
             raise ValueError(f"chunked_prefill requires a block-aligned prefix; got {prefix_len} tokens "
                              f"with block_size={block_size}.")
-        _prefill(vm, list(prefix_ids[:block_size]), cache)
+        _prefill(vm, list(prefix_ids[:block_size]), cache, block_size=block_size)
         for start in range(block_size, prefix_len, block_size):
             _forward_cached(vm, list(prefix_ids[start:start + block_size]), cache)
             cache.commit(block_size)
         return cache
-    _prefill(vm, list(prefix_ids), cache)
+    _prefill(vm, list(prefix_ids), cache, block_size=block_size)
     return cache
 
 
-def _prefill(vm: HipVM, prefix_ids, cache: PrefixCache) -> None:
+def _prefill(vm: HipVM, prefix_ids, cache: PrefixCache, *, block_size: int) -> None:
+    """build_prefix_cache into an empty cache (runtime.py:312-323).  The kernels apply the block-causal
+    rule of build_prefix_block_attention_bias arithmetically with the model's bd_size; another
+    block_size passes the reference's explicit bias instead."""
     if cache.prefix_len != 0:
         raise ValueError("build_prefix_cache writes from row 0; the cache already has a prefix")
     _check_write(cache, 0, len(prefix_ids))
-    vm.build_prefix_cache(_embed(vm, prefix_ids), None, cache.k, cache.v)
+    bias = None
+    if block_size != vm.cfg.bd_size:
+        bias = torch.from_numpy(build_prefix_block_attention_bias(0, len(prefix_ids), block_size=block_size)).cuda()
+    vm.build_prefix_cache(_embed(vm, prefix_ids), bias, cache.k, cache.v)
     cache.commit(len(prefix_ids))
 
 

@@ -276,10 +276,11 @@ class OracleModel:
 
 
 def random_params(cfg: OracleConfig, seed: int, dtype: str = "bfloat16", std: float = 0.02,
-                  embed_std: float | None = None) -> dict[str, np.ndarray]:
+                  embed_std: float | None = None, lm_head_std: float | None = None) -> dict[str, np.ndarray]:
     """Seeded N(0, std) weights in packed order, norm weights = 1 (tests/test_tiny_compile.py:45-55).
 
-    ``embed_std`` scales the (tied) embedding separately (BASELINE cfg3 uses N(0, 0.5)).
+    ``embed_std`` scales the (tied) embedding separately; ``lm_head_std`` scales an untied lm_head
+    separately (a peaked head, as BASELINE cfg3's N(0, 0.5), so that rows cross the 0.9 threshold).
     Values are rounded to ``dtype`` and returned as fp32 arrays.
     """
     rnd = rounder(dtype)
@@ -291,7 +292,11 @@ def random_params(cfg: OracleConfig, seed: int, dtype: str = "bfloat16", std: fl
         if name.endswith("norm.weight"):
             out[name] = np.ones(shape, dtype=F32)
         else:
-            s = embed_std if (embed_std is not None and name == "model.embed_tokens.weight") else std
+            s = std
+            if embed_std is not None and name == "model.embed_tokens.weight":
+                s = embed_std
+            if lm_head_std is not None and name == "lm_head.weight":
+                s = lm_head_std
             out[name] = rnd((F32(s) * rng.standard_normal(shape, dtype=F32)).astype(F32))
     return out
 

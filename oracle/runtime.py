@@ -11,9 +11,16 @@ Follows ``fast_dllm_relax/runtime.py``:
 The confidence of a cached step is ``oracle.confidence`` (maxp = 1 / sum exp(x - max), metal.py:316-374);
 the stateless first block keeps the reference's float64 host formula (runtime.py:820-833).
 
-Pinned by: the loop restatement in the reference's docs/notebooks/_helpers.py:890-1021, which the
-reference verified token-identical to relax_greedy_generate (06_runtime_and_decode_loop.ipynb:261);
-tests/test_oracle_pinning.py checks this loop against an independent transcription of that helper.
+Pinned by (tests/test_oracle_pinning.py):
+  * greedy_generate with the block cache off is token- and trace-identical with a transcription of the
+    reference's traced loop, docs/notebooks/_helpers.py:890-1021 (which the reference verified
+    token-identical to relax_greedy_generate, 06_runtime_and_decode_loop.ipynb:261), on the cfg1 model
+    and on a head_dim-128 model with a peaked lm_head (aligned and unaligned prompts, a stop token);
+  * with the block cache on, on the near-uniform cfg1 model, it picks the same tokens as with it off
+    (partial rows reproduce full-step rows for identical tokens, runtime.py:762-766);
+  * score_masked_continuation equals one dense forward of transformers' Qwen2 over prefix + tail with an
+    explicit block mask, shifted (runtime.py:505-515), for aligned and partial prefixes, continuations
+    longer than a block, the eos pad and the stateless short branch.
 """
 
 from __future__ import annotations
