@@ -85,13 +85,22 @@ def main() -> int:
     ap.add_argument("--no-prefix512", action="store_true")
     ap.add_argument("--no-long-context", action="store_true")
     ap.add_argument("--cpu-iters", type=int, default=2)
-    ap.add_argument("--profile-target", choices=("batched", "prefill8192"),
+    ap.add_argument("--profile-target", choices=("batched", "prefill8192", "decode"),
                     help="only run a short workload for rocprofv3: 'batched' = config 4's 512-row and 128-row "
-                         "batched steps (5 each), 'prefill8192' = two 8192-row prefills")
+                         "batched steps (5 each), 'prefill8192' = two 8192-row prefills, 'decode' = config 3's "
+                         "decode loop (one warm-up and one timed generation of --new-tokens after the prompt; "
+                         "--host-loop runs the loop with the host-side unmask instead of the device one)")
+    ap.add_argument("--host-loop", action="store_true",
+                    help="decode with the host-side unmask (a readback per step) instead of the device loop")
+    ap.add_argument("--trace-gaps", metavar="KERNEL_TRACE_CSV",
+                    help="host only: read a rocprofv3 kernel trace of the decode loop and print the GPU idle time "
+                         "between consecutive model calls")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the dominant kernel over the 28 layers and a plain 256 MiB copy (for rocprofv3 --pmc)")
     args = ap.parse_args()
 
+    if args.trace_gaps:
+        return trace_gaps(args.trace_gaps)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: the cached block step is batch-1 and this build has no "
               f"multi-GPU path (asked for --gpus {args.gpus})", file=sys.stderr, flush=True)
@@ -104,7 +113,7 @@ def main() -> int:
 
     __graft_entry__.load_package()
     if args.profile_target is not None:
-        return profile_target(args.profile_target)
+        return profile_target(args.profile_target, args)
     from fast_dllm_relax_amd import _lib
     from fast_dllm_relax_amd.config import DEFAULT_MASK_ID, fast_dllm_v2_1p5b
     from fast_dllm_relax_amd.params import random_params_torch
@@ -137,7 +146,7 @@ def main() -> int:
         t0 = time.perf_counter()
         out, stats = relax_greedy_generate(vm, prompt, max_new_tokens=args.new_tokens, block_size=32,
                                            small_block_size=8, threshold=0.9, mask_id=DEFAULT_MASK_ID,
-                                           stop_token=None, timing=timing)
+                                           stop_token=None, timing=timing, device_loop=not args.host_loop)
         torch.cuda.synchronize()
         total = time.perf_counter() - t0
         return out, stats, total, timing["prefill_latency_s"]
@@ -429,15 +438,29 @@ def batched_bench(args) -> dict:
     return res
 
 
-def profile_target(which: str) -> int:
+def profile_target(which: str, args) -> int:
     """Short workloads for rocprofv3 (the commands in profiles/ name them)."""
     import numpy as np
     import torch
 
-    from fast_dllm_relax_amd.config import fast_dllm_v2_1p5b
+    from fast_dllm_relax_amd.config import DEFAULT_MASK_ID, fast_dllm_v2_1p5b
     from fast_dllm_relax_amd.params import random_params_torch
-    from fast_dllm_relax_amd.runtime import _embed, batched_shifted_confidence, build_prefix_cache_from_ids
+    from fast_dllm_relax_amd.runtime import (_embed, batched_shifted_confidence, build_prefix_cache_from_ids,
+                                             relax_greedy_generate)
     from fast_dllm_relax_amd.vm import HipVM
+
+    if which == "decode":
+        cfg = fast_dllm_v2_1p5b(tie_word_embeddings=False)
+        params = random_params_torch(cfg, SEED, dtype="bfloat16", device="cuda", std=0.02, lm_head_std=0.5)
+        vm = HipVM(cfg, params, dtype="bfloat16", max_rows=args.prefix)
+        prompt = np.random.default_rng(SEED).integers(0, 150000, args.prefix).tolist()
+        for i in range(2):
+            out, stats = relax_greedy_generate(vm, prompt, max_new_tokens=args.new_tokens, block_size=32,
+                                               small_block_size=8, threshold=0.9, mask_id=DEFAULT_MASK_ID,
+                                               stop_token=None, device_loop=not args.host_loop)
+            torch.cuda.synchronize()
+            log(f"profile target: generation {i + 1}/2 done ({len(out)} tokens, {stats['block_recomputes']} calls)")
+        return 0
 
     if which == "prefill8192":
         cfg = fast_dllm_v2_1p5b()
@@ -469,6 +492,54 @@ def profile_target(which: str) -> int:
         batched_shifted_confidence(vm, vm.forward_block_partial_batch(8, emb8, k, v, off + 8, a0s))
     torch.cuda.synchronize()
     log("profile target: 5 full + 5 partial batched steps done")
+    return 0
+
+
+def trace_gaps(path: str) -> int:
+    """GPU idle time between model calls of the decode loop, from a rocprofv3 kernel trace (csv).
+
+    A model call starts with its embedding gather (embed_kernel) and ends with the confidence reduction
+    (confidence_unmask_kernel on the device loop, confidence_combine_kernel on the host loop).  The gap
+    is the time from the end of one call's last kernel to the start of the next call's first, over the
+    calls of the last generation in the trace (the loop's steady state); it holds whatever the host
+    does in between (readback, unmask, uploads, launch of the next call)."""
+    import csv
+
+    rows = []
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    rows.sort()
+    calls, cur = [], None
+    for s, e, n in rows:
+        if "embed_kernel" in n:
+            cur = [s, None, 0]
+        if cur is None:
+            continue
+        cur[2] += e - s
+        if "confidence_unmask_kernel" in n or "confidence_combine_kernel" in n:
+            cur[1] = e
+            calls.append(cur)
+            cur = None
+    # the last generation: calls after the last prefill-sized gap (> 5 ms)
+    start = 0
+    for i in range(1, len(calls)):
+        if calls[i][0] - calls[i - 1][1] > 5_000_000:
+            start = i
+    calls = calls[start:]
+    gaps = sorted((b[0] - a[1]) / 1e3 for a, b in zip(calls, calls[1:]))
+    spans = [(c[1] - c[0]) / 1e3 for c in calls]
+    busy = [c[2] / 1e3 for c in calls]
+    if not gaps:
+        print(json.dumps({"calls": len(calls), "error": "fewer than two model calls in the trace"}))
+        return 1
+    q = lambda v, f: v[min(len(v) - 1, int(f * len(v)))]  # noqa: E731
+    out = {"calls": len(calls), "gap_us_median": round(statistics.median(gaps), 1),
+           "gap_us_mean": round(statistics.mean(gaps), 1), "gap_us_p10": round(q(gaps, 0.1), 1),
+           "gap_us_p90": round(q(gaps, 0.9), 1), "call_span_us_median": round(statistics.median(spans), 1),
+           "call_kernel_busy_us_median": round(statistics.median(busy), 1),
+           "gap_share_of_loop": round(sum(gaps) / (sum(spans) + sum(gaps)), 4)}
+    print(json.dumps(out))
     return 0
 
 

@@ -22,7 +22,8 @@ EXPORTS = (
     "fdllm_forward_cached", "fdllm_forward_block_partial", "fdllm_forward_block_partial_rp0",
     "fdllm_forward_block_partial_rp8", "fdllm_forward_block_partial_rp16", "fdllm_forward_block_partial_rp24",
     "fdllm_forward_cached_batch", "fdllm_forward_block_partial_batch", "fdllm_build_prefix_cache_seq",
-    "fdllm_get_confidence", "fdllm_confidence_from_logits", "fdllm_bench_op", "fdllm_persistent_steps",
+    "fdllm_get_confidence", "fdllm_confidence_from_logits", "fdllm_unmask", "fdllm_get_confidence_unmask",
+    "fdllm_host_alloc", "fdllm_host_free", "fdllm_bench_op", "fdllm_persistent_steps",
     "fdllm_frag_calls",
     "fdllm_last_error",
 )
@@ -64,6 +65,10 @@ _SIGS = {
     "fdllm_build_prefix_cache_seq": ([_P, _P, _I, _P, _P, _P, _I, _I, _I, _P], _I),
     "fdllm_get_confidence": ([_P, _P, _I, _P, _P, _P, _P], _I),
     "fdllm_confidence_from_logits": ([_P, _P, _I, _I, _I, _P, _P, _P], _I),
+    "fdllm_unmask": ([_P, _P, _P, _I, _I, _P, _I, _I, ctypes.c_int32, _F, _P, ctypes.c_int32, _P], _I),
+    "fdllm_get_confidence_unmask": ([_P, _P, _I, _I, _P, _I, _I, ctypes.c_int32, _F, _P, _P, _P, ctypes.c_int32, _P], _I),
+    "fdllm_host_alloc": ([ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p)], _I),
+    "fdllm_host_free": ([_P], None),
     "fdllm_bench_op": ([_P, _I, _I, _I, _I, _P, _P, _I, _I, _P], _I),
     "fdllm_persistent_steps": ([_P], ctypes.c_longlong),
     "fdllm_frag_calls": ([_P], ctypes.c_longlong),

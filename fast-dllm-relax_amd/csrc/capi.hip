@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <string>
 #include <vector>
 
@@ -783,6 +784,82 @@ int fdllm_get_confidence(fdllm_ctx* c, const void* hidden, int rows, int32_t* id
   HIPCHK(launch_confidence_combine((float*)base, (int32_t*)(base + c->stats_rows * T * 4),
                                    (float*)(base + c->stats_rows * T * 8), T, rows, ids, maxp, st));
   return FDLLM_OK;
+}
+
+// The sub-block arguments of the unmask entry points (block rows [s0, s0 + sub) take confidence rows
+// [row0, row0 + sub) after the shift).
+static int check_unmask(const fdllm_ctx* c, int rows, int row0, const int32_t* block, int s0, int sub,
+                        float threshold) {
+  const int bd = c->cfg.bd_size;
+  if (!block) return fail(FDLLM_EINVAL, "null block");
+  if (bd > 64) return fail(FDLLM_EINVAL, "the device unmask takes blocks of at most 64 rows (bd_size %d)", bd);
+  if (rows <= 0) return fail(FDLLM_EINVAL, "confidence rows must be positive, got %d", rows);
+  if (sub < 0 || s0 < 0 || s0 + sub > bd)
+    return fail(FDLLM_EINVAL, "sub-block [%d, %d) outside the block of %d rows", s0, s0 + sub, bd);
+  if (row0 < 0 || row0 + sub > rows)
+    return fail(FDLLM_EINVAL, "confidence rows [%d, %d) outside the call's %d rows", row0, row0 + sub, rows);
+  if (!(threshold == threshold)) return fail(FDLLM_EINVAL, "threshold is NaN");
+  return FDLLM_OK;
+}
+
+static UnmaskP unmask_args(const fdllm_ctx* c, int rows, int row0, int32_t* block, int s0, int sub, int32_t mask_id,
+                           float threshold, int32_t* report, int32_t seq) {
+  UnmaskP u{};
+  u.rows = rows; u.row0 = row0; u.block = block; u.bd = c->cfg.bd_size; u.s0 = s0; u.sub = sub;
+  u.mask_id = mask_id; u.thr = threshold; u.report = report; u.seq = seq;
+  return u;
+}
+
+int fdllm_unmask(fdllm_ctx* c, const int32_t* ids, const float* maxp, int rows, int row0, int32_t* block, int s0,
+                 int sub_rows, int32_t mask_id, float threshold, int32_t* report, int32_t seq, void* stream) {
+  if (!c) return fail(FDLLM_EINVAL, "null context");
+  if (!ids || !maxp) return fail(FDLLM_EINVAL, "null confidence argument");
+  int rc = check_unmask(c, rows, row0, block, s0, sub_rows, threshold);
+  if (rc) return rc;
+  HIPCHK(launch_unmask(ids, maxp, unmask_args(c, rows, row0, block, s0, sub_rows, mask_id, threshold, report, seq),
+                       (hipStream_t)stream));
+  return FDLLM_OK;
+}
+
+int fdllm_get_confidence_unmask(fdllm_ctx* c, const void* hidden, int rows, int row0, int32_t* block, int s0,
+                                int sub_rows, int32_t mask_id, float threshold, int32_t* ids, float* maxp,
+                                int32_t* report, int32_t seq, void* stream) {
+  int rc = check_ready(c);
+  if (rc) return rc;
+  if (!hidden) return fail(FDLLM_EINVAL, "null hidden states");
+  if ((ids == nullptr) != (maxp == nullptr)) return fail(FDLLM_EINVAL, "ids and maxp must both be given or both be null");
+  rc = check_unmask(c, rows, row0, block, s0, sub_rows, threshold);
+  if (rc) return rc;
+  if (rows > 1024) return fail(FDLLM_EINVAL, "the fused unmask combines at most 1024 rows, got %d", rows);
+  rc = ensure_stats(c, rows);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  rc = run_lm_head(c, (const uint16_t*)hidden, rows, nullptr, true, st);
+  if (rc) return rc;
+  const int T = c->tiles();
+  char* base = (char*)c->stats;
+  HIPCHK(launch_confidence_unmask((float*)base, (int32_t*)(base + c->stats_rows * T * 4),
+                                  (float*)(base + c->stats_rows * T * 8), T, (int)c->stats_rows, ids, maxp,
+                                  unmask_args(c, rows, row0, block, s0, sub_rows, mask_id, threshold, report, seq), st));
+  return FDLLM_OK;
+}
+
+int fdllm_host_alloc(size_t bytes, void** host_ptr, void** device_ptr) {
+  if (!host_ptr || !device_ptr || bytes == 0) return fail(FDLLM_EINVAL, "invalid host_alloc arguments");
+  *host_ptr = *device_ptr = nullptr;
+  HIPCHK(hipHostMalloc(host_ptr, bytes, hipHostMallocMapped | hipHostMallocCoherent));
+  std::memset(*host_ptr, 0, bytes);
+  const hipError_t e = hipHostGetDevicePointer(device_ptr, *host_ptr, 0);
+  if (e != hipSuccess) {
+    (void)hipHostFree(*host_ptr);
+    *host_ptr = nullptr;
+    return fail(FDLLM_EHIP, "hipHostGetDevicePointer: %s", hipGetErrorString(e));
+  }
+  return FDLLM_OK;
+}
+
+void fdllm_host_free(void* host_ptr) {
+  if (host_ptr) (void)hipHostFree(host_ptr);
 }
 
 long long fdllm_persistent_steps(const fdllm_ctx* c) { return c ? c->step_launches : 0; }

@@ -1,5 +1,6 @@
 // Skinny GEMM launch planning and launchers, the confidence kernels and the weight repack; the GEMM
 // kernels and their bodies are in gemm_body.hpp.
+#include "confidence.hpp"
 #include "gemm_body.hpp"
 #include "gemm_mm.hpp"
 #include "gemm_wt.hpp"
@@ -12,32 +13,15 @@ namespace fdllm {
 __global__ __launch_bounds__(64) void confidence_combine_kernel(const float* stat_m, const int32_t* stat_a,
                                                                 const float* stat_s, int tiles, int rows,
                                                                 int32_t* ids, float* maxp) {
-#pragma clang fp contract(off)
   const int r = blockIdx.x, lane = threadIdx.x;
   if (r >= rows) return;
-  const float* m = stat_m + (size_t)r * tiles;
-  const int32_t* am = stat_a + (size_t)r * tiles;
-  const float* s = stat_s + (size_t)r * tiles;
-  float vmax = -INFINITY;
-  int amax = 0x7fffffff;
-  for (int t = lane; t < tiles; t += 64) {
-    const float x = m[t];
-    if (x > vmax) { vmax = x; amax = am[t]; }
-  }
-  for (int k = 32; k >= 1; k >>= 1) {
-    const float ov = __shfl_xor(vmax, k, WAVE);
-    const int oa = __shfl_xor(amax, k, WAVE);
-    if (ov > vmax || (ov == vmax && oa < amax)) { vmax = ov; amax = oa; }
-  }
-  float acc = 0.0f;
-  for (int t = lane; t < tiles; t += 64) {
-    const float wgt = s[t] * fd_exp_neg(m[t] - vmax);
-    acc = acc + wgt;
-  }
-  for (int k = 32; k >= 1; k >>= 1) acc = acc + __shfl_xor(acc, k, WAVE);
+  int32_t id;
+  float p;
+  confidence_row(stat_m + (size_t)r * tiles, stat_a + (size_t)r * tiles, stat_s + (size_t)r * tiles, tiles, lane, &id,
+                 &p);
   if (lane == 0) {
-    ids[r] = amax;
-    maxp[r] = 1.0f / acc;
+    ids[r] = id;
+    maxp[r] = p;
   }
 }
 

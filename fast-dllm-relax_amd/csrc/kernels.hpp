@@ -73,6 +73,32 @@ hipError_t launch_confidence_combine(const float* sm, const int32_t* sa, const f
 hipError_t launch_confidence_tiles(const float* logits, int ld, int vocab, int rows, float* sm, int32_t* sa,
                                    float* ss, hipStream_t st);
 
+// ---- the decode loop's threshold unmask (unmask.hip, confidence.hpp) ------------------------------
+// Words of an unmask report (int32): the sequence number (written last), masks left in the sub-block,
+// rows unmasked, the unshifted argmax of the last confidence row, the block after the update, then the
+// sub-block's shifted ids and probabilities (fp32 bits) and the masked / selected row bitmasks.
+constexpr int REP_SEQ = 0, REP_LEFT = 1, REP_COUNT = 2, REP_LAST = 3, REP_BLOCK = 4;
+__host__ __device__ constexpr int report_words(int bd, int sub) { return REP_BLOCK + bd + 2 * sub + 2; }
+
+struct UnmaskP {
+  int rows;            // confidence rows of the call
+  int row0;            // confidence row of block row s0 (s0 for a full step, 0 for a partial one)
+  int32_t* block;      // [bd] ids of the active block (device), updated in place
+  int bd;              // block length
+  int s0, sub;         // the sub-block [s0, s0 + sub); sub = 0: no unmask (an append step)
+  int32_t mask_id;
+  float thr;           // threshold, rounded to fp32 toward -inf (numpy's fp32 > Python-float decision)
+  int32_t* report;     // optional: report_words(bd, sub) words, written when the update is done
+  int32_t seq;
+};
+
+// Fused confidence combine of the lm_head tile statistics (rows u.rows) + the unmask of u; ids / maxp
+// (optional) receive the unshifted confidence as launch_confidence_combine writes it.
+hipError_t launch_confidence_unmask(const float* sm, const int32_t* sa, const float* ss, int tiles, int stat_rows,
+                                    int32_t* ids, float* maxp, const UnmaskP& u, hipStream_t st);
+// The unmask of u on a given confidence ids / maxp [u.rows].
+hipError_t launch_unmask(const int32_t* ids, const float* maxp, const UnmaskP& u, hipStream_t st);
+
 // ---- row kernels --------------------------------------------------------------------------------
 hipError_t launch_embed(const int32_t* ids, int n, const uint16_t* table, int vocab, int hidden, uint16_t* out,
                         hipStream_t st);

@@ -180,6 +180,131 @@ def score_active_block_partial_perlayer(vm: HipVM, small_block_ids, prefix_cache
     return ids, probs
 
 
+def threshold_f32(threshold: float) -> float:
+    """Largest fp32 value <= threshold: the device's fp32 `p > t` then decides exactly as the reference's
+    numpy `p > threshold` on an fp32 probability (runtime.py:796)."""
+    t = np.float32(threshold)
+    if float(t) > threshold:
+        t = np.nextafter(t, np.float32(-np.inf))
+    return float(t)
+
+
+@dataclasses.dataclass
+class UnmaskReport:
+    """What one device step reports (include/fdllm.h, fdllm_unmask): the block after the update, the
+    selected rows of the sub-block, and the sub-block's shifted ids / probabilities."""
+
+    block: list
+    selected: list
+    masked: list
+    ids: list
+    probs: np.ndarray
+    left: int
+    last: int
+
+
+class DeviceBlock:
+    """The active block of the decode loop (runtime.py:748-843) held on the device.
+
+    The block's ids and its RoPE offsets live in device memory, uploaded once per block.  Each model
+    call embeds its rows straight from there, and fdllm_get_confidence_unmask applies the threshold
+    rule on the device and writes a report into pinned host memory, which the host polls: no readback
+    copy and no upload per step."""
+
+    REPORT_TIMEOUT_S = 60.0
+
+    def __init__(self, vm: HipVM, block_size: int, sub_rows: int, mask_id: int, threshold: float):
+        import ctypes
+
+        from . import _lib
+
+        self.vm, self.lib, self._lib = vm, vm.lib, _lib
+        self.bd, self.sub = int(block_size), int(sub_rows)
+        self.mask_id, self.thr = int(mask_id), threshold_f32(threshold)
+        self.buf = torch.zeros(self.bd + 1 + self.bd // self.sub, dtype=torch.int32, device="cuda")
+        self.block = self.buf[:self.bd]
+        self.words = 4 + self.bd + 2 * self.sub + 2
+        host, dev = ctypes.c_void_p(), ctypes.c_void_p()
+        _lib.check(self.lib.fdllm_host_alloc(self.words * 4, ctypes.byref(host), ctypes.byref(dev)))
+        self._host, self._dev = host, dev
+        self.rep = np.ctypeslib.as_array(ctypes.cast(host, ctypes.POINTER(ctypes.c_int32)), shape=(self.words,))
+        self.seq = int(self.rep[0])
+
+    def close(self) -> None:
+        if self._host is not None:
+            torch.cuda.synchronize()
+            self.lib.fdllm_host_free(self._host)
+            self._host = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001 - interpreter shutdown
+            pass
+
+    def load(self, ids, prefix_len: int) -> None:
+        """Upload the block's ids and the RoPE offsets of its full step (prefix_len) and partial steps
+        (prefix_len + rp)."""
+        vals = [int(t) for t in ids] + [prefix_len] + [prefix_len + rp for rp in range(0, self.bd, self.sub)]
+        if len(vals) != self.buf.numel():
+            raise ValueError(f"block of {len(ids)} ids, expected {self.bd}")
+        self.buf.copy_(torch.tensor(vals, dtype=torch.int32).pin_memory(), non_blocking=True)
+
+    def _embed(self, start: int, rows: int) -> torch.Tensor:
+        return self.vm.embed_unchecked(self.block[start:start + rows])[None]
+
+    def forward_full(self, cache: PrefixCache) -> torch.Tensor:
+        """forward_cached over the whole block at the cache frontier (runtime.py:333-343)."""
+        _check_write(cache, cache.prefix_len, cache.prefix_len + self.bd)
+        return self.vm.forward_cached(self._embed(0, self.bd), cache.k, cache.v, self.buf[self.bd], cache.prefix_len)
+
+    def forward_partial(self, cache: PrefixCache, rp: int) -> torch.Tensor:
+        """forward_block_partial_rp{rp} over rows [rp, rp + sub) (runtime.py:401-436)."""
+        _check_write(cache, cache.prefix_len + rp, cache.prefix_len + self.bd)
+        fn = self.vm[f"forward_block_partial_rp{rp}"]
+        return fn(self._embed(rp, self.sub), cache.k, cache.v, self.buf[self.bd + 1 + rp // self.sub],
+                  cache.prefix_len)
+
+    def unmask(self, hidden: torch.Tensor, row0: int, s0: int, sub: int) -> UnmaskReport:
+        """lm_head + confidence + the threshold rule on block rows [s0, s0 + sub) (sub = 0: report only),
+        then wait for the report."""
+        from .vm import _ptr, _stream
+
+        rows = self.vm._check_rows(hidden)
+        self.seq = (self.seq + 1) & 0x7FFFFFFF
+        seq = self.seq
+        self._lib.check(self.lib.fdllm_get_confidence_unmask(
+            self.vm.ctx, _ptr(hidden), rows, row0, _ptr(self.block), s0, sub, self.mask_id, self.thr, None, None,
+            self._dev, seq, _stream()))
+        rep = self.rep
+        if rep[0] != seq:
+            deadline = time.perf_counter() + self.REPORT_TIMEOUT_S
+            n = 0
+            while rep[0] != seq:
+                n += 1
+                if n & 0xFFFF == 0 and time.perf_counter() > deadline:
+                    torch.cuda.synchronize()  # surfaces a device error, if there is one
+                    if rep[0] != seq:
+                        raise RuntimeError(f"device unmask report {seq} did not arrive")
+        words = rep[:4 + self.bd + 2 * sub + 2].copy()
+        b = 4 + self.bd
+        masked_bits, sel_bits = int(words[b + 2 * sub]) & 0xFFFFFFFF, int(words[b + 2 * sub + 1]) & 0xFFFFFFFF
+        return UnmaskReport(block=words[4:b].tolist(), selected=[r for r in range(sub) if sel_bits >> r & 1],
+                            masked=[r for r in range(sub) if masked_bits >> r & 1], ids=words[b:b + sub].tolist(),
+                            probs=words[b + sub:b + 2 * sub].view(np.float32).copy(), left=int(words[1]),
+                            last=int(words[3]))
+
+
+def _device_block(vm: HipVM, block_size: int, sub_rows: int, mask_id: int, threshold: float) -> DeviceBlock:
+    """The vm's DeviceBlock for these loop parameters (kept across calls: its pinned report buffer is
+    allocated once)."""
+    key = (block_size, sub_rows, mask_id, threshold_f32(threshold))
+    cache = vm.__dict__.setdefault("_device_blocks", {})
+    if key not in cache:
+        cache[key] = DeviceBlock(vm, block_size, sub_rows, mask_id, threshold)
+    return cache[key]
+
+
 def build_prefix_block_attention_bias(prefix_len: int, block_len: int, *, block_size: int | None = None,
                                       blocked_value: float = -1e9) -> np.ndarray:
     """[1, 1, T, T] block-causal bias (cuda.py:148-177)."""
@@ -265,10 +390,17 @@ def relax_greedy_generate(vm: HipVM, prompt_token_ids, *, max_new_tokens: int, b
                           small_block_size: int = 8, threshold: float = 0.9, temperature: float = 0.0,
                           top_p: float = 0.95, use_block_cache: bool = True, mask_id: int,
                           stop_token: int | None, timing: dict | None = None, chunked_prefill: bool = False,
-                          trace: list | None = None):
+                          trace: list | None = None, decisions: list | None = None, device_loop: bool = True):
     """Fast-dLLM v2 block-diffusion generation (runtime.py:591-880), temperature 0.
 
-    ``trace`` (optional) receives one tuple per model call, as oracle.runtime.greedy_generate logs."""
+    ``trace`` (optional) receives one tuple per model call, as oracle.runtime.greedy_generate logs.
+    With ``device_loop`` (the default, when block_size is the model's bd_size, at most 64, and a multiple
+    of small_block_size) the cached block's ids stay on the device: each refinement step embeds from
+    there and ends with the fused lm_head + confidence + threshold unmask (fdllm_get_confidence_unmask),
+    and the host reads only the step's report.  ``decisions`` (optional) then receives, per cached
+    refinement step, the report's sub-block view: the rows that were masked, their shifted probabilities
+    and ids, and the rows the device selected (and {"kind": "append", "token": t} per block append).  Without it, each step reads the confidence back and
+    applies the rule on the host, as the reference does."""
     if temperature != 0.0:
         raise NotImplementedError("Fast-dLLM Relax runner currently supports only temperature=0.")
     if top_p <= 0:
@@ -280,6 +412,10 @@ def relax_greedy_generate(vm: HipVM, prompt_token_ids, *, max_new_tokens: int, b
 
     t_start = time.perf_counter()
     prefill_recorded = False
+    dblk = None
+    if (device_loop and block_size == vm.cfg.bd_size and block_size <= 64 and small_block_size <= block_size
+            and block_size % small_block_size == 0):
+        dblk = _device_block(vm, block_size, small_block_size, mask_id, threshold)
     generated = list(prompt_token_ids)
     plen0 = len(generated)
     unmask_updates = block_recomputes = partial_recomputes = block_appends = 0
@@ -339,6 +475,8 @@ def relax_greedy_generate(vm: HipVM, prompt_token_ids, *, max_new_tokens: int, b
                 torch.cuda.synchronize()
                 timing["prefill_latency_s"] = time.perf_counter() - t_start
             prefill_recorded = True
+        if use_cache and dblk is not None:
+            dblk.load(x_t[a0:], prefix_cache.prefix_len)
 
         for s0 in range(0, block_size, small_block_size):
             s1 = min(block_size, s0 + small_block_size)
@@ -348,7 +486,26 @@ def relax_greedy_generate(vm: HipVM, prompt_token_ids, *, max_new_tokens: int, b
                     break
                 if has_completed_stop(x_t, prompt_length):
                     return make_continuation(x_t), stats()
-                if use_cache:
+                if use_cache and dblk is not None:
+                    use_partial = use_block_cache and block_kv_valid and x_t[a0 + s0] != mask_id
+                    if use_partial:
+                        hidden = dblk.forward_partial(prefix_cache, s0)
+                    else:
+                        hidden = dblk.forward_full(prefix_cache)
+                        block_kv_valid = use_block_cache
+                    block_recomputes += 1
+                    if use_partial:
+                        partial_recomputes += 1
+                    rep = dblk.unmask(hidden, 0 if use_partial else s0, s0, s1 - s0)
+                    x_t[a0:a0 + block_size] = rep.block
+                    rows = rep.selected
+                    unmask_updates += len(rows)
+                    log("partial" if use_partial else "full", s0, tuple(rows), tuple(rep.ids[r] for r in rows))
+                    if decisions is not None:
+                        decisions.append({"kind": "partial" if use_partial else "full", "s0": s0,
+                                          "masked": rep.masked, "probs": rep.probs, "ids": rep.ids,
+                                          "selected": rows})
+                elif use_cache:
                     use_partial = use_block_cache and block_kv_valid and x_t[a0 + s0] != mask_id
                     if use_partial:
                         ids, probs = score_active_block_partial_perlayer(vm, x_t[a0 + s0:a0 + s1], prefix_cache,
@@ -398,7 +555,14 @@ def relax_greedy_generate(vm: HipVM, prompt_token_ids, *, max_new_tokens: int, b
             break
         if has_completed_stop(generated, plen0):
             break
-        if use_cache:
+        if use_cache and dblk is not None:
+            hidden = dblk.forward_full(prefix_cache)
+            prefix_cache.commit(block_size)
+            nxt = dblk.unmask(hidden, 0, 0, 0).last
+            block_kv_valid = False
+            if decisions is not None:
+                decisions.append({"kind": "append", "token": nxt})
+        elif use_cache:
             _, _, nxt, prefix_cache = score_active_block_cached_fast(vm, generated[a0:], prefix_cache)
             block_kv_valid = False
         else:

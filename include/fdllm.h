@@ -21,6 +21,7 @@
 #ifndef FDLLM_H
 #define FDLLM_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -140,6 +141,40 @@ int fdllm_get_confidence(fdllm_ctx* ctx, const void* hidden, int rows, int32_t* 
 /* The same confidence of given fp32 logits [rows, ld] (the host reduction of runtime.py:176-181). */
 int fdllm_confidence_from_logits(fdllm_ctx* ctx, const float* logits, int rows, int vocab, int ld, int32_t* ids,
                                  float* maxp, void* stream);
+
+/* Threshold unmask of one sub-block on the device: the rule of fast_dllm_relax/runtime.py:794-805 (the
+ * masked rows whose max probability is above `threshold`, else the first masked row of largest
+ * probability) with the shift of runtime.py:172-174, replacing the host loop's per-step readback of the
+ * confidence (runtime.py:179-181; device-confidence precedent model/metal.py:316-374).
+ *   ids, maxp   [rows] unshifted confidence of one model call, as fdllm_get_confidence writes it.
+ *   block       [bd_size] int32 ids of the active block (device); block rows [s0, s0 + sub_rows) are the
+ *               sub-block, and block row s0 + r reads the shifted confidence row row0 + r (that is, the
+ *               prediction of row row0 + r - 1; row 0 its own): row0 = s0 for a full 32-row step,
+ *               0 for a partial step.  The selected rows are overwritten with their predicted ids.
+ *   threshold   compared as `p > threshold` in fp32 (pass the fp32 rounding toward -inf of the host
+ *               threshold to reproduce numpy's fp32-vs-Python-float comparison).
+ *   report      optional int32 [4 + bd_size + 2 sub_rows + 2] (device memory, or host memory from
+ *               fdllm_host_alloc that the host polls): word 0 = seq, written after everything else;
+ *               1 = masked rows left in the sub-block; 2 = rows unmasked; 3 = unshifted argmax of the
+ *               last confidence row (the append step's next token, runtime.py:360-363); 4.. = the block
+ *               after the update; then the sub-block's shifted ids, their probabilities (fp32 bits), and
+ *               bitmasks of the rows that were masked and that were selected.
+ * sub_rows = 0 updates nothing (an append step that only needs the report).  bd_size must be <= 64. */
+int fdllm_unmask(fdllm_ctx* ctx, const int32_t* ids, const float* maxp, int rows, int row0, int32_t* block, int s0,
+                 int sub_rows, int32_t mask_id, float threshold, int32_t* report, int32_t seq, void* stream);
+
+/* The fused north-star head of one decode step: lm_head + max-softmax / first-argmax over the vocabulary
+ * (fdllm_get_confidence) + the threshold unmask of fdllm_unmask, in two launches and without a
+ * readback.  ids / maxp: optional (both or neither) [rows] outputs of the unshifted confidence. */
+int fdllm_get_confidence_unmask(fdllm_ctx* ctx, const void* hidden, int rows, int row0, int32_t* block, int s0,
+                                int sub_rows, int32_t mask_id, float threshold, int32_t* ids, float* maxp,
+                                int32_t* report, int32_t seq, void* stream);
+
+/* Pinned, device-mapped, coherent host memory for unmask reports (zeroed): the host polls what the
+ * device writes there instead of waiting for a copy.  No reference counterpart (the reference reads
+ * the confidence back with a blocking copy, runtime.py:179-181). */
+int fdllm_host_alloc(size_t bytes, void** host_ptr, void** device_ptr);
+void fdllm_host_free(void* host_ptr);
 
 /* Profiling hook; it has no counterpart in the reference.  Launches one operator of the cached step
  * `iters` times back to back on `stream`, reading and writing the context's own workspace (the values

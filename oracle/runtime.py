@@ -155,8 +155,10 @@ def score_masked_continuation(model, prefix_ids, continuation_ids, *, block_size
 
 def greedy_generate(model: OracleModel, prompt_ids, *, max_new_tokens: int, block_size: int = 32,
                     small_block_size: int = 8, threshold: float = 0.9, use_block_cache: bool = True,
-                    mask_id: int, stop_token: int | None, trace: list | None = None):
-    """relax_greedy_generate (runtime.py:591-880), temperature 0.  ``trace`` collects one tuple per call."""
+                    mask_id: int, stop_token: int | None, trace: list | None = None, decisions: list | None = None):
+    """relax_greedy_generate (runtime.py:591-880), temperature 0.  ``trace`` collects one tuple per call;
+    ``decisions`` (optional) one dict per cached refinement step: the sub-block's masked rows, shifted
+    probabilities and ids, the selected rows, and each row's gap between its two largest logits."""
     generated = list(prompt_ids)
     plen0 = len(generated)
     stats = dict(unmask_updates=0, block_recomputes=0, partial_recomputes=0, block_appends=0)
@@ -214,11 +216,15 @@ def greedy_generate(model: OracleModel, prompt_ids, *, max_new_tokens: int, bloc
                 if use_cache:
                     use_partial = use_block_cache and block_kv_valid and x_t[a0 + s0] != mask_id
                     if use_partial:
-                        ids, probs = score_active_block_partial_perlayer(model, x_t[a0 + s0:a0 + s1], cache, s0,
-                                                                          block_size=block_size)
+                        ws = cache.prefix_len + s0
+                        _check_write(cache, ws, cache.prefix_len + block_size)
+                        hidden = model.forward_block_partial(s0, model.embed(x_t[a0 + s0:a0 + s1])[None], cache.k,
+                                                             cache.v, ws, cache.prefix_len)
                     else:
-                        ids, probs = score_active_block_refine(model, x_t[a0:], cache)
+                        hidden = forward_cached(model, x_t[a0:], cache)
                         block_kv_valid = use_block_cache
+                    logits = model.get_logits(hidden)[0]
+                    ids, probs, _ = conf.shifted_confidence(logits)
                     stats["block_recomputes"] += 1
                     if use_partial:
                         stats["partial_recomputes"] += 1
@@ -231,6 +237,12 @@ def greedy_generate(model: OracleModel, prompt_ids, *, max_new_tokens: int, bloc
                         x_t[a0 + s0 + r] = int(bids[r])
                         stats["unmask_updates"] += 1
                     log("partial" if use_partial else "full", s0, tuple(rows), tuple(int(bids[r]) for r in rows))
+                    if decisions is not None:
+                        sh = np.concatenate([logits[:1], logits[:-1]])[(0 if use_partial else s0):][:s1 - s0]
+                        top2 = np.sort(sh, axis=-1)[:, -2:]
+                        decisions.append({"kind": "partial" if use_partial else "full", "s0": s0, "masked": local,
+                                          "probs": np.asarray(bp, np.float32), "ids": [int(t) for t in bids],
+                                          "selected": rows, "gap": top2[:, 1] - top2[:, 0]})
                 else:
                     _, shifted = score_sequence_block(model, x_t, block_size=block_size)
                     stats["block_recomputes"] += 1
@@ -259,8 +271,14 @@ def greedy_generate(model: OracleModel, prompt_ids, *, max_new_tokens: int, bloc
         if len(generated) - plen0 >= max_new_tokens or stop_done(generated, plen0):
             break
         if use_cache:
-            _, _, nxt, cache = score_active_block_cached_fast(model, generated[a0:], cache)
+            hidden = forward_cached(model, generated[a0:], cache)
+            cache.commit(len(generated[a0:]))
+            last = model.get_logits(hidden)[0, -1]
+            nxt = int(np.argmax(last))
             block_kv_valid = False
+            if decisions is not None:
+                top2 = np.sort(last)[-2:]
+                decisions.append({"kind": "append", "token": nxt, "gap": float(top2[1] - top2[0])})
         else:
             cur, _ = score_sequence_block(model, generated, block_size=block_size)
             nxt = int(cur[0, -1, :].argmax())

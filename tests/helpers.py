@@ -13,14 +13,14 @@ WIDE2 = dict(vocab_size=151936, hidden_size=1536, intermediate_size=8960, num_hi
              num_attention_heads=12, num_key_value_heads=2, head_dim=128)
 
 
-def make_pair(kw: dict, seed: int, dtype: str = "bfloat16", embed_std=None, max_rows: int = 64):
+def make_pair(kw: dict, seed: int, dtype: str = "bfloat16", embed_std=None, max_rows: int = 64, lm_head_std=None):
     import torch  # noqa: F401
 
     from fast_dllm_relax_amd.config import FastDLLMConfig
     from fast_dllm_relax_amd.params import from_numpy
     from fast_dllm_relax_amd.vm import HipVM
 
-    arrays = random_params(OracleConfig(**kw), seed, dtype, embed_std=embed_std)
+    arrays = random_params(OracleConfig(**kw), seed, dtype, embed_std=embed_std, lm_head_std=lm_head_std)
     ref = OracleModel(OracleConfig(**kw), arrays, dtype)
     cfg = FastDLLMConfig(**kw)
     vm = HipVM(cfg, from_numpy(arrays, cfg, dtype=dtype), dtype=dtype, max_rows=max_rows)

@@ -1,0 +1,114 @@
+"""Full-depth parity of the 1.5B model (28 layers) at BASELINE cfg2 and cfg3, on the exact weights bench.py
+times (params.random_params_torch, generated on the GPU), against the oracle in bf16 (the reference's
+rounding points) and in fp32 (the precision the logit tolerance is quoted against).  Marked gpu.
+
+The numbers each case logs (max / mean |dlogit| of the HIP path and of the bf16 oracle against fp32) are
+the ones recorded in the design notes; the reference measured its own full-model logit error against HF
+(03_numerical_parity.ipynb: max |dlogit| 0.8672, Relax vs HF, model/cuda.py:704-711).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bf16_parity, log, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(seed: int, P: int, tied: bool, lm_head_std):
+    from fast_dllm_relax_amd.config import fast_dllm_v2_1p5b
+    from fast_dllm_relax_amd.params import param_names, random_params_torch
+    from fast_dllm_relax_amd.vm import HipVM
+    from oracle.model import OracleConfig, OracleModel
+
+    cfg = fast_dllm_v2_1p5b(tie_word_embeddings=tied)
+    log(f"setup: 1.5B bf16, 28 layers, seed {seed}, tied={tied}, lm_head_std={lm_head_std}")
+    params = random_params_torch(cfg, seed, dtype="bfloat16", device="cuda", lm_head_std=lm_head_std)
+    vm = HipVM(cfg, params, dtype="bfloat16", max_rows=P)
+    ocfg = OracleConfig(vocab_size=cfg.vocab_size, hidden_size=cfg.hidden_size, intermediate_size=cfg.intermediate_size,
+                        num_hidden_layers=cfg.num_hidden_layers, num_attention_heads=cfg.num_attention_heads,
+                        num_key_value_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim, tie_word_embeddings=tied)
+    arrays = {n: p.float().cpu().numpy() for n, p in zip(param_names(cfg), params)}
+    return vm, params, OracleModel(ocfg, arrays, "bfloat16"), OracleModel(ocfg, arrays, "float32")
+
+
+def _prefill_all(vm, r16, r32, ids, cap):
+    from fast_dllm_relax_amd.runtime import build_prefix_cache_from_ids
+    from oracle.runtime import build_prefix_cache_from_ids as o_build
+
+    P = len(ids)
+    hc = build_prefix_cache_from_ids(vm, ids, block_size=32, capacity=cap)
+    torch.cuda.synchronize()
+    log(f"  HIP prefill {P} rows done; oracle bf16 prefill ...")
+    c16 = o_build(r16, ids, block_size=32, capacity=cap)
+    log("  oracle fp32 prefill ...")
+    c32 = o_build(r32, ids, block_size=32, capacity=cap)
+    return hc, c16, c32
+
+
+def _report(name, got, w16, w32, max_abs):
+    s = bf16_parity(name, got, w16, w32, max_abs=max_abs, max_outside=2e-2)
+    return s
+
+
+@pytest.mark.timeout(900)
+def test_cfg2_full_depth_cached_and_partial_steps():
+    """cfg2: seed 1, tied head, prefix 512; forward_cached over a block of 32 masks, then the four partial
+    steps rp0/8/16/24 over the same block (their block K/V rows come from the full step)."""
+    from fast_dllm_relax_amd.config import DEFAULT_MASK_ID
+    from fast_dllm_relax_amd.runtime import _embed, _offset_tensor
+
+    P = 512
+    vm, params, r16, r32 = _setup(1, P, True, None)
+    ids = [int(t) for t in np.random.default_rng(1).integers(0, 150000, P)]
+    hc, c16, c32 = _prefill_all(vm, r16, r32, ids, P + 32)
+    blk = [DEFAULT_MASK_ID] * 32
+    h = vm.forward_cached(_embed(vm, blk), hc.k, hc.v, _offset_tensor(P), P)
+    got = to_np(vm.get_logits(h))[0]
+    e16, e32 = r16.embed(blk)[None], r32.embed(blk)[None]
+    w16 = r16.get_logits(r16.forward_cached(e16, c16.k, c16.v, P, P))[0]
+    w32 = r32.get_logits(r32.forward_cached(e32, c32.k, c32.v, P, P))[0]
+    _report("cfg2 forward_cached logits (28 layers)", got, w16, w32, max_abs=0.5)
+    for rp in (0, 8, 16, 24):
+        hp = vm[f"forward_block_partial_rp{rp}"](_embed(vm, blk[rp:rp + 8]), hc.k, hc.v, _offset_tensor(P + rp), P)
+        got_p = to_np(vm.get_logits(hp))[0]
+        w16p = r16.get_logits(r16.forward_block_partial(rp, e16[:, rp:rp + 8], c16.k, c16.v, P + rp, P))[0]
+        w32p = r32.get_logits(r32.forward_block_partial(rp, e32[:, rp:rp + 8], c32.k, c32.v, P + rp, P))[0]
+        _report(f"cfg2 partial rp{rp} logits (28 layers)", got_p, w16p, w32p, max_abs=0.5)
+    vm.close()
+
+
+@pytest.mark.timeout(900)
+def test_cfg3_full_depth_refinement_step():
+    """cfg3: seed 2, untied lm_head N(0, 0.5), prefix 2048; one 32-row refinement step (the block's first
+    token known, 31 masks): logits and the fused confidence."""
+    from fast_dllm_relax_amd.config import DEFAULT_MASK_ID
+    from fast_dllm_relax_amd.runtime import _embed, _offset_tensor
+    from oracle import confidence as oconf
+
+    P = 2048
+    vm, params, r16, r32 = _setup(2, P, False, 0.5)
+    ids = [int(t) for t in np.random.default_rng(2).integers(0, 150000, P + 1)]
+    hc, c16, c32 = _prefill_all(vm, r16, r32, ids[:P], P + 32)
+    blk = ids[P:P + 1] + [DEFAULT_MASK_ID] * 31
+    h = vm.forward_cached(_embed(vm, blk), hc.k, hc.v, _offset_tensor(P), P)
+    logits_d = vm.get_logits(h)
+    got = to_np(logits_d)[0]
+    w16 = r16.get_logits(r16.forward_cached(r16.embed(blk)[None], c16.k, c16.v, P, P))[0]
+    w32 = r32.get_logits(r32.forward_cached(r32.embed(blk)[None], c32.k, c32.v, P, P))[0]
+    # logits of magnitude ~80 rounded to bf16 (ulp 0.5 above 64): the bf16 oracle's own error sets the scale
+    _report("cfg3 refinement logits (28 layers)", got, w16, w32, max_abs=2.0)
+    ids_d, maxp_d = vm.get_confidence(h)
+    ids_h, maxp_h = ids_d.cpu().numpy()[0], maxp_d.cpu().numpy()[0]
+    # the fused confidence equals the oracle confidence of the HIP path's own logits, bit for bit
+    ci, cp = oconf.confidence(got)
+    np.testing.assert_array_equal(ids_h, ci)
+    np.testing.assert_array_equal(maxp_h.view(np.int32), cp.view(np.int32))
+    i16, p16 = oconf.confidence(w16)
+    log(f"  confidence: argmax agrees with the bf16 oracle on {int((ids_h == i16).sum())}/32 rows, "
+        f"max |dmaxp| {float(np.abs(maxp_h - p16).max()):.4g}; rows above 0.9: HIP {int((maxp_h > 0.9).sum())}, "
+        f"oracle {int((p16 > 0.9).sum())}")
+    vm.close()
