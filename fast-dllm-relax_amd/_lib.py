@@ -19,7 +19,7 @@ DTYPE_BF16, DTYPE_F16 = 0, 1
 EXPORTS = (
     "fdllm_create", "fdllm_destroy", "fdllm_num_params", "fdllm_param_name", "fdllm_bind_weights",
     "fdllm_embed", "fdllm_forward_hidden", "fdllm_get_logits", "fdllm_build_prefix_cache",
-    "fdllm_forward_cached", "fdllm_forward_block_partial", "fdllm_forward_block_partial_rp0",
+    "fdllm_forward_cached", "fdllm_forward_cached_noalloc", "fdllm_forward_block_partial", "fdllm_forward_block_partial_rp0",
     "fdllm_forward_block_partial_rp8", "fdllm_forward_block_partial_rp16", "fdllm_forward_block_partial_rp24",
     "fdllm_forward_cached_batch", "fdllm_forward_block_partial_batch", "fdllm_build_prefix_cache_seq",
     "fdllm_get_confidence", "fdllm_confidence_from_logits", "fdllm_unmask", "fdllm_get_confidence_unmask",
@@ -55,6 +55,7 @@ _SIGS = {
     "fdllm_get_logits": ([_P, _P, _I, _P, _P], _I),
     "fdllm_build_prefix_cache": ([_P, _P, _I, _P, _P, _P, _I, _P], _I),
     "fdllm_forward_cached": ([_P, _P, _I, _P, _P, _I, _P, _I64, _P, _P], _I),
+    "fdllm_forward_cached_noalloc": ([_P, _P, _I, _P, _P, _I, _P, _I64, _P, _P], _I),
     "fdllm_forward_block_partial": ([_P, _I, _P, _I, _P, _P, _I, _P, _I64, _P, _P], _I),
     "fdllm_forward_block_partial_rp0": ([_P, _P, _I, _P, _P, _I, _P, _I64, _P, _P], _I),
     "fdllm_forward_block_partial_rp8": ([_P, _P, _I, _P, _P, _I, _P, _I64, _P, _P], _I),

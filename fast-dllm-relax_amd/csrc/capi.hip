@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -18,6 +19,20 @@ using namespace fdllm;
 namespace {
 
 thread_local std::string g_err;
+
+// Set while fdllm_forward_cached_noalloc runs: a workspace that would have to grow is an error instead
+// of an allocation.
+thread_local bool t_no_alloc = false;
+
+// The allocation-free cached step's workspace (fdllm_forward_cached_noalloc): one array per GPU, held
+// until the process ends.  Host code never uses this name as an address: each device's copy is found
+// once with hipGetSymbolAddress (scratch_base) and that pointer is what the kernels receive.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)24 << 20;
+constexpr int NOALLOC_MAX_ROWS = 32;
+__device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES] = {};
 
 int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -101,6 +116,7 @@ struct fdllm_ctx {
   long long frag_calls = 0;            // layer loops run in MFMA-fragment order (fdllm_frag_calls)
   std::string step_trace_path;         // FDLLM_STEP_TRACE: write each launch's barrier timeline there
   unsigned long long* step_trace = nullptr;
+  unsigned char* scratch_dev = nullptr;  // this device's copy of `scratch` (fdllm_forward_cached_noalloc)
 
   int qkv_dim() const { return (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim; }
   int q_dim() const { return cfg.num_attention_heads * cfg.head_dim; }
@@ -113,6 +129,8 @@ namespace {
 
 int ensure_rows(fdllm_ctx* c, int rows) {
   if (rows <= c->ws_rows) return FDLLM_OK;
+  if (t_no_alloc)
+    return fail(FDLLM_EINVAL, "%d rows exceed the allocation-free step's %d", rows, c->ws_rows);
   int R = (int)align_up((size_t)std::max(rows, 32), 32);
   const fdllm_config& f = c->cfg;
   size_t e_h = (size_t)R * f.hidden_size, e_qkv = (size_t)R * c->qkv_dim(), e_q = (size_t)R * c->q_dim();
@@ -136,6 +154,9 @@ int ensure_rows(fdllm_ctx* c, int rows) {
 
 int ensure_floats(float** buf, size_t* have, size_t need) {
   if (need <= *have) return FDLLM_OK;
+  if (t_no_alloc)
+    return fail(FDLLM_EINVAL, "the call needs %zu floats of split partials; the allocation-free step's scratch holds %zu",
+                need, *have);
   if (*buf) {
     HIPCHK(hipDeviceSynchronize());
     HIPCHK(hipFree(*buf));
@@ -589,6 +610,22 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
     return fail(FDLLM_EHIP, "workspace allocation failed: %s", hipGetErrorString(e));
   }
   c->zero_i32 = (int32_t*)(c->counters + c->n_counters);
+  {
+    // this device's copy of the allocation-free step's scratch array, found once per device
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (c->dev >= 0 && c->dev < MAX_DEVICES) {
+      if (g_scratch_ptr[c->dev] == nullptr) {
+        void* ptr = nullptr;
+        const hipError_t se = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (se != hipSuccess) {
+          (void)hipGetLastError();
+          ptr = nullptr;  // the allocation-free entry point then reports that it is unavailable
+        }
+        g_scratch_ptr[c->dev] = ptr;
+      }
+      c->scratch_dev = (unsigned char*)g_scratch_ptr[c->dev];
+    }
+  }
   if (c->step_on) {
     // the persistent step needs a cooperative launch of one workgroup per compute unit
     int coop = 0, cus = 0, khz = 0;
@@ -712,6 +749,87 @@ int fdllm_build_prefix_cache(fdllm_ctx* c, const void* x, int P, const float* bi
 
 int fdllm_forward_cached(fdllm_ctx* c, const void* x, int rows, void* k, void* v, int cap, const int32_t* off,
                          int64_t prefix_len, void* out, void* stream) {
+  return cached_step(c, x, rows, k, v, cap, off, prefix_len, 0, rows, out, stream);
+}
+
+// The workspace a call of the allocation-free step sees: views of this device's scratch array swapped
+// into the context for the duration of the call (the context is single-threaded by contract) and
+// restored after it, with t_no_alloc turning any growth into an error.
+struct ScratchView {
+  fdllm_ctx* c;
+  uint16_t *h, *qkv, *attn, *act, *kscr, *vscr, *xn;
+  float *ssq, *gpart, *apart, *rope;
+  size_t gpart_floats, apart_floats, rope_floats;
+  int ws_rows;
+  bool step_on;
+  explicit ScratchView(fdllm_ctx* ctx) : c(ctx) {
+    h = c->h; qkv = c->qkv; attn = c->attn; act = c->act; kscr = c->kscr; vscr = c->vscr; xn = c->xn;
+    ssq = c->ssq; gpart = c->gpart; apart = c->apart; rope = c->rope;
+    gpart_floats = c->gpart_floats; apart_floats = c->apart_floats; rope_floats = c->rope_floats;
+    ws_rows = c->ws_rows; step_on = c->step_on;
+    t_no_alloc = true;
+  }
+  ~ScratchView() {
+    c->h = h; c->qkv = qkv; c->attn = attn; c->act = act; c->kscr = kscr; c->vscr = vscr; c->xn = xn;
+    c->ssq = ssq; c->gpart = gpart; c->apart = apart; c->rope = rope;
+    c->gpart_floats = gpart_floats; c->apart_floats = apart_floats; c->rope_floats = rope_floats;
+    c->ws_rows = ws_rows; c->step_on = step_on;
+    t_no_alloc = false;
+  }
+};
+
+// Largest split-partial need of the four projections at up to NOALLOC_MAX_ROWS rows (fp32 floats).
+static size_t noalloc_gemm_partials(const fdllm_ctx* c) {
+  const fdllm_config& f = c->cfg;
+  size_t need = 0;
+  for (int rows = 1; rows <= NOALLOC_MAX_ROWS; ++rows) {
+    LayerGemms g = layer_gemms(c, c->layers[0], rows, false);
+    const std::pair<int, GemmP*> all[] = {{CFG_QKV, &g.q}, {CFG_OPROJ, &g.o}, {CFG_GATE_UP, &g.gu}, {CFG_DOWN, &g.d}};
+    for (const auto& [cfg, a] : all) {
+      GemmP t = *a;
+      const GemmPlan pl = gemm_plan(cfg, t, cfg == CFG_DOWN ? g.dsplit : 1, c->mm_target_wgs, c->mm_min_stages);
+      need = std::max(need, pl.part_floats);
+    }
+  }
+  (void)f;
+  return need;
+}
+
+int fdllm_forward_cached_noalloc(fdllm_ctx* c, const void* x, int rows, void* k, void* v, int cap, const int32_t* off,
+                                 int64_t prefix_len, void* out, void* stream) {
+  int rc = check_ready(c);
+  if (rc) return rc;
+  if (c->scratch_dev == nullptr)
+    return fail(FDLLM_EHIP, "the allocation-free step's scratch array is not available on device %d", c->dev);
+  if (rows <= 0 || rows > NOALLOC_MAX_ROWS)
+    return fail(FDLLM_EINVAL, "the allocation-free step takes 1 .. %d rows, got %d", NOALLOC_MAX_ROWS, rows);
+  const fdllm_config& f = c->cfg;
+  const size_t R = NOALLOC_MAX_ROWS, H = f.hidden_size, I = f.intermediate_size;
+  size_t off_b = 0;
+  auto take = [&](size_t bytes) {
+    unsigned char* p = c->scratch_dev + off_b;
+    off_b += align_up(bytes, 256);
+    return p;
+  };
+  ScratchView keep(c);
+  c->h = (uint16_t*)take(R * H * 2);
+  c->qkv = (uint16_t*)take(R * c->qkv_dim() * 2);
+  c->attn = (uint16_t*)take(R * c->q_dim() * 2);
+  c->act = (uint16_t*)take(R * I * 2);
+  c->xn = (uint16_t*)take(R * H * 2);
+  c->ssq = (float*)take((size_t)c->ssq_tiles() * R * 4);
+  c->kscr = c->vscr = nullptr;
+  c->ws_rows = (int)R;
+  c->rope = (float*)take(R * 128 * 4);
+  c->rope_floats = R * 128;
+  c->gpart_floats = noalloc_gemm_partials(c);
+  c->gpart = (float*)take(c->gpart_floats * 4);
+  c->step_on = false;  // the persistent step sizes its own buffers
+  if (off_b >= NOALLOC_SCRATCH_BYTES)
+    return fail(FDLLM_EINVAL, "the model's workspace (%zu bytes) exceeds the allocation-free step's scratch (%zu bytes)",
+                off_b, NOALLOC_SCRATCH_BYTES);
+  c->apart = (float*)(c->scratch_dev + off_b);
+  c->apart_floats = (NOALLOC_SCRATCH_BYTES - off_b) / 4;
   return cached_step(c, x, rows, k, v, cap, off, prefix_len, 0, rows, out, stream);
 }
 

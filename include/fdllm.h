@@ -92,6 +92,20 @@ int fdllm_build_prefix_cache(fdllm_ctx* ctx, const void* prefix_embed, int prefi
 int fdllm_forward_cached(fdllm_ctx* ctx, const void* active_embed, int block_len, void* k_cache, void* v_cache,
                          int cap, const int32_t* cache_offset, int64_t prefix_len, void* out, void* stream);
 
+/* Allocation-free variant of fdllm_forward_cached.  It has no counterpart in the reference: it is for
+ * callers that cannot allocate device memory inside a call (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments, semantics and results (bit for bit) as
+ * fdllm_forward_cached, but the step's workspace (residual stream, projections, norms, RoPE table and
+ * the split partials of the projections and the attention) lives in a fixed 24 MiB device array of the
+ * library, one per GPU, held until the process ends, and the call allocates and frees nothing.
+ * Limits: at most 32 rows, and the attended keys must fit the scratch (the 1.5B shapes: up to 8192
+ * keys through the chunked attention, more through the looped one); larger calls return FDLLM_EINVAL.
+ * Every call on one GPU shares that GPU's array and leaves its contents behind: calls that overlap on
+ * one GPU (two streams, threads or contexts) race. */
+int fdllm_forward_cached_noalloc(fdllm_ctx* ctx, const void* active_embed, int block_len, void* k_cache,
+                                 void* v_cache, int cap, const int32_t* cache_offset, int64_t prefix_len, void* out,
+                                 void* stream);
+
 /* forward_block_partial_rp{0,8,16,24} (cuda.py:740-788): bd_size/4 rows written at
  * [prefix_len + rp, + bd_size/4), attending over [0, prefix_len + bd_size). */
 int fdllm_forward_block_partial(fdllm_ctx* ctx, int replace_position, const void* active_embed, int rows,
