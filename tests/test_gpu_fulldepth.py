@@ -50,7 +50,12 @@ def _prefill_all(vm, r16, r32, ids, cap):
 
 
 def _report(name, got, w16, w32, max_abs):
-    s = bf16_parity(name, got, w16, w32, max_abs=max_abs, max_outside=2e-2)
+    """At 28 layers two bf16 paths with different accumulation orders drift apart element by element (the
+    bf16 roundings of the residual stream flip independently), so the bound is against fp32: the HIP
+    error must stay within 1.5x the bf16 oracle's own error (mean and max), and the HIP - bf16-oracle
+    distance within twice the oracle's distance from fp32."""
+    s = bf16_parity(name, got, w16, w32, max_abs=max_abs, max_outside=1.0)
+    assert s["max_abs"] <= 2 * s["oracle_vs_f32_max"] + 1e-6, (name, s)
     return s
 
 
@@ -99,8 +104,9 @@ def test_cfg3_full_depth_refinement_step():
     got = to_np(logits_d)[0]
     w16 = r16.get_logits(r16.forward_cached(r16.embed(blk)[None], c16.k, c16.v, P, P))[0]
     w32 = r32.get_logits(r32.forward_cached(r32.embed(blk)[None], c32.k, c32.v, P, P))[0]
-    # logits of magnitude ~80 rounded to bf16 (ulp 0.5 above 64): the bf16 oracle's own error sets the scale
-    _report("cfg3 refinement logits (28 layers)", got, w16, w32, max_abs=2.0)
+    # the N(0, 0.5) head (row norm ~19.6) scales the hidden states' bf16 error by ~20 into logits of
+    # magnitude ~80: the bf16 oracle's own error against fp32 (max ~3.6) sets the scale, not a fixed bound
+    _report("cfg3 refinement logits (28 layers)", got, w16, w32, max_abs=16.0)
     ids_d, maxp_d = vm.get_confidence(h)
     ids_h, maxp_h = ids_d.cpu().numpy()[0], maxp_d.cpu().numpy()[0]
     # the fused confidence equals the oracle confidence of the HIP path's own logits, bit for bit
