@@ -84,7 +84,7 @@ def main() -> int:
     ap.add_argument("--no-batched", action="store_true")
     ap.add_argument("--no-prefix512", action="store_true")
     ap.add_argument("--no-long-context", action="store_true")
-    ap.add_argument("--cpu-iters", type=int, default=2)
+    ap.add_argument("--cpu-iters", type=int, default=5)
     ap.add_argument("--profile-target", choices=("batched", "prefill8192", "decode"),
                     help="only run a short workload for rocprofv3: 'batched' = config 4's 512-row and 128-row "
                          "batched steps (5 each), 'prefill8192' = two 8192-row prefills, 'decode' = config 3's "
@@ -95,12 +95,19 @@ def main() -> int:
     ap.add_argument("--trace-gaps", metavar="KERNEL_TRACE_CSV",
                     help="host only: read a rocprofv3 kernel trace of the decode loop and print the GPU idle time "
                          "between consecutive model calls")
-    ap.add_argument("--traffic-probe", action="store_true",
-                    help="only launch the dominant kernel over the 28 layers and a plain 256 MiB copy (for rocprofv3 --pmc)")
+    ap.add_argument("--traffic-probe", nargs="?", const="gate_up", choices=("gate_up", "step"),
+                    help="for rocprofv3 --pmc: 'gate_up' (default) launches the dominant kernel over the 28 layers, "
+                         "then a plain 256 MiB copy; 'step' builds the 2048-row prefix, copies 256 MiB, then runs one "
+                         "32-row refinement step (forward_cached + lm_head + confidence)")
+    ap.add_argument("--traffic-report", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="host only: per-kernel HBM bytes of the step from the two counter_collection.csv files of "
+                         "`--traffic-probe step` runs, scaled by the calibration copy")
     args = ap.parse_args()
 
     if args.trace_gaps:
         return trace_gaps(args.trace_gaps)
+    if args.traffic_report:
+        return traffic_report(*args.traffic_report)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: the cached block step is batch-1 and this build has no "
               f"multi-GPU path (asked for --gpus {args.gpus})", file=sys.stderr, flush=True)
@@ -133,6 +140,8 @@ def main() -> int:
     log("generating random weights on the GPU")
     params = random_params_torch(cfg, SEED, dtype="bfloat16", device="cuda", std=0.02, lm_head_std=0.5)
     vm = HipVM(cfg, params, dtype="bfloat16", max_rows=PREFIX)
+    if args.traffic_probe == "step":
+        return traffic_probe_step(vm, cfg)
     if args.traffic_probe:
         return traffic_probe(vm, cfg)
     rng = np.random.default_rng(SEED)
@@ -192,6 +201,7 @@ def main() -> int:
     gu_bytes = 2 * I * H * 2 + 32 * H * 2 + 32 * I * 2  # weights + input rows + output rows
     gu_gbps = gu_bytes / (gu_ms * 1e-3) / 1e9
     traffic = measured_traffic()
+    step_traffic = measured_step_traffic()
 
     # ---- CPU baseline: the oracle's refinement step on the host ------------------------------------
     cpu = None
@@ -240,7 +250,10 @@ def main() -> int:
         "roofline": {"kernel": "gemm_os_kernel<bf16, EPI_SILU_PAIR, XF_RMS> (RMSNorm + gate_up + SiLU*up, 32 rows)",
                      "bound": "hbm", "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "avg_launch_us": round(gu_ms * 1e3, 2), "bytes_per_launch": gu_bytes},
+                     "avg_launch_us": round(gu_ms * 1e3, 2), "bytes_per_launch": gu_bytes,
+                     "step_traffic": step_traffic,
+                     "step_traffic_ratio": round(step_traffic / bytes_r32, 4) if step_traffic else None,
+                     "step_counter_gbps": round(step_traffic / (refine_ms * 1e-3) / 1e9, 1) if step_traffic else None},
         "cpu_baseline": cpu,
         "prefix512": prefix512,
         "long_context": long_context,
@@ -559,10 +572,98 @@ def traffic_probe(vm, cfg) -> int:
     return 0
 
 
+def traffic_probe_step(vm, cfg) -> int:
+    """The 2048-row prefix, a plain 256 MiB copy (the counters' scale), then one 32-row refinement step."""
+    import numpy as np
+    import torch
+
+    from fast_dllm_relax_amd.runtime import build_prefix_cache_from_ids, score_active_block_refine
+
+    rng = np.random.default_rng(SEED)
+    cache = build_prefix_cache_from_ids(vm, rng.integers(0, 150000, PREFIX).tolist(), block_size=32,
+                                        capacity=PREFIX + 32)
+    block = rng.integers(0, 150000, 32).tolist()
+    score_active_block_refine(vm, block, cache)  # warm-up: every buffer of the step allocated
+    src = torch.ones(128 << 20, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    score_active_block_refine(vm, block, cache)
+    torch.cuda.synchronize()
+    log("traffic probe done: prefix, one 256 MiB copy, one 32-row refinement step")
+    return 0
+
+
+def traffic_report(fetch_csv: str, write_csv: str) -> int:
+    """Per-kernel FETCH_SIZE / WRITE_SIZE of the refinement step that follows the last 256 MiB copy in two
+    `--traffic-probe step` counter runs, each scaled by what the counter reads for that copy."""
+    import csv
+
+    import __graft_entry__
+
+    __graft_entry__.load_package()
+    from fast_dllm_relax_amd.config import fast_dllm_v2_1p5b
+
+    copy_bytes = 256 << 20
+
+    def load(path, counter):
+        rows = []
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] == counter:
+                    rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"]) * 1024.0))
+        rows.sort()
+        # the calibration copy: the largest dispatch of a copy kernel (the step's own readback is tiny)
+        copies = [i for i, (_, n, _) in enumerate(rows) if "copyBuffer" in n]
+        if not copies:
+            raise SystemExit(f"{path}: no calibration copy found")
+        cal = max(copies, key=lambda i: rows[i][2])
+        return rows[cal][2], rows[cal + 1:]
+
+    fcopy, fstep = load(fetch_csv, "FETCH_SIZE")
+    wcopy, wstep = load(write_csv, "WRITE_SIZE")
+    fs, ws = copy_bytes / fcopy, copy_bytes / wcopy
+
+    def short(n):
+        n = n.split("(")[0].replace("void ", "").replace("fdllm::", "")
+        return n[:60]
+
+    per = {}
+    for _, n, v in fstep:
+        e = per.setdefault(short(n), [0, 0.0, 0.0])
+        e[0] += 1
+        e[1] += v * fs
+    for _, n, v in wstep:
+        per.setdefault(short(n), [0, 0.0, 0.0])[2] += v * ws
+    total = sum(e[1] + e[2] for e in per.values())
+    cfg = fast_dllm_v2_1p5b(tie_word_embeddings=False)
+    algo = cfg.step_bytes(32, PREFIX)
+    print("| kernel | dispatches | fetched MB | written MB |")
+    print("|---|---|---|---|")
+    for n, (cnt, fb, wb) in sorted(per.items(), key=lambda kv: -(kv[1][1] + kv[1][2])):
+        print(f"| `{n}` | {cnt} | {fb / 1e6:.2f} | {wb / 1e6:.2f} |")
+    print(json.dumps({"fetch_scale": round(fs, 4), "write_scale": round(ws, 4), "step_traffic_bytes": int(total),
+                      "algorithmic_bytes": algo, "ratio": round(total / algo, 4)}))
+    return 0
+
+
 def vm_lib():
     from fast_dllm_relax_amd import _lib
 
     return _lib
+
+
+def measured_step_traffic():
+    """HBM bytes of one 32-row refinement step at prefix 2048 from the committed rocprofv3 --pmc summary
+    (profiles/step_traffic_p2048.md, line 'step_traffic_bytes: N'), or None."""
+    path = ROOT / "profiles" / "step_traffic_p2048.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.strip().startswith("step_traffic_bytes:"):
+            return int(line.split(":", 1)[1].strip().strip("`"))
+    return None
 
 
 def measured_traffic():
@@ -577,9 +678,82 @@ def measured_traffic():
     return None
 
 
+def hf_reference_model(cfg, params, dtype):
+    """transformers' Qwen2ForCausalLM built from a Qwen2Config (no download) with the weights of ``params``
+    (host tensors in the packed parameter order), q/k/v and gate/up split back out of the fused tensors
+    (the "HF reference forward").  Constructed on the meta device and then given the
+    weights, so no random initialisation is spent on 1.5B parameters."""
+    import torch
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    from fast_dllm_relax_amd.params import param_names
+
+    hc = Qwen2Config(vocab_size=cfg.vocab_size, hidden_size=cfg.hidden_size, intermediate_size=cfg.intermediate_size,
+                     num_hidden_layers=cfg.num_hidden_layers, num_attention_heads=cfg.num_attention_heads,
+                     num_key_value_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim, rms_norm_eps=cfg.rms_norm_eps,
+                     rope_theta=cfg.rope_theta, tie_word_embeddings=cfg.tie_word_embeddings,
+                     max_position_embeddings=max(4096, 2 * cfg.bd_size), attn_implementation="sdpa")
+    with torch.device("meta"):
+        model = Qwen2ForCausalLM(hc)
+    model = model.to_empty(device="cpu")
+    arr = dict(zip(param_names(cfg), params))
+    qd, kd = cfg.num_attention_heads * cfg.head_dim, cfg.num_key_value_heads * cfg.head_dim
+    inter = cfg.intermediate_size
+    sd = {"model.embed_tokens.weight": arr["model.embed_tokens.weight"], "model.norm.weight": arr["model.norm.weight"]}
+    if not cfg.tie_word_embeddings:
+        sd["lm_head.weight"] = arr["lm_head.weight"]
+    for i in range(cfg.num_hidden_layers):
+        pre = f"model.layers.{i}"
+        w, b = arr[f"{pre}.self_attn.qkv_proj.weight"], arr[f"{pre}.self_attn.qkv_proj.bias"]
+        sd[f"{pre}.self_attn.q_proj.weight"], sd[f"{pre}.self_attn.q_proj.bias"] = w[:qd], b[:qd]
+        sd[f"{pre}.self_attn.k_proj.weight"], sd[f"{pre}.self_attn.k_proj.bias"] = w[qd:qd + kd], b[qd:qd + kd]
+        sd[f"{pre}.self_attn.v_proj.weight"], sd[f"{pre}.self_attn.v_proj.bias"] = w[qd + kd:], b[qd + kd:]
+        sd[f"{pre}.self_attn.o_proj.weight"] = arr[f"{pre}.self_attn.o_proj.weight"]
+        gu = arr[f"{pre}.mlp.gate_up_proj.weight"]
+        sd[f"{pre}.mlp.gate_proj.weight"], sd[f"{pre}.mlp.up_proj.weight"] = gu[:inter], gu[inter:]
+        sd[f"{pre}.mlp.down_proj.weight"] = arr[f"{pre}.mlp.down_proj.weight"]
+        sd[f"{pre}.input_layernorm.weight"] = arr[f"{pre}.input_layernorm.weight"]
+        sd[f"{pre}.post_attention_layernorm.weight"] = arr[f"{pre}.post_attention_layernorm.weight"]
+    sd = {k: v.to(dtype).contiguous() for k, v in sd.items()}
+    missing, unexpected = model.load_state_dict(sd, strict=False, assign=True)
+    if unexpected or not set(missing) <= {"lm_head.weight"}:
+        raise RuntimeError(f"HF weight mapping: missing {missing}, unexpected {unexpected}")
+    if cfg.tie_word_embeddings:
+        model.tie_weights()
+    # the rotary buffers were left uninitialised by to_empty: rebuild them from the config
+    model.model.rotary_emb = type(model.model.rotary_emb)(config=hc)
+    return model.to(dtype).eval()
+
+
+def hf_cached_step(model, k_prefix, v_prefix, block_ids, P):
+    """One HF cached refinement step: a DynamicCache holding the P-row prefix (k/v [L, 1, P, nkv, hd], the
+    reference's inplace_bsnh layout, after RoPE as HF caches keys), then the 32-row block forward with the
+    all-allowed mask of the cached step and RoPE positions P.. (runtime.py:333-343), lm_head included.
+    Returns (logits [rows, vocab] fp32, the forward's seconds)."""
+    import torch
+    from transformers import DynamicCache
+
+    dt = next(model.parameters()).dtype
+    cache = DynamicCache(config=model.config)
+    for layer in range(k_prefix.shape[0]):
+        cache.update(k_prefix[layer, 0].transpose(0, 1)[None].to(dt), v_prefix[layer, 0].transpose(0, 1)[None].to(dt),
+                     layer)
+    rows = len(block_ids)
+    ids = torch.tensor([block_ids], dtype=torch.long)
+    mask = {"full_attention": torch.zeros((1, 1, rows, P + rows), dtype=dt)}
+    with torch.no_grad():
+        t0 = time.perf_counter()
+        out = model(input_ids=ids, position_ids=torch.arange(P, P + rows)[None], past_key_values=cache,
+                    attention_mask=mask, use_cache=True)
+        sec = time.perf_counter() - t0
+    return out.logits[0].float(), sec
+
+
 def cpu_baseline(vm, params, cache, block, P, iters, tokens_per_call):
-    """Time the CPU oracle's 32-row refinement step (28 layers + lm_head + confidence) at prefix P on
-    the same weights and KV cache as the GPU run."""
+    """The CPU baseline of BASELINE.md section 3, on the same weights and KV-cache prefix as the GPU run,
+    all host cores: the HF reference forward (transformers' Qwen2, one 32-row cached forward + lm_head
+    against the P-row prefix) in bf16 and fp32, and this build's numpy oracle for the same step.  Medians
+    of ``iters`` (>= 5) after one warm-up each; tokens/s uses the GPU loop's tokens per model call."""
     import numpy as np
     import torch
     from threadpoolctl import threadpool_info
@@ -587,38 +761,66 @@ def cpu_baseline(vm, params, cache, block, P, iters, tokens_per_call):
     from oracle import confidence as oconf
     from oracle.model import OracleConfig, OracleModel, param_names
 
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
     c = vm.cfg
+    log("cpu baseline: copying weights and cache to the host")
+    host = [p.cpu() for p in params]
+    kpre = cache.k[:, :, :P].cpu()
+    vpre = cache.v[:, :, :P].cpu()
+    res = {}
+
+    def med(fn, n):
+        fn()  # warm-up
+        ts = []
+        for i in range(n):
+            ts.append(fn())
+            log(f"cpu baseline step {i + 1}/{n}: {ts[-1]:.3f} s")
+        return statistics.median(ts)
+
+    for name, dt in (("bf16", torch.bfloat16), ("fp32", torch.float32)):
+        log(f"cpu baseline: HF Qwen2 {name}")
+        model = hf_reference_model(c, host, dt)
+        res[name] = med(lambda: hf_cached_step(model, kpre, vpre, block, P)[1], iters)
+        del model
+    log("cpu baseline: numpy oracle")
     ocfg = OracleConfig(vocab_size=c.vocab_size, hidden_size=c.hidden_size, intermediate_size=c.intermediate_size,
                         num_hidden_layers=c.num_hidden_layers, num_attention_heads=c.num_attention_heads,
                         num_key_value_heads=c.num_key_value_heads, head_dim=c.head_dim,
                         tie_word_embeddings=c.tie_word_embeddings)
-    log("cpu baseline: copying weights and cache to the host")
-    arrays = {n: p.float().cpu().numpy() for n, p in zip(param_names(ocfg), params)}
+    arrays = {n: p.float().numpy() for n, p in zip(param_names(ocfg), host)}
     model = OracleModel(ocfg, arrays, "bfloat16")
-    kc = cache.k[:, :, :P + 32].float().cpu().numpy()
-    vc = cache.v[:, :, :P + 32].float().cpu().numpy()
+    kc = torch.cat([kpre, torch.zeros_like(kpre[:, :, :32])], 2).float().numpy()
+    vc = torch.cat([vpre, torch.zeros_like(vpre[:, :, :32])], 2).float().numpy()
     emb = model.embed(block)[None]
 
-    def step():
-        h = model.forward_cached(emb, kc, vc, P, P)
-        return oconf.shifted_confidence(model.get_logits(h)[0])
-
-    step()  # warm-up
-    times = []
-    for i in range(iters):
+    def oracle_step():
         t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-        log(f"cpu baseline step {i + 1}/{iters}: {times[-1]:.2f} s")
-    sec = statistics.median(times)
-    threads = max([d.get("num_threads", 1) for d in threadpool_info()] or [1])
-    del arrays, model
+        h = model.forward_cached(emb, kc, vc, P, P)
+        oconf.shifted_confidence(model.get_logits(h)[0])
+        return time.perf_counter() - t0
+
+    port_s = med(oracle_step, max(2, iters // 2))
+    blas = max([d.get("num_threads", 1) for d in threadpool_info()] or [1])
+    del arrays, model, host
     torch.cuda.empty_cache()
-    return {"value": round(tokens_per_call / sec, 3), "unit": "tokens/s", "cores": int(threads), "kind": "port",
-            "step_s": round(sec, 3), "host_cpus": os.cpu_count(),
-            "sample": f"oracle (numpy fp32 + bf16 rounding) 32-row refinement step at prefix {P}, 28 layers + "
-                      f"lm_head + confidence, median of {iters} after 1 warm-up; tokens/s = "
-                      f"{tokens_per_call:.3f} tokens per model call (the GPU loop's) / step time"}
+    return {"value": round(tokens_per_call / res["bf16"], 3), "unit": "tokens/s", "cores": threads,
+            "kind": "reference",
+            "step_s_bf16": round(res["bf16"], 4), "step_s_fp32": round(res["fp32"], 4),
+            "value_fp32": round(tokens_per_call / res["fp32"], 3),
+            "port_step_s": round(port_s, 4), "port_value": round(tokens_per_call / port_s, 3), "port_cores": int(blas),
+            "host_cpus": os.cpu_count(),
+            "sample": f"HF reference forward (BASELINE.md section 3): transformers {_hf_version()} Qwen2ForCausalLM "
+                      f"from a Qwen2Config with the bench weights, one 32-row cached forward + lm_head against a "
+                      f"{P}-row DynamicCache (the GPU-built prefix), torch threads = {threads}; median of {iters} "
+                      f"after 1 warm-up, bf16 (value) and fp32; tokens/s = {tokens_per_call:.3f} tokens per model "
+                      f"call (the GPU loop's) / step time.  port_*: this build's numpy oracle, same step"}
+
+
+def _hf_version():
+    import transformers
+
+    return transformers.__version__
 
 
 if __name__ == "__main__":
