@@ -87,7 +87,10 @@ static hipError_t launch_chunk_kh(const AttnP& a, const AttnPlan& p, hipStream_t
   auto kern = attn_chunk_kernel<DT, QPW, KH, CH, MASK>;
   raise_lds(kern, lds);
   const int nseq = std::max(a.nseq, 1);
-  hipLaunchKernelGGL(kern, dim3(p.qg * nseq, a.nkv, a.S), dim3(64 * QPW * KH), lds, st, a);
+  if (nseq == 1)
+    hipLaunchKernelGGL(kern, dim3(attn_chunk_grid_1seq(p.qg, a.nkv, a.S)), dim3(64 * QPW * KH), lds, st, a);
+  else
+    hipLaunchKernelGGL(kern, dim3(p.qg * nseq, a.nkv, a.S), dim3(64 * QPW * KH), lds, st, a);
   if (a.S > 1) {
     const int QT = ((a.nq / a.nkv) * a.rows + 15) / 16;
     hipLaunchKernelGGL(merge_kernel_for<DT>(a.S), dim3(HD / 16, QT, a.nkv * nseq), dim3(64), 0, st, a);

@@ -626,12 +626,26 @@ __device__ __forceinline__ void seq_view(AttnP& a, const AttnP& p, int b) {
   a.part = p.part + (size_t)b * p.nkv * QT * p.S * PSZ;
 }
 
-// gridDim.x = query-tile groups x sequences (sequence-major); MASK is the launch's AttnP::mask
+// One sequence: a 1-D grid in XCD-aware order.  The qg workgroups that read one (kv head, key chunk)
+// pair -- one per query-tile group -- get linear indices 8 apart, so they run on one XCD (workgroup i is
+// placed on XCD i % 8) and share its L2: the chunk's K/V comes from HBM once instead of once per group.
+// Linear index i: XCD slot i % 8, round i / 8; pair = (round / qg) x 8 + slot (kv head pair % nkv, chunk
+// pair / nkv), query-tile group round % qg.  Indices past the last pair have nothing to do.
+// Batched calls: gridDim.x = query-tile groups x sequences (sequence-major), y = kv heads, z = chunks.
+// MASK is the launch's AttnP::mask.
+__host__ __device__ __forceinline__ int attn_chunk_grid_1seq(int qg, int nkv, int S) {
+  return (nkv * S + 7) / 8 * 8 * qg;
+}
+
 template <int DT, int QPW, int KH, int CH, int MASK>
 __global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP p) {
   extern __shared__ __align__(16) unsigned char smem[];
   if (p.nseq <= 1) {
-    attn_chunk_body<DT, QPW, KH, CH, MASK, false>(p, blockIdx.x, blockIdx.y, blockIdx.z, smem);
+    const int QT = ((p.nq / p.nkv) * p.rows + 15) / 16, qg = (QT + QPW - 1) / QPW;
+    const int i = blockIdx.x, round = i >> 3;
+    const int pair = (round / qg) * 8 + (i & 7), x = round % qg;
+    if (pair >= p.nkv * p.S) return;
+    attn_chunk_body<DT, QPW, KH, CH, MASK, false>(p, x, pair % p.nkv, pair / p.nkv, smem);
     return;
   }
   const int qg = (int)gridDim.x / p.nseq, b = (int)blockIdx.x / qg;
