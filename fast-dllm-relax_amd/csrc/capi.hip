@@ -98,8 +98,7 @@ struct fdllm_ctx {
   int attn_target = 64;   // attention workgroups aimed for when splitting the keys
   int prefill_hpw = 0;    // query heads per prefill-attention workgroup (0: chosen per launch)
   int down_split = 10;    // cross-workgroup k splits of the down projection (largest divisor of K/32 <= this)
-  int mm_target_wgs = 256;  // large-M GEMM: split k while the launch has fewer workgroups than this
-  int mm_min_stages = 8;    // ... into splits of at least this many stages
+  MmPolicy mm;              // large-M GEMM planning (k splits, register-weight kernel)
   bool frag_on = true;      // one-shot chains keep activations in MFMA-fragment order (FDLLM_XFRAG=0: row-major)
   // the persistent cached step (step_body.hpp)
   bool step_on = false;                // FDLLM_PERSISTENT=1 turns it on (measured slower than the kernels)
@@ -199,7 +198,7 @@ int divisor_at_most(int n, int cap) {
 int run_gemm(fdllm_ctx* c, int cfg, GemmP a, int ksplit, hipStream_t st) {
   const fdllm_config& f = c->cfg;
   if (ksplit < 1 || a.KS % ksplit) return fail(FDLLM_EINVAL, "k split %d does not divide %d k steps", ksplit, a.KS);
-  const GemmPlan pl = gemm_plan(cfg, a, ksplit, c->mm_target_wgs, c->mm_min_stages);
+  const GemmPlan pl = gemm_plan(cfg, a, ksplit, c->mm);
   if (pl.kind == GK_MM && a.nw != nullptr) {
     // RMSNorm once for all column blocks (the large-M kernel takes normalised rows; the LDS-staged one
     // in its fragment blocks)
@@ -315,7 +314,7 @@ int try_step(fdllm_ctx* c, int rows, uint16_t* kbase, uint16_t* vbase, size_t la
   p.nt_q = c->qkv_dim() / 16; p.nt_o = f.hidden_size / 16; p.np_u = f.intermediate_size / 16;
   // down: the one-shot kernel's tile groups and k split
   GemmP dp = gemm_args(nullptr, d_tiles(c), f.hidden_size, f.intermediate_size, nullptr, f.intermediate_size, rows);
-  const GemmPlan dpl = gemm_plan(CFG_DOWN, dp, 1, c->mm_target_wgs, c->mm_min_stages);
+  const GemmPlan dpl = gemm_plan(CFG_DOWN, dp, 1, c->mm);
   if (dpl.kind != GK_ONESHOT || dpl.tiles_per_wg != STEP_DNT) return FDLLM_OK;
   p.d_groups = dpl.groups; p.d_splits = dpl.ksplit;
   p.sync.ctr = c->step_sync;
@@ -394,8 +393,8 @@ LayerGemms layer_gemms(const fdllm_ctx* c, const Layer& L, int rows, bool frag) 
     // large M: when gate_up and down both run the LDS-staged kernel, SiLU * up goes straight into the
     // fragment blocks down copies
     GemmP tg = g.gu, td = g.d;
-    const GemmPlan pg = gemm_plan(CFG_GATE_UP, tg, 1, c->mm_target_wgs, c->mm_min_stages);
-    const GemmPlan pd = gemm_plan(CFG_DOWN, td, g.dsplit, c->mm_target_wgs, c->mm_min_stages);
+    const GemmPlan pg = gemm_plan(CFG_GATE_UP, tg, 1, c->mm);
+    const GemmPlan pd = gemm_plan(CFG_DOWN, td, g.dsplit, c->mm);
     if (gemm_takes_blocks(pg) && gemm_takes_blocks(pd)) g.gu.yfrag = g.d.xfrag = 2;
   }
   return g;
@@ -409,7 +408,7 @@ bool frag_chain(const fdllm_ctx* c, int rows) {
   const std::pair<int, GemmP*> all[] = {{CFG_QKV, &g.q}, {CFG_OPROJ, &g.o}, {CFG_GATE_UP, &g.gu}, {CFG_DOWN, &g.d}};
   for (const auto& [cfg, a] : all) {
     GemmP t = *a;
-    const GemmPlan pl = gemm_plan(cfg, t, cfg == CFG_DOWN ? g.dsplit : 1, c->mm_target_wgs, c->mm_min_stages);
+    const GemmPlan pl = gemm_plan(cfg, t, cfg == CFG_DOWN ? g.dsplit : 1, c->mm);
     if (!gemm_takes_frag(cfg, pl)) return false;
   }
   return true;
@@ -585,8 +584,10 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   if (const char* e = std::getenv("FDLLM_ATTN_TARGET")) c->attn_target = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_PREFILL_HPW")) c->prefill_hpw = std::max(0, atoi(e));
   if (const char* e = std::getenv("FDLLM_DOWN_SPLIT")) c->down_split = std::max(1, atoi(e));
-  if (const char* e = std::getenv("FDLLM_MM_TARGET_WGS")) c->mm_target_wgs = std::max(1, atoi(e));
-  if (const char* e = std::getenv("FDLLM_MM_MIN_STAGES")) c->mm_min_stages = std::max(1, atoi(e));
+  if (const char* e = std::getenv("FDLLM_MM_TARGET_WGS")) c->mm.target_wgs = std::max(1, atoi(e));
+  if (const char* e = std::getenv("FDLLM_MM_MIN_STAGES")) c->mm.min_stages = std::max(1, atoi(e));
+  if (const char* e = std::getenv("FDLLM_WR_OPS")) c->mm.wr_ops = atoi(e) & 15;
+  if (const char* e = std::getenv("FDLLM_WR_MIN_ROWS")) c->mm.wr_min_rows = std::max(0, atoi(e));
   if (const char* e = std::getenv("FDLLM_PERSISTENT")) c->step_on = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_XFRAG")) c->frag_on = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_STEP_CHECK")) c->step_check = atoi(e) != 0;
@@ -787,7 +788,7 @@ static size_t noalloc_gemm_partials(const fdllm_ctx* c) {
     const std::pair<int, GemmP*> all[] = {{CFG_QKV, &g.q}, {CFG_OPROJ, &g.o}, {CFG_GATE_UP, &g.gu}, {CFG_DOWN, &g.d}};
     for (const auto& [cfg, a] : all) {
       GemmP t = *a;
-      const GemmPlan pl = gemm_plan(cfg, t, cfg == CFG_DOWN ? g.dsplit : 1, c->mm_target_wgs, c->mm_min_stages);
+      const GemmPlan pl = gemm_plan(cfg, t, cfg == CFG_DOWN ? g.dsplit : 1, c->mm);
       need = std::max(need, pl.part_floats);
     }
   }

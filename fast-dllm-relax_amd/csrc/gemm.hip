@@ -141,6 +141,11 @@ GemmShape gemm_shape(int cfg) {
   return GemmShape{l, 0};
 }
 
+// stages in flight of the register-weight kernel
+#ifndef FD_WR_DEPTH
+#define FD_WR_DEPTH 3
+#endif
+
 // large-M kernel configurations (rows x columns per workgroup)
 using MmSmall = MmCfg<4, 2, 1, 4, 2, 2>;  // 64 x 128, weights two stages ahead
 using MmWide = MmCfg<4, 4, 1, 4, 2, 1>;   // 64 x 256
@@ -155,7 +160,16 @@ struct WtCfg {
   static constexpr size_t lds = (size_t)NBUF * (MF * WM + TPW * WN) * 1024;
 };
 using WtBig = WtCfg<4, 6, 2, 2, 4>;
-enum MmId : int { MM_SMALL = 0, MM_WIDE = 1, MM_WIDE_D = 2, MM_BIG = 3, MM_WT = 4 };
+// register-weight kernel (gemm_wt.hpp, gemm_wr_kernel): four waves of 16 MF rows x TPW tiles, a
+// 16 MF x 64 TPW block, D stages in flight
+template <int MF, int TPW, int D>
+struct WrCfg {
+  static constexpr int mf = MF, tpw = TPW, d = D;
+  static constexpr int bm = 16 * MF, bn_tiles = 4 * TPW, kss = 1;
+  static constexpr size_t lds = (size_t)(D + 1) * MF * 1024;
+};
+using WrBig = WrCfg<8, 4, FD_WR_DEPTH>;  // 128 x 256
+enum MmId : int { MM_SMALL = 0, MM_WIDE = 1, MM_WIDE_D = 2, MM_BIG = 3, MM_WT = 4, MM_WR = 5 };
 struct MmInfo { int bm, bn_tiles, kss; };
 template <class M> constexpr MmInfo mm_info_of() { return MmInfo{M::bm, M::bn_tiles, M::kss}; }
 static MmInfo mm_info(int id) {
@@ -164,10 +178,18 @@ static MmInfo mm_info(int id) {
     case MM_WIDE_D: return mm_info_of<MmWideD>();
     case MM_BIG: return mm_info_of<MmBig>();
     case MM_WT: return mm_info_of<WtBig>();
+    case MM_WR: return mm_info_of<WrBig>();
     default: return mm_info_of<MmSmall>();
   }
 }
-static int mm_choice(int cfg, int M, int ntiles) {
+// Rows from which a projection takes the register-weight kernel by default.  Measured (1.5B, us per
+// launch, register-weight / previous kernel): gate_up 53 / 47 at 512 rows, 110 / 118 at 2048, 377 / 448
+// at 8192; down 40 / 30, 79 / 80, 189 / 192; qkv 37 / 31 at 2048, 75 / 106 at 8192; o_proj 38 / 23,
+// 57 / 70.  Below these sizes its 128 x 256 blocks leave too few workgroups without a k split.
+static int wr_default_min_rows(int cfg) { return cfg == CFG_GATE_UP || cfg == CFG_DOWN ? 2048 : 4096; }
+static int mm_choice(int cfg, int M, int ntiles, const MmPolicy& pol) {
+  const int min_rows = pol.wr_min_rows > 0 ? pol.wr_min_rows : wr_default_min_rows(cfg);
+  if (cfg != CFG_LM_HEAD && M >= std::max(min_rows, 33) && ((pol.wr_ops >> cfg) & 1)) return MM_WR;
   switch (cfg) {
     case CFG_LM_HEAD: return MM_WIDE;  // one 256-column confidence tile per block column
     case CFG_GATE_UP:
@@ -181,11 +203,11 @@ static int mm_choice(int cfg, int M, int ntiles) {
   }
 }
 
-GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, int mm_target_wgs, int mm_min_stages) {
+GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol) {
   GemmPlan p{};
   p.mchunks = (a.M + 31) / 32;
   if (a.M > 32) {
-    const int id = mm_choice(cfg, a.M, a.ntiles);
+    const int id = mm_choice(cfg, a.M, a.ntiles, pol);
     const MmInfo mi = mm_info(id);
     if (a.KS % mi.kss == 0) {
       const int nst = a.KS / mi.kss;
@@ -198,10 +220,11 @@ GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, int mm_target_wgs, int m
       const int wgs = p.nbm * p.nbn;
       // (up to 128 rows, half the target: a split's fp32 partials and its epilogue launch cost more
       // than the idle compute units; measured on the 128-row batched step, 3.15 -> 2.93 ms)
-      const int target = a.M <= 128 ? mm_target_wgs / 2 : mm_target_wgs;
+      const int target = a.M <= 128 ? pol.target_wgs / 2 : pol.target_wgs;
       int split = 1;
-      for (int d = 2; d <= 8 && wgs * split < target && cfg != CFG_LM_HEAD; ++d)
-        if (nst % d == 0 && nst / d >= mm_min_stages) split = d;
+      const int max_split = id == MM_WR ? 16 : 8;
+      for (int d = 2; d <= max_split && wgs * split < target && cfg != CFG_LM_HEAD; ++d)
+        if (nst % d == 0 && nst / d >= pol.min_stages) split = d;
       p.ksplit = split;
       a.kps = a.KS / split;
       p.part_floats = split > 1 ? (size_t)split * a.ntiles * ((a.M + 15) / 16) * 256 : 0;
@@ -264,6 +287,20 @@ static hipError_t launch_os(const GemmP& a, const GemmPlan& p, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <int DT, int EPI, class W>
+static hipError_t launch_wr_cfg(const GemmP& a, const GemmPlan& p, hipStream_t st) {
+  static_assert(W::lds <= 64 * 1024, "no LDS attribute needed");
+  auto kern = gemm_wr_kernel<DT, EPI, W::mf, W::tpw, W::d>;
+  const int total = p.nbm * p.nbn, per = (total + 7) / 8;
+  hipLaunchKernelGGL(kern, dim3(8 * per, p.ksplit), dim3(256), W::lds, st, a, p.nbm, p.nbn);
+  if (p.ksplit > 1) {
+    const int nblk = (a.M + 15) / 16;
+    hipLaunchKernelGGL((gemm_mm_split_epilogue_kernel<DT, EPI>), dim3((a.N + 15) / 16, (nblk + 3) / 4), dim3(256), 0,
+                       st, a, p.ksplit);
+  }
+  return hipGetLastError();
+}
+
 template <int DT, int EPI, int XF, class M>
 static hipError_t launch_mm_cfg(const GemmP& a, const GemmPlan& p, hipStream_t st) {
   auto kern = gemm_mm_kernel<DT, EPI, XF, M::mf, M::tpw, M::nwm, M::nwn, M::kss, M::wd>;
@@ -301,6 +338,9 @@ static hipError_t launch_wt_cfg(const GemmP& a, const GemmPlan& p, hipStream_t s
 // GK_MM rows arrive normalised (see GemmKind), so every large-M launch runs without the norm transform.
 template <int DT, int CFG, class C>
 static hipError_t launch_mm(const GemmP& a, const GemmPlan& p, hipStream_t st) {
+  if constexpr (CFG != CFG_LM_HEAD) {
+    if (p.mm_id == MM_WR) return launch_wr_cfg<DT, C::epi, WrBig>(a, p, st);
+  }
   if constexpr (CFG == CFG_GATE_UP) {
     if (p.mm_id == MM_WT) return launch_wt_cfg<DT, C::epi, WtBig>(a, p, st);
     if (p.mm_id == MM_BIG) return launch_mm_cfg<DT, C::epi, XF_NONE, MmBig>(a, p, st);
@@ -348,7 +388,7 @@ bool gemm_takes_frag(int cfg, const GemmPlan& p) {
   return p.kind == GK_ONESHOT && p.mchunks == 1 && nt > 0 && (nt <= 4 || (cfg == CFG_GATE_UP && p.ksplit == 1));
 }
 
-bool gemm_takes_blocks(const GemmPlan& p) { return p.kind == GK_MM && p.mm_id == MM_WT; }
+bool gemm_takes_blocks(const GemmPlan& p) { return p.kind == GK_MM && (p.mm_id == MM_WT || p.mm_id == MM_WR); }
 
 hipError_t launch_gemm(int dt, int cfg, const GemmP& a, const GemmPlan& p, hipStream_t st) {
   if ((a.xfrag == 1 || a.yfrag == 1) && !gemm_takes_frag(cfg, p)) return hipErrorInvalidValue;

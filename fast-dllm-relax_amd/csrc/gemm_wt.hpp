@@ -22,6 +22,8 @@
 #pragma once
 #include "gemm_mm.hpp"
 
+#include <type_traits>
+
 namespace fdllm {
 
 template <int DT, int EPI, int MF, int TPW, int WM, int WN, int NBUF>
@@ -141,6 +143,158 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_wt_kernel(GemmP a, int nbm,
       for (int f = 0; f < MF; ++f) {
         const f32x4 v[1] = {acc[j][f]};
         os_epilogue<DT, EPI, 1, false>(a, v, m0 + 16 * (f0 + f) + lr, tw0 + j, lg);
+      }
+  }
+}
+
+// Large-M GEMM with the weights loaded straight into registers and only the activations staged in LDS.
+// Same arithmetic, split partials and epilogues as gemm_wt_kernel (per output element one MFMA chain
+// over the k steps in order), so for the same k split the results are the same bits.
+//
+// Why: in gemm_wt_kernel every operand byte crosses LDS twice (the global -> LDS copy, then one
+// fragment read per wave that uses it), and LDS bandwidth (128 B per clock per compute unit) runs out
+// before the MFMAs do.  Here the four waves of a workgroup share the BM = 16 MF activation rows (one
+// LDS copy, four reads) and each wave owns TPW weight tiles, which no other wave needs: its packed
+// 1 KB weight blocks are already in MFMA fragment order, so they go from global memory to registers
+// with one coalesced 16-byte load per lane.  A block is 16 MF rows x 64 TPW columns.
+//
+// Pipeline: D stages in flight.  Stage st uses LDS buffer st % R and weight register set st % R
+// (R = D + 1), so the copies for stage st + D, issued right after the barrier of stage st, go into the
+// buffer and register set that stage st - 1 used.  Each stage issues exactly VPS = TPW + MF / 4 vector
+// memory instructions per wave (stages past the last re-read the last), weights first, and the issue is
+// fenced against compiler motion, so "all but the (D - 1) VPS most recent" is exactly "stage st has
+// landed".  The k loop is unrolled by R so that the register sets are named at compile time.
+// f(integral_constant<int, I>) for I = B .. E - 1, unrolled at compile time
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+template <int DT, int EPI, int MF, int TPW, int D>
+// (up to 32 accumulator tiles per wave, two workgroups per compute unit: at most 256 registers per lane,
+// accumulators included; more tiles, one workgroup)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MF * TPW <= 32 ? 2 : 1, MF * TPW <= 32 ? 2 : 1)))
+void gemm_wr_kernel(GemmP a, int nbm, int nbn) {
+  constexpr int NW = 4, R = D + 1;
+  constexpr int DPW = MF / NW;        // activation blocks each wave copies per stage
+  constexpr int VPS = TPW + DPW;      // vector memory instructions per wave per stage
+  static_assert(MF % NW == 0, "every wave copies the same number of activation blocks");
+  static_assert(D >= 1 && (D - 1) * VPS < 64, "outstanding copies fit the memory counter");
+  static_assert(EPI != EPI_SILU_PAIR || TPW % 2 == 0, "gate/up pairs stay within a wave");
+  static_assert(EPI != EPI_LOGITS, "the lm_head takes the streaming kernel");
+  extern __shared__ __align__(16) unsigned char smem[];  // [R][MF][1 KB]
+
+  const int total = nbm * nbn;
+  const int per = (total + 7) / 8;
+  // the row blocks of one weight column block on one XCD (workgroup i runs on XCD i % 8), so its
+  // weights come from HBM once per XCD
+  const int logical = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if (logical >= total) return;
+  const int nb = logical / nbm, mb = logical - nb * nbm;
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int m0 = mb * 16 * MF, mlast = a.M - 1;
+  const int tw0 = (nb * NW + w) * TPW, tlast = a.ntiles - 1;  // this wave's first tile
+  const int nst = a.KS / (int)gridDim.y;
+  const int kb = (int)blockIdx.y * nst;
+
+  const u16* xs[DPW];
+  size_t xstep[DPW];
+#pragma unroll
+  for (int q = 0; q < DPW; ++q) {
+    const int i = w + NW * q;
+    if (a.xfrag == 2) {
+      const int b = min(m0 / 16 + i, mlast / 16);
+      xs[q] = a.X + ((size_t)b * a.KS + kb) * 512 + 8 * lane;
+      xstep[q] = 512;
+    } else {
+      const int m = min(m0 + 16 * i + lr, mlast);
+      xs[q] = a.X + (size_t)m * a.ldx + 32 * kb + 8 * lg;
+      xstep[q] = 32;
+    }
+  }
+  const u16* ws[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) ws[j] = a.W + ((size_t)min(tw0 + j, tlast) * a.KS + kb) * 512 + 8 * lane;
+
+  u32x4 wv[R][TPW];
+  auto issue = [&](int st, u32x4 (&dst)[TPW], int buf) {
+    const int s = min(st, nst - 1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) dst[j] = *reinterpret_cast<const u32x4*>(ws[j] + (size_t)s * 512);
+#pragma unroll
+    for (int q = 0; q < DPW; ++q)
+      lds_copy16(xs[q] + (size_t)s * xstep[q], smem + ((size_t)buf * MF + w + NW * q) * 1024);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  f32x4 acc[TPW][MF];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j)
+#pragma unroll
+    for (int f = 0; f < MF; ++f) acc[j][f] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int u = 0; u < D; ++u) issue(u, wv[u], u);
+
+  // stage st = st0 + u with u = st % R known at compile time
+  const u32x4* lds = reinterpret_cast<const u32x4*>(smem);
+  auto stage = [&](int st, auto uc) {
+    constexpr int u = decltype(uc)::value;
+    wait_vmcnt<(D - 1) * VPS>();     // this wave's copies and weights of stage st have landed
+    __builtin_amdgcn_s_barrier();    // every wave's copies have; buffer (u - 1) % R is free
+    issue(st + D, wv[(u + D) % R], (u + D) % R);
+    const u32x4* blk = lds + (size_t)u * MF * 64;
+    u32x4 xf[MF];
+#pragma unroll
+    for (int f = 0; f < MF; ++f) xf[f] = blk[f * 64 + lane];
+#pragma unroll
+    for (int j = 0; j < TPW; ++j)
+#pragma unroll
+      for (int f = 0; f < MF; ++f) acc[j][f] = mfma16<DT>(wv[u][j], xf[f], acc[j][f]);
+  };
+  // whole rounds of R stages, then the last nst % R stages outside the loop (an exit from inside the
+  // unrolled round would make the compiler's own counter bookkeeping wait for everything at its top)
+  int st0 = 0;
+#pragma nounroll
+  for (; st0 + R <= nst; st0 += R) static_for<0, R>([&](auto uc) { stage(st0 + decltype(uc)::value, uc); });
+  static_for<0, R - 1>([&](auto uc) {
+    if (st0 + decltype(uc)::value < nst) stage(st0 + decltype(uc)::value, uc);
+  });
+  wait_vmcnt<0>();  // no copy may still be writing LDS when the workgroup ends
+
+  if (gridDim.y > 1) {
+    const int nblk = (a.M + 15) / 16;
+    f32x4* part = reinterpret_cast<f32x4*>(a.part);
+#pragma unroll
+    for (int j = 0; j < TPW; ++j)
+#pragma unroll
+      for (int f = 0; f < MF; ++f) {
+        const int t = tw0 + j, b = mb * MF + f;
+        if (t < a.ntiles && b < nblk) part[(((size_t)blockIdx.y * a.ntiles + t) * nblk + b) * 64 + lane] = acc[j][f];
+      }
+    return;
+  }
+  if constexpr (EPI == EPI_SILU_PAIR) {
+#pragma unroll
+    for (int p = 0; p < TPW / 2; ++p)
+#pragma unroll
+      for (int f = 0; f < MF; ++f) {
+        const f32x4 v[2] = {acc[2 * p][f], acc[2 * p + 1][f]};
+        os_epilogue<DT, EPI, 2, false>(a, v, m0 + 16 * f + lr, tw0 + 2 * p, lg);
+      }
+  } else {
+#pragma unroll
+    for (int j = 0; j < TPW; ++j)
+#pragma unroll
+      for (int f = 0; f < MF; ++f) {
+        const f32x4 v[1] = {acc[j][f]};
+        os_epilogue<DT, EPI, 1, false>(a, v, m0 + 16 * f + lr, tw0 + j, lg);
       }
   }
 }

@@ -58,9 +58,18 @@ struct GemmPlan {
   int kind; int ksplit; int tiles_per_wg; int groups; int mchunks; size_t part_floats;
   int mm_id; int nbm; int nbn;
 };
-// mm_target_wgs / mm_min_stages: the large-M kernel splits k only while the launch has fewer than
-// mm_target_wgs workgroups, and only into splits of at least mm_min_stages stages.
-GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, int mm_target_wgs = 256, int mm_min_stages = 8);
+// How large-M launches are planned.  target_wgs / min_stages: k is split only while the launch has fewer
+// than target_wgs workgroups, and only into splits of at least min_stages stages.  wr_ops: the
+// projections (bit cfg) that may take the register-weight kernel, from wr_min_rows rows (0: from 2048
+// rows for gate_up and down, from 4096 for qkv and o_proj, where it measured faster than the
+// LDS-staged and streaming kernels).
+struct MmPolicy {
+  int target_wgs = 256;
+  int min_stages = 8;
+  int wr_ops = (1 << CFG_QKV) | (1 << CFG_OPROJ) | (1 << CFG_GATE_UP) | (1 << CFG_DOWN);
+  int wr_min_rows = 0;
+};
+GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol = MmPolicy{});
 // whether the plan runs the one-shot register-fragment body, the only one that takes xfrag / yfrag 1
 bool gemm_takes_frag(int cfg, const GemmPlan& p);
 // whether the plan runs the large-M LDS-staged kernel, the only one that takes xfrag 2

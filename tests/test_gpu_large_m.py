@@ -1,0 +1,58 @@
+"""The register-weight large-M GEMM against the LDS-staged and streaming large-M GEMMs.
+
+By default gate_up and down run gemm_wr_kernel from 2048 rows and qkv and o_proj from 4096
+(FDLLM_WR_OPS selects the projections, one bit per GemmCfg; FDLLM_WR_MIN_ROWS lowers the threshold,
+here to 256 so that ragged and small row counts take it too).  Every large-M kernel accumulates each
+output element's k steps in order in one MFMA chain and shares the epilogues, so with k splits off
+(FDLLM_MM_TARGET_WGS=1) the hidden states must agree bit for bit whichever kernel ran.  Parity of the default configuration with the oracle is
+established by the prefill, forward_hidden and batched-step tests."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import WIDE2, log
+
+pytestmark = pytest.mark.gpu
+
+
+def _vm(kw, params, dtype, monkeypatch, wr_ops, max_rows):
+    from fast_dllm_relax_amd.config import FastDLLMConfig
+    from fast_dllm_relax_amd.vm import HipVM
+
+    monkeypatch.setenv("FDLLM_WR_OPS", str(wr_ops))
+    monkeypatch.setenv("FDLLM_WR_MIN_ROWS", "256")
+    monkeypatch.setenv("FDLLM_MM_TARGET_WGS", "1")
+    vm = HipVM(FastDLLMConfig(**kw), params, dtype=dtype, max_rows=max_rows)
+    for k in ("FDLLM_WR_OPS", "FDLLM_WR_MIN_ROWS", "FDLLM_MM_TARGET_WGS"):
+        monkeypatch.delenv(k)
+    return vm
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16).cpu().numpy()
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_register_weight_kernel_bit_identical(dtype, monkeypatch):
+    from fast_dllm_relax_amd.config import FastDLLMConfig
+    from fast_dllm_relax_amd.params import from_numpy
+    from oracle.model import OracleConfig, random_params
+
+    kw = WIDE2
+    params = from_numpy(random_params(OracleConfig(**kw), 5, dtype), FastDLLMConfig(**kw), dtype=dtype)
+    sizes = (300, 512, 1056)
+    vm_wr = _vm(kw, params, dtype, monkeypatch, 15, max(sizes))
+    vm_old = _vm(kw, params, dtype, monkeypatch, 0, max(sizes))
+    rng = np.random.default_rng(17)
+    for S in sizes:
+        log(f"case: forward_hidden {S} rows, 1.5B width, 2 layers, {dtype}, register-weight vs LDS-staged")
+        ids = torch.tensor(rng.integers(0, kw["vocab_size"] - 1, S), dtype=torch.int32, device="cuda")
+        x = vm_old.embed(ids)[None]
+        h_old = vm_old.forward_hidden(x, None)
+        h_wr = vm_wr.forward_hidden(x, None)
+        torch.cuda.synchronize()
+        assert torch.isfinite(h_wr.float()).all()
+        np.testing.assert_array_equal(_bits(h_wr), _bits(h_old), err_msg=f"S={S}")
