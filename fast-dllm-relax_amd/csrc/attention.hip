@@ -122,10 +122,22 @@ static hipError_t launch_prefill_cfg(const AttnP& a, int hpw, hipStream_t st) {
   return hipGetLastError();
 }
 
+// The paired-query-block kernel (all heads of a kv head per workgroup, tiles per wave) for models with
+// 6 query heads per kv head, and its K/V blocks in flight.
+constexpr int PAIR_TQ = 3, PAIR_DEPTH = 3;
+
 template <int DT, int MASK>
 static hipError_t launch_prefill(const AttnP& a, hipStream_t st) {
   hipLaunchKernelGGL(rope_kv_kernel<DT>, dim3(a.rows), dim3(128), 0, st, a);
   const int nqb = (a.rows + 31) / 32, grp = a.nq / a.nkv;
+  const int pairs = (nqb + 1) / 2;
+  if (grp == 2 * PAIR_TQ && (a.prefill_pair == 2 || (a.prefill_pair == 1 && pairs * a.nkv >= 256))) {
+    auto kern = attn_prefill_pair_kernel<DT, MASK, PAIR_TQ, PAIR_DEPTH>;
+    constexpr size_t lds = (size_t)(PAIR_DEPTH + 1) * 2 * 64 * HD * 2;  // K and V of D + 1 key blocks
+    raise_lds(kern, lds);
+    hipLaunchKernelGGL(kern, dim3(pairs, a.nkv), dim3(256), lds, st, a);
+    return hipGetLastError();
+  }
   int hpw = grp % 2 == 0 && nqb * (grp / 2) * a.nkv >= 1024 ? 2 : 1;
   const int ph = a.prefill_hpw;
   if ((ph == 1 || ph == 2 || ph == 3 || ph == 6) && grp % ph == 0) hpw = ph;

@@ -974,4 +974,239 @@ __global__ __launch_bounds__(64 * NWQ) void attn_prefill_kernel(AttnP a, int hpw
   }
 }
 
+// attn_prefill_pair_kernel: the long-prefill form of attn_prefill_kernel.  Workgroup (p, g) owns kv head
+// g and the pair of 32-row query blocks nqb - 1 - p and p: under the block-causal mask their key ranges
+// add up to the same number of 64-key blocks for every pair, so with one workgroup per compute unit all
+// finish together (one block per workgroup, as in attn_prefill_kernel, leaves the longest query block
+// alone on its compute unit at the end).  All grp heads of the kv head are in the workgroup (2 grp query
+// tiles, TQ per wave), so each K/V block fetched serves all of them, and a wave reads each K or V
+// fragment from LDS once for its TQ tiles.  Per query the key blocks, their order and every rounding are
+// those of attn_prefill_kernel, so the results are the same bits.
+//
+// The work is a list of tasks t = (query block, key block): the first block's key blocks, then the
+// second's.  Task t's K and V rows go from global memory straight into LDS buffer t % R (R = D + 1) by
+// the gfx950 global-to-LDS copy, D tasks ahead, so no registers hold data in flight and no VALU work
+// stages it.  Both are stored row-major (a 256-byte row per key) with the 16-byte chunk c of row r at
+// slot c ^ (r % 16): the copy's lanes fetch their chunks in that order, the K fragment reads (16 rows,
+// one chunk each) then hit 16 different slots, and so do the V reads.  V^T fragments come from the
+// transposing LDS read (ds_read_b64_tr_b16): within each 16-lane group, lane q supplies 4 dims of one
+// key (key q / 4, dims 4 (q % 4) ..) and lane m receives dim m of the 4 keys, which is the A operand of
+// O^T = V^T P^T for keys 4 lg .. 4 lg + 3 (and, from a second read, 16 + 4 lg ..): the k-slot order the
+// scores already have in registers.
+template <int DT, int MASK, int TQ, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void attn_prefill_pair_kernel(AttnP a) {
+  constexpr int NWQ = 4, R = D + 1;
+  constexpr int KBP = 64;               // keys per block (task)
+  constexpr int BUFE = 2 * KBP * HD;    // u16 per buffer: K rows, then V rows
+  constexpr int CPW = KBP * HD * 2 / 1024 / NWQ;  // 1 KB copies of K (and of V) per wave per task
+  static_assert(MASK == 0 || MASK == 1, "explicit biases take attn_kernel");
+  static_assert(D >= 1 && (D - 1) * 2 * CPW < 64, "outstanding copies fit the memory counter");
+  constexpr int DT16 = HD / 16;
+  extern __shared__ __align__(16) unsigned char smem[];
+  u16* const lds16 = reinterpret_cast<u16*>(smem);
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int grp = a.nq / a.nkv;  // = NWQ TQ / 2 (the launcher checks)
+  const int nqb = (a.rows + 31) / 32;
+  const int p = blockIdx.x, g = blockIdx.y;
+  const int qA = nqb - 1 - p, qB = p;  // qA == qB: the middle block of an odd count, alone
+  const int rlast = a.rows - 1;
+  const size_t krow = (size_t)a.nkv * HD;
+  const u16* kc = a.kc + g * HD;
+  const u16* vc = a.vc + g * HD;
+  const float c2 = a.scale * LOG2E;
+
+  auto kend_of = [&](int r) {
+    if constexpr (MASK == 1) return min(a.Lk, ((a.q_pos0 + r) / a.block + 1) * a.block);
+    return a.Lk;
+  };
+  auto kend_blk = [&](int qb) { return kend_of(min(qb * 32 + 31, rlast)); };
+  const int keA = kend_blk(qA), keB = kend_blk(qB);
+  const int nA = (keA + KBP - 1) / KBP;
+  const int T = nA + (qA == qB ? 0 : (keB + KBP - 1) / KBP);
+
+  // ---- copies of task t (tasks past the last re-read the last) into buffer t % R: this wave's 1 KB
+  // blocks d = w CPW .. + CPW - 1 of K and of V, 4 rows each; lane l fills row 4 d + l / 16, slot l % 16
+  // with chunk (l % 16) ^ (row % 16) ----
+  auto issue = [&](int t) __attribute__((always_inline)) {
+    const int tt = min(t, T - 1);
+    const int k0 = (tt < nA ? tt : tt - nA) * KBP, kend = tt < nA ? keA : keB;
+    unsigned char* buf = smem + (size_t)(t % R) * BUFE * 2;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      const int d = w * CPW + c, row = 4 * d + (lane >> 4);
+      const int chunk = (lane & 15) ^ (row & 15);
+      const size_t src = (size_t)min(k0 + row, kend - 1) * krow + 8 * chunk;
+      lds_copy16(kc + src, buf + (size_t)d * 1024);
+      lds_copy16(vc + src, buf + (size_t)KBP * HD * 2 + (size_t)d * 1024);
+    }
+  };
+
+  // ---- the wave's query tiles of the current query block: tile w TQ + i = head (w TQ + i) / 2, rows
+  // q0 + 16 ((w TQ + i) % 2) + lr ----
+  u32x4 qf[TQ][4];
+  int kend_q[TQ];
+  int kend_min = 0;  // the block's first row's key bound, the smallest of its rows
+  float m_run[TQ], l_run[TQ];
+  f32x4 o[TQ][DT16];
+  auto begin_block = [&](int qb) __attribute__((always_inline)) {
+    const int q0 = qb * 32;
+    kend_min = kend_of(q0);
+#pragma unroll
+    for (int i = 0; i < TQ; ++i) {
+      const int t = w * TQ + i, hh = t / 2;
+      const int r = min(q0 + 16 * (t % 2) + lr, rlast);
+      kend_q[i] = kend_of(r);
+      const u16* qp = a.out + (size_t)r * a.nq * HD + (g * grp + hh) * HD + 8 * lg;
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds) qf[i][ds] = *reinterpret_cast<const u32x4*>(qp + 32 * ds);
+      m_run[i] = -INFINITY;
+      l_run[i] = 0.f;
+#pragma unroll
+      for (int dt = 0; dt < DT16; ++dt) o[i][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  auto end_block = [&](int qb) __attribute__((always_inline)) {
+    const int q0 = qb * 32;
+#pragma unroll
+    for (int i = 0; i < TQ; ++i) {
+      const int t = w * TQ + i, hh = t / 2;
+      const int r = q0 + 16 * (t % 2) + lr;
+      if (r > rlast) continue;
+      const float inv = 1.0f / l_run[i];
+      u16* dst = a.out + (size_t)r * a.nq * HD + (g * grp + hh) * HD + 4 * lg;
+#pragma unroll
+      for (int dt = 0; dt < DT16; ++dt)
+        *reinterpret_cast<u32x2*>(dst + 16 * dt) =
+            u32x2{pack_f32x2<DT>(o[i][dt][0] * inv, o[i][dt][1] * inv), pack_f32x2<DT>(o[i][dt][2] * inv, o[i][dt][3] * inv)};
+    }
+  };
+
+  // ---- one key block of task t against the wave's TQ tiles ----
+  auto compute = [&](int t) __attribute__((always_inline)) {
+    const u16* kbuf = lds16 + (size_t)(t % R) * BUFE;
+    const u16* vbuf = kbuf + KBP * HD;
+    const int k0 = (t < nA ? t : t - nA) * KBP;
+    // S^T = K Q^T: lane holds S^T[key k0 + 16 kt + 4 lg + e][query lr]; K row 16 kt + lr, chunk lg + 4 ds
+    f32x4 s[TQ][4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+      for (int i = 0; i < TQ; ++i) s[i][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const u16* kp = kbuf + (16 * kt + lr) * HD;
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds) {
+        const u32x4 kf = *reinterpret_cast<const u32x4*>(kp + 8 * ((lg + 4 * ds) ^ lr));
+#pragma unroll
+        for (int i = 0; i < TQ; ++i) s[i][kt] = mfma16<DT>(kf, qf[i][ds], s[i][kt]);
+      }
+    }
+    u32x4 pb[TQ][2];
+    const bool whole = k0 + KBP <= kend_min;  // no key of the block is masked for any query of the block
+#pragma unroll
+    for (int i = 0; i < TQ; ++i) {
+      float mx = -INFINITY;
+      if (whole) {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            s[i][kt][e] *= c2;
+            mx = fmaxf(mx, s[i][kt][e]);
+          }
+      } else {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int key = k0 + 16 * kt + 4 * lg + e;
+            const float v = key < kend_q[i] ? s[i][kt][e] * c2 : -INFINITY;
+            s[i][kt][e] = v;
+            mx = fmaxf(mx, v);
+          }
+      }
+      mx = rows_max(mx);
+      const float m_new = fmaxf(m_run[i], mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run[i] - m_use);
+      float ps = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float pe = __builtin_amdgcn_exp2f(s[i][kt][e] - m_use);
+          s[i][kt][e] = pe;
+          ps += pe;
+        }
+      ps = rows_sum(ps);
+      l_run[i] = l_run[i] * alpha + ps;
+      m_run[i] = m_new;
+      // rescale only when some query's running maximum moved (alpha = 1 leaves o unchanged bit for bit);
+      // past the first blocks it rarely does, and o can stay in the accumulation registers
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+        for (int dt = 0; dt < DT16; ++dt) o[i][dt] *= alpha;
+      }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        pb[i][ks] = u32x4{pack_f32x2<DT>(s[i][2 * ks][0], s[i][2 * ks][1]),
+                          pack_f32x2<DT>(s[i][2 * ks][2], s[i][2 * ks][3]),
+                          pack_f32x2<DT>(s[i][2 * ks + 1][0], s[i][2 * ks + 1][1]),
+                          pack_f32x2<DT>(s[i][2 * ks + 1][2], s[i][2 * ks + 1][3])};
+    }
+    // O^T += V^T P^T over the block's two 32-key k steps.  Transposing reads: this lane supplies key
+    // 32 ks + 4 lg + lr / 4 (+ 16 for the second half), dims 16 dt + 4 (lr % 4) .. + 3
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int dt = 0; dt < DT16; ++dt) {
+        u32x2 half[2];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const int row = 32 * ks + 16 * hf + 4 * lg + (lr >> 2);
+          const int dim = 16 * dt + 4 * (lr & 3);
+          const u16* vp = vbuf + row * HD + 8 * ((dim >> 3) ^ (row & 15)) + (dim & 7);
+          const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)vp);
+          half[hf] = __builtin_bit_cast(u32x2, r);
+        }
+        const u32x4 vf = u32x4{half[0][0], half[0][1], half[1][0], half[1][1]};
+#pragma unroll
+        for (int i = 0; i < TQ; ++i) o[i][dt] = mfma16<DT>(vf, pb[i][ks], o[i][dt]);
+      }
+  };
+
+  // ---- task t: wait for its copies, free buffer (t - 1) % R, issue task t + D into it, compute.
+  // EXACT: the D - 1 tasks issued after task t each issued 2 CPW copies per wave, so a count wait is
+  // exact (loads and stores of queries and outputs issued in between only make it wait longer); the last
+  // T % D tasks, after the loop, wait for everything ----
+  auto iter = [&](int t, auto exact) __attribute__((always_inline)) {
+    if constexpr (decltype(exact)::value) wait_vmcnt<(D - 1) * 2 * CPW>();
+    else wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();  // every wave's copies of task t have landed; buffer (t - 1) % R is free
+    __builtin_amdgcn_sched_barrier(0);
+    issue(t + D);
+    __builtin_amdgcn_sched_barrier(0);
+    if (t == nA) begin_block(qB);
+    compute(t);
+    if (t == nA - 1) end_block(qA);
+    else if (t == T - 1) end_block(qB);
+  };
+
+#pragma unroll
+  for (int t = 0; t < D; ++t) issue(t);
+  begin_block(qA);
+  int t0 = 0;
+#pragma nounroll
+  for (; t0 + D <= T; t0 += D)
+    static_for<0, D>([&](auto uc) __attribute__((always_inline)) { iter(t0 + decltype(uc)::value, std::true_type{}); });
+  static_for<0, D - 1>([&](auto uc) __attribute__((always_inline)) {
+    if (t0 + decltype(uc)::value < T) iter(t0 + decltype(uc)::value, std::false_type{});
+  });
+  wait_vmcnt<0>();  // no copy may still be writing LDS when the workgroup ends
+}
+
 }  // namespace fdllm

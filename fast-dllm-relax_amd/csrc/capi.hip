@@ -97,6 +97,7 @@ struct fdllm_ctx {
   float* rope = nullptr; size_t rope_floats = 0;  // RoPE (cos, sin) table of the current call's rows
   int attn_target = 64;   // attention workgroups aimed for when splitting the keys
   int prefill_hpw = 0;    // query heads per prefill-attention workgroup (0: chosen per launch)
+  int prefill_pair = 1;   // paired-query-block prefill attention (0 off, 1 when it fills the chip, 2 always)
   int down_split = 10;    // cross-workgroup k splits of the down projection (largest divisor of K/32 <= this)
   MmPolicy mm;              // large-M GEMM planning (k splits, register-weight kernel)
   bool frag_on = true;      // one-shot chains keep activations in MFMA-fragment order (FDLLM_XFRAG=0: row-major)
@@ -276,7 +277,7 @@ int run_attention(fdllm_ctx* c, int rows, uint16_t* kc, uint16_t* vc, int ws, in
   const AttnPlan pl = attn_plan(a.rows, a.nq, a.nkv, a.Lk, target);
   if (sb != nullptr && !pl.chunked)
     return fail(FDLLM_EINVAL, "batched call of %d rows per sequence over %d keys is too long for one step", a.rows, a.Lk);
-  a.S = pl.S; a.chunk = pl.chunk; a.target_wgs = target; a.prefill_hpw = c->prefill_hpw;
+  a.S = pl.S; a.chunk = pl.chunk; a.target_wgs = target; a.prefill_hpw = c->prefill_hpw; a.prefill_pair = c->prefill_pair;
   if (a.S > 1) {
     int rc = ensure_floats(&c->apart, &c->apart_floats, attn_partial_floats(a));
     if (rc) return rc;
@@ -583,6 +584,7 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   (void)hipGetDevice(&c->dev);
   if (const char* e = std::getenv("FDLLM_ATTN_TARGET")) c->attn_target = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_PREFILL_HPW")) c->prefill_hpw = std::max(0, atoi(e));
+  if (const char* e = std::getenv("FDLLM_PREFILL_PAIR")) c->prefill_pair = std::min(2, std::max(0, atoi(e)));
   if (const char* e = std::getenv("FDLLM_DOWN_SPLIT")) c->down_split = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_MM_TARGET_WGS")) c->mm.target_wgs = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_MM_MIN_STAGES")) c->mm.min_stages = std::max(1, atoi(e));

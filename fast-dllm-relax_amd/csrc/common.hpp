@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace fdllm {
 
 typedef uint16_t u16;
@@ -41,6 +43,18 @@ template <int DT> __device__ __forceinline__ float to_f32(u16 h) {
 }
 template <int DT> __device__ __forceinline__ u16 from_f32(float f) {
   if constexpr (DT == DT_BF16) return f32_to_bf16(f); else return f32_to_f16(f);
+}
+// two values rounded to the model dtype and packed (a in the low half), the same bits as two from_f32
+// calls: bf16 by one v_cvt_pk_bf16_f32; fp16 by two scalar conversions (the packed fp16 conversion
+// measured different on results that fall in the fp16 subnormal range)
+template <int DT> __device__ __forceinline__ uint32_t pack_f32x2(float a, float b) {
+  if constexpr (DT == DT_BF16) {
+    typedef float f32x2v __attribute__((ext_vector_type(2)));
+    typedef __bf16 b16x2v __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v{a, b}), b16x2v));
+  } else {
+    return (uint32_t)f32_to_f16(a) | ((uint32_t)f32_to_f16(b) << 16);
+  }
 }
 // value rounded to the model dtype, kept in fp32
 template <int DT> __device__ __forceinline__ float rnd(float f) { return to_f32<DT>(from_f32<DT>(f)); }
@@ -248,6 +262,16 @@ __device__ __forceinline__ size_t frag_off(int r, int c) {
 // per row.  Element (r, c):
 __device__ __forceinline__ size_t frag_blk_off(int r, int c, int KS) {
   return ((size_t)(r >> 4) * KS + (c >> 5)) * 512 + (size_t)((r & 15) + 16 * ((c >> 3) & 3)) * 8 + (c & 7);
+}
+
+// f(integral_constant<int, I>) for I = B .. E - 1, unrolled at compile time (register arrays indexed by
+// I stay in registers)
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
 }
 
 // ---- LDS helpers ---------------------------------------------------------------------------------

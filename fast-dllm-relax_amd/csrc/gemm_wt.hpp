@@ -22,8 +22,6 @@
 #pragma once
 #include "gemm_mm.hpp"
 
-#include <type_traits>
-
 namespace fdllm {
 
 template <int DT, int EPI, int MF, int TPW, int WM, int WN, int NBUF>
@@ -160,19 +158,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_wt_kernel(GemmP a, int nbm,
 //
 // Pipeline: D stages in flight.  Stage st uses LDS buffer st % R and weight register set st % R
 // (R = D + 1), so the copies for stage st + D, issued right after the barrier of stage st, go into the
-// buffer and register set that stage st - 1 used.  Each stage issues exactly VPS = TPW + MF / 4 vector
-// memory instructions per wave (stages past the last re-read the last), weights first, and the issue is
-// fenced against compiler motion, so "all but the (D - 1) VPS most recent" is exactly "stage st has
-// landed".  The k loop is unrolled by R so that the register sets are named at compile time.
-// f(integral_constant<int, I>) for I = B .. E - 1, unrolled at compile time
-template <int B, int E, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (B < E) {
-    f(std::integral_constant<int, B>{});
-    static_for<B + 1, E>(f);
-  }
-}
-
+// buffer and register set that stage st - 1 used.  In the k loop (unrolled by R so that the register sets
+// are named at compile time) each stage issues exactly VPS = TPW + MF / 4 vector memory instructions per
+// wave (stages past the last re-read the last), weights first, and the issue is fenced against compiler
+// motion, so "all but the (D - 1) VPS most recent" is exactly "stage st has landed"; the last nst % R
+// stages, after the loop, wait for all.
 template <int DT, int EPI, int MF, int TPW, int D>
 // (up to 32 accumulator tiles per wave, two workgroups per compute unit: at most 256 registers per lane,
 // accumulators included; more tiles, one workgroup)
@@ -242,11 +232,16 @@ void gemm_wr_kernel(GemmP a, int nbm, int nbn) {
 #pragma unroll
   for (int u = 0; u < D; ++u) issue(u, wv[u], u);
 
-  // stage st = st0 + u with u = st % R known at compile time
+  // stage st = st0 + u with u = st % R known at compile time.  EXACT: the D - 1 stages issued after stage
+  // st each issued VPS instructions, so the count wait is exact.  The last nst % R stages (after the loop)
+  // wait for everything instead: there the compiler drops the weight loads of stages past the last, whose
+  // registers are never read, so fewer than VPS instructions per stage follow and a count wait would
+  // return before stage st's copies landed.
   const u32x4* lds = reinterpret_cast<const u32x4*>(smem);
-  auto stage = [&](int st, auto uc) {
+  auto stage = [&](int st, auto uc, auto exact) {
     constexpr int u = decltype(uc)::value;
-    wait_vmcnt<(D - 1) * VPS>();     // this wave's copies and weights of stage st have landed
+    if constexpr (decltype(exact)::value) wait_vmcnt<(D - 1) * VPS>();  // stage st's copies and weights
+    else wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();    // every wave's copies have; buffer (u - 1) % R is free
     issue(st + D, wv[(u + D) % R], (u + D) % R);
     const u32x4* blk = lds + (size_t)u * MF * 64;
@@ -262,9 +257,10 @@ void gemm_wr_kernel(GemmP a, int nbm, int nbn) {
   // unrolled round would make the compiler's own counter bookkeeping wait for everything at its top)
   int st0 = 0;
 #pragma nounroll
-  for (; st0 + R <= nst; st0 += R) static_for<0, R>([&](auto uc) { stage(st0 + decltype(uc)::value, uc); });
+  for (; st0 + R <= nst; st0 += R)
+    static_for<0, R>([&](auto uc) { stage(st0 + decltype(uc)::value, uc, std::true_type{}); });
   static_for<0, R - 1>([&](auto uc) {
-    if (st0 + decltype(uc)::value < nst) stage(st0 + decltype(uc)::value, uc);
+    if (st0 + decltype(uc)::value < nst) stage(st0 + decltype(uc)::value, uc, std::false_type{});
   });
   wait_vmcnt<0>();  // no copy may still be writing LDS when the workgroup ends
 
