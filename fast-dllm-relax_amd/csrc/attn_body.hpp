@@ -1062,10 +1062,10 @@ void attn_prefill_pair_kernel(AttnP a) {
       const u16* qp = a.out + (size_t)r * a.nq * HD + (g * grp + hh) * HD + 8 * lg;
 #pragma unroll
       for (int ds = 0; ds < 4; ++ds) qf[i][ds] = *reinterpret_cast<const u32x4*>(qp + 32 * ds);
+      // o is not cleared here: with m_run = -inf the block's first key block rescales it by
+      // alpha = 2^-inf = 0 (o is always finite, and -0 + x = x)
       m_run[i] = -INFINITY;
       l_run[i] = 0.f;
-#pragma unroll
-      for (int dt = 0; dt < DT16; ++dt) o[i][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   };
   auto end_block = [&](int qb) __attribute__((always_inline)) {
@@ -1198,6 +1198,10 @@ void attn_prefill_pair_kernel(AttnP a) {
 
 #pragma unroll
   for (int t = 0; t < D; ++t) issue(t);
+#pragma unroll
+  for (int i = 0; i < TQ; ++i)
+#pragma unroll
+    for (int dt = 0; dt < DT16; ++dt) o[i][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   begin_block(qA);
   int t0 = 0;
 #pragma nounroll
