@@ -434,7 +434,8 @@ def batched_bench(args) -> dict:
     tf_part = f_part / (part_ms * 1e-3) / 1e12
     res = {
         "workload": f"BASELINE config 4: 1.5B fp16, seed 3, {BATCH_SEQS} sequences, prefixes U[128, 1024], one "
-                    f"32-token masked block each, sub-blocks of 8, threshold 0.9, untied lm_head N(0, 0.5)",
+                    f"32-token block each starting at the prefix rounded down to 32 (the prompt's tail + masks), "
+                    f"sub-blocks of 8, threshold 0.9, untied lm_head N(0, 0.5) (BASELINE.json: tied head)",
         "prefixes": prefixes,
         "tokens_per_s": round(unmasked / refine_s, 2), "tokens": unmasked, "refine_s": round(refine_s, 4),
         "steps": steps, "partial_steps": partial_steps,
