@@ -588,7 +588,7 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   if (const char* e = std::getenv("FDLLM_DOWN_SPLIT")) c->down_split = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_MM_TARGET_WGS")) c->mm.target_wgs = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_MM_MIN_STAGES")) c->mm.min_stages = std::max(1, atoi(e));
-  if (const char* e = std::getenv("FDLLM_WR_OPS")) c->mm.wr_ops = atoi(e) & 15;
+  if (const char* e = std::getenv("FDLLM_WR_OPS")) c->mm.wr_ops = atoi(e) & 31;
   if (const char* e = std::getenv("FDLLM_WR_MIN_ROWS")) c->mm.wr_min_rows = std::max(0, atoi(e));
   if (const char* e = std::getenv("FDLLM_PERSISTENT")) c->step_on = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_XFRAG")) c->frag_on = atoi(e) != 0;

@@ -141,6 +141,10 @@ GemmShape gemm_shape(int cfg) {
   return GemmShape{l, 0};
 }
 
+// rows from which the lm_head (with its confidence statistics) takes the register-weight kernel
+#ifndef FD_WR_LM_MIN_ROWS
+#define FD_WR_LM_MIN_ROWS 512
+#endif
 // stages in flight of the register-weight kernel
 #ifndef FD_WR_DEPTH
 #define FD_WR_DEPTH 3
@@ -167,6 +171,7 @@ struct WrCfg {
   static constexpr int mf = MF, tpw = TPW, d = D;
   static constexpr int bm = 16 * MF, bn_tiles = 4 * TPW, kss = 1;
   static constexpr size_t lds = (size_t)(D + 1) * MF * 1024;
+  static constexpr size_t lds_logits = (size_t)16 * MF * 256 * 2;  // the lm_head's [BM][256] logit tile
 };
 using WrBig = WrCfg<8, 4, FD_WR_DEPTH>;  // 128 x 256
 enum MmId : int { MM_SMALL = 0, MM_WIDE = 1, MM_WIDE_D = 2, MM_BIG = 3, MM_WT = 4, MM_WR = 5 };
@@ -186,10 +191,13 @@ static MmInfo mm_info(int id) {
 // launch, register-weight / previous kernel): gate_up 53 / 47 at 512 rows, 110 / 118 at 2048, 377 / 448
 // at 8192; down 40 / 30, 79 / 80, 189 / 192; qkv 37 / 31 at 2048, 75 / 106 at 8192; o_proj 38 / 23,
 // 57 / 70.  Below these sizes its 128 x 256 blocks leave too few workgroups without a k split.
-static int wr_default_min_rows(int cfg) { return cfg == CFG_GATE_UP || cfg == CFG_DOWN ? 2048 : 4096; }
+static int wr_default_min_rows(int cfg) {
+  if (cfg == CFG_LM_HEAD) return FD_WR_LM_MIN_ROWS;
+  return cfg == CFG_GATE_UP || cfg == CFG_DOWN ? 2048 : 4096;
+}
 static int mm_choice(int cfg, int M, int ntiles, const MmPolicy& pol) {
   const int min_rows = pol.wr_min_rows > 0 ? pol.wr_min_rows : wr_default_min_rows(cfg);
-  if (cfg != CFG_LM_HEAD && M >= std::max(min_rows, 33) && ((pol.wr_ops >> cfg) & 1)) return MM_WR;
+  if (M >= std::max(min_rows, 33) && ((pol.wr_ops >> cfg) & 1)) return MM_WR;
   switch (cfg) {
     case CFG_LM_HEAD: return MM_WIDE;  // one 256-column confidence tile per block column
     case CFG_GATE_UP:
@@ -289,10 +297,11 @@ static hipError_t launch_os(const GemmP& a, const GemmPlan& p, hipStream_t st) {
 
 template <int DT, int EPI, class W>
 static hipError_t launch_wr_cfg(const GemmP& a, const GemmPlan& p, hipStream_t st) {
-  static_assert(W::lds <= 64 * 1024, "no LDS attribute needed");
+  constexpr size_t lds = EPI == EPI_LOGITS ? std::max(W::lds, W::lds_logits) : W::lds;
+  static_assert(lds <= 64 * 1024, "no LDS attribute needed");
   auto kern = gemm_wr_kernel<DT, EPI, W::mf, W::tpw, W::d>;
   const int total = p.nbm * p.nbn, per = (total + 7) / 8;
-  hipLaunchKernelGGL(kern, dim3(8 * per, p.ksplit), dim3(256), W::lds, st, a, p.nbm, p.nbn);
+  hipLaunchKernelGGL(kern, dim3(8 * per, p.ksplit), dim3(256), lds, st, a, p.nbm, p.nbn);
   if (p.ksplit > 1) {
     const int nblk = (a.M + 15) / 16;
     hipLaunchKernelGGL((gemm_mm_split_epilogue_kernel<DT, EPI>), dim3((a.N + 15) / 16, (nblk + 3) / 4), dim3(256), 0,
@@ -338,9 +347,7 @@ static hipError_t launch_wt_cfg(const GemmP& a, const GemmPlan& p, hipStream_t s
 // GK_MM rows arrive normalised (see GemmKind), so every large-M launch runs without the norm transform.
 template <int DT, int CFG, class C>
 static hipError_t launch_mm(const GemmP& a, const GemmPlan& p, hipStream_t st) {
-  if constexpr (CFG != CFG_LM_HEAD) {
-    if (p.mm_id == MM_WR) return launch_wr_cfg<DT, C::epi, WrBig>(a, p, st);
-  }
+  if (p.mm_id == MM_WR) return launch_wr_cfg<DT, C::epi, WrBig>(a, p, st);
   if constexpr (CFG == CFG_GATE_UP) {
     if (p.mm_id == MM_WT) return launch_wt_cfg<DT, C::epi, WtBig>(a, p, st);
     if (p.mm_id == MM_BIG) return launch_mm_cfg<DT, C::epi, XF_NONE, MmBig>(a, p, st);

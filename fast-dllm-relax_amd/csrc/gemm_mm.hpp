@@ -25,6 +25,51 @@
 
 namespace fdllm {
 
+// Confidence statistics of one block's 256-column logit tile, held in LDS as [BM][256] model-dtype
+// values: one wave per row (rows w, w + NW, ...) reduces the row's columns to (max, first argmax, sum of
+// exp(x - max)) with the streaming kernel's lane order and butterflies, so every kernel that produces
+// the tile gives identical bits.
+template <int DT, int BM, int NW>
+__device__ __forceinline__ void logits_tile_stats(const GemmP& a, const u16* tile, int m0, int nb, int w, int lane) {
+  const int n0 = nb * 256;
+  for (int ml = w; ml < BM; ml += NW) {
+    if (m0 + ml >= a.M) break;
+    const u16* row = tile + ml * 256;
+    float vmax = -INFINITY;
+    int amax = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = lane + 64 * i;
+      if (n0 + c < a.N) {
+        const float x = to_f32<DT>(row[c]);
+        if (x > vmax) { vmax = x; amax = n0 + c; }
+      }
+    }
+    for (int k = 32; k >= 1; k >>= 1) {
+      const float ov = __shfl_xor(vmax, k, WAVE);
+      const int oa = __shfl_xor(amax, k, WAVE);
+      if (ov > vmax || (ov == vmax && oa < amax)) { vmax = ov; amax = oa; }
+    }
+    float sum;
+    {
+#pragma clang fp contract(off)
+      sum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = lane + 64 * i;
+        if (n0 + c < a.N) sum = sum + fd_exp_neg(to_f32<DT>(row[c]) - vmax);
+      }
+      for (int k = 32; k >= 1; k >>= 1) sum = sum + __shfl_xor(sum, k, WAVE);
+    }
+    if (lane == 0) {
+      const size_t o = (size_t)(m0 + ml) * a.stat_tiles + nb;
+      a.stat_m[o] = vmax;
+      a.stat_a[o] = amax;
+      a.stat_s[o] = sum;
+    }
+  }
+}
+
 template <int DT, int EPI, int XF, int MF, int TPW, int NWM, int NWN, int KSS, int WD>
 __global__ __launch_bounds__(64 * NWM * NWN) void gemm_mm_kernel(GemmP a, int nbm, int nbn) {
   constexpr int NW = NWM * NWN;
@@ -186,42 +231,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void gemm_mm_kernel(GemmP a, int nb
       }
     if (a.stat_m == nullptr) return;
     __syncthreads();
-    for (int ml = w; ml < BM; ml += NW) {
-      if (m0 + ml >= a.M) break;
-      const u16* row = tile + ml * 256;
-      float vmax = -INFINITY;
-      int amax = 0x7fffffff;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int c = lane + 64 * i;
-        if (n0 + c < a.N) {
-          const float x = to_f32<DT>(row[c]);
-          if (x > vmax) { vmax = x; amax = n0 + c; }
-        }
-      }
-      for (int k = 32; k >= 1; k >>= 1) {
-        const float ov = __shfl_xor(vmax, k, WAVE);
-        const int oa = __shfl_xor(amax, k, WAVE);
-        if (ov > vmax || (ov == vmax && oa < amax)) { vmax = ov; amax = oa; }
-      }
-      float sum;
-      {
-#pragma clang fp contract(off)
-        sum = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int c = lane + 64 * i;
-          if (n0 + c < a.N) sum = sum + fd_exp_neg(to_f32<DT>(row[c]) - vmax);
-        }
-        for (int k = 32; k >= 1; k >>= 1) sum = sum + __shfl_xor(sum, k, WAVE);
-      }
-      if (lane == 0) {
-        const size_t o = (size_t)(m0 + ml) * a.stat_tiles + nb;
-        a.stat_m[o] = vmax;
-        a.stat_a[o] = amax;
-        a.stat_s[o] = sum;
-      }
-    }
+    logits_tile_stats<DT, BM, NW>(a, tile, m0, nb, w, lane);
   } else if constexpr (EPI == EPI_SILU_PAIR) {
 #pragma unroll
     for (int p = 0; p < TPW / 2; ++p)

@@ -174,8 +174,8 @@ void gemm_wr_kernel(GemmP a, int nbm, int nbn) {
   static_assert(MF % NW == 0, "every wave copies the same number of activation blocks");
   static_assert(D >= 1 && (D - 1) * VPS < 64, "outstanding copies fit the memory counter");
   static_assert(EPI != EPI_SILU_PAIR || TPW % 2 == 0, "gate/up pairs stay within a wave");
-  static_assert(EPI != EPI_LOGITS, "the lm_head takes the streaming kernel");
-  extern __shared__ __align__(16) unsigned char smem[];  // [R][MF][1 KB]
+  static_assert(EPI != EPI_LOGITS || NW * TPW == 16, "one 256-column confidence tile per block column");
+  extern __shared__ __align__(16) unsigned char smem[];  // [R][MF][1 KB]; EPI_LOGITS: then [16 MF][256] u16
 
   const int total = nbm * nbn;
   const int per = (total + 7) / 8;
@@ -276,7 +276,37 @@ void gemm_wr_kernel(GemmP a, int nbm, int nbn) {
       }
     return;
   }
-  if constexpr (EPI == EPI_SILU_PAIR) {
+  if constexpr (EPI == EPI_LOGITS) {
+    // the lm_head: the block's logits rounded to the model dtype (cuda.py:708-711) into an LDS tile
+    // (and the optional fp32 output), then the confidence statistics of its 256 columns, exactly as
+    // gemm_mm_kernel does
+    __syncthreads();  // every wave is done with the stage buffers the tile overwrites
+    u16* tile = reinterpret_cast<u16*>(smem);
+    const int n0 = nb * 256;
+#pragma unroll
+    for (int j = 0; j < TPW; ++j)
+#pragma unroll
+      for (int f = 0; f < MF; ++f) {
+        const int ml = 16 * f + lr, nl = 16 * (w * TPW + j) + 4 * lg, n = n0 + nl, m = m0 + ml;
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = rnd<DT>(acc[j][f][i]);
+        *reinterpret_cast<u32x2*>(tile + ml * 256 + nl) = u32x2{pack_f32x2<DT>(v[0], v[1]), pack_f32x2<DT>(v[2], v[3])};
+        if (a.logits != nullptr && m < a.M) {
+          float* dst = a.logits + (size_t)m * a.ldl + n;
+          if (n + 3 < a.N) {
+            *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (n + i < a.N) dst[i] = v[i];
+          }
+        }
+      }
+    if (a.stat_m == nullptr) return;
+    __syncthreads();
+    logits_tile_stats<DT, 16 * MF, NW>(a, tile, m0, nb, w, lane);
+  } else if constexpr (EPI == EPI_SILU_PAIR) {
 #pragma unroll
     for (int p = 0; p < TPW / 2; ++p)
 #pragma unroll

@@ -61,12 +61,12 @@ struct GemmPlan {
 // How large-M launches are planned.  target_wgs / min_stages: k is split only while the launch has fewer
 // than target_wgs workgroups, and only into splits of at least min_stages stages.  wr_ops: the
 // projections (bit cfg) that may take the register-weight kernel, from wr_min_rows rows (0: from 2048
-// rows for gate_up and down, from 4096 for qkv and o_proj, where it measured faster than the
-// LDS-staged and streaming kernels).
+// rows for gate_up and down, 4096 for qkv and o_proj, 512 for the lm_head, where it measured faster
+// than the LDS-staged and streaming kernels).
 struct MmPolicy {
   int target_wgs = 256;
   int min_stages = 8;
-  int wr_ops = (1 << CFG_QKV) | (1 << CFG_OPROJ) | (1 << CFG_GATE_UP) | (1 << CFG_DOWN);
+  int wr_ops = (1 << CFG_QKV) | (1 << CFG_OPROJ) | (1 << CFG_GATE_UP) | (1 << CFG_DOWN) | (1 << CFG_LM_HEAD);
   int wr_min_rows = 0;
 };
 GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol = MmPolicy{});

@@ -47,21 +47,47 @@ __global__ __launch_bounds__(256) void load_rows_kernel(const u16* x, int hidden
 
 // FastDLLMRMSNorm (cuda.py:269-275) from the producer's sums of squares: fp32 mean of squares,
 // x * 1/sqrt(var + eps) cast to the model dtype, then the weight multiply in the model dtype.
+// A workgroup normalises 4 rows, one per wave.  A row's sum of squares is the sum of its per-16-column
+// tile sums in a fixed order: four partial sums P_q (q = 0..3), P_q adding tiles 64 q + l + 256 j (j in
+// order) in lane l and then a butterfly over the 64 lanes, and the total (P_0 + P_1) + (P_2 + P_3).  The
+// rows then move in 16-byte units of 8 columns (consecutive threads take consecutive rows of one column
+// group): read from h (row-major, or fragment order with hfrag), written row-major or, with yblk, in the
+// large-M GEMMs' 1 KB fragment blocks.
 template <int DT>
-__global__ __launch_bounds__(256) void norm_rows_kernel(const u16* h, int hidden, const float* ssq, int ssq_ld,
-                                                        const u16* w, float eps, u16* y, int hfrag, int yblk) {
-  __shared__ float part_s[4];
-  const int r = blockIdx.x;
-  float ss = 0.f;
-  for (int t = threadIdx.x; t < hidden / 16; t += 256) ss += ssq[(size_t)t * ssq_ld + r];
-  ss = wave_sum(ss);
-  if ((threadIdx.x & 63) == 0) part_s[threadIdx.x >> 6] = ss;
+__global__ __launch_bounds__(256) void norm_rows_kernel(const u16* h, int rows, int hidden, const float* ssq,
+                                                        int ssq_ld, const u16* w, float eps, u16* y, int hfrag,
+                                                        int yblk) {
+  constexpr int RPW = 4;  // rows per workgroup
+  __shared__ float inv_s[RPW];
+  const int r0 = blockIdx.x * RPW;
+  const int ntiles = hidden / 16;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (r0 + wave < rows) {
+    const int m = r0 + wave;
+    float part[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float v = 0.f;
+      for (int t = 64 * q + lane; t < ntiles; t += 256) v += ssq[(size_t)t * ssq_ld + m];
+      part[q] = 64 * q < ntiles ? wave_sum(v) : 0.f;
+    }
+    if (lane == 0) inv_s[wave] = 1.0f / sqrtf(((part[0] + part[1]) + (part[2] + part[3])) / (float)hidden + eps);
+  }
   __syncthreads();
-  const float inv = 1.0f / sqrtf(((part_s[0] + part_s[1]) + (part_s[2] + part_s[3])) / (float)hidden + eps);
-  for (int c = threadIdx.x; c < hidden; c += 256) {
-    const u16 hv = h[hfrag ? frag_off(r, c) : (size_t)r * hidden + c];
-    y[yblk ? frag_blk_off(r, c, hidden / 32) : (size_t)r * hidden + c] =
-        from_f32<DT>(to_f32<DT>(w[c]) * rnd<DT>(to_f32<DT>(hv) * inv));
+  const int ks = hidden / 32;  // k steps (fragment blocks per 16-row block)
+  for (int u = threadIdx.x; u < RPW * (hidden / 8); u += 256) {
+    const int rl = u % RPW, c = 8 * (u / RPW);
+    const int r = r0 + rl;
+    if (r >= rows) continue;
+    const float inv = inv_s[rl];
+    const u32x4 hv = *reinterpret_cast<const u32x4*>(h + (hfrag ? frag_off(r, c) : (size_t)r * hidden + c));
+    const u32x4 wv = *reinterpret_cast<const u32x4*>(w + c);
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = pack_f32x2<DT>(lo_f32<DT>(wv[e]) * rnd<DT>(lo_f32<DT>(hv[e]) * inv),
+                            hi_f32<DT>(wv[e]) * rnd<DT>(hi_f32<DT>(hv[e]) * inv));
+    *reinterpret_cast<u32x4*>(y + (yblk ? frag_blk_off(r, c, ks) : (size_t)r * hidden + c)) = o;
   }
 }
 
@@ -108,13 +134,14 @@ hipError_t launch_rope_table(int dt, const int32_t* pos_offset, int rows, int ro
 
 hipError_t launch_norm_rows(int dt, const uint16_t* h, int rows, int hidden, const float* ssq, int ssq_ld,
                             const uint16_t* w, float eps, uint16_t* y, hipStream_t st, int hfrag, int yblk) {
-  if ((hfrag && rows > 32) || (yblk && hidden % 32)) return hipErrorInvalidValue;
+  if ((hfrag && rows > 32) || hidden % 32) return hipErrorInvalidValue;
+  const int wgs = (rows + 3) / 4;
   if (dt == DT_BF16)
-    hipLaunchKernelGGL(norm_rows_kernel<DT_BF16>, dim3(rows), dim3(256), 0, st, h, hidden, ssq, ssq_ld, w, eps, y, hfrag,
-                       yblk);
+    hipLaunchKernelGGL(norm_rows_kernel<DT_BF16>, dim3(wgs), dim3(256), 0, st, h, rows, hidden, ssq, ssq_ld, w, eps, y,
+                       hfrag, yblk);
   else
-    hipLaunchKernelGGL(norm_rows_kernel<DT_F16>, dim3(rows), dim3(256), 0, st, h, hidden, ssq, ssq_ld, w, eps, y, hfrag,
-                       yblk);
+    hipLaunchKernelGGL(norm_rows_kernel<DT_F16>, dim3(wgs), dim3(256), 0, st, h, rows, hidden, ssq, ssq_ld, w, eps, y,
+                       hfrag, yblk);
   return hipGetLastError();
 }
 

@@ -110,3 +110,43 @@ def test_prefill_pair_kernel_bit_identical(dtype, monkeypatch):
         caches[name] = (k, v, h)
     for i, what in enumerate(("k cache", "v cache", "cached-forward hidden")):
         np.testing.assert_array_equal(_bits(caches["pair"][i]), _bits(caches["old"][i]), err_msg=what)
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_lm_head_register_weight_bit_identical(dtype, monkeypatch):
+    """The lm_head with its confidence statistics on the register-weight kernel (from 512 rows by default;
+    FDLLM_WR_MIN_ROWS=128 here) against gemm_mm_kernel (FDLLM_WR_OPS without the lm_head bit): logits, ids
+    and maxp bit for bit, at ragged and whole row counts, with and without the fp32 logits output."""
+    from fast_dllm_relax_amd.config import FastDLLMConfig
+    from fast_dllm_relax_amd.params import from_numpy
+    from fast_dllm_relax_amd.vm import HipVM
+    from oracle.model import OracleConfig, random_params
+
+    kw = dict(WIDE2, tie_word_embeddings=False)
+    params = from_numpy(random_params(OracleConfig(**kw), 8, dtype, lm_head_std=0.5), FastDLLMConfig(**kw),
+                        dtype=dtype)
+    vms = {}
+    for name, ops in (("wr", 16), ("mm", 0)):
+        monkeypatch.setenv("FDLLM_WR_OPS", str(ops))
+        monkeypatch.setenv("FDLLM_WR_MIN_ROWS", "128")
+        vms[name] = HipVM(FastDLLMConfig(**kw), params, dtype=dtype, max_rows=512)
+        monkeypatch.delenv("FDLLM_WR_OPS")
+        monkeypatch.delenv("FDLLM_WR_MIN_ROWS")
+    tdt = torch.bfloat16 if dtype == "bfloat16" else torch.float16
+    g = torch.Generator(device="cuda").manual_seed(31)
+    for rows in (130, 300, 512):
+        log(f"case: lm_head + confidence, {rows} rows, 1.5B vocab, {dtype}, register-weight vs gemm_mm")
+        h = torch.randn((1, rows, kw["hidden_size"]), generator=g, device="cuda").to(tdt)
+        out = {}
+        for name, vm in vms.items():
+            logits = torch.empty((1, rows, kw["vocab_size"]), dtype=torch.float32, device="cuda")
+            ids, maxp = vm.get_confidence(h, logits)
+            ids2, maxp2 = vm.get_confidence(h)
+            torch.cuda.synchronize()
+            out[name] = (logits, ids, maxp, ids2, maxp2)
+        assert torch.isfinite(out["wr"][0]).all()
+        for i, what in enumerate(("logits", "ids", "maxp", "ids (no logits)", "maxp (no logits)")):
+            np.testing.assert_array_equal(out["wr"][i].cpu().numpy(), out["mm"][i].cpu().numpy(),
+                                          err_msg=f"{what}, rows={rows}")
+    for vm in vms.values():
+        vm.close()
