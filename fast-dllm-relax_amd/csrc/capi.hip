@@ -13,6 +13,7 @@
 
 #include "../../include/fdllm.h"
 #include "kernels.hpp"
+#include "step_status.hpp"
 
 using namespace fdllm;
 
@@ -103,7 +104,7 @@ struct fdllm_ctx {
   bool frag_on = true;      // one-shot chains keep activations in MFMA-fragment order (FDLLM_XFRAG=0: row-major)
   // the persistent cached step (step_body.hpp)
   bool step_on = false;                // FDLLM_PERSISTENT=1 turns it on (measured slower than the kernels)
-  bool step_check = false;             // FDLLM_STEP_CHECK=1: wait for every launch and check its status
+  bool step_check = false;             // wait for every persistent launch and check its status (on with FDLLM_PERSISTENT unless FDLLM_STEP_CHECK=0)
   int step_attn_target = 0;            // attention workgroups aimed for (0: attn_target)
   int step_grid = 0;                   // workgroups of the launch (compute units, at most 256)
   long long step_limit = 0;            // wall-clock ticks a barrier wait may take
@@ -358,10 +359,8 @@ int try_step(fdllm_ctx* c, int rows, uint16_t* kbase, uint16_t* vbase, size_t la
   }
   if (c->step_check) {
     HIPCHK(hipStreamSynchronize(st));
-    if (*(volatile unsigned*)c->step_status != 0u) {
-      *c->step_status = 0u;
+    if (take_step_abort(c->step_status, &c->step_on))
       return fail(FDLLM_EHIP, "persistent step aborted: a grid barrier wait timed out");
-    }
   }
   ++c->step_launches;
   *done = true;
@@ -471,17 +470,20 @@ int check_ready(const fdllm_ctx* c) {
   return FDLLM_OK;
 }
 
+// An earlier persistent launch timed out at a barrier (its outputs are wrong): report it once and run the
+// per-operator kernels from now on (step_status.hpp).
+int pending_step_abort(fdllm_ctx* c) {
+  if (take_step_abort(c->step_status, &c->step_on))
+    return fail(FDLLM_EHIP, "an earlier persistent step aborted (grid barrier timeout); its results are invalid");
+  return FDLLM_OK;
+}
+
 int cached_step(fdllm_ctx* c, const void* x, int rows, void* k, void* v, int cap, const int32_t* off,
                 int64_t prefix_len, int write_rel, int attend_rel, void* out, void* stream) {
   int rc = check_ready(c);
   if (rc) return rc;
-  if (c->step_status != nullptr && *(volatile unsigned*)c->step_status != 0u) {
-    // an earlier persistent launch timed out at a barrier (its outputs are wrong): report it once and
-    // run the per-operator kernels from now on
-    *c->step_status = 0u;
-    c->step_on = false;
-    return fail(FDLLM_EHIP, "an earlier persistent step aborted (grid barrier timeout); its results are invalid");
-  }
+  rc = pending_step_abort(c);
+  if (rc) return rc;
   if (!x || !k || !v || !off || !out) return fail(FDLLM_EINVAL, "null tensor argument");
   if (rows <= 0) return fail(FDLLM_EINVAL, "active rows must be positive, got %d", rows);
   int64_t write_start = prefix_len + write_rel, attend_len = prefix_len + attend_rel;
@@ -592,7 +594,7 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   if (const char* e = std::getenv("FDLLM_WR_MIN_ROWS")) c->mm.wr_min_rows = std::max(0, atoi(e));
   if (const char* e = std::getenv("FDLLM_PERSISTENT")) c->step_on = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_XFRAG")) c->frag_on = atoi(e) != 0;
-  if (const char* e = std::getenv("FDLLM_STEP_CHECK")) c->step_check = atoi(e) != 0;
+  c->step_check = step_check_default(c->step_on, std::getenv("FDLLM_STEP_CHECK"));
   if (const char* e = std::getenv("FDLLM_STEP_ATTN_TARGET")) c->step_attn_target = std::max(0, atoi(e));
   if (const char* e = std::getenv("FDLLM_STEP_TRACE")) c->step_trace_path = e;
   c->names.push_back("model.embed_tokens.weight");
@@ -730,6 +732,8 @@ int fdllm_forward_hidden(fdllm_ctx* c, const void* x, int S, const float* bias, 
 
 int fdllm_get_logits(fdllm_ctx* c, const void* hidden, int rows, float* logits, void* stream) {
   int rc = check_ready(c);
+  if (rc) return rc;
+  rc = pending_step_abort(c);
   if (rc) return rc;
   if (rows <= 0 || !hidden || !logits) return fail(FDLLM_EINVAL, "invalid get_logits arguments");
   return run_lm_head(c, (const uint16_t*)hidden, rows, logits, false, (hipStream_t)stream);
@@ -894,6 +898,8 @@ int fdllm_get_confidence(fdllm_ctx* c, const void* hidden, int rows, int32_t* id
                          void* stream) {
   int rc = check_ready(c);
   if (rc) return rc;
+  rc = pending_step_abort(c);
+  if (rc) return rc;
   if (rows <= 0 || !hidden || !ids || !maxp) return fail(FDLLM_EINVAL, "invalid get_confidence arguments");
   rc = ensure_stats(c, rows);
   if (rc) return rc;
@@ -934,8 +940,10 @@ static UnmaskP unmask_args(const fdllm_ctx* c, int rows, int row0, int32_t* bloc
 int fdllm_unmask(fdllm_ctx* c, const int32_t* ids, const float* maxp, int rows, int row0, int32_t* block, int s0,
                  int sub_rows, int32_t mask_id, float threshold, int32_t* report, int32_t seq, void* stream) {
   if (!c) return fail(FDLLM_EINVAL, "null context");
+  int rc = pending_step_abort(c);
+  if (rc) return rc;
   if (!ids || !maxp) return fail(FDLLM_EINVAL, "null confidence argument");
-  int rc = check_unmask(c, rows, row0, block, s0, sub_rows, threshold);
+  rc = check_unmask(c, rows, row0, block, s0, sub_rows, threshold);
   if (rc) return rc;
   HIPCHK(launch_unmask(ids, maxp, unmask_args(c, rows, row0, block, s0, sub_rows, mask_id, threshold, report, seq),
                        (hipStream_t)stream));
@@ -946,6 +954,8 @@ int fdllm_get_confidence_unmask(fdllm_ctx* c, const void* hidden, int rows, int 
                                 int sub_rows, int32_t mask_id, float threshold, int32_t* ids, float* maxp,
                                 int32_t* report, int32_t seq, void* stream) {
   int rc = check_ready(c);
+  if (rc) return rc;
+  rc = pending_step_abort(c);
   if (rc) return rc;
   if (!hidden) return fail(FDLLM_EINVAL, "null hidden states");
   if ((ids == nullptr) != (maxp == nullptr)) return fail(FDLLM_EINVAL, "ids and maxp must both be given or both be null");

@@ -45,15 +45,21 @@ template <int DT> __device__ __forceinline__ u16 from_f32(float f) {
   if constexpr (DT == DT_BF16) return f32_to_bf16(f); else return f32_to_f16(f);
 }
 // two values rounded to the model dtype and packed (a in the low half), the same bits as two from_f32
-// calls: bf16 by one v_cvt_pk_bf16_f32; fp16 by two scalar conversions (the packed fp16 conversion
-// measured different on results that fall in the fp16 subnormal range)
+// calls: bf16 by one v_cvt_pk_bf16_f32; fp16 by two scalar conversions, each behind an empty asm.  The
+// conversions themselves agree bit for bit (packed or not), but an fp16 rounding of a product compiles
+// either to an fp32 multiply and a conversion (two roundings) or to one mixed-precision fma
+// (v_fma_mixlo_f16, one rounding); keeping the two values apart keeps the compiler's choice the same as
+// for a lone from_f32, which is what the other kernels compile to
 template <int DT> __device__ __forceinline__ uint32_t pack_f32x2(float a, float b) {
   if constexpr (DT == DT_BF16) {
     typedef float f32x2v __attribute__((ext_vector_type(2)));
     typedef __bf16 b16x2v __attribute__((ext_vector_type(2)));
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v{a, b}), b16x2v));
   } else {
-    return (uint32_t)f32_to_f16(a) | ((uint32_t)f32_to_f16(b) << 16);
+    u16 lo = f32_to_f16(a), hi = f32_to_f16(b);
+    asm volatile("" : "+v"(lo));
+    asm volatile("" : "+v"(hi));
+    return (uint32_t)lo | ((uint32_t)hi << 16);
   }
 }
 // value rounded to the model dtype, kept in fp32

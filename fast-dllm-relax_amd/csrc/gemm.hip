@@ -228,7 +228,10 @@ GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol) {
       const int wgs = p.nbm * p.nbn;
       // (up to 128 rows, half the target: a split's fp32 partials and its epilogue launch cost more
       // than the idle compute units; measured on the 128-row batched step, 3.15 -> 2.93 ms)
-      const int target = a.M <= 128 ? pol.target_wgs / 2 : pol.target_wgs;
+      // o_proj (48 k steps) a quarter: at 512 rows its 96 workgroups without a split took 15.4 us against
+      // 18.9 us split three ways with the epilogue launch
+      int target = a.M <= 128 ? pol.target_wgs / 2 : pol.target_wgs;
+      if (cfg == CFG_OPROJ) target /= 4;
       int split = 1;
       const int max_split = id == MM_WR ? 16 : 8;
       for (int d = 2; d <= max_split && wgs * split < target && cfg != CFG_LM_HEAD; ++d)

@@ -45,6 +45,18 @@ __global__ __launch_bounds__(256) void load_rows_kernel(const u16* x, int hidden
   }
 }
 
+// One normalised element, w * rnd(x * inv) rounded to the model dtype.  Each element is computed on its
+// own (an empty asm on the result): for fp16 the compiler rounds x * inv either by an fp32 multiply and
+// a conversion or by one mixed-precision fma (v_fma_mixlo_f16, a single rounding), and with eight
+// elements in flight it mixed the two, which changed results against the one-element-per-thread form
+// the rest of the build compiles to.
+template <int DT>
+__device__ __forceinline__ u16 norm_elem(float w, float x, float inv) {
+  u16 r = from_f32<DT>(w * rnd<DT>(x * inv));
+  asm volatile("" : "+v"(r));
+  return r;
+}
+
 // FastDLLMRMSNorm (cuda.py:269-275) from the producer's sums of squares: fp32 mean of squares,
 // x * 1/sqrt(var + eps) cast to the model dtype, then the weight multiply in the model dtype.
 // A workgroup normalises 4 rows, one per wave.  A row's sum of squares is the sum of its per-16-column
@@ -85,8 +97,8 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(const u16* h, int rows, 
     u32x4 o;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      o[e] = pack_f32x2<DT>(lo_f32<DT>(wv[e]) * rnd<DT>(lo_f32<DT>(hv[e]) * inv),
-                            hi_f32<DT>(wv[e]) * rnd<DT>(hi_f32<DT>(hv[e]) * inv));
+      o[e] = pack2(norm_elem<DT>(lo_f32<DT>(wv[e]), lo_f32<DT>(hv[e]), inv),
+                   norm_elem<DT>(hi_f32<DT>(wv[e]), hi_f32<DT>(hv[e]), inv));
     *reinterpret_cast<u32x4*>(y + (yblk ? frag_blk_off(r, c, ks) : (size_t)r * hidden + c)) = o;
   }
 }
