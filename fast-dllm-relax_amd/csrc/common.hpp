@@ -280,6 +280,28 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// ---- shift-down lane exchange --------------------------------------------------------------------
+// lane_down<K>(v) returns, in lanes l < K, the value lane l + K holds (K a power of two up to 32; the
+// other lanes get unspecified values): gfx950's permlane32 / permlane16 swaps for K = 32 / 16 and a DPP
+// row shift within 16 lanes below that, none of them through LDS.  A reduction that applies it for
+// K = 32, 16, ..., 1 leaves in lane 0 exactly the value the xor butterfly (__shfl_xor with 32, 16, ...,
+// 1) leaves in every lane, since each lane it reads holds what the butterfly's lane of that index holds.
+template <int K>
+__device__ __forceinline__ unsigned lane_down(unsigned v) {
+  static_assert(K == 1 || K == 2 || K == 4 || K == 8 || K == 16 || K == 32, "power of two up to 32");
+  if constexpr (K == 32) {
+    return __builtin_amdgcn_permlane32_swap(v, v, false, false)[1];
+  } else if constexpr (K == 16) {
+    return __builtin_amdgcn_permlane16_swap(v, v, false, false)[1];
+  } else {
+    return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x100 + K, 0xf, 0xf, false);  // row_shl:K
+  }
+}
+template <int K>
+__device__ __forceinline__ float lane_down(float v) { return __uint_as_float(lane_down<K>(__float_as_uint(v))); }
+template <int K>
+__device__ __forceinline__ int lane_down(int v) { return (int)lane_down<K>((unsigned)v); }
+
 // ---- LDS helpers ---------------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_raw;
 
