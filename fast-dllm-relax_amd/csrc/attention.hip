@@ -152,12 +152,30 @@ static hipError_t launch_prefill(const AttnP& a, hipStream_t st) {
 // the prefill kernel takes row blocks of at least this many rows without an explicit bias
 constexpr int PREFILL_MIN_ROWS = 128;
 
+// Batched calls without a mask: the RoPE + KV append pass over the call's rows, then attn_seq_kernel with
+// its key blocks SEQ_DEPTH ahead.
+constexpr int SEQ_DEPTH = 3;
+
+template <int DT>
+static hipError_t launch_seq(const AttnP& a, hipStream_t st) {
+  hipLaunchKernelGGL(rope_kv_kernel<DT>, dim3(a.nseq * a.rows), dim3(128), 0, st, a);
+  const int QT = ((a.nq / a.nkv) * a.rows + 15) / 16, xg = (QT + 3) / 4;
+  const int pairs = a.nseq * a.nkv;
+  auto kern = attn_seq_kernel<DT, SEQ_DEPTH>;
+  constexpr size_t lds = (size_t)(SEQ_DEPTH + 1) * 2 * 64 * HD * 2;  // K and V of D + 1 key blocks
+  raise_lds(kern, lds);
+  hipLaunchKernelGGL(kern, dim3((pairs + 7) / 8 * 8 * xg), dim3(256), lds, st, a);
+  return hipGetLastError();
+}
+
 template <int DT>
 static hipError_t launch_dt(const AttnP& a, hipStream_t st) {
   const AttnPlan p = attn_plan(a.rows, a.nq, a.nkv, a.Lk, a.target_wgs);
   if (p.S != a.S || p.chunk != a.chunk) return hipErrorInvalidValue;
-  if (a.nseq > 1 && (!p.chunked || a.nseq > MAX_SEQS)) return hipErrorInvalidValue;
   if (a.ofrag && (a.nseq > 1 || a.rows > 32)) return hipErrorInvalidValue;
+  if (a.nseq > MAX_SEQS) return hipErrorInvalidValue;
+  if (a.nseq > 1 && a.seq_attn && a.mask == 0) return launch_seq<DT>(a, st);
+  if (a.nseq > 1 && !p.chunked) return hipErrorInvalidValue;
   if (!p.chunked && a.nseq <= 1 && a.rows >= PREFILL_MIN_ROWS && a.mask != 2) {
     if (a.mask == 1) return launch_prefill<DT, 1>(a, st);
     return launch_prefill<DT, 0>(a, st);

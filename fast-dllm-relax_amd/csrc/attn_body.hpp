@@ -746,9 +746,9 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(AttnP p) {
 // [rows][nq * 128]: the prefill kernel reads each query from there before it writes that query's
 // output), k heads are RoPE'd and v copied into the cache rows ws + r (the KV append of
 // fast_dllm.attn_inplace, runtime.py:51-60).  Same RoPE arithmetic as the chunk kernels.
+// Batched calls (nseq > 1): workgroup b rows + r is row r of sequence b, in that sequence's view.
 template <int DT>
-__global__ __launch_bounds__(128) void rope_kv_kernel(AttnP a) {
-  const int r = blockIdx.x;
+__device__ __forceinline__ void rope_kv_row(const AttnP& a, int r) {
   const u16* src = a.qkv + (size_t)r * a.ldq;
   const float* cs = a.rope + (size_t)r * 128;
   const size_t krow = (size_t)a.nkv * HD;
@@ -770,6 +770,17 @@ __global__ __launch_bounds__(128) void rope_kv_kernel(AttnP a) {
           *reinterpret_cast<const u32x4*>(src + (a.nq + a.nkv + g) * HD + 8 * c);
     }
   }
+}
+template <int DT>
+__global__ __launch_bounds__(128) void rope_kv_kernel(AttnP p) {
+  if (p.nseq <= 1) {
+    rope_kv_row<DT>(p, blockIdx.x);
+    return;
+  }
+  const int b = (int)blockIdx.x / p.rows;
+  AttnP a = p;
+  seq_view(a, p, b);
+  rope_kv_row<DT>(a, (int)blockIdx.x - b * p.rows);
 }
 
 // attn_prefill_kernel: workgroup (query block of 32 rows, head subset hg of kv head g) with NWQ waves x
@@ -1067,6 +1078,10 @@ void attn_prefill_pair_kernel(AttnP a) {
       m_run[i] = -INFINITY;
       l_run[i] = 0.f;
     }
+    // the query loads land here, once per query block: otherwise the compiler's wait before the first
+    // MFMA of every key block covers them (they may be the youngest loads on the other path of the
+    // branch), which waits for every copy in flight and drains the copy pipeline on each block
+    wait_vmcnt<0>();
   };
   auto end_block = [&](int qb) __attribute__((always_inline)) {
     const int q0 = qb * 32;
@@ -1156,27 +1171,30 @@ void attn_prefill_pair_kernel(AttnP a) {
                           pack_f32x2<DT>(s[i][2 * ks + 1][0], s[i][2 * ks + 1][1]),
                           pack_f32x2<DT>(s[i][2 * ks + 1][2], s[i][2 * ks + 1][3])};
     }
-    // O^T += V^T P^T over the block's two 32-key k steps.  Transposing reads: this lane supplies key
-    // 32 ks + 4 lg + lr / 4 (+ 16 for the second half), dims 16 dt + 4 (lr % 4) .. + 3
-    typedef short s16x4 __attribute__((ext_vector_type(4)));
-    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    // O^T += V^T P^T over the block's two 32-key k steps.  Transposing reads (ds_read_tr16: the builtin
+    // would make the compiler wait for every copy in flight first): this lane supplies key
+    // 32 ks + 4 lg + lr / 4 (+ 16 for the second half), dims 16 dt + 4 (lr % 4) .. + 3; one k step's 16
+    // reads, then one wait
+    const uint32_t vbase = lds_addr(vbuf);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int ks = 0; ks < 2; ++ks) {
+      u32x2 vh[DT16 * 2];
 #pragma unroll
-      for (int dt = 0; dt < DT16; ++dt) {
-        u32x2 half[2];
+      for (int dt = 0; dt < DT16; ++dt)
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
           const int row = 32 * ks + 16 * hf + 4 * lg + (lr >> 2);
           const int dim = 16 * dt + 4 * (lr & 3);
-          const u16* vp = vbuf + row * HD + 8 * ((dim >> 3) ^ (row & 15)) + (dim & 7);
-          const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)vp);
-          half[hf] = __builtin_bit_cast(u32x2, r);
+          vh[dt * 2 + hf] = ds_read_tr16(vbase + 2 * (row * HD + 8 * ((dim >> 3) ^ (row & 15)) + (dim & 7)));
         }
-        const u32x4 vf = u32x4{half[0][0], half[0][1], half[1][0], half[1][1]};
+      lds_wait(vh);
+#pragma unroll
+      for (int dt = 0; dt < DT16; ++dt) {
+        const u32x4 vf = u32x4{vh[2 * dt][0], vh[2 * dt][1], vh[2 * dt + 1][0], vh[2 * dt + 1][1]};
 #pragma unroll
         for (int i = 0; i < TQ; ++i) o[i][dt] = mfma16<DT>(vf, pb[i][ks], o[i][dt]);
       }
+    }
   };
 
   // ---- task t: wait for its copies, free buffer (t - 1) % R, issue task t + D into it, compute.
@@ -1211,6 +1229,205 @@ void attn_prefill_pair_kernel(AttnP a) {
     if (t0 + decltype(uc)::value < T) iter(t0 + decltype(uc)::value, std::false_type{});
   });
   wait_vmcnt<0>();  // no copy may still be writing LDS when the workgroup ends
+}
+
+// attn_seq_kernel: the attention of a batched call (nseq sequences of `rows` rows each, no mask) without
+// key splits, so without partials or a merge launch.  Workgroup (sequence b, kv head g, group x of four
+// query tiles): wave w takes query tile 4 x + w of the stacked rows of the chunk kernels (row qi = head in
+// group x rows + r, 16 per tile) and every key of the sequence, [0, Lk_b).  The keys stream through LDS in
+// blocks of 64, D blocks ahead, by the global-to-LDS copy in the paired prefill kernel's layout (a
+// 256-byte row per key, 16-byte chunk c of row r at slot c ^ (r % 16); V^T fragments from the transposing
+// LDS read).  rope_kv_kernel has already appended this call's K/V rows to the cache and put the RoPE'd
+// queries in out, so every key comes from the cache and each query is read from out before its output
+// is written there.  Per query: one online softmax over the key blocks in order (scores in fp32, base 2),
+// P rounded to the model dtype, fp32 accumulation, one rounding of the output.
+// 1-D grid in XCD-aware order: linear index i, slot i % 8, round i / 8; pair (b, g) = (round / XG) x 8 +
+// slot, query group x = round % XG, so the XG workgroups that read one sequence's K/V run on one XCD and
+// share its L2.  Indices past the last pair have nothing to do.
+template <int DT, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void attn_seq_kernel(AttnP p) {
+  constexpr int NW = 4, R = D + 1;
+  constexpr int KBP = 64;                        // keys per block
+  constexpr int BUFE = 2 * KBP * HD;             // u16 per buffer: K rows, then V rows
+  constexpr int CPW = KBP * HD * 2 / 1024 / NW;  // 1 KB copies of K (and of V) per wave per block
+  constexpr int DT16 = HD / 16;
+  static_assert(D >= 1 && (D - 1) * 2 * CPW < 64, "outstanding copies fit the memory counter");
+  extern __shared__ __align__(16) unsigned char smem[];
+  u16* const lds16 = reinterpret_cast<u16*>(smem);
+
+  const int grp = p.nq / p.nkv, QR = grp * p.rows, QT = (QR + 15) / 16, XG = (QT + NW - 1) / NW;
+  const int i = blockIdx.x, round = i >> 3;
+  const int pair = (round / XG) * 8 + (i & 7), x = round % XG;
+  if (pair >= p.nseq * p.nkv) return;
+  const int b = pair / p.nkv, g = pair - b * p.nkv;
+  AttnP a = p;
+  seq_view(a, p, b);
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int Lk = a.Lk, T = (Lk + KBP - 1) / KBP;
+  const size_t krow = (size_t)a.nkv * HD;
+  const u16* kc = a.kc + g * HD;
+  const u16* vc = a.vc + g * HD;
+  const float c2 = a.scale * LOG2E;
+
+  // copies of block t (blocks past the last re-read the last) into buffer t % R: this wave's 1 KB pieces
+  // d = w CPW .. + CPW - 1 of K and of V, 4 rows each; lane l fills row 4 d + l / 16, slot l % 16 with
+  // chunk (l % 16) ^ (row % 16); rows past Lk repeat row Lk - 1 (masked below)
+  auto issue = [&](int t) __attribute__((always_inline)) {
+    const int k0 = min(t, T - 1) * KBP;
+    unsigned char* buf = smem + (size_t)(t % R) * BUFE * 2;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      const int d = w * CPW + c, row = 4 * d + (lane >> 4);
+      const int chunk = (lane & 15) ^ (row & 15);
+      const size_t src = (size_t)min(k0 + row, Lk - 1) * krow + 8 * chunk;
+      lds_copy16(kc + src, buf + (size_t)d * 1024);
+      lds_copy16(vc + src, buf + (size_t)KBP * HD * 2 + (size_t)d * 1024);
+    }
+  };
+#pragma unroll
+  for (int t = 0; t < D; ++t) issue(t);
+
+  // this lane's query: qi = 16 tile + lr (lanes past the stacked rows read row 0 and store nothing)
+  const int tile = x * NW + w;
+  const int qi = tile * 16 + lr;
+  const bool qvalid = tile < QT && qi < QR;
+  const int hh = qvalid ? qi / a.rows : 0;
+  const int r = qvalid ? qi - hh * a.rows : 0;
+  u32x4 qf[4];
+  {
+    const u16* qp = a.out + (size_t)r * a.nq * HD + (g * grp + hh) * HD + 8 * lg;
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) qf[ds] = *reinterpret_cast<const u32x4*>(qp + 32 * ds);
+  }
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4 o[DT16];
+#pragma unroll
+  for (int dt = 0; dt < DT16; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // one key block against the wave's query tile
+  auto compute = [&](int t) __attribute__((always_inline)) {
+    const u16* kbuf = lds16 + (size_t)(t % R) * BUFE;
+    const u16* vbuf = kbuf + KBP * HD;
+    const int k0 = t * KBP;
+    // S^T = K Q^T: lane holds S^T[key k0 + 16 kt + 4 lg + e][query lr]; K row 16 kt + lr, chunk lg + 4 ds
+    // (the block's 16 fragments read at once, then one wait)
+    u32x4 kf[16];
+    const uint32_t kbase = lds_addr(kbuf);
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds)
+        kf[kt * 4 + ds] = ds_read16(kbase + 2 * ((16 * kt + lr) * HD + 8 * ((lg + 4 * ds) ^ lr)));
+    lds_wait(kf);
+    f32x4 s[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds) s[kt] = mfma16<DT>(kf[kt * 4 + ds], qf[ds], s[kt]);
+    }
+    float mx = -INFINITY;
+    if (k0 + KBP <= Lk) {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s[kt][e] *= c2;
+          mx = fmaxf(mx, s[kt][e]);
+        }
+    } else {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float v = k0 + 16 * kt + 4 * lg + e < Lk ? s[kt][e] * c2 : -INFINITY;
+          s[kt][e] = v;
+          mx = fmaxf(mx, v);
+        }
+    }
+    mx = rows_max(mx);
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    float ps = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float pe = __builtin_amdgcn_exp2f(s[kt][e] - m_use);
+        s[kt][e] = pe;
+        ps += pe;
+      }
+    ps = rows_sum(ps);
+    l_run = l_run * alpha + ps;
+    m_run = m_new;
+    // rescale only when some query's running maximum moved (alpha = 1 leaves o unchanged bit for bit)
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+      for (int dt = 0; dt < DT16; ++dt) o[dt] *= alpha;
+    }
+    u32x4 pb[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      pb[ks] = u32x4{pack_f32x2<DT>(s[2 * ks][0], s[2 * ks][1]), pack_f32x2<DT>(s[2 * ks][2], s[2 * ks][3]),
+                     pack_f32x2<DT>(s[2 * ks + 1][0], s[2 * ks + 1][1]),
+                     pack_f32x2<DT>(s[2 * ks + 1][2], s[2 * ks + 1][3])};
+    // O^T += V^T P^T over the block's two 32-key k steps: V^T fragments by the transposing read (this
+    // lane supplies key 32 ks + 4 lg + lr / 4 (+ 16 for the second half), dims 16 dt + 4 (lr % 4) .. + 3),
+    // all 32 reads issued after the scores were formed, then one wait
+    u32x2 vh[2 * DT16 * 2];
+    const uint32_t vbase = lds_addr(vbuf);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int dt = 0; dt < DT16; ++dt)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const int row = 32 * ks + 16 * hf + 4 * lg + (lr >> 2);
+          const int dim = 16 * dt + 4 * (lr & 3);
+          vh[(ks * DT16 + dt) * 2 + hf] = ds_read_tr16(vbase + 2 * (row * HD + 8 * ((dim >> 3) ^ (row & 15)) + (dim & 7)));
+        }
+    lds_wait(vh);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int dt = 0; dt < DT16; ++dt) {
+        const u32x2 h0 = vh[(ks * DT16 + dt) * 2], h1 = vh[(ks * DT16 + dt) * 2 + 1];
+        o[dt] = mfma16<DT>(u32x4{h0[0], h0[1], h1[0], h1[1]}, pb[ks], o[dt]);
+      }
+  };
+
+  // block t: wait for its copies (EXACT: the D - 1 blocks issued after it each issued 2 CPW copies per
+  // wave; the query loads above only make the first waits longer), free buffer (t - 1) % R, issue block
+  // t + D into it, compute.  The last T % D blocks, after the loop, wait for everything.
+  auto iter = [&](int t, auto exact) __attribute__((always_inline)) {
+    if constexpr (decltype(exact)::value) wait_vmcnt<(D - 1) * 2 * CPW>();
+    else wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(t + D);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(t);
+  };
+  int t0 = 0;
+#pragma nounroll
+  for (; t0 + D <= T; t0 += D)
+    static_for<0, D>([&](auto uc) __attribute__((always_inline)) { iter(t0 + decltype(uc)::value, std::true_type{}); });
+  static_for<0, D - 1>([&](auto uc) __attribute__((always_inline)) {
+    if (t0 + decltype(uc)::value < T) iter(t0 + decltype(uc)::value, std::false_type{});
+  });
+  wait_vmcnt<0>();  // no copy may still be writing LDS when the workgroup ends
+
+  if (!qvalid) return;
+  const float inv = 1.0f / l_run;
+  u16* dst = a.out + (size_t)r * a.nq * HD + (g * grp + hh) * HD + 4 * lg;
+#pragma unroll
+  for (int dt = 0; dt < DT16; ++dt)
+    *reinterpret_cast<u32x2*>(dst + 16 * dt) =
+        u32x2{pack_f32x2<DT>(o[dt][0] * inv, o[dt][1] * inv), pack_f32x2<DT>(o[dt][2] * inv, o[dt][3] * inv)};
 }
 
 }  // namespace fdllm

@@ -99,6 +99,7 @@ struct fdllm_ctx {
   int attn_target = 64;   // attention workgroups aimed for when splitting the keys
   int prefill_hpw = 0;    // query heads per prefill-attention workgroup (0: chosen per launch)
   int prefill_pair = 1;   // paired-query-block prefill attention (0 off, 1 when it fills the chip, 2 always)
+  int seq_attn = 1;       // batched calls: attn_seq_kernel (0: the chunk kernel with key splits + merge)
   int down_split = 10;    // cross-workgroup k splits of the down projection (largest divisor of K/32 <= this)
   MmPolicy mm;              // large-M GEMM planning (k splits, register-weight kernel)
   bool frag_on = true;      // one-shot chains keep activations in MFMA-fragment order (FDLLM_XFRAG=0: row-major)
@@ -276,10 +277,17 @@ int run_attention(fdllm_ctx* c, int rows, uint16_t* kc, uint16_t* vc, int ws, in
     target = std::max(1, target / sb->nseq);
   }
   const AttnPlan pl = attn_plan(a.rows, a.nq, a.nkv, a.Lk, target);
-  if (sb != nullptr && !pl.chunked)
+  // batched calls without a mask take attn_seq_kernel (every key of a sequence in one workgroup, no
+  // partials) from 32 rows per sequence, or when the chunk plan cannot cover the longest sequence in one
+  // step; otherwise the chunk kernel.  Measured on config 4 (16 sequences, prefixes up to 1024): 32 rows
+  // 23.2 + 4.3 us (RoPE / KV append pass) against 21.6 + 8.5 us (chunks + merge); 8 rows 24.1 + 4.3 us
+  // against 11.8 + 4 us (each workgroup walks all of its sequence's keys, one 64-key block at a time)
+  const bool seq_kernel = sb != nullptr && c->seq_attn && mask == 0 && (sb->rows >= 32 || !pl.chunked);
+  if (sb != nullptr && !seq_kernel && !pl.chunked)
     return fail(FDLLM_EINVAL, "batched call of %d rows per sequence over %d keys is too long for one step", a.rows, a.Lk);
   a.S = pl.S; a.chunk = pl.chunk; a.target_wgs = target; a.prefill_hpw = c->prefill_hpw; a.prefill_pair = c->prefill_pair;
-  if (a.S > 1) {
+  a.seq_attn = seq_kernel;
+  if (a.S > 1 && !seq_kernel) {
     int rc = ensure_floats(&c->apart, &c->apart_floats, attn_partial_floats(a));
     if (rc) return rc;
     a.part = c->apart;
@@ -587,6 +595,7 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   if (const char* e = std::getenv("FDLLM_ATTN_TARGET")) c->attn_target = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_PREFILL_HPW")) c->prefill_hpw = std::max(0, atoi(e));
   if (const char* e = std::getenv("FDLLM_PREFILL_PAIR")) c->prefill_pair = std::min(2, std::max(0, atoi(e)));
+  if (const char* e = std::getenv("FDLLM_SEQ_ATTN")) c->seq_attn = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_DOWN_SPLIT")) c->down_split = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_MM_TARGET_WGS")) c->mm.target_wgs = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_MM_MIN_STAGES")) c->mm.min_stages = std::max(1, atoi(e));

@@ -105,8 +105,9 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // ---- deterministic exp for the confidence reduction ------------------------------------------
 // exp(x) for x <= 0: Cody-Waite reduction with ln2 split into a 16-bit head and a tail, a degree-7
-// Taylor polynomial in Horner form with fused multiply-adds, and the 2^n scale built in the
-// exponent field; 0 below -86 so nothing is subnormal.  Every operation is one IEEE fp32 op with
+// Taylor polynomial in Horner form with fused multiply-adds, and the 2^n scale applied exactly
+// (ldexp; the same product as a multiply by 2^n built in the exponent field); 0 below -86 so nothing
+// is subnormal.  Every operation is one IEEE fp32 op with
 // contraction off, so the CPU restatement of the confidence reproduces it bit for bit.
 __device__ __forceinline__ float fd_exp_neg(float x) {
 #pragma clang fp contract(off)
@@ -126,9 +127,8 @@ __device__ __forceinline__ float fd_exp_neg(float x) {
   p = __builtin_fmaf(p, r, 0.5f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  int ni = (int)n;
-  float scale = __uint_as_float((uint32_t)(ni + 127) << 23);
-  return p * scale;
+  // p * 2^n, exact: n >= -125 here, so 2^n and the product are normal
+  return __builtin_ldexpf(p, (int)n);
 }
 
 // ---- agent-coherent exchange between workgroups of one launch ---------------------------------
@@ -311,6 +311,39 @@ typedef __attribute__((address_space(3))) void lds_raw;
 // kernel's launch stub.
 __device__ __forceinline__ void lds_copy16(const u16* g, unsigned char* l) {
   __builtin_amdgcn_global_load_lds(g, (lds_raw*)l, 16, 0, 0);
+}
+
+// ds_read_b64_tr_b16 (gfx950 transposing LDS read: within each 16-lane group, lane q supplies 4 16-bit
+// values at its address and lane m receives value m % 4 of lanes 4 (m / 4) .. + 3, i.e. one column of a
+// 4 x 4 block per 16 lanes) written as inline asm.  The builtin form makes the compiler's wait-count pass
+// wait for every outstanding global-to-LDS copy before the read (it cannot tell which LDS bytes a copy
+// writes), which drains a copy pipeline on every block; in asm the read is invisible to that pass.  So the
+// caller must (1) have waited for and published (barrier) the copies that wrote the bytes it reads, and
+// (2) wait for the results with lds_wait() before using them.  `lds` is an LDS byte address.
+__device__ __forceinline__ u32x2 ds_read_tr16(uint32_t lds) {
+  u32x2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(lds) : "memory");
+  return r;
+}
+// ds_read_b128 in asm, for blocks of LDS reads the caller waits for at once (lds_wait): the compiler,
+// left to itself, interleaves such reads with their MFMAs and waits for each pair (the whole LDS latency
+// per pair).  Same contract as ds_read_tr16.
+__device__ __forceinline__ u32x4 ds_read16(uint32_t lds) {
+  u32x4 r;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(lds) : "memory");
+  return r;
+}
+// Wait for every outstanding LDS read (lgkmcnt(0)) and make the registers v depend on the wait, so no use
+// of them is scheduled above it.
+template <typename V, int N>
+__device__ __forceinline__ void lds_wait(V (&v)[N]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
+}
+// LDS byte address of a pointer into dynamic shared memory
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
 // s_waitcnt with the vector-memory count N (gfx9 encoding: vmcnt bits [3:0] and [15:14]; export and LDS

@@ -49,6 +49,92 @@ __device__ __forceinline__ u32x4 xform(u32x4 raw, u32x4 wv, float inv) {
   }
 }
 
+// Confidence statistics of one block's 256-column logit tile, held in LDS as [BM][256] values (model
+// dtype, or fp32 already rounded to it): one wave per row (rows w, w + NW, ...) reduces the row's columns to (max, first argmax, sum of
+// exp(x - max)) with one lane order and reduction order, so every kernel that produces the tile gives
+// identical bits.  A wave works on RP of its rows at once, and the cross-lane steps are
+// register exchanges (lane_down) instead of LDS permutes: each row's reduction is a chain of exchanges
+// whose latency, one row at a time through LDS, cost more than the tile's MFMAs.
+template <int DT> __device__ __forceinline__ float tile_value(u16 v) { return to_f32<DT>(v); }
+template <int DT> __device__ __forceinline__ float tile_value(float v) { return v; }
+
+template <int DT, int BM, int NW, typename T>
+__device__ __forceinline__ void logits_tile_stats(const GemmP& a, const T* tile, int m0, int nb, int w, int lane) {
+  constexpr int RPW = BM / NW;  // rows of each wave
+  constexpr int RP = RPW % 4 == 0 ? 4 : (RPW % 2 == 0 ? 2 : 1);
+  static_assert(BM % NW == 0, "whole rows per wave");
+  const int n0 = nb * 256;
+  const bool whole = n0 + 256 <= a.N;  // every column of the tile is a vocabulary entry
+  for (int ml0 = w; ml0 < BM; ml0 += NW * RP) {
+    if (m0 + ml0 >= a.M) break;
+    float x[RP][4], vmax[RP];
+    int amax[RP];
+    // the row max (NaN never wins): per lane over its columns, then a shift-down tree into lane 0
+#pragma unroll
+    for (int r = 0; r < RP; ++r) {
+      const T* row = tile + (ml0 + NW * r) * 256;
+      vmax[r] = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = lane + 64 * i;
+        x[r][i] = tile_value<DT>(row[c]);
+        if ((whole || n0 + c < a.N) && x[r][i] > vmax[r]) vmax[r] = x[r][i];
+      }
+    }
+    static_for<0, 6>([&](auto s) {
+      constexpr int k = 32 >> decltype(s)::value;
+#pragma unroll
+      for (int r = 0; r < RP; ++r) {
+        const float o = lane_down<k>(vmax[r]);
+        vmax[r] = o > vmax[r] ? o : vmax[r];
+      }
+    });
+    // the first column holding it (none when the max is -inf): the smallest candidate index, by a min tree
+#pragma unroll
+    for (int r = 0; r < RP; ++r) {
+      vmax[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vmax[r]), 0));
+      amax[r] = 0x7fffffff;
+#pragma unroll
+      for (int i = 3; i >= 0; --i) {
+        const int c = lane + 64 * i;
+        if ((whole || n0 + c < a.N) && x[r][i] == vmax[r] && vmax[r] > -INFINITY) amax[r] = n0 + c;
+      }
+    }
+    static_for<0, 6>([&](auto s) {
+      constexpr int k = 32 >> decltype(s)::value;
+#pragma unroll
+      for (int r = 0; r < RP; ++r) amax[r] = min(amax[r], lane_down<k>(amax[r]));
+    });
+    float sum[RP];
+    {
+#pragma clang fp contract(off)
+#pragma unroll
+      for (int r = 0; r < RP; ++r) {
+        sum[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (whole || n0 + lane + 64 * i < a.N) sum[r] = sum[r] + fd_exp_neg(x[r][i] - vmax[r]);
+      }
+      // the butterfly's sum order, in lane 0
+      static_for<0, 6>([&](auto s) {
+        constexpr int k = 32 >> decltype(s)::value;
+#pragma unroll
+        for (int r = 0; r < RP; ++r) sum[r] = sum[r] + lane_down<k>(sum[r]);
+      });
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < RP; ++r) {
+        if (m0 + ml0 + NW * r >= a.M) break;
+        const size_t o = (size_t)(m0 + ml0 + NW * r) * a.stat_tiles + nb;
+        a.stat_m[o] = vmax[r];
+        a.stat_a[o] = amax[r];
+        a.stat_s[o] = sum[r];
+      }
+    }
+  }
+}
+
 template <int DT, int EPI, int XF, int MT, int TPW, int TW, int KW, int U>
 __global__ __launch_bounds__(64 * TW * KW) void gemm_pk_kernel(GemmP a) {
   __shared__ float inv_s[32];
@@ -248,43 +334,7 @@ __global__ __launch_bounds__(64 * TW * KW) void gemm_pk_kernel(GemmP a) {
       }
     if (a.stat_m == nullptr) return;
     __syncthreads();
-    const int n0 = blockIdx.x * 256;
-    for (int m = w; m < 16 * MT; m += TW * KW) {
-      if (m0 + m >= a.M) break;
-      const float* row = tile + m * 256;
-      float vmax = -INFINITY;
-      int amax = 0x7fffffff;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int c = lane + 64 * i;
-        if (n0 + c < a.N) {
-          const float x = row[c];
-          if (x > vmax) { vmax = x; amax = n0 + c; }
-        }
-      }
-      for (int k = 32; k >= 1; k >>= 1) {
-        const float ov = __shfl_xor(vmax, k, WAVE);
-        const int oa = __shfl_xor(amax, k, WAVE);
-        if (ov > vmax || (ov == vmax && oa < amax)) { vmax = ov; amax = oa; }
-      }
-      float s;
-      {
-#pragma clang fp contract(off)
-        s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int c = lane + 64 * i;
-          if (n0 + c < a.N) s = s + fd_exp_neg(row[c] - vmax);
-        }
-        for (int k = 32; k >= 1; k >>= 1) s = s + __shfl_xor(s, k, WAVE);
-      }
-      if (lane == 0) {
-        const size_t o = (size_t)(m0 + m) * a.stat_tiles + blockIdx.x;
-        a.stat_m[o] = vmax;
-        a.stat_a[o] = amax;
-        a.stat_s[o] = s;
-      }
-    }
+    logits_tile_stats<DT, 16 * MT, TW * KW>(a, tile, m0, (int)blockIdx.x, w, lane);
   } else if constexpr (EPI == EPI_SILU_PAIR) {
     if (kw != 0) return;
     const int p = t0 / 2;  // tiles t0 (gate) and t0 + 1 (up) of pair p

@@ -25,81 +25,6 @@
 
 namespace fdllm {
 
-// Confidence statistics of one block's 256-column logit tile, held in LDS as [BM][256] model-dtype
-// values: one wave per row (rows w, w + NW, ...) reduces the row's columns to (max, first argmax, sum of
-// exp(x - max)) with the streaming kernel's lane order and butterflies, so every kernel that produces
-// the tile gives identical bits.  A wave works on RP of its rows at once, and the cross-lane steps are
-// register exchanges (lane_down) instead of LDS permutes: each row's reduction is a chain of exchanges
-// whose latency, one row at a time through LDS, cost more than the tile's MFMAs.
-template <int DT, int BM, int NW>
-__device__ __forceinline__ void logits_tile_stats(const GemmP& a, const u16* tile, int m0, int nb, int w, int lane) {
-  constexpr int RPW = BM / NW;  // rows of each wave
-  constexpr int RP = RPW % 4 == 0 ? 4 : (RPW % 2 == 0 ? 2 : 1);
-  static_assert(BM % NW == 0, "whole rows per wave");
-  const int n0 = nb * 256;
-  for (int ml0 = w; ml0 < BM; ml0 += NW * RP) {
-    if (m0 + ml0 >= a.M) break;
-    float x[RP][4], vmax[RP];
-    int amax[RP];
-#pragma unroll
-    for (int r = 0; r < RP; ++r) {
-      const u16* row = tile + (ml0 + NW * r) * 256;
-      vmax[r] = -INFINITY;
-      amax[r] = 0x7fffffff;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int c = lane + 64 * i;
-        x[r][i] = to_f32<DT>(row[c]);
-        if (n0 + c < a.N && x[r][i] > vmax[r]) { vmax[r] = x[r][i]; amax[r] = n0 + c; }
-      }
-    }
-    // (max, first index) is an order-free combine: a shift-down tree into lane 0, then broadcast
-    static_for<0, 6>([&](auto s) {
-      constexpr int k = 32 >> decltype(s)::value;
-#pragma unroll
-      for (int r = 0; r < RP; ++r) {
-        const float ov = lane_down<k>(vmax[r]);
-        const int oa = lane_down<k>(amax[r]);
-        const bool take = (ov > vmax[r]) | ((ov == vmax[r]) & (oa < amax[r]));
-        vmax[r] = take ? ov : vmax[r];
-        amax[r] = take ? oa : amax[r];
-      }
-    });
-#pragma unroll
-    for (int r = 0; r < RP; ++r) {
-      vmax[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vmax[r]), 0));
-      amax[r] = __builtin_amdgcn_readlane(amax[r], 0);
-    }
-    float sum[RP];
-    {
-#pragma clang fp contract(off)
-#pragma unroll
-      for (int r = 0; r < RP; ++r) {
-        sum[r] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (n0 + lane + 64 * i < a.N) sum[r] = sum[r] + fd_exp_neg(x[r][i] - vmax[r]);
-      }
-      // the butterfly's sum order, in lane 0
-      static_for<0, 6>([&](auto s) {
-        constexpr int k = 32 >> decltype(s)::value;
-#pragma unroll
-        for (int r = 0; r < RP; ++r) sum[r] = sum[r] + lane_down<k>(sum[r]);
-      });
-    }
-    if (lane == 0) {
-#pragma unroll
-      for (int r = 0; r < RP; ++r) {
-        if (m0 + ml0 + NW * r >= a.M) break;
-        const size_t o = (size_t)(m0 + ml0 + NW * r) * a.stat_tiles + nb;
-        a.stat_m[o] = vmax[r];
-        a.stat_a[o] = amax[r];
-        a.stat_s[o] = sum[r];
-      }
-    }
-  }
-}
-
 template <int DT, int EPI, int XF, int MF, int TPW, int NWM, int NWN, int KSS, int WD>
 __global__ __launch_bounds__(64 * NWM * NWN) void gemm_mm_kernel(GemmP a, int nbm, int nbn) {
   constexpr int NW = NWM * NWN;

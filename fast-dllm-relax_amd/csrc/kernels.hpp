@@ -140,6 +140,7 @@ struct AttnP {
   int target_wgs;                     // workgroups the plan aims for (attn_plan)
   int prefill_hpw;                    // query heads per workgroup of the prefill kernel (0: chosen per launch)
   int prefill_pair;                   // paired-query-block prefill kernel: 0 off, 1 when it fills the chip, 2 always
+  int seq_attn;                       // batched calls without a mask: attn_seq_kernel (no key splits) instead of chunks + merge
   float* part;                        // split partials (merged by attn_merge_kernel)
   uint16_t* out;                      // [rows][nq * 128]
   int ofrag;                          // out in MFMA-fragment order (frag_off; rows <= 32, nseq 1)

@@ -146,3 +146,62 @@ def test_wide_batched_step_16_sequences(wide2):
     wid, wp = oconf.confidence(to_np(logits)[0])
     np.testing.assert_array_equal(ids.cpu().numpy()[0], wid)
     np.testing.assert_array_equal(maxp.cpu().numpy()[0].view(np.uint32), wp.view(np.uint32))
+
+
+def test_seq_attention_kernel_matches_chunk_kernel(monkeypatch):
+    """Batched calls take attn_seq_kernel (every key of a sequence streamed through one workgroup, no key
+    splits) by default; FDLLM_SEQ_ATTN=0 keeps the chunk kernel with key splits and the merge launch.  Both
+    append the same RoPE'd K/V rows at layer 0 (bit for bit) and agree on the hidden states, and so on later
+    layers' appended rows, to the bf16 criterion (their fp32 softmax sums run in different orders).  Prefixes off the 64-key block grid, up to 1000
+    keys, full (32-row) and partial (8-row) steps; 16 sequences of the 1.5B width."""
+    from fast_dllm_relax_amd.config import FastDLLMConfig
+    from fast_dllm_relax_amd.params import from_numpy
+    from fast_dllm_relax_amd.vm import HipVM
+    from oracle.model import OracleConfig, random_params
+
+    kw = WIDE2
+    params = from_numpy(random_params(OracleConfig(**kw), 4, "bfloat16"), FastDLLMConfig(**kw), dtype="bfloat16")
+    vms = {}
+    for name, on in (("seq", "1"), ("chunk", "0")):
+        monkeypatch.setenv("FDLLM_SEQ_ATTN", on)
+        vms[name] = HipVM(FastDLLMConfig(**kw), params, dtype="bfloat16", max_rows=512)
+        monkeypatch.delenv("FDLLM_SEQ_ATTN")
+    rng = np.random.default_rng(41)
+    prefixes = [1000, 32, 96, 511, 200, 64, 992, 130, 700, 33, 257, 960, 448, 5, 640, 801]
+    L, nkv, hd = kw["num_hidden_layers"], kw["num_key_value_heads"], kw["head_dim"]
+    B, R = len(prefixes), 32
+    cap = max(prefixes) + 2 * R
+    ids = [rng.integers(0, kw["vocab_size"] - 1, P + R) for P in prefixes]
+    out = {}
+    for name, vm in vms.items():
+        k = torch.full((L, B, cap, nkv, hd), SENTINEL, dtype=torch.bfloat16, device="cuda")
+        v = torch.full_like(k, SENTINEL)
+        log(f"case: {name} attention, build_prefix_cache_seq x {B}")
+        for b, P in enumerate(prefixes):
+            vm.build_prefix_cache_seq(vm.embed(_dev_ids(ids[b][:P]))[None], None, k, v, b)
+        x = torch.stack([vm.embed(_dev_ids(ids[b][P:])) for b, P in enumerate(prefixes)])
+        off = torch.tensor(prefixes, dtype=torch.int32, device="cuda")
+        log(f"case: {name} attention, forward_cached_batch nseq={B} rows={R}")
+        h = vm.forward_cached_batch(x, k, v, off, prefixes)
+        kf, vf = to_np(k), to_np(v)
+        offp = torch.tensor([P + 8 for P in prefixes], dtype=torch.int32, device="cuda")
+        log(f"case: {name} attention, forward_block_partial_batch rp=8")
+        hp = vm.forward_block_partial_batch(8, x[:, 8:16].contiguous(), k, v, offp, prefixes)
+        torch.cuda.synchronize()
+        out[name] = (to_np(h), kf, vf, to_np(hp))
+    for i, what in ((1, "K cache"), (2, "V cache")):
+        # layer 0's appended rows and every prefix row are the same bits; later layers' appended rows follow
+        # hidden states that agree to the bf16 criterion
+        np.testing.assert_array_equal(out["seq"][i][0], out["chunk"][i][0], err_msg=f"{what}, layer 0")
+        for b, P in enumerate(prefixes):
+            np.testing.assert_array_equal(out["seq"][i][:, b, :P], out["chunk"][i][:, b, :P],
+                                          err_msg=f"{what}, sequence {b} prefix rows")
+            assert (out["seq"][i][:, b, P + R:] == SENTINEL).all(), f"{what}, sequence {b}: rows past its window"
+        bf16_parity(f"seq vs chunk attention, {what} appended rows",
+                    np.stack([out["seq"][i][1:, b, P:P + R] for b, P in enumerate(prefixes)]),
+                    np.stack([out["chunk"][i][1:, b, P:P + R] for b, P in enumerate(prefixes)]))
+    assert np.isfinite(out["seq"][0]).all() and np.isfinite(out["seq"][3]).all()
+    bf16_parity("seq vs chunk attention, full step hidden", out["seq"][0], out["chunk"][0])
+    bf16_parity("seq vs chunk attention, partial step hidden", out["seq"][3], out["chunk"][3])
+    for vm in vms.values():
+        vm.close()
