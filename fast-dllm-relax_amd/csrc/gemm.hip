@@ -174,7 +174,12 @@ struct WrCfg {
   static constexpr size_t lds_logits = (size_t)16 * MF * 256 * 2;  // the lm_head's [BM][256] logit tile
 };
 using WrBig = WrCfg<8, 4, FD_WR_DEPTH>;  // 128 x 256
-enum MmId : int { MM_SMALL = 0, MM_WIDE = 1, MM_WIDE_D = 2, MM_BIG = 3, MM_WT = 4, MM_WR = 5 };
+// stages in flight of the small register-weight blocks (8 MFMAs per k step and wave cover little latency)
+#ifndef FD_WR_SMALL_DEPTH
+#define FD_WR_SMALL_DEPTH 8
+#endif
+using WrSmall = WrCfg<4, 2, FD_WR_SMALL_DEPTH>;  // 64 x 128
+enum MmId : int { MM_SMALL = 0, MM_WIDE = 1, MM_WIDE_D = 2, MM_BIG = 3, MM_WT = 4, MM_WR = 5, MM_WR_S = 6 };
 struct MmInfo { int bm, bn_tiles, kss; };
 template <class M> constexpr MmInfo mm_info_of() { return MmInfo{M::bm, M::bn_tiles, M::kss}; }
 static MmInfo mm_info(int id) {
@@ -184,6 +189,7 @@ static MmInfo mm_info(int id) {
     case MM_BIG: return mm_info_of<MmBig>();
     case MM_WT: return mm_info_of<WtBig>();
     case MM_WR: return mm_info_of<WrBig>();
+    case MM_WR_S: return mm_info_of<WrSmall>();
     default: return mm_info_of<MmSmall>();
   }
 }
@@ -198,6 +204,12 @@ static int wr_default_min_rows(int cfg) {
 static int mm_choice(int cfg, int M, int ntiles, const MmPolicy& pol) {
   const int min_rows = pol.wr_min_rows > 0 ? pol.wr_min_rows : wr_default_min_rows(cfg);
   if (M >= std::max(min_rows, 33) && ((pol.wr_ops >> cfg) & 1)) return MM_WR;
+  // qkv and o_proj below that: 64 x 128 register-weight blocks (us per launch, qkv including its norm pass,
+  // against the LDS-staged 64 x 128 kernel): qkv 16.2 / 14.9 at 128 rows, 23.2 / 20.2 at 512, 26.2 / 19.4
+  // at 1024, 30.8 / 28.6 at 2048; o_proj 15.2 / 14.0 at 384, 15.4 / 14.0 at 512, 19.3 / 15.1 at 1024, but
+  // 23.3 / 26.4 at 2048 (equal below 384)
+  if (M >= 33 && ((pol.wr_small_ops >> cfg) & 1) && (cfg == CFG_QKV || (cfg == CFG_OPROJ && M < 2048)))
+    return MM_WR_S;
   switch (cfg) {
     case CFG_LM_HEAD: return MM_WIDE;  // one 256-column confidence tile per block column
     case CFG_GATE_UP:
@@ -233,7 +245,7 @@ GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol) {
       int target = a.M <= 128 ? pol.target_wgs / 2 : pol.target_wgs;
       if (cfg == CFG_OPROJ) target /= 4;
       int split = 1;
-      const int max_split = id == MM_WR ? 16 : 8;
+      const int max_split = id == MM_WR || id == MM_WR_S ? 16 : 8;
       for (int d = 2; d <= max_split && wgs * split < target && cfg != CFG_LM_HEAD; ++d)
         if (nst % d == 0 && nst / d >= pol.min_stages) split = d;
       p.ksplit = split;
@@ -351,6 +363,10 @@ static hipError_t launch_wt_cfg(const GemmP& a, const GemmPlan& p, hipStream_t s
 template <int DT, int CFG, class C>
 static hipError_t launch_mm(const GemmP& a, const GemmPlan& p, hipStream_t st) {
   if (p.mm_id == MM_WR) return launch_wr_cfg<DT, C::epi, WrBig>(a, p, st);
+  if (p.mm_id == MM_WR_S) {
+    if constexpr (CFG == CFG_QKV || CFG == CFG_OPROJ) return launch_wr_cfg<DT, C::epi, WrSmall>(a, p, st);
+    return hipErrorInvalidValue;
+  }
   if constexpr (CFG == CFG_GATE_UP) {
     if (p.mm_id == MM_WT) return launch_wt_cfg<DT, C::epi, WtBig>(a, p, st);
     if (p.mm_id == MM_BIG) return launch_mm_cfg<DT, C::epi, XF_NONE, MmBig>(a, p, st);
@@ -398,7 +414,9 @@ bool gemm_takes_frag(int cfg, const GemmPlan& p) {
   return p.kind == GK_ONESHOT && p.mchunks == 1 && nt > 0 && (nt <= 4 || (cfg == CFG_GATE_UP && p.ksplit == 1));
 }
 
-bool gemm_takes_blocks(const GemmPlan& p) { return p.kind == GK_MM && (p.mm_id == MM_WT || p.mm_id == MM_WR); }
+bool gemm_takes_blocks(const GemmPlan& p) {
+  return p.kind == GK_MM && (p.mm_id == MM_WT || p.mm_id == MM_WR || p.mm_id == MM_WR_S);
+}
 
 hipError_t launch_gemm(int dt, int cfg, const GemmP& a, const GemmPlan& p, hipStream_t st) {
   if ((a.xfrag == 1 || a.yfrag == 1) && !gemm_takes_frag(cfg, p)) return hipErrorInvalidValue;

@@ -68,6 +68,7 @@ struct MmPolicy {
   int min_stages = 8;
   int wr_ops = (1 << CFG_QKV) | (1 << CFG_OPROJ) | (1 << CFG_GATE_UP) | (1 << CFG_DOWN) | (1 << CFG_LM_HEAD);
   int wr_min_rows = 0;
+  int wr_small_ops = (1 << CFG_QKV) | (1 << CFG_OPROJ);  // take the 64 x 128 register-weight blocks below the 128 x 256 ones
 };
 GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol = MmPolicy{});
 // whether the plan runs the one-shot register-fragment body, the only one that takes xfrag / yfrag 1

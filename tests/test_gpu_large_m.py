@@ -1,8 +1,9 @@
 """The register-weight large-M GEMM against the LDS-staged and streaming large-M GEMMs.
 
-By default gate_up and down run gemm_wr_kernel from 2048 rows and qkv and o_proj from 4096
-(FDLLM_WR_OPS selects the projections, one bit per GemmCfg; FDLLM_WR_MIN_ROWS lowers the threshold,
-here to 256 so that ragged and small row counts take it too).  Every large-M kernel accumulates each
+By default gate_up and down run gemm_wr_kernel's 128 x 256 blocks from 2048 rows and qkv and o_proj from
+4096 (FDLLM_WR_OPS selects the projections, one bit per GemmCfg; FDLLM_WR_MIN_ROWS lowers the threshold,
+here to 256 so that ragged and small row counts take it too); below that qkv, and o_proj below 2048 rows,
+run its 64 x 128 blocks (FDLLM_WR_SMALL, bits of qkv and o_proj).  Every large-M kernel accumulates each
 output element's k steps in order in one MFMA chain and shares the epilogues, so with k splits off
 (FDLLM_MM_TARGET_WGS=1) the hidden states must agree bit for bit whichever kernel ran.  Parity of the default configuration with the oracle is
 established by the prefill, forward_hidden and batched-step tests."""
@@ -18,15 +19,16 @@ from helpers import WIDE2, log
 pytestmark = pytest.mark.gpu
 
 
-def _vm(kw, params, dtype, monkeypatch, wr_ops, max_rows):
+def _vm(kw, params, dtype, monkeypatch, wr_ops, max_rows, wr_small=0):
     from fast_dllm_relax_amd.config import FastDLLMConfig
     from fast_dllm_relax_amd.vm import HipVM
 
     monkeypatch.setenv("FDLLM_WR_OPS", str(wr_ops))
     monkeypatch.setenv("FDLLM_WR_MIN_ROWS", "256")
     monkeypatch.setenv("FDLLM_MM_TARGET_WGS", "1")
+    monkeypatch.setenv("FDLLM_WR_SMALL", str(wr_small))
     vm = HipVM(FastDLLMConfig(**kw), params, dtype=dtype, max_rows=max_rows)
-    for k in ("FDLLM_WR_OPS", "FDLLM_WR_MIN_ROWS", "FDLLM_MM_TARGET_WGS"):
+    for k in ("FDLLM_WR_OPS", "FDLLM_WR_MIN_ROWS", "FDLLM_MM_TARGET_WGS", "FDLLM_WR_SMALL"):
         monkeypatch.delenv(k)
     return vm
 
@@ -46,6 +48,7 @@ def test_register_weight_kernel_bit_identical(dtype, monkeypatch):
     sizes = (300, 512, 1056)
     vm_wr = _vm(kw, params, dtype, monkeypatch, 15, max(sizes))
     vm_old = _vm(kw, params, dtype, monkeypatch, 0, max(sizes))
+    vm_small = _vm(kw, params, dtype, monkeypatch, 0, max(sizes), wr_small=3)  # 64 x 128 blocks for qkv, o_proj
     rng = np.random.default_rng(17)
     for S in sizes:
         log(f"case: forward_hidden {S} rows, 1.5B width, 2 layers, {dtype}, register-weight vs LDS-staged")
@@ -53,9 +56,11 @@ def test_register_weight_kernel_bit_identical(dtype, monkeypatch):
         x = vm_old.embed(ids)[None]
         h_old = vm_old.forward_hidden(x, None)
         h_wr = vm_wr.forward_hidden(x, None)
+        h_small = vm_small.forward_hidden(x, None)
         torch.cuda.synchronize()
         assert torch.isfinite(h_wr.float()).all()
         np.testing.assert_array_equal(_bits(h_wr), _bits(h_old), err_msg=f"S={S}")
+        np.testing.assert_array_equal(_bits(h_small), _bits(h_old), err_msg=f"S={S}, 64 x 128 blocks")
 
 
 def _prefill_vm(kw, params, dtype, monkeypatch, pair, max_rows):
