@@ -153,18 +153,25 @@ static hipError_t launch_prefill(const AttnP& a, hipStream_t st) {
 constexpr int PREFILL_MIN_ROWS = 128;
 
 // Batched calls without a mask: the RoPE + KV append pass over the call's rows, then attn_seq_kernel with
-// its key blocks SEQ_DEPTH ahead.
+// its key blocks SEQ_DEPTH ahead and SEQ_KH key parts (waves per query tile).
 constexpr int SEQ_DEPTH = 3;
+#ifndef FD_SEQ_KH
+#define FD_SEQ_KH 2
+#endif
+#ifndef FD_SEQ_NQW
+#define FD_SEQ_NQW 2
+#endif
+constexpr int SEQ_KH = FD_SEQ_KH, SEQ_NQW = FD_SEQ_NQW;
 
 template <int DT>
 static hipError_t launch_seq(const AttnP& a, hipStream_t st) {
   hipLaunchKernelGGL(rope_kv_kernel<DT>, dim3(a.nseq * a.rows), dim3(128), 0, st, a);
-  const int QT = ((a.nq / a.nkv) * a.rows + 15) / 16, xg = (QT + 3) / 4;
+  const int QT = ((a.nq / a.nkv) * a.rows + 15) / 16, xg = (QT + SEQ_NQW - 1) / SEQ_NQW;
   const int pairs = a.nseq * a.nkv;
-  auto kern = attn_seq_kernel<DT, SEQ_DEPTH>;
+  auto kern = attn_seq_kernel<DT, SEQ_DEPTH, SEQ_NQW, SEQ_KH>;
   constexpr size_t lds = (size_t)(SEQ_DEPTH + 1) * 2 * 64 * HD * 2;  // K and V of D + 1 key blocks
   raise_lds(kern, lds);
-  hipLaunchKernelGGL(kern, dim3((pairs + 7) / 8 * 8 * xg), dim3(256), lds, st, a);
+  hipLaunchKernelGGL(kern, dim3((pairs + 7) / 8 * 8 * xg), dim3(64 * SEQ_NQW * SEQ_KH), lds, st, a);
   return hipGetLastError();
 }
 

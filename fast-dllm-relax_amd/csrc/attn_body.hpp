@@ -1232,31 +1232,37 @@ void attn_prefill_pair_kernel(AttnP a) {
 }
 
 // attn_seq_kernel: the attention of a batched call (nseq sequences of `rows` rows each, no mask) without
-// key splits, so without partials or a merge launch.  Workgroup (sequence b, kv head g, group x of four
-// query tiles): wave w takes query tile 4 x + w of the stacked rows of the chunk kernels (row qi = head in
-// group x rows + r, 16 per tile) and every key of the sequence, [0, Lk_b).  The keys stream through LDS in
-// blocks of 64, D blocks ahead, by the global-to-LDS copy in the paired prefill kernel's layout (a
-// 256-byte row per key, 16-byte chunk c of row r at slot c ^ (r % 16); V^T fragments from the transposing
-// LDS read).  rope_kv_kernel has already appended this call's K/V rows to the cache and put the RoPE'd
-// queries in out, so every key comes from the cache and each query is read from out before its output
-// is written there.  Per query: one online softmax over the key blocks in order (scores in fp32, base 2),
-// P rounded to the model dtype, fp32 accumulation, one rounding of the output.
+// key splits, so without partials or a merge launch.  Workgroup (sequence b, kv head g, group x of NQW
+// query tiles) with NQW KH waves: wave w takes query tile NQW x + w % NQW of the stacked rows of the
+// chunk kernels (row qi = head in group x rows + r, 16 per tile) and key part kh = w / NQW, i.e. keys
+// 64 j + 64 / KH kh .. of every 64-key block j of the sequence's [0, Lk_b).  The blocks stream through
+// LDS, D blocks ahead, by the global-to-LDS copy in the paired prefill kernel's layout (a 256-byte row per
+// key, 16-byte chunk c of row r at slot c ^ (r % 16); V^T fragments from the transposing LDS read).
+// rope_kv_kernel has already appended this call's K/V rows to the cache and put the RoPE'd queries in
+// out, so every key comes from the cache and each query is read from out before its output is written
+// there.  Per query and key part: one online softmax over the part's keys in order (scores in fp32, base
+// 2), P rounded to the model dtype, fp32 accumulation; the KH parts are merged in LDS in part order (the
+// chunk kernel's merge), then one rounding of the output.
 // 1-D grid in XCD-aware order: linear index i, slot i % 8, round i / 8; pair (b, g) = (round / XG) x 8 +
 // slot, query group x = round % XG, so the XG workgroups that read one sequence's K/V run on one XCD and
 // share its L2.  Indices past the last pair have nothing to do.
-template <int DT, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+template <int DT, int D, int NQW, int KH>
+__global__ __launch_bounds__(64 * NQW * KH) __attribute__((amdgpu_waves_per_eu(NQW * KH > 4 ? 2 : 1, NQW * KH > 4 ? 2 : 1)))
 void attn_seq_kernel(AttnP p) {
-  constexpr int NW = 4, R = D + 1;
+  constexpr int NW = NQW * KH, R = D + 1;
   constexpr int KBP = 64;                        // keys per block
+  constexpr int KPP = KBP / KH;                  // keys of a block per key part
   constexpr int BUFE = 2 * KBP * HD;             // u16 per buffer: K rows, then V rows
   constexpr int CPW = KBP * HD * 2 / 1024 / NW;  // 1 KB copies of K (and of V) per wave per block
   constexpr int DT16 = HD / 16;
+  constexpr int KT = KPP / 16;                   // 16-key score tiles per part
+  constexpr int KS = KPP / 32;                   // 32-key P.V steps per part
+  static_assert(KH == 1 || KH == 2, "one or two key parts");
   static_assert(D >= 1 && (D - 1) * 2 * CPW < 64, "outstanding copies fit the memory counter");
+  static_assert((size_t)KH * NQW * (DT16 * 64 * 16 + 2 * 16 * 4) <= (size_t)R * BUFE * 2, "merge fits the buffers");
   extern __shared__ __align__(16) unsigned char smem[];
-  u16* const lds16 = reinterpret_cast<u16*>(smem);
 
-  const int grp = p.nq / p.nkv, QR = grp * p.rows, QT = (QR + 15) / 16, XG = (QT + NW - 1) / NW;
+  const int grp = p.nq / p.nkv, QR = grp * p.rows, QT = (QR + 15) / 16, XG = (QT + NQW - 1) / NQW;
   const int i = blockIdx.x, round = i >> 3;
   const int pair = (round / XG) * 8 + (i & 7), x = round % XG;
   if (pair >= p.nseq * p.nkv) return;
@@ -1265,6 +1271,7 @@ void attn_seq_kernel(AttnP p) {
   seq_view(a, p, b);
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int qw = w % NQW, kh = w / NQW;
   const int lr = lane & 15, lg = lane >> 4;
   const int Lk = a.Lk, T = (Lk + KBP - 1) / KBP;
   const size_t krow = (size_t)a.nkv * HD;
@@ -1274,24 +1281,41 @@ void attn_seq_kernel(AttnP p) {
 
   // copies of block t (blocks past the last re-read the last) into buffer t % R: this wave's 1 KB pieces
   // d = w CPW .. + CPW - 1 of K and of V, 4 rows each; lane l fills row 4 d + l / 16, slot l % 16 with
-  // chunk (l % 16) ^ (row % 16); rows past Lk repeat row Lk - 1 (masked below)
+  // chunk (l % 16) ^ (row % 16); in the last block rows past Lk repeat row Lk - 1 (masked below).  The
+  // lane's offsets within a block are computed once.
+  int src_off[CPW];
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    const int row = 4 * (w * CPW + c) + (lane >> 4);
+    src_off[c] = row * (int)krow + 8 * ((lane & 15) ^ (row & 15));
+  }
   auto issue = [&](int t) __attribute__((always_inline)) {
     const int k0 = min(t, T - 1) * KBP;
     unsigned char* buf = smem + (size_t)(t % R) * BUFE * 2;
+    const u16* kb = kc + (size_t)k0 * krow;
+    const u16* vb = vc + (size_t)k0 * krow;
+    if (k0 + KBP <= Lk) {
 #pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-      const int d = w * CPW + c, row = 4 * d + (lane >> 4);
-      const int chunk = (lane & 15) ^ (row & 15);
-      const size_t src = (size_t)min(k0 + row, Lk - 1) * krow + 8 * chunk;
-      lds_copy16(kc + src, buf + (size_t)d * 1024);
-      lds_copy16(vc + src, buf + (size_t)KBP * HD * 2 + (size_t)d * 1024);
+      for (int c = 0; c < CPW; ++c) {
+        const int d = w * CPW + c;
+        lds_copy16(kb + src_off[c], buf + (size_t)d * 1024);
+        lds_copy16(vb + src_off[c], buf + (size_t)KBP * HD * 2 + (size_t)d * 1024);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < CPW; ++c) {
+        const int d = w * CPW + c, row = 4 * d + (lane >> 4);
+        const int src = (min(k0 + row, Lk - 1) - k0) * (int)krow + 8 * ((lane & 15) ^ (row & 15));
+        lds_copy16(kb + src, buf + (size_t)d * 1024);
+        lds_copy16(vb + src, buf + (size_t)KBP * HD * 2 + (size_t)d * 1024);
+      }
     }
   };
 #pragma unroll
   for (int t = 0; t < D; ++t) issue(t);
 
   // this lane's query: qi = 16 tile + lr (lanes past the stacked rows read row 0 and store nothing)
-  const int tile = x * NW + w;
+  const int tile = x * NQW + qw;
   const int qi = tile * 16 + lr;
   const bool qvalid = tile < QT && qi < QR;
   const int hh = qvalid ? qi / a.rows : 0;
@@ -1307,32 +1331,46 @@ void attn_seq_kernel(AttnP p) {
 #pragma unroll
   for (int dt = 0; dt < DT16; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // one key block against the wave's query tile
+  // LDS byte offsets of this lane's fragments within a buffer: K row kp0 + lr, chunk lg + 4 ds (+ 16 rows
+  // = 4096 bytes per score tile kt); V^T read at key kp0 + 4 lg + lr / 4, dims 16 dt + 4 (lr % 4) .. + 3
+  // (+ 16 keys = 4096 bytes for the second half of a 32-key step, + 8192 per step); swizzled chunks
+  const int kp0 = kh * KPP;  // the part's first key within a block
+  uint32_t koff[4], voff[DT16];
+#pragma unroll
+  for (int ds = 0; ds < 4; ++ds) koff[ds] = 2 * ((kp0 + lr) * HD + 8 * ((lg + 4 * ds) ^ lr));
+#pragma unroll
+  for (int dt = 0; dt < DT16; ++dt) {
+    const int row = kp0 + 4 * lg + (lr >> 2), dim = 16 * dt + 4 * (lr & 3);
+    voff[dt] = 2 * (KBP * HD + row * HD + 8 * ((dim >> 3) ^ (row & 15)) + (dim & 7));
+  }
+  const uint32_t lds0 = lds_addr(smem);
+
+  // this wave's part of one key block against its query tile
   auto compute = [&](int t) __attribute__((always_inline)) {
-    const u16* kbuf = lds16 + (size_t)(t % R) * BUFE;
-    const u16* vbuf = kbuf + KBP * HD;
-    const int k0 = t * KBP;
-    // S^T = K Q^T: lane holds S^T[key k0 + 16 kt + 4 lg + e][query lr]; K row 16 kt + lr, chunk lg + 4 ds
-    // (the block's 16 fragments read at once, then one wait)
-    u32x4 kf[16];
-    const uint32_t kbase = lds_addr(kbuf);
+    const uint32_t bufb = lds0 + (uint32_t)(t % R) * (BUFE * 2);
+    const int k0 = t * KBP + kp0;   // the part's first key in the sequence
+    // S^T = K Q^T: lane holds S^T[key k0 + 16 kt + 4 lg + e][query lr] (the part's fragments read at
+    // once, then one wait)
+    u32x4 kf[KT * 4];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int ds = 0; ds < 4; ++ds)
-        kf[kt * 4 + ds] = ds_read16(kbase + 2 * ((16 * kt + lr) * HD + 8 * ((lg + 4 * ds) ^ lr)));
+    for (int ds = 0; ds < 4; ++ds) {
+      const uint32_t ka = bufb + koff[ds];
+      static_for<0, KT>([&](auto kt) __attribute__((always_inline)) {
+        kf[decltype(kt)::value * 4 + ds] = ds_read16<decltype(kt)::value * 4096>(ka);
+      });
+    }
     lds_wait(kf);
-    f32x4 s[4];
+    f32x4 s[KT];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
+    for (int kt = 0; kt < KT; ++kt) {
       s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ds = 0; ds < 4; ++ds) s[kt] = mfma16<DT>(kf[kt * 4 + ds], qf[ds], s[kt]);
     }
     float mx = -INFINITY;
-    if (k0 + KBP <= Lk) {
+    if (k0 + KPP <= Lk) {
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           s[kt][e] *= c2;
@@ -1340,7 +1378,7 @@ void attn_seq_kernel(AttnP p) {
         }
     } else {
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float v = k0 + 16 * kt + 4 * lg + e < Lk ? s[kt][e] * c2 : -INFINITY;
@@ -1354,7 +1392,7 @@ void attn_seq_kernel(AttnP p) {
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
     float ps = 0.f;
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
+    for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float pe = __builtin_amdgcn_exp2f(s[kt][e] - m_use);
@@ -1369,30 +1407,28 @@ void attn_seq_kernel(AttnP p) {
 #pragma unroll
       for (int dt = 0; dt < DT16; ++dt) o[dt] *= alpha;
     }
-    u32x4 pb[2];
+    u32x4 pb[KS];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int ks = 0; ks < KS; ++ks)
       pb[ks] = u32x4{pack_f32x2<DT>(s[2 * ks][0], s[2 * ks][1]), pack_f32x2<DT>(s[2 * ks][2], s[2 * ks][3]),
                      pack_f32x2<DT>(s[2 * ks + 1][0], s[2 * ks + 1][1]),
                      pack_f32x2<DT>(s[2 * ks + 1][2], s[2 * ks + 1][3])};
-    // O^T += V^T P^T over the block's two 32-key k steps: V^T fragments by the transposing read (this
-    // lane supplies key 32 ks + 4 lg + lr / 4 (+ 16 for the second half), dims 16 dt + 4 (lr % 4) .. + 3),
-    // all 32 reads issued after the scores were formed, then one wait
-    u32x2 vh[2 * DT16 * 2];
-    const uint32_t vbase = lds_addr(vbuf);
+    // O^T += V^T P^T over the part's 32-key k steps: V^T fragments by the transposing read (this lane
+    // supplies key kp0 + 32 ks + 4 lg + lr / 4 (+ 16 for the second half), dims 16 dt + 4 (lr % 4) .. + 3),
+    // all issued after the scores were formed, then one wait
+    u32x2 vh[KS * DT16 * 2];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int dt = 0; dt < DT16; ++dt)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const int row = 32 * ks + 16 * hf + 4 * lg + (lr >> 2);
-          const int dim = 16 * dt + 4 * (lr & 3);
-          vh[(ks * DT16 + dt) * 2 + hf] = ds_read_tr16(vbase + 2 * (row * HD + 8 * ((dim >> 3) ^ (row & 15)) + (dim & 7)));
-        }
+    for (int dt = 0; dt < DT16; ++dt) {
+      const uint32_t va = bufb + voff[dt];
+      static_for<0, KS>([&](auto ks) __attribute__((always_inline)) {
+        constexpr int KSI = decltype(ks)::value;
+        vh[(KSI * DT16 + dt) * 2] = ds_read_tr16<KSI * 8192>(va);
+        vh[(KSI * DT16 + dt) * 2 + 1] = ds_read_tr16<KSI * 8192 + 4096>(va);
+      });
+    }
     lds_wait(vh);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int dt = 0; dt < DT16; ++dt) {
         const u32x2 h0 = vh[(ks * DT16 + dt) * 2], h1 = vh[(ks * DT16 + dt) * 2 + 1];
@@ -1419,10 +1455,42 @@ void attn_seq_kernel(AttnP p) {
   static_for<0, D - 1>([&](auto uc) __attribute__((always_inline)) {
     if (t0 + decltype(uc)::value < T) iter(t0 + decltype(uc)::value, std::false_type{});
   });
-  wait_vmcnt<0>();  // no copy may still be writing LDS when the workgroup ends
+  wait_vmcnt<0>();  // no copy may still be writing LDS when the parts are merged in it
 
+  float L = l_run;
+  if constexpr (KH > 1) {
+    // merge the key parts in LDS, in part order (the chunk kernel's merge): parts > 0 leave (m, l) and O^T,
+    // part 0 combines them
+    __syncthreads();  // every wave is done with the key buffers the merge overwrites
+    float* cm = reinterpret_cast<float*>(smem);
+    float* cl = cm + KH * NQW * 16;
+    f32x4* co = reinterpret_cast<f32x4*>(cl + KH * NQW * 16);
+    if (lg == 0) {
+      cm[(kh * NQW + qw) * 16 + lr] = m_run;
+      cl[(kh * NQW + qw) * 16 + lr] = l_run;
+    }
+    if (kh > 0) {
+#pragma unroll
+      for (int dt = 0; dt < DT16; ++dt) co[(((kh - 1) * NQW + qw) * DT16 + dt) * 64 + lane] = o[dt];
+    }
+    __syncthreads();
+    if (kh > 0) return;
+    float M = -INFINITY;
+    for (int k = 0; k < KH; ++k) M = fmaxf(M, cm[(k * NQW + qw) * 16 + lr]);
+    const float Mu = M == -INFINITY ? 0.f : M;
+    L = 0.f;
+    for (int k = 0; k < KH; ++k) L += cl[(k * NQW + qw) * 16 + lr] * __builtin_amdgcn_exp2f(cm[(k * NQW + qw) * 16 + lr] - Mu);
+    const float f0 = __builtin_amdgcn_exp2f(cm[qw * 16 + lr] - Mu);
+#pragma unroll
+    for (int dt = 0; dt < DT16; ++dt) o[dt] *= f0;
+    for (int k = 1; k < KH; ++k) {
+      const float fk = __builtin_amdgcn_exp2f(cm[(k * NQW + qw) * 16 + lr] - Mu);
+#pragma unroll
+      for (int dt = 0; dt < DT16; ++dt) o[dt] += co[(((k - 1) * NQW + qw) * DT16 + dt) * 64 + lane] * fk;
+    }
+  }
   if (!qvalid) return;
-  const float inv = 1.0f / l_run;
+  const float inv = 1.0f / L;
   u16* dst = a.out + (size_t)r * a.nq * HD + (g * grp + hh) * HD + 4 * lg;
 #pragma unroll
   for (int dt = 0; dt < DT16; ++dt)

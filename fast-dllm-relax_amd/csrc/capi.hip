@@ -280,8 +280,8 @@ int run_attention(fdllm_ctx* c, int rows, uint16_t* kc, uint16_t* vc, int ws, in
   // batched calls without a mask take attn_seq_kernel (every key of a sequence in one workgroup, no
   // partials) from 32 rows per sequence, or when the chunk plan cannot cover the longest sequence in one
   // step; otherwise the chunk kernel.  Measured on config 4 (16 sequences, prefixes up to 1024): 32 rows
-  // 23.2 + 4.3 us (RoPE / KV append pass) against 21.6 + 8.5 us (chunks + merge); 8 rows 24.1 + 4.3 us
-  // against 11.8 + 4 us (each workgroup walks all of its sequence's keys, one 64-key block at a time)
+  // 17.0 + 4.8 us (RoPE / KV append pass) against 22.2 + 8.4 us (chunks + merge); at 8 rows the chunk
+  // kernel keeps the job (11.4 + 4.3 us: each workgroup of this kernel walks all of its sequence's keys)
   const bool seq_kernel = sb != nullptr && c->seq_attn && mask == 0 && (sb->rows >= 32 || !pl.chunked);
   if (sb != nullptr && !seq_kernel && !pl.chunked)
     return fail(FDLLM_EINVAL, "batched call of %d rows per sequence over %d keys is too long for one step", a.rows, a.Lk);

@@ -320,17 +320,21 @@ __device__ __forceinline__ void lds_copy16(const u16* g, unsigned char* l) {
 // writes), which drains a copy pipeline on every block; in asm the read is invisible to that pass.  So the
 // caller must (1) have waited for and published (barrier) the copies that wrote the bytes it reads, and
 // (2) wait for the results with lds_wait() before using them.  `lds` is an LDS byte address.
+template <int OFF = 0>
 __device__ __forceinline__ u32x2 ds_read_tr16(uint32_t lds) {
+  static_assert(OFF >= 0 && OFF < 65536, "16-bit immediate offset");
   u32x2 r;
-  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(lds) : "memory");
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(lds), "i"(OFF) : "memory");
   return r;
 }
 // ds_read_b128 in asm, for blocks of LDS reads the caller waits for at once (lds_wait): the compiler,
 // left to itself, interleaves such reads with their MFMAs and waits for each pair (the whole LDS latency
 // per pair).  Same contract as ds_read_tr16.
+template <int OFF = 0>
 __device__ __forceinline__ u32x4 ds_read16(uint32_t lds) {
+  static_assert(OFF >= 0 && OFF < 65536, "16-bit immediate offset");
   u32x4 r;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(lds) : "memory");
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(lds), "i"(OFF) : "memory");
   return r;
 }
 // Wait for every outstanding LDS read (lgkmcnt(0)) and make the registers v depend on the wait, so no use

@@ -244,6 +244,9 @@ GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol) {
       // 18.9 us split three ways with the epilogue launch
       int target = a.M <= 128 ? pol.target_wgs / 2 : pol.target_wgs;
       if (cfg == CFG_OPROJ) target /= 4;
+      // qkv on the 64 x 128 register-weight blocks half: 17.1 against 20.4 us at 512 rows (128 workgroups
+      // without a split against 256 with one), 13.8 against 14.5 at 128 (two splits against four)
+      if (cfg == CFG_QKV && id == MM_WR_S) target /= 2;
       int split = 1;
       const int max_split = id == MM_WR || id == MM_WR_S ? 16 : 8;
       for (int d = 2; d <= max_split && wgs * split < target && cfg != CFG_LM_HEAD; ++d)
