@@ -39,10 +39,7 @@ template <int DT> __device__ __forceinline__ float elem(const u32x4& v, int e) {
 // the (cos, sin) entries i0 .. i0 + 7 of the position's table row (cuda.py:314-315 with _rotate_half
 // 207-209: q' = q cos + rot(q) sin, every product and sum rounded to the model dtype).
 template <int DT>
-__device__ __forceinline__ void rope_tab(u32x4& lo, u32x4& hi, const float* cs) {
-  f32x4 t[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) t[c] = *reinterpret_cast<const f32x4*>(cs + 4 * c);
+__device__ __forceinline__ void rope_pairs(u32x4& lo, u32x4& hi, const f32x4 (&t)[4]) {
   u16 o1[8], o2[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -56,6 +53,13 @@ __device__ __forceinline__ void rope_tab(u32x4& lo, u32x4& hi, const float* cs) 
     lo[c] = pack2(o1[2 * c], o1[2 * c + 1]);
     hi[c] = pack2(o2[2 * c], o2[2 * c + 1]);
   }
+}
+template <int DT>
+__device__ __forceinline__ void rope_tab(u32x4& lo, u32x4& hi, const float* cs) {
+  f32x4 t[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) t[c] = *reinterpret_cast<const f32x4*>(cs + 4 * c);
+  rope_pairs<DT>(lo, hi, t);
 }
 
 // Output element (row r, column c = head x 128 + dim): row-major [rows][nq x 128], or MFMA-fragment
@@ -303,21 +307,27 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
 // workgroups produce the qkv rows; the kernel below uses plain accesses.
 enum ChunkPart : int { CHUNK_ALL = 0, CHUNK_CACHE = 1, CHUNK_WINDOW = 2 };
 
-template <int QPW, int KH, int CH>
+// WCS: also hold the RoPE (cos, sin) entries of items whose key is one of this call's rows, requested
+// with the K/V (the persistent step, which keeps these registers live across a wait, leaves it off)
+template <int QPW, int KH, int CH, bool WCS = false>
 struct AttnChunkRegs {
   static constexpr int NT = 64 * QPW * KH;
   static constexpr int KIT = (CH * 8 + NT - 1) / NT;        // K items (rotation-pair chunks) per thread
   static constexpr int VIT = ((CH / 4) * 16 + NT - 1) / NT;  // V items (key quad x dim chunk) per thread
+  static constexpr bool wcs = WCS;
   u32x4 klo[KIT], khi[KIT], vv[VIT][4];
+  f32x4 kcs[WCS ? KIT : 1][4];
 };
 
-// Item -> (key, chunk) maps: 16 consecutive lanes take 16 keys of one K chunk, and 32 consecutive lanes
-// take 16 key quads x 2 dim chunks of V, so the LDS stores of attn_chunk_compute hit 64 distinct banks
+// Item -> (key, chunk) maps: 16 consecutive lanes take 16 keys of one K chunk (with, for this call's own
+// rows, the key's RoPE table entries, so the RoPE at staging waits for no further load), and 32
+// consecutive lanes take 16 key quads x 2 dim chunks of V, so the LDS stores of attn_chunk_compute hit 64 distinct banks
 // per pass (rows are 68 dwords apart, 4 banks on).  Rows past kend read row kbeg and are masked or
 // zeroed later.
-template <int QPW, int KH, int CH, bool COH, int PART>
-__device__ __forceinline__ void attn_chunk_load(const AttnP& a, int by, int bz, AttnChunkRegs<QPW, KH, CH>& R, int tid) {
-  typedef AttnChunkRegs<QPW, KH, CH> Regs;
+template <int QPW, int KH, int CH, bool COH, int PART, bool WCS = false>
+__device__ __forceinline__ void attn_chunk_load(const AttnP& a, int by, int bz, AttnChunkRegs<QPW, KH, CH, WCS>& R,
+                                                int tid) {
+  typedef AttnChunkRegs<QPW, KH, CH, WCS> Regs;
   constexpr int NT = Regs::NT, KIT = Regs::KIT, VIT = Regs::VIT;
   const int g = by;
   const size_t krow = (size_t)a.nkv * HD;
@@ -337,6 +347,11 @@ __device__ __forceinline__ void attn_chunk_load(const AttnP& a, int by, int bz, 
         const u16* src = kq_base + (size_t)(key - a.ws) * a.ldq;
         R.klo[it] = ld16<COH>(src + 8 * p);
         R.khi[it] = ld16<COH>(src + 64 + 8 * p);
+        if constexpr (WCS) {
+          const float* cs = a.rope + (size_t)(key - a.ws) * 128 + 16 * p;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) R.kcs[it][c] = *reinterpret_cast<const f32x4*>(cs + 4 * c);
+        }
       }
     } else if (PART != CHUNK_WINDOW) {
       const u16* src = a.kc + key * krow + g * HD;
@@ -362,10 +377,10 @@ __device__ __forceinline__ void attn_chunk_load(const AttnP& a, int by, int bz, 
   }
 }
 
-template <int DT, int QPW, int KH, int CH, int MASK, bool COH>
+template <int DT, int QPW, int KH, int CH, int MASK, bool COH, bool WCS = false>
 __device__ __forceinline__ void attn_chunk_compute(const AttnP& a, int bx, int by, int bz, unsigned char* smem,
-                                                   AttnChunkRegs<QPW, KH, CH>& R, int tid) {
-  typedef AttnChunkRegs<QPW, KH, CH> Regs;
+                                                   AttnChunkRegs<QPW, KH, CH, WCS>& R, int tid) {
+  typedef AttnChunkRegs<QPW, KH, CH, WCS> Regs;
   constexpr int NT = Regs::NT, KIT = Regs::KIT, VIT = Regs::VIT;
   constexpr int VLDC = CH + 8;                        // u16 stride of a transposed V row
   constexpr int DT16 = HD / 16;
@@ -426,7 +441,8 @@ __device__ __forceinline__ void attn_chunk_compute(const AttnP& a, int bx, int b
     if (key >= kend) {
       lo = hi = u32x4{0u, 0u, 0u, 0u};
     } else if (key >= a.ws && key < a.ws + a.rows) {
-      rope_tab<DT>(lo, hi, a.rope + (size_t)(key - a.ws) * 128 + 16 * p);
+      if constexpr (WCS) rope_pairs<DT>(lo, hi, R.kcs[it]);
+      else rope_tab<DT>(lo, hi, a.rope + (size_t)(key - a.ws) * 128 + 16 * p);
       if (writer) {
         u16* dst = a.kc + key * krow + g * HD;
         *reinterpret_cast<u32x4*>(dst + 8 * p) = lo;
@@ -606,9 +622,9 @@ __device__ __forceinline__ void attn_chunk_compute(const AttnP& a, int bx, int b
 
 template <int DT, int QPW, int KH, int CH, int MASK, bool COH>
 __device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, int bz, unsigned char* smem) {
-  AttnChunkRegs<QPW, KH, CH> R;
-  attn_chunk_load<QPW, KH, CH, COH, CHUNK_ALL>(a, by, bz, R, threadIdx.x);
-  attn_chunk_compute<DT, QPW, KH, CH, MASK, COH>(a, bx, by, bz, smem, R, threadIdx.x);
+  AttnChunkRegs<QPW, KH, CH, true> R;
+  attn_chunk_load<QPW, KH, CH, COH, CHUNK_ALL, true>(a, by, bz, R, threadIdx.x);
+  attn_chunk_compute<DT, QPW, KH, CH, MASK, COH, true>(a, bx, by, bz, smem, R, threadIdx.x);
 }
 
 // Batched call: the view of sequence b (its rows, cache, window and split partials) in a, a copy of the
