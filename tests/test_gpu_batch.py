@@ -205,3 +205,35 @@ def test_seq_attention_kernel_matches_chunk_kernel(monkeypatch):
     bf16_parity("seq vs chunk attention, partial step hidden", out["seq"][3], out["chunk"][3])
     for vm in vms.values():
         vm.close()
+
+
+def test_batched_step_beyond_one_step_key_split_plan(wide2):
+    """A batched call whose longest prefix (8300 keys) is past the chunk kernel's one-step plan (64 chunks of
+    128 keys): attn_seq_kernel streams every key, so the call runs; each sequence's hidden states match the
+    batch-1 cached forward of the same sequence (the long-block loop kernel) to the bf16 criterion."""
+    _, vm = wide2
+    kw = WIDE2
+    rng = np.random.default_rng(43)
+    prefixes = [8300, 100]
+    L, nkv, hd = kw["num_hidden_layers"], kw["num_key_value_heads"], kw["head_dim"]
+    R = 32
+    cap = max(prefixes) + R
+    ids = [rng.integers(0, kw["vocab_size"] - 1, P + R) for P in prefixes]
+    k = torch.zeros((L, len(prefixes), cap, nkv, hd), dtype=vm.torch_dtype, device="cuda")
+    v = torch.zeros_like(k)
+    log(f"case: batched step over prefixes {prefixes} (build_prefix_cache_seq)")
+    for b, P in enumerate(prefixes):
+        vm.build_prefix_cache_seq(vm.embed(_dev_ids(ids[b][:P]))[None], None, k, v, b)
+    x = torch.stack([vm.embed(_dev_ids(ids[b][P:])) for b, P in enumerate(prefixes)])
+    k1, v1 = k.clone(), v.clone()
+    off = torch.tensor(prefixes, dtype=torch.int32, device="cuda")
+    h = vm.forward_cached_batch(x, k, v, off, prefixes)
+    torch.cuda.synchronize()
+    for b, P in enumerate(prefixes):
+        log(f"case: batch-1 forward_cached of sequence {b} (prefix {P})")
+        kb = k1[:, b:b + 1].contiguous()
+        vb = v1[:, b:b + 1].contiguous()
+        hb = vm.forward_cached(x[b:b + 1], kb, vb, torch.tensor(P, dtype=torch.int32, device="cuda"), P)
+        torch.cuda.synchronize()
+        bf16_parity(f"batched vs batch-1, sequence {b} hidden", to_np(h[b]), to_np(hb[0]))
+        bf16_parity(f"batched vs batch-1, sequence {b} K rows", to_np(k[:, b, P:P + R]), to_np(kb[:, 0, P:P + R]))
