@@ -179,7 +179,8 @@ using WrBig = WrCfg<8, 4, FD_WR_DEPTH>;  // 128 x 256
 #define FD_WR_SMALL_DEPTH 8
 #endif
 using WrSmall = WrCfg<4, 2, FD_WR_SMALL_DEPTH>;  // 64 x 128
-enum MmId : int { MM_SMALL = 0, MM_WIDE = 1, MM_WIDE_D = 2, MM_BIG = 3, MM_WT = 4, MM_WR = 5, MM_WR_S = 6 };
+using WrMid = WrCfg<8, 2, 6>;    // 128 x 128 (six stages: 56 KB of LDS)
+enum MmId : int { MM_SMALL = 0, MM_WIDE = 1, MM_WIDE_D = 2, MM_BIG = 3, MM_WT = 4, MM_WR = 5, MM_WR_S = 6, MM_WR_M = 7 };
 struct MmInfo { int bm, bn_tiles, kss; };
 template <class M> constexpr MmInfo mm_info_of() { return MmInfo{M::bm, M::bn_tiles, M::kss}; }
 static MmInfo mm_info(int id) {
@@ -190,6 +191,7 @@ static MmInfo mm_info(int id) {
     case MM_WT: return mm_info_of<WtBig>();
     case MM_WR: return mm_info_of<WrBig>();
     case MM_WR_S: return mm_info_of<WrSmall>();
+    case MM_WR_M: return mm_info_of<WrMid>();
     default: return mm_info_of<MmSmall>();
   }
 }
@@ -210,6 +212,16 @@ static int mm_choice(int cfg, int M, int ntiles, const MmPolicy& pol) {
   // 23.3 / 26.4 at 2048 (equal below 384)
   if (M >= 33 && ((pol.wr_small_ops >> cfg) & 1) && (cfg == CFG_QKV || (cfg == CFG_OPROJ && M < 2048)))
     return MM_WR_S;
+  // gate_up and down below 256 rows: register-weight blocks too (us per launch, gate_up including its norm
+  // pass; LDS-staged kernel / 64 x 128 / 128 x 128 blocks): gate_up 24.8 / 21.3 / 22.7 at 64 rows, 30.0 /
+  // 29.9 / 26.1 at 128, 38.6 / 29.5 / 35.6 at 192; down 21.4 / 16.8 / 18.0, 21.4 / 18.0 / 20.8, 27.1 / 24.7 /
+  // 25.2.  The 128 x 128 blocks win where they make one round of workgroups and the 64 x 128 ones two.
+  if (M >= 33 && M < 256 && (cfg == CFG_GATE_UP || cfg == CFG_DOWN)) {
+    const int sh = cfg == CFG_GATE_UP ? 0 : 1;
+    const int ffn = pol.wr_ffn >= 0 ? pol.wr_ffn : (M > 64 && M <= 128 ? 4 | 2 : 1 | 2);
+    if ((ffn >> sh) & 1) return MM_WR_S;
+    if ((ffn >> (sh + 2)) & 1) return MM_WR_M;
+  }
   switch (cfg) {
     case CFG_LM_HEAD: return MM_WIDE;  // one 256-column confidence tile per block column
     case CFG_GATE_UP:
@@ -248,7 +260,7 @@ GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol) {
       // without a split against 256 with one), 13.8 against 14.5 at 128 (two splits against four)
       if (cfg == CFG_QKV && id == MM_WR_S) target /= 2;
       int split = 1;
-      const int max_split = id == MM_WR || id == MM_WR_S ? 16 : 8;
+      const int max_split = id == MM_WR || id == MM_WR_S || id == MM_WR_M ? 16 : 8;
       for (int d = 2; d <= max_split && wgs * split < target && cfg != CFG_LM_HEAD; ++d)
         if (nst % d == 0 && nst / d >= pol.min_stages) split = d;
       p.ksplit = split;
@@ -367,7 +379,11 @@ template <int DT, int CFG, class C>
 static hipError_t launch_mm(const GemmP& a, const GemmPlan& p, hipStream_t st) {
   if (p.mm_id == MM_WR) return launch_wr_cfg<DT, C::epi, WrBig>(a, p, st);
   if (p.mm_id == MM_WR_S) {
-    if constexpr (CFG == CFG_QKV || CFG == CFG_OPROJ) return launch_wr_cfg<DT, C::epi, WrSmall>(a, p, st);
+    if constexpr (CFG != CFG_LM_HEAD) return launch_wr_cfg<DT, C::epi, WrSmall>(a, p, st);
+    return hipErrorInvalidValue;
+  }
+  if (p.mm_id == MM_WR_M) {
+    if constexpr (CFG == CFG_GATE_UP || CFG == CFG_DOWN) return launch_wr_cfg<DT, C::epi, WrMid>(a, p, st);
     return hipErrorInvalidValue;
   }
   if constexpr (CFG == CFG_GATE_UP) {
@@ -418,7 +434,7 @@ bool gemm_takes_frag(int cfg, const GemmPlan& p) {
 }
 
 bool gemm_takes_blocks(const GemmPlan& p) {
-  return p.kind == GK_MM && (p.mm_id == MM_WT || p.mm_id == MM_WR || p.mm_id == MM_WR_S);
+  return p.kind == GK_MM && (p.mm_id == MM_WT || p.mm_id == MM_WR || p.mm_id == MM_WR_S || p.mm_id == MM_WR_M);
 }
 
 hipError_t launch_gemm(int dt, int cfg, const GemmP& a, const GemmPlan& p, hipStream_t st) {

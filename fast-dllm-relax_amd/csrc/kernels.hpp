@@ -69,6 +69,9 @@ struct MmPolicy {
   int wr_ops = (1 << CFG_QKV) | (1 << CFG_OPROJ) | (1 << CFG_GATE_UP) | (1 << CFG_DOWN) | (1 << CFG_LM_HEAD);
   int wr_min_rows = 0;
   int wr_small_ops = (1 << CFG_QKV) | (1 << CFG_OPROJ);  // take the 64 x 128 register-weight blocks below the 128 x 256 ones
+  // gate_up / down below 256 rows: -1 the measured choice of register-weight blocks, else bit 0 / 1 the 64 x 128
+  // blocks, bit 2 / 3 the 128 x 128 ones (0: the LDS-staged kernel)
+  int wr_ffn = -1;
 };
 GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol = MmPolicy{});
 // whether the plan runs the one-shot register-fragment body, the only one that takes xfrag / yfrag 1

@@ -63,6 +63,40 @@ def test_register_weight_kernel_bit_identical(dtype, monkeypatch):
         np.testing.assert_array_equal(_bits(h_small), _bits(h_old), err_msg=f"S={S}, 64 x 128 blocks")
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_small_m_ffn_register_weight_bit_identical(dtype, monkeypatch):
+    """Below 256 rows gate_up and down take the register-weight kernel's 64 x 128 or 128 x 128 blocks by
+    default (FDLLM_WR_FFN: bits 0 / 1 the 64 x 128 blocks for gate_up / down, bits 2 / 3 the 128 x 128 ones,
+    0 the LDS-staged gemm_mm_kernel); with k splits off all three accumulate each output's k steps in
+    order, so the hidden states agree bit for bit."""
+    from fast_dllm_relax_amd.config import FastDLLMConfig
+    from fast_dllm_relax_amd.params import from_numpy
+    from fast_dllm_relax_amd.vm import HipVM
+    from oracle.model import OracleConfig, random_params
+
+    kw = WIDE2
+    params = from_numpy(random_params(OracleConfig(**kw), 9, dtype), FastDLLMConfig(**kw), dtype=dtype)
+    vms = {}
+    for name, ffn in (("mm", 0), ("64x128", 3), ("128x128", 12)):
+        monkeypatch.setenv("FDLLM_WR_FFN", str(ffn))
+        monkeypatch.setenv("FDLLM_MM_TARGET_WGS", "1")
+        vms[name] = HipVM(FastDLLMConfig(**kw), params, dtype=dtype, max_rows=256)
+        monkeypatch.delenv("FDLLM_WR_FFN")
+        monkeypatch.delenv("FDLLM_MM_TARGET_WGS")
+    rng = np.random.default_rng(19)
+    for S in (40, 100, 200):
+        log(f"case: forward_hidden {S} rows, 1.5B width, 2 layers, {dtype}, FFN register-weight blocks vs gemm_mm")
+        ids = torch.tensor(rng.integers(0, kw["vocab_size"] - 1, S), dtype=torch.int32, device="cuda")
+        x = vms["mm"].embed(ids)[None]
+        h = {name: vm.forward_hidden(x, None) for name, vm in vms.items()}
+        torch.cuda.synchronize()
+        assert torch.isfinite(h["64x128"].float()).all()
+        for name in ("64x128", "128x128"):
+            np.testing.assert_array_equal(_bits(h[name]), _bits(h["mm"]), err_msg=f"S={S}, {name}")
+    for vm in vms.values():
+        vm.close()
+
+
 def _prefill_vm(kw, params, dtype, monkeypatch, pair, max_rows):
     from fast_dllm_relax_amd.config import FastDLLMConfig
     from fast_dllm_relax_amd.vm import HipVM
