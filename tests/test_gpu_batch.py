@@ -237,3 +237,32 @@ def test_batched_step_beyond_one_step_key_split_plan(wide2):
         torch.cuda.synchronize()
         bf16_parity(f"batched vs batch-1, sequence {b} hidden", to_np(h[b]), to_np(hb[0]))
         bf16_parity(f"batched vs batch-1, sequence {b} K rows", to_np(k[:, b, P:P + R]), to_np(kb[:, 0, P:P + R]))
+
+
+def test_batched_step_ragged_query_tiles(wide2):
+    """40 rows per sequence: 240 stacked query rows per kv head, so the last query tile is part padding (and
+    the chunk plan, at most 12 tiles, does not cover it); each sequence's hidden states and appended K rows
+    match its batch-1 cached forward to the bf16 criterion."""
+    _, vm = wide2
+    kw = WIDE2
+    rng = np.random.default_rng(47)
+    prefixes, R = [64, 250, 97], 40
+    L, nkv, hd = kw["num_hidden_layers"], kw["num_key_value_heads"], kw["head_dim"]
+    cap = max(prefixes) + R
+    ids = [rng.integers(0, kw["vocab_size"] - 1, P + R) for P in prefixes]
+    k = torch.zeros((L, len(prefixes), cap, nkv, hd), dtype=vm.torch_dtype, device="cuda")
+    v = torch.zeros_like(k)
+    for b, P in enumerate(prefixes):
+        vm.build_prefix_cache_seq(vm.embed(_dev_ids(ids[b][:P]))[None], None, k, v, b)
+    x = torch.stack([vm.embed(_dev_ids(ids[b][P:])) for b, P in enumerate(prefixes)])
+    k1, v1 = k.clone(), v.clone()
+    log(f"case: batched step, {R} rows per sequence, prefixes {prefixes}")
+    h = vm.forward_cached_batch(x, k, v, torch.tensor(prefixes, dtype=torch.int32, device="cuda"), prefixes)
+    torch.cuda.synchronize()
+    for b, P in enumerate(prefixes):
+        kb, vb = k1[:, b:b + 1].contiguous(), v1[:, b:b + 1].contiguous()
+        hb = vm.forward_cached(x[b:b + 1], kb, vb, torch.tensor(P, dtype=torch.int32, device="cuda"), P)
+        torch.cuda.synchronize()
+        bf16_parity(f"{R}-row batched vs batch-1, sequence {b} hidden", to_np(h[b]), to_np(hb[0]))
+        bf16_parity(f"{R}-row batched vs batch-1, sequence {b} K rows", to_np(k[:, b, P:P + R]),
+                    to_np(kb[:, 0, P:P + R]))
