@@ -180,7 +180,8 @@ using WrBig = WrCfg<8, 4, FD_WR_DEPTH>;  // 128 x 256
 #endif
 using WrSmall = WrCfg<4, 2, FD_WR_SMALL_DEPTH>;  // 64 x 128
 using WrMid = WrCfg<8, 2, 6>;    // 128 x 128 (six stages: 56 KB of LDS)
-enum MmId : int { MM_SMALL = 0, MM_WIDE = 1, MM_WIDE_D = 2, MM_BIG = 3, MM_WT = 4, MM_WR = 5, MM_WR_S = 6, MM_WR_M = 7 };
+using WrTiny = WrCfg<4, 1, 12>;  // 64 x 64 (4 MFMAs per k step and wave: twelve stages in flight)
+enum MmId : int { MM_SMALL = 0, MM_WIDE = 1, MM_WIDE_D = 2, MM_BIG = 3, MM_WT = 4, MM_WR = 5, MM_WR_S = 6, MM_WR_M = 7, MM_WR_T = 8 };
 struct MmInfo { int bm, bn_tiles, kss; };
 template <class M> constexpr MmInfo mm_info_of() { return MmInfo{M::bm, M::bn_tiles, M::kss}; }
 static MmInfo mm_info(int id) {
@@ -192,6 +193,7 @@ static MmInfo mm_info(int id) {
     case MM_WR: return mm_info_of<WrBig>();
     case MM_WR_S: return mm_info_of<WrSmall>();
     case MM_WR_M: return mm_info_of<WrMid>();
+    case MM_WR_T: return mm_info_of<WrTiny>();
     default: return mm_info_of<MmSmall>();
   }
 }
@@ -209,9 +211,11 @@ static int mm_choice(int cfg, int M, int ntiles, const MmPolicy& pol) {
   // qkv and o_proj below that: 64 x 128 register-weight blocks (us per launch, qkv including its norm pass,
   // against the LDS-staged 64 x 128 kernel): qkv 16.2 / 14.9 at 128 rows, 23.2 / 20.2 at 512, 26.2 / 19.4
   // at 1024, 30.8 / 28.6 at 2048; o_proj 15.2 / 14.0 at 384, 15.4 / 14.0 at 512, 19.3 / 15.1 at 1024, but
-  // 23.3 / 26.4 at 2048 (equal below 384)
+  // 23.3 / 26.4 at 2048 (equal below 384).  Up to 512 rows 64 x 64 blocks, twice the workgroups, do better
+  // still (us, 64 x 128 / 64 x 64 blocks): qkv 14.4 / 13.4 at 128 rows, 15.7 / 13.7 at 256, 16.8 / 14.9 at
+  // 512 (but 19.4 / 21.2 at 1024); o_proj 12.8 / 11.9, 12.8 / 11.9, 14.0 / 12.0 (15.1 / 21.4 at 1024)
   if (M >= 33 && ((pol.wr_small_ops >> cfg) & 1) && (cfg == CFG_QKV || (cfg == CFG_OPROJ && M < 2048)))
-    return MM_WR_S;
+    return M <= 512 ? MM_WR_T : MM_WR_S;
   // gate_up and down below 256 rows: register-weight blocks too (us per launch, gate_up including its norm
   // pass; LDS-staged kernel / 64 x 128 / 128 x 128 blocks): gate_up 24.8 / 21.3 / 22.7 at 64 rows, 30.0 /
   // 29.9 / 26.1 at 128, 38.6 / 29.5 / 35.6 at 192; down 21.4 / 16.8 / 18.0, 21.4 / 18.0 / 20.8, 27.1 / 24.7 /
@@ -256,11 +260,11 @@ GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol) {
       // 18.9 us split three ways with the epilogue launch
       int target = a.M <= 128 ? pol.target_wgs / 2 : pol.target_wgs;
       if (cfg == CFG_OPROJ) target /= 4;
-      // qkv on the 64 x 128 register-weight blocks half: 17.1 against 20.4 us at 512 rows (128 workgroups
+      // qkv on the 64 x 128 (and 64 x 64) register-weight blocks half: 17.1 against 20.4 us at 512 rows (128 workgroups
       // without a split against 256 with one), 13.8 against 14.5 at 128 (two splits against four)
-      if (cfg == CFG_QKV && id == MM_WR_S) target /= 2;
+      if (cfg == CFG_QKV && (id == MM_WR_S || id == MM_WR_T)) target /= 2;
       int split = 1;
-      const int max_split = id == MM_WR || id == MM_WR_S || id == MM_WR_M ? 16 : 8;
+      const int max_split = id == MM_WR || id == MM_WR_S || id == MM_WR_M || id == MM_WR_T ? 16 : 8;
       for (int d = 2; d <= max_split && wgs * split < target && cfg != CFG_LM_HEAD; ++d)
         if (nst % d == 0 && nst / d >= pol.min_stages) split = d;
       p.ksplit = split;
@@ -382,6 +386,10 @@ static hipError_t launch_mm(const GemmP& a, const GemmPlan& p, hipStream_t st) {
     if constexpr (CFG != CFG_LM_HEAD) return launch_wr_cfg<DT, C::epi, WrSmall>(a, p, st);
     return hipErrorInvalidValue;
   }
+  if (p.mm_id == MM_WR_T) {
+    if constexpr (CFG == CFG_QKV || CFG == CFG_OPROJ) return launch_wr_cfg<DT, C::epi, WrTiny>(a, p, st);
+    return hipErrorInvalidValue;
+  }
   if (p.mm_id == MM_WR_M) {
     if constexpr (CFG == CFG_GATE_UP || CFG == CFG_DOWN) return launch_wr_cfg<DT, C::epi, WrMid>(a, p, st);
     return hipErrorInvalidValue;
@@ -434,7 +442,7 @@ bool gemm_takes_frag(int cfg, const GemmPlan& p) {
 }
 
 bool gemm_takes_blocks(const GemmPlan& p) {
-  return p.kind == GK_MM && (p.mm_id == MM_WT || p.mm_id == MM_WR || p.mm_id == MM_WR_S || p.mm_id == MM_WR_M);
+  return p.kind == GK_MM && p.mm_id >= MM_WT;
 }
 
 hipError_t launch_gemm(int dt, int cfg, const GemmP& a, const GemmPlan& p, hipStream_t st) {

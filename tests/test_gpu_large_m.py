@@ -3,7 +3,7 @@
 By default gate_up and down run gemm_wr_kernel's 128 x 256 blocks from 2048 rows and qkv and o_proj from
 4096 (FDLLM_WR_OPS selects the projections, one bit per GemmCfg; FDLLM_WR_MIN_ROWS lowers the threshold,
 here to 256 so that ragged and small row counts take it too); below that qkv, and o_proj below 2048 rows,
-run its 64 x 128 blocks (FDLLM_WR_SMALL, bits of qkv and o_proj).  Every large-M kernel accumulates each
+run its 64 x 128 blocks, or up to 512 rows its 64 x 64 blocks (FDLLM_WR_SMALL, bits of qkv and o_proj).  Every large-M kernel accumulates each
 output element's k steps in order in one MFMA chain and shares the epilogues, so with k splits off
 (FDLLM_MM_TARGET_WGS=1) the hidden states must agree bit for bit whichever kernel ran.  Parity of the default configuration with the oracle is
 established by the prefill, forward_hidden and batched-step tests."""
@@ -45,7 +45,7 @@ def test_register_weight_kernel_bit_identical(dtype, monkeypatch):
 
     kw = WIDE2
     params = from_numpy(random_params(OracleConfig(**kw), 5, dtype), FastDLLMConfig(**kw), dtype=dtype)
-    sizes = (300, 512, 1056)
+    sizes = (300, 512, 1056)  # 64 x 64 blocks for qkv / o_proj up to 512 rows, 64 x 128 above
     vm_wr = _vm(kw, params, dtype, monkeypatch, 15, max(sizes))
     vm_old = _vm(kw, params, dtype, monkeypatch, 0, max(sizes))
     vm_small = _vm(kw, params, dtype, monkeypatch, 0, max(sizes), wr_small=3)  # 64 x 128 blocks for qkv, o_proj
