@@ -100,6 +100,7 @@ struct fdllm_ctx {
   int prefill_hpw = 0;    // query heads per prefill-attention workgroup (0: chosen per launch)
   int prefill_pair = 1;   // paired-query-block prefill attention (0 off, 1 when it fills the chip, 2 always)
   int seq_attn = 1;       // batched calls: attn_seq_kernel (0: the chunk kernel with key splits + merge)
+  int fuse_down = 1;      // large-M down launches with k splits: split sum + residual + next RMSNorm in one launch
   int down_split = 10;    // cross-workgroup k splits of the down projection (largest divisor of K/32 <= this)
   MmPolicy mm;              // large-M GEMM planning (k splits, register-weight kernel)
   bool frag_on = true;      // one-shot chains keep activations in MFMA-fragment order (FDLLM_XFRAG=0: row-major)
@@ -224,10 +225,37 @@ int run_gemm(fdllm_ctx* c, int cfg, GemmP a, int ksplit, hipStream_t st) {
   return FDLLM_OK;
 }
 
+// The down projection of a large-M call with its k-split sum, residual and the next RMSNorm (weight
+// next_w) in one launch after the GEMM (launch_resid_norm) instead of the split-sum launch plus a
+// norm_rows launch; y: the normalised rows (yblk: fragment blocks).  Only for launches that split k
+// (fused_down_ok).
+int run_down_fused(fdllm_ctx* c, GemmP a, int ksplit, const uint16_t* next_w, uint16_t* y, int yblk, hipStream_t st);
+
 GemmP gemm_args(const uint16_t* W, int ntiles, int N, int K, const uint16_t* X, int ldx, int M) {
   GemmP a{};
   a.W = W; a.KS = K / 32; a.ntiles = ntiles; a.N = N; a.X = X; a.ldx = ldx; a.M = M; a.kps = a.KS;
   return a;
+}
+
+bool fused_down_ok(const fdllm_ctx* c, GemmP a, int ksplit) {
+  if (!c->fuse_down || a.nw != nullptr || a.N % 4 || a.N > 2048 || a.N % 32) return false;
+  const GemmPlan pl = gemm_plan(CFG_DOWN, a, ksplit, c->mm);
+  return pl.kind == GK_MM && pl.ksplit > 1;
+}
+
+int run_down_fused(fdllm_ctx* c, GemmP a, int ksplit, const uint16_t* next_w, uint16_t* y, int yblk, hipStream_t st) {
+  const fdllm_config& f = c->cfg;
+  const GemmPlan pl = gemm_plan(CFG_DOWN, a, ksplit, c->mm);
+  if (pl.kind != GK_MM || pl.ksplit < 2) return fail(FDLLM_EINVAL, "fused down epilogue needs a k split");
+  int rc = ensure_floats(&c->gpart, &c->gpart_floats, std::max(pl.part_floats, (size_t)pl.ksplit * a.M * a.N));
+  if (rc) return rc;
+  a.part = c->gpart;
+  a.counters = c->counters;
+  a.part_rows = 1;
+  HIPCHK(launch_gemm(f.dtype, CFG_DOWN, a, pl, st));
+  HIPCHK(launch_resid_norm(f.dtype, c->gpart, pl.ksplit, a.M, a.N, (uint16_t*)a.Y, a.ssq_out, a.ssq_ld, next_w,
+                           f.rms_norm_eps, y, yblk, st));
+  return FDLLM_OK;
 }
 
 int run_lm_head(fdllm_ctx* c, const uint16_t* hidden, int rows, float* logits, bool stats, hipStream_t st) {
@@ -451,11 +479,20 @@ int run_layers(fdllm_ctx* c, const void* x_in, int rows, uint16_t* kbase, uint16
     }
   }
   if (frag) ++c->frag_calls;
+  // xn_ready: the previous layer's down launch also normalised this layer's qkv input into c->xn
+  // (run_down_fused), in the layout the qkv launch takes; final_done: the last one wrote out
+  bool xn_ready = false, final_done = false;
+  int xn_layout = 0;
   for (int l = 0; l < f.num_hidden_layers; ++l) {
     const Layer& L = c->layers[l];
     uint16_t* kc = kbase + (size_t)l * layer_stride;
     uint16_t* vc = vbase + (size_t)l * layer_stride;
     LayerGemms g = layer_gemms(c, L, rows, frag);
+    if (xn_ready) {
+      g.q.X = c->xn;
+      g.q.nw = nullptr;
+      g.q.xfrag = xn_layout;
+    }
     rc = run_gemm(c, CFG_QKV, g.q, 1, st);
     if (rc) return rc;
     rc = run_attention(c, rows, kc, vc, write_start, attend_len, mask, bias, bias_ld, st, sb, frag);
@@ -464,10 +501,30 @@ int run_layers(fdllm_ctx* c, const void* x_in, int rows, uint16_t* kbase, uint16
     if (rc) return rc;
     rc = run_gemm(c, CFG_GATE_UP, g.gu, 1, st);
     if (rc) return rc;
+    xn_ready = false;
+    if (!frag && fused_down_ok(c, g.d, g.dsplit)) {
+      if (l + 1 < f.num_hidden_layers) {
+        // the next layer's qkv: its launch takes normalised rows (row-major or fragment blocks)
+        GemmP tq = layer_gemms(c, c->layers[l + 1], rows, frag).q;
+        const GemmPlan pq = gemm_plan(CFG_QKV, tq, 1, c->mm);
+        if (pq.kind == GK_MM) {
+          xn_layout = gemm_takes_blocks(pq) ? 2 : 0;
+          rc = run_down_fused(c, g.d, g.dsplit, c->layers[l + 1].ln_in, c->xn, xn_layout, st);
+          if (rc) return rc;
+          xn_ready = true;
+          continue;
+        }
+      } else if (out != nullptr) {
+        rc = run_down_fused(c, g.d, g.dsplit, c->final_norm, (uint16_t*)out, 0, st);
+        if (rc) return rc;
+        final_done = true;
+        continue;
+      }
+    }
     rc = run_gemm(c, CFG_DOWN, g.d, g.dsplit, st);
     if (rc) return rc;
   }
-  if (out != nullptr)
+  if (out != nullptr && !final_done)
     HIPCHK(launch_norm_rows(f.dtype, c->h, rows, H, c->ssq, ssq_ld, c->final_norm, f.rms_norm_eps, (uint16_t*)out, st, frag));
   return FDLLM_OK;
 }
@@ -596,6 +653,7 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   if (const char* e = std::getenv("FDLLM_PREFILL_HPW")) c->prefill_hpw = std::max(0, atoi(e));
   if (const char* e = std::getenv("FDLLM_PREFILL_PAIR")) c->prefill_pair = std::min(2, std::max(0, atoi(e)));
   if (const char* e = std::getenv("FDLLM_SEQ_ATTN")) c->seq_attn = atoi(e) != 0;
+  if (const char* e = std::getenv("FDLLM_FUSE_DOWN")) c->fuse_down = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_DOWN_SPLIT")) c->down_split = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_MM_TARGET_WGS")) c->mm.target_wgs = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_MM_MIN_STAGES")) c->mm.min_stages = std::max(1, atoi(e));

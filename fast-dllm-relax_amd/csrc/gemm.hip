@@ -336,7 +336,7 @@ static hipError_t launch_wr_cfg(const GemmP& a, const GemmPlan& p, hipStream_t s
   auto kern = gemm_wr_kernel<DT, EPI, W::mf, W::tpw, W::d>;
   const int total = p.nbm * p.nbn, per = (total + 7) / 8;
   hipLaunchKernelGGL(kern, dim3(8 * per, p.ksplit), dim3(256), lds, st, a, p.nbm, p.nbn);
-  if (p.ksplit > 1) {
+  if (p.ksplit > 1 && !a.part_rows) {
     const int nblk = (a.M + 15) / 16;
     hipLaunchKernelGGL((gemm_mm_split_epilogue_kernel<DT, EPI>), dim3((a.N + 15) / 16, (nblk + 3) / 4), dim3(256), 0,
                        st, a, p.ksplit);
@@ -350,7 +350,7 @@ static hipError_t launch_mm_cfg(const GemmP& a, const GemmPlan& p, hipStream_t s
   const int total = p.nbm * p.nbn, per = (total + 7) / 8;
   const size_t lds = EPI == EPI_LOGITS ? std::max(M::lds, M::lds_logits) : M::lds;
   hipLaunchKernelGGL(kern, dim3(8 * per, p.ksplit), dim3(64 * M::nw), lds, st, a, p.nbm, p.nbn);
-  if (p.ksplit > 1) {
+  if (p.ksplit > 1 && !a.part_rows) {
     const int nblk = (a.M + 15) / 16;
     hipLaunchKernelGGL((gemm_mm_split_epilogue_kernel<DT, EPI>), dim3((a.N + 15) / 16, (nblk + 3) / 4), dim3(256), 0,
                        st, a, p.ksplit);
@@ -370,7 +370,7 @@ static hipError_t launch_wt_cfg(const GemmP& a, const GemmPlan& p, hipStream_t s
   }
   const int total = p.nbm * p.nbn, per = (total + 7) / 8;
   hipLaunchKernelGGL(kern, dim3(8 * per, p.ksplit), dim3(64 * W::nw), W::lds, st, a, p.nbm, p.nbn);
-  if (p.ksplit > 1) {
+  if (p.ksplit > 1 && !a.part_rows) {
     const int nblk = (a.M + 15) / 16;
     hipLaunchKernelGGL((gemm_mm_split_epilogue_kernel<DT, EPI>), dim3((a.N + 15) / 16, (nblk + 3) / 4), dim3(256), 0,
                        st, a, p.ksplit);
@@ -446,6 +446,7 @@ bool gemm_takes_blocks(const GemmPlan& p) {
 }
 
 hipError_t launch_gemm(int dt, int cfg, const GemmP& a, const GemmPlan& p, hipStream_t st) {
+  if (a.part_rows && (p.kind != GK_MM || a.N % 4)) return hipErrorInvalidValue;
   if ((a.xfrag == 1 || a.yfrag == 1) && !gemm_takes_frag(cfg, p)) return hipErrorInvalidValue;
   if ((a.xfrag == 2 || a.yfrag == 2) && !gemm_takes_blocks(p)) return hipErrorInvalidValue;
   if (a.yfrag == 2 && cfg != CFG_GATE_UP) return hipErrorInvalidValue;

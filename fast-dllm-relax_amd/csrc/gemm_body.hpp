@@ -33,6 +33,21 @@ __device__ __forceinline__ const u32x4* wblock(const u16* W, int KS, int t, int 
   return reinterpret_cast<const u32x4*>(W + ((size_t)t * KS + s) * 512) + (threadIdx.x & 63);
 }
 
+// A k split's fp32 sums of one (16-column tile t, 16-row block b) unit, lane (lr, lg) holding rows
+// 16 b + lr, columns 16 t + 4 lg .. + 3: in the unit layout the split-sum kernel reads
+// (part[split][tile][block][lane]), or with a.part_rows row-major (part[split][M][N]) for a caller that
+// sums the splits itself.
+__device__ __forceinline__ void store_split_unit(const GemmP& a, int split, int t, int b, int lane, const f32x4& v) {
+  const int nblk = (a.M + 15) / 16;
+  if (t >= a.ntiles || b >= nblk) return;
+  if (a.part_rows) {
+    const int m = 16 * b + (lane & 15), n = 16 * t + 4 * (lane >> 4);
+    if (m < a.M && n < a.N) *reinterpret_cast<f32x4*>(a.part + ((size_t)split * a.M + m) * a.N + n) = v;
+  } else {
+    reinterpret_cast<f32x4*>(a.part)[(((size_t)split * a.ntiles + t) * nblk + b) * 64 + lane] = v;
+  }
+}
+
 template <int DT, int XF>
 __device__ __forceinline__ u32x4 xform(u32x4 raw, u32x4 wv, float inv) {
   if constexpr (XF == XF_NONE) {

@@ -142,16 +142,11 @@ __global__ __launch_bounds__(64 * NWM * NWN) void gemm_mm_kernel(GemmP a, int nb
   }
 
   if (gridDim.y > 1) {
-    // this split's sums, unit by unit: part[split][tile][16-row block][lane]
-    const int nblk = (a.M + 15) / 16;
-    f32x4* part = reinterpret_cast<f32x4*>(a.part);
+    // this split's sums, unit by unit
 #pragma unroll
     for (int j = 0; j < TPW; ++j)
 #pragma unroll
-      for (int f = 0; f < MF; ++f) {
-        const int t = t0 + j, b = mb * MFT + f0 + f;
-        if (t < a.ntiles && b < nblk) part[(((size_t)blockIdx.y * a.ntiles + t) * nblk + b) * 64 + lane] = acc[j][f];
-      }
+      for (int f = 0; f < MF; ++f) store_split_unit(a, blockIdx.y, t0 + j, mb * MFT + f0 + f, lane, acc[j][f]);
     return;
   }
 

@@ -115,15 +115,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_wt_kernel(GemmP a, int nbm,
 
   const int f0 = wm * MF, tw0 = t0 + wn * TPW;
   if (gridDim.y > 1) {
-    const int nblk = (a.M + 15) / 16;
-    f32x4* part = reinterpret_cast<f32x4*>(a.part);
 #pragma unroll
     for (int j = 0; j < TPW; ++j)
 #pragma unroll
-      for (int f = 0; f < MF; ++f) {
-        const int t = tw0 + j, b = mb * BMB + f0 + f;
-        if (t < a.ntiles && b < nblk) part[(((size_t)blockIdx.y * a.ntiles + t) * nblk + b) * 64 + lane] = acc[j][f];
-      }
+      for (int f = 0; f < MF; ++f) store_split_unit(a, blockIdx.y, tw0 + j, mb * BMB + f0 + f, lane, acc[j][f]);
     return;
   }
   if constexpr (EPI == EPI_SILU_PAIR) {
@@ -265,15 +260,10 @@ void gemm_wr_kernel(GemmP a, int nbm, int nbn) {
   wait_vmcnt<0>();  // no copy may still be writing LDS when the workgroup ends
 
   if (gridDim.y > 1) {
-    const int nblk = (a.M + 15) / 16;
-    f32x4* part = reinterpret_cast<f32x4*>(a.part);
 #pragma unroll
     for (int j = 0; j < TPW; ++j)
 #pragma unroll
-      for (int f = 0; f < MF; ++f) {
-        const int t = tw0 + j, b = mb * MF + f;
-        if (t < a.ntiles && b < nblk) part[(((size_t)blockIdx.y * a.ntiles + t) * nblk + b) * 64 + lane] = acc[j][f];
-      }
+      for (int f = 0; f < MF; ++f) store_split_unit(a, blockIdx.y, tw0 + j, mb * MF + f, lane, acc[j][f]);
     return;
   }
   if constexpr (EPI == EPI_LOGITS) {

@@ -39,6 +39,9 @@ struct GemmP {
   // EPI_SILU_PAIR, in MFMA-fragment order (frag_off) instead of row-major; 2: X, and the Y of
   // EPI_SILU_PAIR, in the large-M LDS-staged kernel's fragment blocks (frag_blk_off)
   int xfrag, yfrag;
+  // large-M k splits: 1 stores the split sums row-major (part[split][M][N], N a multiple of 4) and launches
+  // no split-sum kernel; the caller sums them (launch_resid_norm)
+  int part_rows;
 };
 
 // Launch configurations (see gemm.hip); the host picks one per projection.
@@ -126,6 +129,12 @@ hipError_t launch_rope_table(int dt, const int32_t* pos_offset, int rows, int ro
 // yblk: y in the large-M kernel's fragment blocks (frag_blk_off) instead of row-major
 hipError_t launch_norm_rows(int dt, const uint16_t* h, int rows, int hidden, const float* ssq, int ssq_ld,
                             const uint16_t* w, float eps, uint16_t* y, hipStream_t st, int hfrag = 0, int yblk = 0);
+// The k-split sum of an EPI_RESID projection (row-major partials of part_rows launches) with its residual
+// epilogue (h updated in place, per-tile sums of squares to ssq, the exact arithmetic of the split-sum
+// kernel), then the next RMSNorm of the new rows (norm_rows_kernel's arithmetic) into y (yblk: fragment
+// blocks), in one launch.
+hipError_t launch_resid_norm(int dt, const float* part, int splits, int rows, int hidden, uint16_t* h, float* ssq,
+                             int ssq_ld, const uint16_t* w, float eps, uint16_t* y, int yblk, hipStream_t st);
 
 // ---- attention ----------------------------------------------------------------------------------
 constexpr int MAX_SEQS = 64;  // sequences of one batched call

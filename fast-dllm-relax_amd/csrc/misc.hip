@@ -103,6 +103,95 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(const u16* h, int rows, 
   }
 }
 
+// The k-split sum + residual epilogue of an EPI_RESID projection (o_proj / down in a batched or
+// prefill-sized call) fused with the next RMSNorm.  The split sums come row-major (part[split][rows][hidden],
+// a part_rows GEMM launch).  A workgroup owns RPW rows.  Each 4-column unit adds its splits in split order
+// (the requests of up to eight splits issued together), forms h = rnd(h + rnd(sum)) and the unit's sum of
+// squares as the split-sum kernel's epilogue does; a 16-column tile's sum is (g0 + g1) + (g2 + g3) of its
+// four units, again as there; h and the tile sums are written, and the rows are normalised exactly as
+// norm_rows_kernel does, from the same sums (kept in LDS with the new rows), into y (row-major, or with
+// yblk the large-M GEMMs' fragment blocks).
+template <int DT>
+__global__ __launch_bounds__(256) void resid_norm_kernel(const float* part, int splits, int rows, int hidden, u16* h,
+                                                         float* ssq, int ssq_ld, const u16* w, float eps, u16* y,
+                                                         int yblk) {
+  constexpr int RPW = 2;                // rows per workgroup
+  constexpr int MAXH = 2048;            // hidden sizes up to this (the launcher checks)
+  constexpr int SB = 8;                 // split sums requested at once
+  __shared__ float gss[RPW][MAXH / 4];
+  __shared__ float tss[RPW][MAXH / 16];
+  __shared__ __align__(16) u16 hl[RPW][MAXH];
+  __shared__ float inv_s[RPW];
+  const int r0 = blockIdx.x * RPW;
+  const int nunits = hidden / 4, ntiles = hidden / 16;
+  for (int u = threadIdx.x; u < RPW * nunits; u += 256) {
+    const int rl = u / nunits, n = 4 * (u - rl * nunits), m = r0 + rl;
+    if (m >= rows) continue;
+    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < splits; s0 += SB) {
+      f32x4 v[SB];
+#pragma unroll
+      for (int q = 0; q < SB; ++q)
+        v[q] = s0 + q < splits ? *reinterpret_cast<const f32x4*>(part + ((size_t)(s0 + q) * rows + m) * hidden + n)
+                               : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < SB; ++q)
+        if (s0 + q < splits) sum = s0 + q == 0 ? v[q] : sum + v[q];
+    }
+    u16* hp = h + (size_t)m * hidden + n;
+    const u32x2 hv = *reinterpret_cast<const u32x2*>(hp);
+    const float hf[4] = {lo_f32<DT>(hv[0]), hi_f32<DT>(hv[0]), lo_f32<DT>(hv[1]), hi_f32<DT>(hv[1])};
+    u16 out[4];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[i] = from_f32<DT>(hf[i] + rnd<DT>(sum[i]));
+      const float yv = to_f32<DT>(out[i]);
+      ss += yv * yv;
+    }
+    const u32x2 o = u32x2{pack2(out[0], out[1]), pack2(out[2], out[3])};
+    *reinterpret_cast<u32x2*>(hp) = o;
+    *reinterpret_cast<u32x2*>(&hl[rl][n]) = o;
+    gss[rl][n / 4] = ss;
+  }
+  __syncthreads();
+  for (int u = threadIdx.x; u < RPW * ntiles; u += 256) {
+    const int rl = u / ntiles, t = u - rl * ntiles, m = r0 + rl;
+    if (m >= rows) continue;
+    const float ts = (gss[rl][4 * t] + gss[rl][4 * t + 1]) + (gss[rl][4 * t + 2] + gss[rl][4 * t + 3]);
+    ssq[(size_t)t * ssq_ld + m] = ts;
+    tss[rl][t] = ts;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (wave < RPW && r0 + wave < rows) {
+    float pq[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float v = 0.f;
+      for (int t = 64 * q + lane; t < ntiles; t += 256) v += tss[wave][t];
+      pq[q] = 64 * q < ntiles ? wave_sum(v) : 0.f;
+    }
+    if (lane == 0) inv_s[wave] = 1.0f / sqrtf(((pq[0] + pq[1]) + (pq[2] + pq[3])) / (float)hidden + eps);
+  }
+  __syncthreads();
+  const int ks = hidden / 32;
+  for (int u = threadIdx.x; u < RPW * (hidden / 8); u += 256) {
+    const int rl = u % RPW, c = 8 * (u / RPW);
+    const int r = r0 + rl;
+    if (r >= rows) continue;
+    const float inv = inv_s[rl];
+    const u32x4 hv = *reinterpret_cast<const u32x4*>(&hl[rl][c]);
+    const u32x4 wv = *reinterpret_cast<const u32x4*>(w + c);
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = pack2(norm_elem<DT>(lo_f32<DT>(wv[e]), lo_f32<DT>(hv[e]), inv),
+                   norm_elem<DT>(hi_f32<DT>(wv[e]), hi_f32<DT>(hv[e]), inv));
+    *reinterpret_cast<u32x4*>(y + (yblk ? frag_blk_off(r, c, ks) : (size_t)r * hidden + c)) = o;
+  }
+}
+
 // RoPE tables of one call (cuda.py:288-299): position pos_offset + r, inv_freq = exp(-ln(theta) * i / 64),
 // angle = pos * inv_freq in fp32, cos / sin in fp32 rounded to the model dtype (emb = [f, f], so one
 // entry serves dims i and i + 64).  Shared by every layer's attention.
@@ -154,6 +243,19 @@ hipError_t launch_norm_rows(int dt, const uint16_t* h, int rows, int hidden, con
   else
     hipLaunchKernelGGL(norm_rows_kernel<DT_F16>, dim3(wgs), dim3(256), 0, st, h, rows, hidden, ssq, ssq_ld, w, eps, y,
                        hfrag, yblk);
+  return hipGetLastError();
+}
+
+hipError_t launch_resid_norm(int dt, const float* part, int splits, int rows, int hidden, uint16_t* h, float* ssq,
+                             int ssq_ld, const uint16_t* w, float eps, uint16_t* y, int yblk, hipStream_t st) {
+  if (hidden % 32 || hidden > 2048 || splits < 1) return hipErrorInvalidValue;
+  const int wgs = (rows + 1) / 2;
+  if (dt == DT_BF16)
+    hipLaunchKernelGGL(resid_norm_kernel<DT_BF16>, dim3(wgs), dim3(256), 0, st, part, splits, rows, hidden, h, ssq, ssq_ld,
+                       w, eps, y, yblk);
+  else
+    hipLaunchKernelGGL(resid_norm_kernel<DT_F16>, dim3(wgs), dim3(256), 0, st, part, splits, rows, hidden, h, ssq, ssq_ld,
+                       w, eps, y, yblk);
   return hipGetLastError();
 }
 

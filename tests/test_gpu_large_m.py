@@ -189,3 +189,58 @@ def test_lm_head_register_weight_bit_identical(dtype, monkeypatch):
                                           err_msg=f"{what}, rows={rows}")
     for vm in vms.values():
         vm.close()
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_fused_down_norm_bit_identical(dtype, monkeypatch):
+    """A large-M down launch that splits k hands its split sums, row-major, to resid_norm_kernel, which adds
+    them, applies the residual epilogue and the next RMSNorm (the next layer's qkv input, or the final norm)
+    in one launch.  Against FDLLM_FUSE_DOWN=0 (the split-sum kernel, then norm_rows) every bit of the hidden
+    states and of the caches must agree: forward_hidden at several sizes and a 16-sequence batched step."""
+    from fast_dllm_relax_amd.config import FastDLLMConfig
+    from fast_dllm_relax_amd.params import from_numpy
+    from fast_dllm_relax_amd.vm import HipVM
+    from oracle.model import OracleConfig, random_params
+
+    kw = WIDE2
+    params = from_numpy(random_params(OracleConfig(**kw), 12, dtype), FastDLLMConfig(**kw), dtype=dtype)
+    tdt = torch.bfloat16 if dtype == "bfloat16" else torch.float16
+    vms = {}
+    for name, on in (("fused", "1"), ("separate", "0")):
+        monkeypatch.setenv("FDLLM_FUSE_DOWN", on)
+        vms[name] = HipVM(FastDLLMConfig(**kw), params, dtype=dtype, max_rows=1024)
+        monkeypatch.delenv("FDLLM_FUSE_DOWN")
+    rng = np.random.default_rng(29)
+    for S in (100, 300, 512, 1056):
+        log(f"case: forward_hidden {S} rows, {dtype}, fused down epilogue + norm vs separate launches")
+        ids = torch.tensor(rng.integers(0, kw["vocab_size"] - 1, S), dtype=torch.int32, device="cuda")
+        x = vms["separate"].embed(ids)[None]
+        h = {name: vm.forward_hidden(x, None) for name, vm in vms.items()}
+        torch.cuda.synchronize()
+        assert torch.isfinite(h["fused"].float()).all()
+        np.testing.assert_array_equal(_bits(h["fused"]), _bits(h["separate"]), err_msg=f"S={S}")
+
+    L, nkv, hd = kw["num_hidden_layers"], kw["num_key_value_heads"], kw["head_dim"]
+    prefixes = [int(p) for p in 32 * rng.integers(1, 9, 16)]
+    cap = max(prefixes) + 32
+    ids = [rng.integers(0, kw["vocab_size"] - 1, P + 32) for P in prefixes]
+    out = {}
+    for name, vm in vms.items():
+        log(f"case: batched step of 16 x 32 rows + partial step, {dtype}, {name}")
+        k = torch.zeros((L, 16, cap, nkv, hd), dtype=tdt, device="cuda")
+        v = torch.zeros_like(k)
+        for b, P in enumerate(prefixes):
+            vm.build_prefix_cache_seq(vm.embed(torch.tensor(ids[b][:P], dtype=torch.int32, device="cuda"))[None],
+                                      None, k, v, b)
+        x = torch.stack([vm.embed(torch.tensor(ids[b][P:], dtype=torch.int32, device="cuda"))
+                         for b, P in enumerate(prefixes)])
+        hf = vm.forward_cached_batch(x, k, v, torch.tensor(prefixes, dtype=torch.int32, device="cuda"), prefixes)
+        hp = vm.forward_block_partial_batch(8, x[:, 8:16].contiguous(), k, v,
+                                            torch.tensor([P + 8 for P in prefixes], dtype=torch.int32, device="cuda"),
+                                            prefixes)
+        torch.cuda.synchronize()
+        out[name] = (hf, hp, k, v)
+    for i, what in enumerate(("full-step hidden", "partial-step hidden", "K cache", "V cache")):
+        np.testing.assert_array_equal(_bits(out["fused"][i]), _bits(out["separate"][i]), err_msg=what)
+    for vm in vms.values():
+        vm.close()
