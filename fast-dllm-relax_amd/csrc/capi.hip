@@ -101,6 +101,10 @@ struct fdllm_ctx {
   int prefill_pair = 1;   // paired-query-block prefill attention (0 off, 1 when it fills the chip, 2 always)
   int seq_attn = 1;       // batched calls: attn_seq_kernel (0: the chunk kernel with key splits + merge)
   int fuse_down = 1;      // large-M down launches with k splits: split sum + residual + next RMSNorm in one launch
+  // large-M o_proj with a forced k split and its split sum + residual + the next norm in one launch: -1 with
+  // three splits up to 256 rows (128-row batched step: 14.8 + 4.8 us norm -> 8.1 + 7.1 us; at 512 rows it
+  // measured slower, 3.88 -> 3.94 ms per step with two splits), 0 never, N > 1 with N splits at any size
+  int fuse_oproj = -1;
   int down_split = 10;    // cross-workgroup k splits of the down projection (largest divisor of K/32 <= this)
   MmPolicy mm;              // large-M GEMM planning (k splits, register-weight kernel)
   bool frag_on = true;      // one-shot chains keep activations in MFMA-fragment order (FDLLM_XFRAG=0: row-major)
@@ -225,11 +229,12 @@ int run_gemm(fdllm_ctx* c, int cfg, GemmP a, int ksplit, hipStream_t st) {
   return FDLLM_OK;
 }
 
-// The down projection of a large-M call with its k-split sum, residual and the next RMSNorm (weight
-// next_w) in one launch after the GEMM (launch_resid_norm) instead of the split-sum launch plus a
-// norm_rows launch; y: the normalised rows (yblk: fragment blocks).  Only for launches that split k
-// (fused_down_ok).
-int run_down_fused(fdllm_ctx* c, GemmP a, int ksplit, const uint16_t* next_w, uint16_t* y, int yblk, hipStream_t st);
+// An EPI_RESID projection (down, or o_proj) of a large-M call with its k-split sum, residual and the next
+// RMSNorm (weight next_w) in one launch after the GEMM (launch_resid_norm) instead of the split-sum launch
+// plus a norm_rows launch; y: the normalised rows (yblk: fragment blocks).  Only for launches that split k
+// under pol (fused_resid_ok).
+int run_resid_fused(fdllm_ctx* c, int cfg, GemmP a, int ksplit, const MmPolicy& pol, const uint16_t* next_w,
+                    uint16_t* y, int yblk, hipStream_t st);
 
 GemmP gemm_args(const uint16_t* W, int ntiles, int N, int K, const uint16_t* X, int ldx, int M) {
   GemmP a{};
@@ -237,22 +242,23 @@ GemmP gemm_args(const uint16_t* W, int ntiles, int N, int K, const uint16_t* X, 
   return a;
 }
 
-bool fused_down_ok(const fdllm_ctx* c, GemmP a, int ksplit) {
-  if (!c->fuse_down || a.nw != nullptr || a.N % 4 || a.N > 2048 || a.N % 32) return false;
-  const GemmPlan pl = gemm_plan(CFG_DOWN, a, ksplit, c->mm);
+bool fused_resid_ok(const fdllm_ctx* c, int cfg, GemmP a, int ksplit, const MmPolicy& pol) {
+  if (a.nw != nullptr || a.N % 32 || a.N > 2048) return false;
+  const GemmPlan pl = gemm_plan(cfg, a, ksplit, pol);
   return pl.kind == GK_MM && pl.ksplit > 1;
 }
 
-int run_down_fused(fdllm_ctx* c, GemmP a, int ksplit, const uint16_t* next_w, uint16_t* y, int yblk, hipStream_t st) {
+int run_resid_fused(fdllm_ctx* c, int cfg, GemmP a, int ksplit, const MmPolicy& pol, const uint16_t* next_w,
+                    uint16_t* y, int yblk, hipStream_t st) {
   const fdllm_config& f = c->cfg;
-  const GemmPlan pl = gemm_plan(CFG_DOWN, a, ksplit, c->mm);
-  if (pl.kind != GK_MM || pl.ksplit < 2) return fail(FDLLM_EINVAL, "fused down epilogue needs a k split");
+  const GemmPlan pl = gemm_plan(cfg, a, ksplit, pol);
+  if (pl.kind != GK_MM || pl.ksplit < 2) return fail(FDLLM_EINVAL, "fused residual epilogue needs a k split");
   int rc = ensure_floats(&c->gpart, &c->gpart_floats, std::max(pl.part_floats, (size_t)pl.ksplit * a.M * a.N));
   if (rc) return rc;
   a.part = c->gpart;
   a.counters = c->counters;
   a.part_rows = 1;
-  HIPCHK(launch_gemm(f.dtype, CFG_DOWN, a, pl, st));
+  HIPCHK(launch_gemm(f.dtype, cfg, a, pl, st));
   HIPCHK(launch_resid_norm(f.dtype, c->gpart, pl.ksplit, a.M, a.N, (uint16_t*)a.Y, a.ssq_out, a.ssq_ld, next_w,
                            f.rms_norm_eps, y, yblk, st));
   return FDLLM_OK;
@@ -480,7 +486,7 @@ int run_layers(fdllm_ctx* c, const void* x_in, int rows, uint16_t* kbase, uint16
   }
   if (frag) ++c->frag_calls;
   // xn_ready: the previous layer's down launch also normalised this layer's qkv input into c->xn
-  // (run_down_fused), in the layout the qkv launch takes; final_done: the last one wrote out
+  // (run_resid_fused), in the layout the qkv launch takes; final_done: the last one wrote out
   bool xn_ready = false, final_done = false;
   int xn_layout = 0;
   for (int l = 0; l < f.num_hidden_layers; ++l) {
@@ -497,25 +503,45 @@ int run_layers(fdllm_ctx* c, const void* x_in, int rows, uint16_t* kbase, uint16
     if (rc) return rc;
     rc = run_attention(c, rows, kc, vc, write_start, attend_len, mask, bias, bias_ld, st, sb, frag);
     if (rc) return rc;
-    rc = run_gemm(c, CFG_OPROJ, g.o, 1, st);
-    if (rc) return rc;
+    // o_proj + the post-attention norm: with a forced k split, when gate_up takes normalised rows
+    bool gu_ready = false;
+    const int oproj_split = c->fuse_oproj > 1 ? c->fuse_oproj : (c->fuse_oproj < 0 && rows <= 256 ? 3 : 0);
+    if (!frag && oproj_split > 1) {
+      MmPolicy po = c->mm;
+      po.force_split = oproj_split;
+      GemmP tg = g.gu;
+      const GemmPlan pg = gemm_plan(CFG_GATE_UP, tg, 1, c->mm);
+      if (pg.kind == GK_MM && fused_resid_ok(c, CFG_OPROJ, g.o, 1, po)) {
+        const int lay = gemm_takes_blocks(pg) ? 2 : 0;
+        rc = run_resid_fused(c, CFG_OPROJ, g.o, 1, po, L.ln_post, c->xn, lay, st);
+        if (rc) return rc;
+        g.gu.X = c->xn;
+        g.gu.nw = nullptr;
+        g.gu.xfrag = lay;
+        gu_ready = true;
+      }
+    }
+    if (!gu_ready) {
+      rc = run_gemm(c, CFG_OPROJ, g.o, 1, st);
+      if (rc) return rc;
+    }
     rc = run_gemm(c, CFG_GATE_UP, g.gu, 1, st);
     if (rc) return rc;
     xn_ready = false;
-    if (!frag && fused_down_ok(c, g.d, g.dsplit)) {
+    if (!frag && c->fuse_down && fused_resid_ok(c, CFG_DOWN, g.d, g.dsplit, c->mm)) {
       if (l + 1 < f.num_hidden_layers) {
         // the next layer's qkv: its launch takes normalised rows (row-major or fragment blocks)
         GemmP tq = layer_gemms(c, c->layers[l + 1], rows, frag).q;
         const GemmPlan pq = gemm_plan(CFG_QKV, tq, 1, c->mm);
         if (pq.kind == GK_MM) {
           xn_layout = gemm_takes_blocks(pq) ? 2 : 0;
-          rc = run_down_fused(c, g.d, g.dsplit, c->layers[l + 1].ln_in, c->xn, xn_layout, st);
+          rc = run_resid_fused(c, CFG_DOWN, g.d, g.dsplit, c->mm, c->layers[l + 1].ln_in, c->xn, xn_layout, st);
           if (rc) return rc;
           xn_ready = true;
           continue;
         }
       } else if (out != nullptr) {
-        rc = run_down_fused(c, g.d, g.dsplit, c->final_norm, (uint16_t*)out, 0, st);
+        rc = run_resid_fused(c, CFG_DOWN, g.d, g.dsplit, c->mm, c->final_norm, (uint16_t*)out, 0, st);
         if (rc) return rc;
         final_done = true;
         continue;
@@ -654,6 +680,7 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   if (const char* e = std::getenv("FDLLM_PREFILL_PAIR")) c->prefill_pair = std::min(2, std::max(0, atoi(e)));
   if (const char* e = std::getenv("FDLLM_SEQ_ATTN")) c->seq_attn = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_FUSE_DOWN")) c->fuse_down = atoi(e) != 0;
+  if (const char* e = std::getenv("FDLLM_FUSE_OPROJ")) c->fuse_oproj = e[0] != '\0' ? std::max(0, atoi(e)) : -1;
   if (const char* e = std::getenv("FDLLM_DOWN_SPLIT")) c->down_split = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_MM_TARGET_WGS")) c->mm.target_wgs = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_MM_MIN_STAGES")) c->mm.min_stages = std::max(1, atoi(e));

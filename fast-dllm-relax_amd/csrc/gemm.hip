@@ -265,8 +265,11 @@ GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol) {
       if (cfg == CFG_QKV && (id == MM_WR_S || id == MM_WR_T)) target /= 2;
       int split = 1;
       const int max_split = id == MM_WR || id == MM_WR_S || id == MM_WR_M || id == MM_WR_T ? 16 : 8;
-      for (int d = 2; d <= max_split && wgs * split < target && cfg != CFG_LM_HEAD; ++d)
-        if (nst % d == 0 && nst / d >= pol.min_stages) split = d;
+      if (pol.force_split > 1 && cfg != CFG_LM_HEAD && nst % pol.force_split == 0 && nst / pol.force_split >= pol.min_stages)
+        split = pol.force_split;
+      else
+        for (int d = 2; d <= max_split && wgs * split < target && cfg != CFG_LM_HEAD; ++d)
+          if (nst % d == 0 && nst / d >= pol.min_stages) split = d;
       p.ksplit = split;
       a.kps = a.KS / split;
       p.part_floats = split > 1 ? (size_t)split * a.ntiles * ((a.M + 15) / 16) * 256 : 0;

@@ -75,6 +75,7 @@ struct MmPolicy {
   // gate_up / down below 256 rows: -1 the measured choice of register-weight blocks, else bit 0 / 1 the 64 x 128
   // blocks, bit 2 / 3 the 128 x 128 ones (0: the LDS-staged kernel)
   int wr_ffn = -1;
+  int force_split = 0;  // > 1: this k split whenever it divides the stages (the fused o_proj + norm)
 };
 GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol = MmPolicy{});
 // whether the plan runs the one-shot register-fragment body, the only one that takes xfrag / yfrag 1

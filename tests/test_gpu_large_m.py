@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import WIDE2, log
+from helpers import WIDE2, bf16_parity, log
 
 pytestmark = pytest.mark.gpu
 
@@ -195,8 +195,12 @@ def test_lm_head_register_weight_bit_identical(dtype, monkeypatch):
 def test_fused_down_norm_bit_identical(dtype, monkeypatch):
     """A large-M down launch that splits k hands its split sums, row-major, to resid_norm_kernel, which adds
     them, applies the residual epilogue and the next RMSNorm (the next layer's qkv input, or the final norm)
-    in one launch.  Against FDLLM_FUSE_DOWN=0 (the split-sum kernel, then norm_rows) every bit of the hidden
-    states and of the caches must agree: forward_hidden at several sizes and a 16-sequence batched step."""
+    in one launch; up to 256 rows o_proj does the same with three k splits (the post-attention norm).  The
+    arithmetic is the split-sum kernel's and norm_rows_kernel's, and k splits add their sums in split order,
+    so the results match the separate launches (FDLLM_FUSE_DOWN=0, FDLLM_FUSE_OPROJ=0) except where o_proj's
+    forced split regroups its fp32 sums: the hidden states at sizes that fuse only down, and the caches and
+    hidden states of a 16-sequence batched step (512 rows), must agree bit for bit; the 128-row partial step
+    and the 100-row forward to the bf16 criterion."""
     from fast_dllm_relax_amd.config import FastDLLMConfig
     from fast_dllm_relax_amd.params import from_numpy
     from fast_dllm_relax_amd.vm import HipVM
@@ -208,8 +212,10 @@ def test_fused_down_norm_bit_identical(dtype, monkeypatch):
     vms = {}
     for name, on in (("fused", "1"), ("separate", "0")):
         monkeypatch.setenv("FDLLM_FUSE_DOWN", on)
+        monkeypatch.setenv("FDLLM_FUSE_OPROJ", "" if on == "1" else "0")
         vms[name] = HipVM(FastDLLMConfig(**kw), params, dtype=dtype, max_rows=1024)
         monkeypatch.delenv("FDLLM_FUSE_DOWN")
+        monkeypatch.delenv("FDLLM_FUSE_OPROJ")
     rng = np.random.default_rng(29)
     for S in (100, 300, 512, 1056):
         log(f"case: forward_hidden {S} rows, {dtype}, fused down epilogue + norm vs separate launches")
@@ -218,29 +224,38 @@ def test_fused_down_norm_bit_identical(dtype, monkeypatch):
         h = {name: vm.forward_hidden(x, None) for name, vm in vms.items()}
         torch.cuda.synchronize()
         assert torch.isfinite(h["fused"].float()).all()
-        np.testing.assert_array_equal(_bits(h["fused"]), _bits(h["separate"]), err_msg=f"S={S}")
+        if S <= 256:  # o_proj's forced k split
+            bf16_parity(f"fused vs separate, S={S}", h["fused"].float().cpu().numpy(), h["separate"].float().cpu().numpy())
+        else:
+            np.testing.assert_array_equal(_bits(h["fused"]), _bits(h["separate"]), err_msg=f"S={S}")
 
     L, nkv, hd = kw["num_hidden_layers"], kw["num_key_value_heads"], kw["head_dim"]
     prefixes = [int(p) for p in 32 * rng.integers(1, 9, 16)]
     cap = max(prefixes) + 32
     ids = [rng.integers(0, kw["vocab_size"] - 1, P + 32) for P in prefixes]
+    # one set of prefix caches for both (prefixes up to 256 rows take the fused o_proj)
+    k0 = torch.zeros((L, 16, cap, nkv, hd), dtype=tdt, device="cuda")
+    v0 = torch.zeros_like(k0)
+    for b, P in enumerate(prefixes):
+        vms["separate"].build_prefix_cache_seq(
+            vms["separate"].embed(torch.tensor(ids[b][:P], dtype=torch.int32, device="cuda"))[None], None, k0, v0, b)
     out = {}
     for name, vm in vms.items():
         log(f"case: batched step of 16 x 32 rows + partial step, {dtype}, {name}")
-        k = torch.zeros((L, 16, cap, nkv, hd), dtype=tdt, device="cuda")
-        v = torch.zeros_like(k)
-        for b, P in enumerate(prefixes):
-            vm.build_prefix_cache_seq(vm.embed(torch.tensor(ids[b][:P], dtype=torch.int32, device="cuda"))[None],
-                                      None, k, v, b)
+        k, v = k0.clone(), v0.clone()
         x = torch.stack([vm.embed(torch.tensor(ids[b][P:], dtype=torch.int32, device="cuda"))
                          for b, P in enumerate(prefixes)])
         hf = vm.forward_cached_batch(x, k, v, torch.tensor(prefixes, dtype=torch.int32, device="cuda"), prefixes)
+        kf, vf = k.clone(), v.clone()
         hp = vm.forward_block_partial_batch(8, x[:, 8:16].contiguous(), k, v,
                                             torch.tensor([P + 8 for P in prefixes], dtype=torch.int32, device="cuda"),
                                             prefixes)
         torch.cuda.synchronize()
-        out[name] = (hf, hp, k, v)
-    for i, what in enumerate(("full-step hidden", "partial-step hidden", "K cache", "V cache")):
+        out[name] = (hf, kf, vf, hp, k, v)
+    for i, what in enumerate(("full-step hidden", "full-step K cache", "full-step V cache")):
         np.testing.assert_array_equal(_bits(out["fused"][i]), _bits(out["separate"][i]), err_msg=what)
+    # 128 rows: o_proj's forced k split
+    for i, what in ((3, "partial-step hidden"), (4, "K cache after the partial step"), (5, "V cache after the partial step")):
+        bf16_parity(what, out["fused"][i].float().cpu().numpy(), out["separate"][i].float().cpu().numpy())
     for vm in vms.values():
         vm.close()
