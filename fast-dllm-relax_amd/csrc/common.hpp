@@ -131,6 +131,23 @@ __device__ __forceinline__ float fd_exp_neg(float x) {
   return __builtin_ldexpf(p, (int)n);
 }
 
+// SiLU(gate) x up with the rounding points of _silu_fp32 (model/cuda.py:319-328): gate and up rounded to
+// DT, silu = gate x (1 / (1 + exp(-gate))) in fp32 rounded to DT, the product rounded to DT.  The
+// reciprocal is the hardware estimate refined by one Newton-Raphson step, r + r (1 - d r), which agrees
+// with the IEEE quotient to within its last bit (the IEEE division sequence costs several times as many
+// instructions, and the gate/up epilogue is VALU-bound); past 2^64 the estimate alone (the step would form
+// inf x 0), for d = inf exactly 0.
+template <int DT>
+__device__ __forceinline__ u16 silu_mul(float g, float u) {
+  const float gt = rnd<DT>(g), up = rnd<DT>(u);
+  const float d = 1.0f + expf(-gt);
+  float r = __builtin_amdgcn_rcpf(d);
+  const float e = __builtin_fmaf(-d, r, 1.0f);
+  r = d < 0x1p64f ? __builtin_fmaf(e, r, r) : r;
+  const float sl = rnd<DT>(gt * r);
+  return from_f32<DT>(sl * up);
+}
+
 // ---- agent-coherent exchange between workgroups of one launch ---------------------------------
 // Each XCD has its own write-back L2, so data one workgroup hands to another inside a launch is
 // written and read with agent-scope relaxed atomics (the sc1 cache policy: written through to memory,

@@ -360,12 +360,7 @@ __global__ __launch_bounds__(64 * TW * KW) void gemm_pk_kernel(GemmP a) {
       if (m >= a.M || n >= a.N) continue;
       u16 out[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float gt = rnd<DT>(acc[0][mt][i]);
-        const float up = rnd<DT>(acc[1][mt][i]);
-        const float sl = rnd<DT>(gt * (1.0f / (1.0f + expf(-gt))));
-        out[i] = from_f32<DT>(sl * up);
-      }
+      for (int i = 0; i < 4; ++i) out[i] = silu_mul<DT>(acc[0][mt][i], acc[1][mt][i]);
       *reinterpret_cast<u32x2*>(a.Y + (size_t)m * a.ldy + n) = u32x2{pack2(out[0], out[1]), pack2(out[2], out[3])};
     }
   } else {
@@ -413,12 +408,7 @@ __device__ __forceinline__ void os_epilogue(const GemmP& a, const f32x4 (&v)[TPU
     if (m < a.M && n < a.N) {
       u16 out[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float gt = rnd<DT>(v[0][i]);
-        const float up = rnd<DT>(v[TPU - 1][i]);
-        const float sl = rnd<DT>(gt * (1.0f / (1.0f + expf(-gt))));
-        out[i] = from_f32<DT>(sl * up);
-      }
+      for (int i = 0; i < 4; ++i) out[i] = silu_mul<DT>(v[0][i], v[TPU - 1][i]);
       const size_t o = a.yfrag == 1 ? frag_off(m, n) : a.yfrag == 2 ? frag_blk_off(m, n, a.ldy >> 5) : (size_t)m * a.ldy + n;
       st8<COH>(a.Y + o, u32x2{pack2(out[0], out[1]), pack2(out[2], out[3])});
     }

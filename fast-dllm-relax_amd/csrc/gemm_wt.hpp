@@ -10,8 +10,9 @@
 // registers (one block per wave instruction: lane l's 16 bytes land at byte 16 l, which is MFMA
 // fragment order for both: the packed weights already are, and lane l of an activation block reads row
 // l % 16, columns 8 (l / 16) .. + 7).  NBUF stage buffers rotate: a wave waits for its own copies of the
-// stage (memory counter), one barrier makes every wave's copies visible and frees the buffer multiplied
-// one stage earlier, which then receives the copies NBUF - 1 stages ahead.  Every copy is unconditional
+// next stage (memory counter), one barrier makes every wave's copies visible and frees the buffer whose
+// fragments every wave has read into registers, which then receives the copies NBUF stages ahead; the
+// fragment reads of stage st + 1 overlap the MFMAs of stage st.  Every copy is unconditional
 // (stages past the last re-read the last; rows past M re-read row M - 1), so every wave issues the same
 // number per stage and the counter waits are exact.
 //
@@ -33,7 +34,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_wt_kernel(GemmP a, int nbm,
   constexpr int DPW = SB / NW;        // copies per wave per stage
   static_assert(SB % NW == 0, "every wave copies the same number of blocks per stage");
   static_assert(NBUF >= 2, "at least two stage buffers");
-  static_assert((NBUF - 2) * DPW < 64, "outstanding copies fit the memory counter");
+  static_assert((NBUF - 1) * DPW < 64, "outstanding copies fit the memory counter");
   static_assert(EPI != EPI_SILU_PAIR || TPW % 2 == 0, "gate/up pairs stay within a wave");
   static_assert(EPI != EPI_LOGITS, "the lm_head takes the streaming kernel");
   extern __shared__ __align__(16) unsigned char smem[];  // [NBUF][SB][1 KB]
@@ -87,30 +88,47 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_wt_kernel(GemmP a, int nbm,
 #pragma unroll
     for (int f = 0; f < MF; ++f) acc[j][f] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Stage s lives in buffer s % NBUF.  A wave reads the fragments of stage st + 1 from LDS into one
+  // register set while its MFMAs consume stage st from the other, so the LDS latency hides behind the
+  // MFMAs; it waits for those reads before the next barrier, after which the buffer of stage st (read one
+  // iteration earlier by every wave) takes the copies of stage st + NBUF.
 #pragma unroll
-  for (int st = 0; st < NBUF - 1; ++st) copy_stage(st, st);
-
-  // one stage per iteration, buffers indexed at run time: an unrolled rotation makes the register
-  // allocator shuffle the accumulators between copies of the loop body
+  for (int st = 0; st < NBUF; ++st) copy_stage(st, st);
   const u32x4* lds = reinterpret_cast<const u32x4*>(smem);
-  int q = 0;  // buffer of stage st
+  auto read_frags = [&](u32x4 (&fr)[MF + TPW], int s) __attribute__((always_inline)) {
+    const u32x4* blk = lds + (size_t)(s % NBUF) * SB * 64;
+#pragma unroll
+    for (int f = 0; f < MF; ++f) fr[f] = blk[(wm * MF + f) * 64 + lane];
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) fr[MF + j] = blk[(BMB + wn * TPW + j) * 64 + lane];
+  };
+  // iteration st: fragments of st in cur; next receives those of st + 1 (past the last stage the buffer
+  // holds a re-read of the last, read and not used)
+  auto step = [&](int st, u32x4 (&cur)[MF + TPW], u32x4 (&next)[MF + TPW]) __attribute__((always_inline)) {
+    wait_vmcnt<(NBUF - 2) * DPW>();  // this wave's copies of stage st + 1 have landed
+    __builtin_amdgcn_s_barrier();    // everyone's have, and every wave's reads of stage st are done
+    copy_stage(st + NBUF, st % NBUF);
+    read_frags(next, st + 1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < TPW; ++j)
+#pragma unroll
+      for (int f = 0; f < MF; ++f) acc[j][f] = mfma16<DT>(cur[MF + j], cur[f], acc[j][f]);
+    __builtin_amdgcn_sched_barrier(0);
+    lds_wait(next);
+  };
+  u32x4 fa[MF + TPW], fb[MF + TPW];
+  wait_vmcnt<(NBUF - 1) * DPW>();  // stage 0
+  __builtin_amdgcn_s_barrier();
+  read_frags(fa, 0);
+  lds_wait(fa);
+  int st = 0;
 #pragma nounroll
-  for (int st = 0; st < nst; ++st) {
-    wait_vmcnt<(NBUF - 2) * DPW>();  // this wave's copies of stage st have landed
-    __builtin_amdgcn_s_barrier();    // everyone's have; buffer (st - 1) % NBUF is free
-    copy_stage(st + NBUF - 1, q == 0 ? NBUF - 1 : q - 1);
-    const u32x4* blk = lds + (size_t)q * SB * 64;
-    u32x4 xf[MF];
-#pragma unroll
-    for (int f = 0; f < MF; ++f) xf[f] = blk[(wm * MF + f) * 64 + lane];
-#pragma unroll
-    for (int j = 0; j < TPW; ++j) {
-      const u32x4 wf = blk[(BMB + wn * TPW + j) * 64 + lane];
-#pragma unroll
-      for (int f = 0; f < MF; ++f) acc[j][f] = mfma16<DT>(wf, xf[f], acc[j][f]);
-    }
-    q = q == NBUF - 1 ? 0 : q + 1;
+  for (; st + 1 < nst; st += 2) {
+    step(st, fa, fb);
+    step(st + 1, fb, fa);
   }
+  if (st < nst) step(st, fa, fb);
   wait_vmcnt<0>();  // no copy may still be writing LDS when the workgroup ends
 
   const int f0 = wm * MF, tw0 = t0 + wn * TPW;
