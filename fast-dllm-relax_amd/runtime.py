@@ -99,6 +99,15 @@ def _embed(vm: HipVM, ids) -> torch.Tensor:
     return vm.embed_unchecked(_ids_tensor(vm, ids))[None]
 
 
+def _to_host(t: torch.Tensor) -> np.ndarray:
+    """Device tensor -> numpy through page-locked memory (torch's caching host allocator, so repeated
+    calls reuse the staging blocks): a pageable copy of the 64 x 151936 fp32 scoring logits ran at
+    4 GB/s (9.4 ms), a pinned one at the link's rate."""
+    host = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+    host.copy_(t)
+    return host.numpy()
+
+
 def _offset_tensor(value: int) -> torch.Tensor:
     return torch.tensor(int(value), dtype=torch.int32).pin_memory().to("cuda", non_blocking=True)
 
@@ -346,7 +355,7 @@ def score_sequence_block(vm: HipVM, sequence_ids, *, block_size: int):
     bias = torch.from_numpy(build_prefix_block_attention_bias(len(prefix_ids), len(active),
                                                               block_size=block_size)).cuda()
     hidden = vm.forward_hidden(_embed(vm, prefix_ids + active), bias)
-    logits = vm.get_logits(hidden).cpu().numpy()
+    logits = _to_host(vm.get_logits(hidden))
     cur = logits[:, -len(active):, :]
     shifted = extract_shifted_block_logits(logits, prefix_len=len(prefix_ids), block_len=len(active))
     return cur, shifted
@@ -383,7 +392,7 @@ def score_masked_continuation(vm: HipVM, prefix_ids, continuation_ids, *, block_
     logits = vm.get_logits(hidden)
     shifted = torch.cat([logits[:, :1, :], logits[:, :-1, :]], dim=1)
     end = len(real) + len(continuation_ids)
-    return shifted[0, len(real):end, :].cpu().numpy(), (aligned, cache)
+    return _to_host(shifted[0, len(real):end, :]), (aligned, cache)
 
 
 def relax_greedy_generate(vm: HipVM, prompt_token_ids, *, max_new_tokens: int, block_size: int = 32,
