@@ -263,6 +263,10 @@ GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol) {
       // qkv on the 64 x 128 (and 64 x 64) register-weight blocks half: 17.1 against 20.4 us at 512 rows (128 workgroups
       // without a split against 256 with one), 13.8 against 14.5 at 128 (two splits against four)
       if (cfg == CFG_QKV && (id == MM_WR_S || id == MM_WR_T)) target /= 2;
+      // down above 128 rows seven eighths: at 512 rows seven splits (224 workgroups) against eight (256)
+      // measured 3.92 against 3.94-3.95 ms per batched step (fewer partials for the split sum; five
+      // splits 4.03, ten 3.95)
+      if (cfg == CFG_DOWN && a.M > 128) target = target * 7 / 8;
       int split = 1;
       const int max_split = id == MM_WR || id == MM_WR_S || id == MM_WR_M || id == MM_WR_T ? 16 : 8;
       if (pol.force_split > 1 && cfg != CFG_LM_HEAD && nst % pol.force_split == 0 && nst / pol.force_split >= pol.min_stages)
