@@ -251,20 +251,45 @@ void gemm_wr_kernel(GemmP a, int nbm, int nbn) {
   // registers are never read, so fewer than VPS instructions per stage follow and a count wait would
   // return before stage st's copies landed.
   const u32x4* lds = reinterpret_cast<const u32x4*>(smem);
+  // PIPE (blocks with registers to spare): a wave reads stage st + 1's activation fragments right after
+  // its MFMAs of stage st are issued, so the LDS latency passes during the next wait and barrier; the
+  // wait of stage st is then for stage st + 1's copies (one stage less of lead, of D).  Otherwise the
+  // fragments of stage st are read after its barrier.
+  constexpr bool PIPE = MF * TPW <= 16 && D >= 3;
+  u32x4 xf[MF];
+  if constexpr (PIPE) {
+    wait_vmcnt<(D - 1) * VPS>();  // stage 0
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int f = 0; f < MF; ++f) xf[f] = lds[f * 64 + lane];
+  }
   auto stage = [&](int st, auto uc, auto exact) {
     constexpr int u = decltype(uc)::value;
-    if constexpr (decltype(exact)::value) wait_vmcnt<(D - 1) * VPS>();  // stage st's copies and weights
-    else wait_vmcnt<0>();
-    __builtin_amdgcn_s_barrier();    // every wave's copies have; buffer (u - 1) % R is free
+    if constexpr (PIPE) {
+      if constexpr (decltype(exact)::value) wait_vmcnt<(D - 2) * VPS>();  // stage st + 1's copies and weights
+      else wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();  // every wave's have; every wave read buffer (u - 1) % R one stage ago
+    } else {
+      if constexpr (decltype(exact)::value) wait_vmcnt<(D - 1) * VPS>();  // stage st's copies and weights
+      else wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();    // every wave's copies have; buffer (u - 1) % R is free
+    }
     issue(st + D, wv[(u + D) % R], (u + D) % R);
-    const u32x4* blk = lds + (size_t)u * MF * 64;
-    u32x4 xf[MF];
+    if constexpr (!PIPE) {
+      const u32x4* blk = lds + (size_t)u * MF * 64;
 #pragma unroll
-    for (int f = 0; f < MF; ++f) xf[f] = blk[f * 64 + lane];
+      for (int f = 0; f < MF; ++f) xf[f] = blk[f * 64 + lane];
+    }
 #pragma unroll
     for (int j = 0; j < TPW; ++j)
 #pragma unroll
       for (int f = 0; f < MF; ++f) acc[j][f] = mfma16<DT>(wv[u][j], xf[f], acc[j][f]);
+    if constexpr (PIPE) {
+      // stage st + 1 (past the last: the copies re-read the last stage, read and not used)
+      const u32x4* nblk = lds + (size_t)((u + 1) % R) * MF * 64;
+#pragma unroll
+      for (int f = 0; f < MF; ++f) xf[f] = nblk[f * 64 + lane];
+    }
   };
   // whole rounds of R stages, then the last nst % R stages outside the loop (an exit from inside the
   // unrolled round would make the compiler's own counter bookkeeping wait for everything at its top)
