@@ -600,6 +600,26 @@ def batched_shifted_confidence(vm: HipVM, hidden: torch.Tensor) -> tuple[np.ndar
     return (np.concatenate([ids[:, :1], ids[:, :-1]], axis=1), np.concatenate([maxp[:, :1], maxp[:, :-1]], axis=1))
 
 
+def batched_shifted_confidence_rows(vm: HipVM, hidden: torch.Tensor, s0: int, s1: int) -> tuple[np.ndarray, np.ndarray]:
+    """Columns [s0, s1) of batched_shifted_confidence(vm, hidden), bit for bit, through the lm_head of only
+    the rows they read: shifted row i takes logit row i - 1 (row 0 its own), so rows max(s0 - 1, 0) ..
+    s1 - 2 of each sequence.  A row's logits and confidence do not depend on the other rows of the call
+    (the lm_head never splits k), so the values are the full call's."""
+    nseq, rows = int(hidden.shape[0]), int(hidden.shape[1])
+    if not 0 <= s0 < s1 <= rows:
+        raise ValueError(f"rows [{s0}, {s1}) outside [0, {rows})")
+    lo, hi = max(s0 - 1, 0), max(s1 - 1, 1)
+    sub = hidden[:, lo:hi].contiguous()
+    n = hi - lo
+    both_d = torch.empty((1, 2 * nseq * n), dtype=torch.int32, device=hidden.device)
+    vm.get_confidence(sub.view(1, nseq * n, -1), out=both_d)
+    both = both_d.cpu().numpy()[0].view(np.float32)
+    ids = both[:nseq * n].view(np.int32).astype(np.int64).reshape(nseq, n)
+    maxp = both[nseq * n:].astype(np.float32).reshape(nseq, n)
+    src = [max(i - 1, 0) - lo for i in range(s0, s1)]
+    return ids[:, src], maxp[:, src]
+
+
 def relax_batched_block_refine(vm: HipVM, prompts, *, mask_id: int, block_size: int = 32,
                                small_block_size: int = 8, threshold: float = 0.9, use_block_cache: bool = True,
                                timing: dict | None = None):
@@ -655,18 +675,19 @@ def relax_batched_block_refine(vm: HipVM, prompts, *, mask_id: int, block_size: 
                 off = torch.tensor([a0 + s0 for a0 in a0s], dtype=torch.int32, device=dev)
                 hidden = vm.forward_block_partial_batch(s0, emb, k, v, off, a0s)
                 partial_steps += 1
+                sids, sprobs = batched_shifted_confidence(vm, hidden)
             else:
                 ids = [t for x, a0 in zip(xs, a0s) for t in x[a0:a0 + block_size]]
                 emb = _embed(vm, ids).view(nseq, block_size, -1)
                 hidden = vm.forward_cached_batch(emb, k, v, off_full, a0s)
                 block_kv_valid = use_block_cache
+                # the rule reads the sub-block's rows only: the lm_head runs on the 8 logit rows they take
+                sids, sprobs = batched_shifted_confidence_rows(vm, hidden, s0, s1)
             steps += 1
-            sids, sprobs = batched_shifted_confidence(vm, hidden)
             for b in range(nseq):
                 if not local[b]:
                     continue
-                bids = sids[b] if use_partial else sids[b][s0:s1]
-                bp = sprobs[b] if use_partial else sprobs[b][s0:s1]
+                bids, bp = sids[b], sprobs[b]
                 rows = [r for r in local[b] if bp[r] > threshold]
                 if not rows:
                     rows = [local[b][int(np.argmax([bp[r] for r in local[b]]))]]

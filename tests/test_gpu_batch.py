@@ -146,6 +146,16 @@ def test_wide_batched_step_16_sequences(wide2):
     wid, wp = oconf.confidence(to_np(logits)[0])
     np.testing.assert_array_equal(ids.cpu().numpy()[0], wid)
     np.testing.assert_array_equal(maxp.cpu().numpy()[0].view(np.uint32), wp.view(np.uint32))
+    # the batched loop's full steps take the confidence of the sub-block's logit rows only (the lm_head at
+    # M = 112 or 128): the same bits as the shifted confidence of all 512 rows, sliced
+    from fast_dllm_relax_amd.runtime import batched_shifted_confidence, batched_shifted_confidence_rows
+
+    all_ids, all_p = batched_shifted_confidence(vm, h)
+    for s0 in (0, 8, 16, 24):
+        log(f"case: shifted confidence of rows [{s0}, {s0 + 8}) of 16 sequences vs all rows")
+        sid, sp = batched_shifted_confidence_rows(vm, h, s0, s0 + 8)
+        np.testing.assert_array_equal(sid, all_ids[:, s0:s0 + 8])
+        np.testing.assert_array_equal(sp.view(np.uint32), all_p[:, s0:s0 + 8].view(np.uint32))
 
 
 def test_seq_attention_kernel_matches_chunk_kernel(monkeypatch):
