@@ -134,9 +134,9 @@ __device__ __forceinline__ float fd_exp_neg(float x) {
 // SiLU(gate) x up with the rounding points of _silu_fp32 (model/cuda.py:319-328): gate and up rounded to
 // DT, silu = gate x (1 / (1 + exp(-gate))) in fp32 rounded to DT, the product rounded to DT.  The
 // reciprocal is the hardware estimate refined by one Newton-Raphson step, r + r (1 - d r), which agrees
-// with the IEEE quotient to within its last bit (the IEEE division sequence costs several times as many
-// instructions, and the gate/up epilogue is VALU-bound); past 2^64 the estimate alone (the step would form
-// inf x 0), for d = inf exactly 0.
+// with the IEEE quotient to within its last bit (the IEEE division sequence is several times as many
+// instructions per element of an epilogue that is VALU work only); past 2^64 the estimate alone (the step
+// would form inf x 0), for d = inf exactly 0.
 template <int DT>
 __device__ __forceinline__ u16 silu_mul(float g, float u) {
   const float gt = rnd<DT>(g), up = rnd<DT>(u);
