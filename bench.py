@@ -435,7 +435,8 @@ def batched_bench(args) -> dict:
     res = {
         "workload": f"BASELINE config 4: 1.5B fp16, seed 3, {BATCH_SEQS} sequences, prefixes U[128, 1024], one "
                     f"32-token block each starting at the prefix rounded down to 32 (the prompt's tail + masks), "
-                    f"sub-blocks of 8, threshold 0.9, untied lm_head N(0, 0.5) (BASELINE.json: tied head)",
+                    f"sub-blocks of 8, threshold 0.9, untied lm_head N(0, 0.5) (BASELINE.json: tied head); the loop's "
+                    f"full steps score only the sub-block's rows (step_full_ms: confidence of all 512 rows)",
         "prefixes": prefixes,
         "tokens_per_s": round(unmasked / refine_s, 2), "tokens": unmasked, "refine_s": round(refine_s, 4),
         "steps": steps, "partial_steps": partial_steps,
