@@ -181,7 +181,11 @@ using WrBig = WrCfg<8, 4, FD_WR_DEPTH>;  // 128 x 256
 using WrSmall = WrCfg<4, 2, FD_WR_SMALL_DEPTH>;  // 64 x 128
 using WrMid = WrCfg<8, 2, 6>;    // 128 x 128 (six stages: 56 KB of LDS)
 using WrTiny = WrCfg<4, 1, 12>;  // 64 x 64 (4 MFMAs per k step and wave: twelve stages in flight)
-enum MmId : int { MM_SMALL = 0, MM_WIDE = 1, MM_WIDE_D = 2, MM_BIG = 3, MM_WT = 4, MM_WR = 5, MM_WR_S = 6, MM_WR_M = 7, MM_WR_T = 8 };
+// 128 x 192 (o_proj / down from the register-weight thresholds: 1536 columns make 8 column blocks, so
+// 64 row blocks of 8192 rows fill 512 slots, two per compute unit, where the 128 x 256 blocks' 384
+// leave half the units with one)
+using WrB3 = WrCfg<8, 3, FD_WR_DEPTH>;
+enum MmId : int { MM_SMALL = 0, MM_WIDE = 1, MM_WIDE_D = 2, MM_BIG = 3, MM_WT = 4, MM_WR = 5, MM_WR_S = 6, MM_WR_M = 7, MM_WR_T = 8, MM_WR_3 = 9 };
 struct MmInfo { int bm, bn_tiles, kss; };
 template <class M> constexpr MmInfo mm_info_of() { return MmInfo{M::bm, M::bn_tiles, M::kss}; }
 static MmInfo mm_info(int id) {
@@ -194,6 +198,7 @@ static MmInfo mm_info(int id) {
     case MM_WR_S: return mm_info_of<WrSmall>();
     case MM_WR_M: return mm_info_of<WrMid>();
     case MM_WR_T: return mm_info_of<WrTiny>();
+    case MM_WR_3: return mm_info_of<WrB3>();
     default: return mm_info_of<MmSmall>();
   }
 }
@@ -207,7 +212,8 @@ static int wr_default_min_rows(int cfg) {
 }
 static int mm_choice(int cfg, int M, int ntiles, const MmPolicy& pol) {
   const int min_rows = pol.wr_min_rows > 0 ? pol.wr_min_rows : wr_default_min_rows(cfg);
-  if (M >= std::max(min_rows, 33) && ((pol.wr_ops >> cfg) & 1)) return MM_WR;
+  if (M >= std::max(min_rows, 33) && ((pol.wr_ops >> cfg) & 1))
+    return pol.wr3 && (cfg == CFG_OPROJ || cfg == CFG_DOWN) && ntiles % WrB3::bn_tiles == 0 ? MM_WR_3 : MM_WR;
   // qkv and o_proj below that: 64 x 128 register-weight blocks (us per launch, qkv including its norm pass,
   // against the LDS-staged 64 x 128 kernel): qkv 16.2 / 14.9 at 128 rows, 23.2 / 20.2 at 512, 26.2 / 19.4
   // at 1024, 30.8 / 28.6 at 2048; o_proj 15.2 / 14.0 at 384, 15.4 / 14.0 at 512, 19.3 / 15.1 at 1024, but
@@ -268,7 +274,7 @@ GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol) {
       // splits 4.03, ten 3.95)
       if (cfg == CFG_DOWN && a.M > 128) target = target * 7 / 8;
       int split = 1;
-      const int max_split = id == MM_WR || id == MM_WR_S || id == MM_WR_M || id == MM_WR_T ? 16 : 8;
+      const int max_split = id == MM_WR || id == MM_WR_S || id == MM_WR_M || id == MM_WR_T || id == MM_WR_3 ? 16 : 8;
       if (pol.force_split > 1 && cfg != CFG_LM_HEAD && nst % pol.force_split == 0 && nst / pol.force_split >= pol.min_stages)
         split = pol.force_split;
       else
@@ -399,6 +405,10 @@ static hipError_t launch_mm(const GemmP& a, const GemmPlan& p, hipStream_t st) {
   }
   if (p.mm_id == MM_WR_M) {
     if constexpr (CFG == CFG_GATE_UP || CFG == CFG_DOWN) return launch_wr_cfg<DT, C::epi, WrMid>(a, p, st);
+    return hipErrorInvalidValue;
+  }
+  if (p.mm_id == MM_WR_3) {
+    if constexpr (CFG == CFG_OPROJ || CFG == CFG_DOWN) return launch_wr_cfg<DT, C::epi, WrB3>(a, p, st);
     return hipErrorInvalidValue;
   }
   if constexpr (CFG == CFG_GATE_UP) {

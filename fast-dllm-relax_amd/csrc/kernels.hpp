@@ -76,6 +76,7 @@ struct MmPolicy {
   // blocks, bit 2 / 3 the 128 x 128 ones (0: the LDS-staged kernel)
   int wr_ffn = -1;
   int force_split = 0;  // > 1: this k split whenever it divides the stages (the fused o_proj + norm)
+  int wr3 = 1;          // o_proj / down at the register-weight thresholds: 128 x 192 blocks (0: 128 x 256)
 };
 GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol = MmPolicy{});
 // whether the plan runs the one-shot register-fragment body, the only one that takes xfrag / yfrag 1
