@@ -141,9 +141,11 @@ GemmShape gemm_shape(int cfg) {
   return GemmShape{l, 0};
 }
 
-// rows from which the lm_head (with its confidence statistics) takes the register-weight kernel
+// rows from which the lm_head (with its confidence statistics) takes the register-weight kernel (us per
+// launch with the statistics, fp16, register-weight / 64 x 256 LDS-staged blocks: 199 / 228-232 at 256 rows,
+// 326 / 386 at 512, even at 112-128)
 #ifndef FD_WR_LM_MIN_ROWS
-#define FD_WR_LM_MIN_ROWS 512
+#define FD_WR_LM_MIN_ROWS 256
 #endif
 // stages in flight of the register-weight kernel
 #ifndef FD_WR_DEPTH

@@ -64,7 +64,7 @@ struct GemmPlan {
 // How large-M launches are planned.  target_wgs / min_stages: k is split only while the launch has fewer
 // than target_wgs workgroups, and only into splits of at least min_stages stages.  wr_ops: the
 // projections (bit cfg) that may take the register-weight kernel, from wr_min_rows rows (0: from 2048
-// rows for gate_up and down, 4096 for qkv and o_proj, 512 for the lm_head, where it measured faster
+// rows for gate_up and down, 4096 for qkv and o_proj, 256 for the lm_head, where it measured faster
 // than the LDS-staged and streaming kernels).
 struct MmPolicy {
   int target_wgs = 256;

@@ -153,7 +153,7 @@ def test_prefill_pair_kernel_bit_identical(dtype, monkeypatch):
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
 def test_lm_head_register_weight_bit_identical(dtype, monkeypatch):
-    """The lm_head with its confidence statistics on the register-weight kernel (from 512 rows by default;
+    """The lm_head with its confidence statistics on the register-weight kernel (from 256 rows by default;
     FDLLM_WR_MIN_ROWS=128 here) against gemm_mm_kernel (FDLLM_WR_OPS without the lm_head bit): logits, ids
     and maxp bit for bit, at ragged and whole row counts, with and without the fp32 logits output."""
     from fast_dllm_relax_amd.config import FastDLLMConfig
