@@ -689,6 +689,7 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   if (const char* e = std::getenv("FDLLM_WR_SMALL")) c->mm.wr_small_ops = atoi(e) & 3;
   if (const char* e = std::getenv("FDLLM_WR_FFN")) c->mm.wr_ffn = e[0] != '\0' ? (atoi(e) & 15) : -1;
   if (const char* e = std::getenv("FDLLM_WR3")) c->mm.wr3 = atoi(e) != 0;
+  if (const char* e = std::getenv("FDLLM_WT8")) c->mm.wt8 = atoi(e);
   if (const char* e = std::getenv("FDLLM_PERSISTENT")) c->step_on = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_XFRAG")) c->frag_on = atoi(e) != 0;
   c->step_check = step_check_default(c->step_on, std::getenv("FDLLM_STEP_CHECK"));

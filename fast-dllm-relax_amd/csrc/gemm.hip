@@ -166,6 +166,10 @@ struct WtCfg {
   static constexpr size_t lds = (size_t)NBUF * (MF * WM + TPW * WN) * 1024;
 };
 using WtBig = WtCfg<4, 6, 2, 2, 4>;
+// 4 x 2 waves of 32 x 96 (124 registers, two workgroups and 16 waves per compute unit; waves copy 3 or 2
+// of the 20 blocks a stage).  gate_up, us per launch with its norm pass, eight / four waves: 43.4 / 43.8 at
+// 384 rows, 44.4 / 44.7 at 512, 58.8 / 59.6 at 768, 60.6 / 61.4 at 1024; down unchanged (28.6 at 512)
+using WtBig8 = WtCfg<2, 6, 4, 2, 4>;
 // register-weight kernel (gemm_wt.hpp, gemm_wr_kernel): four waves of 16 MF rows x TPW tiles, a
 // 16 MF x 64 TPW block, D stages in flight
 template <int MF, int TPW, int D>
@@ -187,7 +191,7 @@ using WrTiny = WrCfg<4, 1, 12>;  // 64 x 64 (4 MFMAs per k step and wave: twelve
 // 64 row blocks of 8192 rows fill 512 slots, two per compute unit, where the 128 x 256 blocks' 384
 // leave half the units with one)
 using WrB3 = WrCfg<8, 3, FD_WR_DEPTH>;
-enum MmId : int { MM_SMALL = 0, MM_WIDE = 1, MM_WIDE_D = 2, MM_BIG = 3, MM_WT = 4, MM_WR = 5, MM_WR_S = 6, MM_WR_M = 7, MM_WR_T = 8, MM_WR_3 = 9 };
+enum MmId : int { MM_SMALL = 0, MM_WIDE = 1, MM_WIDE_D = 2, MM_BIG = 3, MM_WT = 4, MM_WR = 5, MM_WR_S = 6, MM_WR_M = 7, MM_WR_T = 8, MM_WR_3 = 9, MM_WT_8 = 10 };
 struct MmInfo { int bm, bn_tiles, kss; };
 template <class M> constexpr MmInfo mm_info_of() { return MmInfo{M::bm, M::bn_tiles, M::kss}; }
 static MmInfo mm_info(int id) {
@@ -201,6 +205,7 @@ static MmInfo mm_info(int id) {
     case MM_WR_M: return mm_info_of<WrMid>();
     case MM_WR_T: return mm_info_of<WrTiny>();
     case MM_WR_3: return mm_info_of<WrB3>();
+    case MM_WT_8: return mm_info_of<WtBig8>();
     default: return mm_info_of<MmSmall>();
   }
 }
@@ -237,10 +242,10 @@ static int mm_choice(int cfg, int M, int ntiles, const MmPolicy& pol) {
   switch (cfg) {
     case CFG_LM_HEAD: return MM_WIDE;  // one 256-column confidence tile per block column
     case CFG_GATE_UP:
-      if (M >= 256 && ntiles % WtBig::bn_tiles == 0) return MM_WT;
+      if (M >= 256 && ntiles % WtBig::bn_tiles == 0) return (pol.wt8 & 1) ? MM_WT_8 : MM_WT;
       return M >= 1024 ? MM_BIG : MM_WIDE;
     case CFG_DOWN:
-      if (M >= 256 && ntiles % WtBig::bn_tiles == 0) return MM_WT;
+      if (M >= 256 && ntiles % WtBig::bn_tiles == 0) return (pol.wt8 & 2) ? MM_WT_8 : MM_WT;
       return M >= 1024 ? MM_WIDE_D : MM_SMALL;
     default:  // qkv, o_proj: the LDS-staged kernel measured slower at their widths (2048 / 1536 columns)
       return MM_SMALL;
@@ -415,10 +420,12 @@ static hipError_t launch_mm(const GemmP& a, const GemmPlan& p, hipStream_t st) {
   }
   if constexpr (CFG == CFG_GATE_UP) {
     if (p.mm_id == MM_WT) return launch_wt_cfg<DT, C::epi, WtBig>(a, p, st);
+    if (p.mm_id == MM_WT_8) return launch_wt_cfg<DT, C::epi, WtBig8>(a, p, st);
     if (p.mm_id == MM_BIG) return launch_mm_cfg<DT, C::epi, XF_NONE, MmBig>(a, p, st);
     return launch_mm_cfg<DT, C::epi, XF_NONE, MmWide>(a, p, st);
   } else if constexpr (CFG == CFG_DOWN) {
     if (p.mm_id == MM_WT) return launch_wt_cfg<DT, C::epi, WtBig>(a, p, st);
+    if (p.mm_id == MM_WT_8) return launch_wt_cfg<DT, C::epi, WtBig8>(a, p, st);
     if (p.mm_id == MM_WIDE_D) return launch_mm_cfg<DT, C::epi, XF_NONE, MmWideD>(a, p, st);
     return launch_mm_cfg<DT, C::epi, XF_NONE, MmSmall>(a, p, st);
   } else if constexpr (CFG == CFG_QKV || CFG == CFG_OPROJ) {

@@ -14,7 +14,8 @@
 // fragments every wave has read into registers, which then receives the copies NBUF stages ahead; the
 // fragment reads of stage st + 1 overlap the MFMAs of stage st.  Every copy is unconditional
 // (stages past the last re-read the last; rows past M re-read row M - 1), so every wave issues the same
-// number per stage and the counter waits are exact.
+// number per stage and the counter waits are exact.  When the waves do not divide a stage's blocks, the
+// first SB % NW waves copy one block more than the rest, and each wave waits for its own count.
 //
 // K splits (gridDim.y > 1) store fp32 sums per (tile, 16-row block) exactly as gemm_mm_kernel does, and
 // gemm_mm_split_epilogue_kernel adds them in split order.  Per output element the k steps are
@@ -31,8 +32,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_wt_kernel(GemmP a, int nbm,
   constexpr int BMB = MF * WM;        // activation blocks (16 rows) per stage
   constexpr int BNT = TPW * WN;       // weight tiles per stage
   constexpr int SB = BMB + BNT;       // 1 KB blocks per stage
-  constexpr int DPW = SB / NW;        // copies per wave per stage
-  static_assert(SB % NW == 0, "every wave copies the same number of blocks per stage");
+  constexpr int DPW = (SB + NW - 1) / NW;  // copies per wave per stage (waves >= NHI: one fewer)
+  constexpr int NHI = SB % NW == 0 ? NW : SB % NW;
   static_assert(NBUF >= 2, "at least two stage buffers");
   static_assert((NBUF - 1) * DPW < 64, "outstanding copies fit the memory counter");
   static_assert(EPI != EPI_SILU_PAIR || TPW % 2 == 0, "gate/up pairs stay within a wave");
@@ -47,10 +48,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_wt_kernel(GemmP a, int nbm,
   if (logical >= total) return;
   const int nb = logical / nbm, mb = logical - nb * nbm;
 
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // wave-uniform: scalar branches
   const int wm = w / WN, wn = w - wm * WN;
   const int lr = lane & 15, lg = lane >> 4;
   const int m0 = mb * 16 * BMB, mlast = a.M - 1;
+  const bool lo = NHI < NW && w >= NHI;  // this wave copies DPW - 1 blocks per stage
   const int t0 = nb * BNT, tlast = a.ntiles - 1;
   const int nst = a.KS / (int)gridDim.y;        // k steps of this split
   const int kb = (int)blockIdx.y * nst;         // its first k step
@@ -60,7 +63,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_wt_kernel(GemmP a, int nbm,
   size_t sstep[DPW];  // elements per k step
 #pragma unroll
   for (int q = 0; q < DPW; ++q) {
-    const int i = w + NW * q;
+    const int i = min(w + NW * q, SB - 1);  // (a low wave's last slot: never copied)
     if (i < BMB && a.xfrag == 2) {
       // fragment blocks: one 1 KB read per block (a block past the last row block re-reads the last)
       const int b = min(m0 / 16 + i, mlast / 16);
@@ -79,7 +82,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_wt_kernel(GemmP a, int nbm,
     const int s = min(st, nst - 1);
 #pragma unroll
     for (int q = 0; q < DPW; ++q)
-      lds_copy16(src[q] + (size_t)s * sstep[q], smem + ((size_t)buf * SB + w + NW * q) * 1024);
+      if (q < DPW - 1 || !lo) lds_copy16(src[q] + (size_t)s * sstep[q], smem + ((size_t)buf * SB + w + NW * q) * 1024);
+  };
+  // this wave's own copies of the next N stages have landed (its count per stage is DPW or DPW - 1)
+  auto wait_stages = [&](auto nc) __attribute__((always_inline)) {
+    constexpr int N = decltype(nc)::value;
+    if (lo) wait_vmcnt<N * (DPW - 1)>();
+    else wait_vmcnt<N * DPW>();
   };
 
   f32x4 acc[TPW][MF];
@@ -105,7 +114,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_wt_kernel(GemmP a, int nbm,
   // iteration st: fragments of st in cur; next receives those of st + 1 (past the last stage the buffer
   // holds a re-read of the last, read and not used)
   auto step = [&](int st, u32x4 (&cur)[MF + TPW], u32x4 (&next)[MF + TPW]) __attribute__((always_inline)) {
-    wait_vmcnt<(NBUF - 2) * DPW>();  // this wave's copies of stage st + 1 have landed
+    wait_stages(std::integral_constant<int, NBUF - 2>{});  // this wave's copies of stage st + 1 have landed
     __builtin_amdgcn_s_barrier();    // everyone's have, and every wave's reads of stage st are done
     copy_stage(st + NBUF, st % NBUF);
     read_frags(next, st + 1);
@@ -118,7 +127,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_wt_kernel(GemmP a, int nbm,
     lds_wait(next);
   };
   u32x4 fa[MF + TPW], fb[MF + TPW];
-  wait_vmcnt<(NBUF - 1) * DPW>();  // stage 0
+  wait_stages(std::integral_constant<int, NBUF - 1>{});  // stage 0
   __builtin_amdgcn_s_barrier();
   read_frags(fa, 0);
   lds_wait(fa);
