@@ -163,11 +163,52 @@ constexpr int SEQ_DEPTH = 3;
 #endif
 constexpr int SEQ_KH = FD_SEQ_KH, SEQ_NQW = FD_SEQ_NQW;
 
+size_t plan_seq_units(AttnP& a, int ncu) {
+  const int QT = ((a.nq / a.nkv) * a.rows + 15) / 16, xg = (QT + SEQ_NQW - 1) / SEQ_NQW;
+  int T[MAX_SEQS], s[MAX_SEQS];
+  for (int b = 0; b < a.nseq; ++b) {
+    T[b] = std::max(1, (a.seq_lk[b] + 63) / 64);
+    s[b] = 1;
+  }
+  int units = a.nseq;
+  const bool cnt_ok = a.seq_cnt != nullptr && (size_t)a.nseq * a.nkv * xg * SEQ_NQW <= (size_t)SEQ_CNT_MAX;
+  const int cap = cnt_ok && ncu > 0 ? std::min(MAX_SEQ_UNITS, std::max(a.nseq, ncu / (a.nkv * xg))) : a.nseq;
+  while (units < cap) {
+    int best = 0, bl = 0;
+    for (int b = 0; b < a.nseq; ++b) {
+      const int l = (T[b] + s[b] - 1) / s[b];
+      if (l > bl) { bl = l; best = b; }
+    }
+    if (bl <= 2 || s[best] >= 16) break;
+    ++s[best];
+    ++units;
+  }
+  // sequence-major units (u0 + j indexes the partials), launched longest first: units past what one
+  // round of workgroups holds wait for the first to finish, and the shortest wait at least cost
+  int ua[MAX_SEQ_UNITS], ut[MAX_SEQ_UNITS], ord[MAX_SEQ_UNITS];
+  int u = 0;
+  for (int b = 0; b < a.nseq; ++b)
+    for (int j = 0; j < s[b]; ++j, ++u) {
+      ua[u] = b | (j << 6) | (s[b] << 11) | ((u - j) << 16);
+      ut[u] = (T[b] * j / s[b]) | ((T[b] * (j + 1) / s[b]) << 16);
+      ord[u] = u;
+    }
+  auto len = [&](int v) { return (ut[v] >> 16) - (ut[v] & 0xffff); };
+  std::stable_sort(ord, ord + u, [&](int x, int y) { return len(x) > len(y); });
+  for (int v = 0; v < u; ++v) {
+    a.unit_a[v] = ua[ord[v]];
+    a.unit_t[v] = ut[ord[v]];
+  }
+  a.nunits = u;
+  return units > a.nseq ? (size_t)u * a.nkv * xg * SEQ_NQW * PSZ : 0;
+}
+
 template <int DT>
 static hipError_t launch_seq(const AttnP& a, hipStream_t st) {
+  if (a.nunits < a.nseq || a.nunits > MAX_SEQ_UNITS) return hipErrorInvalidValue;
   hipLaunchKernelGGL(rope_kv_kernel<DT>, dim3(a.nseq * a.rows), dim3(128), 0, st, a);
   const int QT = ((a.nq / a.nkv) * a.rows + 15) / 16, xg = (QT + SEQ_NQW - 1) / SEQ_NQW;
-  const int pairs = a.nseq * a.nkv;
+  const int pairs = a.nunits * a.nkv;
   auto kern = attn_seq_kernel<DT, SEQ_DEPTH, SEQ_NQW, SEQ_KH>;
   constexpr size_t lds = (size_t)(SEQ_DEPTH + 1) * 2 * 64 * HD * 2;  // K and V of D + 1 key blocks
   raise_lds(kern, lds);

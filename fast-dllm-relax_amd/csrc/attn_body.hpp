@@ -1248,10 +1248,10 @@ void attn_prefill_pair_kernel(AttnP a) {
 }
 
 // attn_seq_kernel: the attention of a batched call (nseq sequences of `rows` rows each, no mask) without
-// key splits, so without partials or a merge launch.  Workgroup (sequence b, kv head g, group x of NQW
-// query tiles) with NQW KH waves: wave w takes query tile NQW x + w % NQW of the stacked rows of the
-// chunk kernels (row qi = head in group x rows + r, 16 per tile) and key part kh = w / NQW, i.e. keys
-// 64 j + 64 / KH kh .. of every 64-key block j of the sequence's [0, Lk_b).  The blocks stream through
+// a merge launch.  Workgroup (unit u = split js of sequence b's 64-key blocks [tb, te), kv head g, group
+// x of NQW query tiles) with NQW KH waves: wave w takes query tile NQW x + w % NQW of the stacked rows of
+// the chunk kernels (row qi = head in group x rows + r, 16 per tile) and key part kh = w / NQW, i.e. keys
+// 64 j + 64 / KH kh .. of every block j of the split (keys past Lk_b masked).  The blocks stream through
 // LDS, D blocks ahead, by the global-to-LDS copy in the paired prefill kernel's layout (a 256-byte row per
 // key, 16-byte chunk c of row r at slot c ^ (r % 16); V^T fragments from the transposing LDS read).
 // rope_kv_kernel has already appended this call's K/V rows to the cache and put the RoPE'd queries in
@@ -1261,8 +1261,9 @@ void attn_prefill_pair_kernel(AttnP a) {
 // chunk kernel's merge), then one rounding of the output.  The block loop is software-pipelined by one
 // block: the scores of block t + 1 are formed while block t's softmax and P.V run (same arithmetic and
 // order per block; measured 16.8 -> 16.0 us per layer on the 512-row batched step).
-// 1-D grid in XCD-aware order: linear index i, slot i % 8, round i / 8; pair (b, g) = (round / XG) x 8 +
-// slot, query group x = round % XG, so the XG workgroups that read one sequence's K/V run on one XCD and
+// A sequence of one split writes its output directly; splits merge as described at the end.
+// 1-D grid in XCD-aware order: linear index i, slot i % 8, round i / 8; pair (u, g) = (round / XG) x 8 +
+// slot, query group x = round % XG, so the XG workgroups that read one split's K/V run on one XCD and
 // share its L2.  Indices past the last pair have nothing to do.
 template <int DT, int D, int NQW, int KH>
 __global__ __launch_bounds__(64 * NQW * KH) __attribute__((amdgpu_waves_per_eu(NQW * KH > 4 ? 2 : 1, NQW * KH > 4 ? 2 : 1)))
@@ -1283,18 +1284,21 @@ void attn_seq_kernel(AttnP p) {
   const int grp = p.nq / p.nkv, QR = grp * p.rows, QT = (QR + 15) / 16, XG = (QT + NQW - 1) / NQW;
   const int i = blockIdx.x, round = i >> 3;
   const int pair = (round / XG) * 8 + (i & 7), x = round % XG;
-  if (pair >= p.nseq * p.nkv) return;
-  const int b = pair / p.nkv, g = pair - b * p.nkv;
+  if (pair >= p.nunits * p.nkv) return;
+  const int u = pair / p.nkv, g = pair - u * p.nkv;
+  const int ua = p.unit_a[u], ut = p.unit_t[u];
+  const int b = ua & 63, js = (ua >> 6) & 31, ns = (ua >> 11) & 31, u0 = ua >> 16;  // partials at u0 + js
+  const int tb = ut & 0xffff;  // this split's key blocks [tb, tb + T)
   AttnP a = p;
   seq_view(a, p, b);
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int qw = w % NQW, kh = w / NQW;
   const int lr = lane & 15, lg = lane >> 4;
-  const int Lk = a.Lk, T = (Lk + KBP - 1) / KBP;
+  const int Lk = a.Lk, T = (ut >> 16) - tb;
   const size_t krow = (size_t)a.nkv * HD;
-  const u16* kc = a.kc + g * HD;
-  const u16* vc = a.vc + g * HD;
+  const u16* kc = a.kc + g * HD + (size_t)tb * KBP * krow;  // block t of the split: the sequence's tb + t
+  const u16* vc = a.vc + g * HD + (size_t)tb * KBP * krow;
   const float c2 = a.scale * LOG2E;
 
   // copies of block t (blocks past the last re-read the last) into buffer t % R: this wave's 1 KB pieces
@@ -1307,12 +1311,13 @@ void attn_seq_kernel(AttnP p) {
     const int row = 4 * (w * CPW + c) + (lane >> 4);
     src_off[c] = row * (int)krow + 8 * ((lane & 15) ^ (row & 15));
   }
+  const int Lks = Lk - tb * KBP;  // the sequence's keys from the split's first
   auto issue = [&](int t) __attribute__((always_inline)) {
     const int k0 = min(t, T - 1) * KBP;
     unsigned char* buf = smem + (size_t)(t % R) * BUFE * 2;
     const u16* kb = kc + (size_t)k0 * krow;
     const u16* vb = vc + (size_t)k0 * krow;
-    if (k0 + KBP <= Lk) {
+    if (k0 + KBP <= Lks) {
 #pragma unroll
       for (int c = 0; c < CPW; ++c) {
         const int d = w * CPW + c;
@@ -1323,7 +1328,7 @@ void attn_seq_kernel(AttnP p) {
 #pragma unroll
       for (int c = 0; c < CPW; ++c) {
         const int d = w * CPW + c, row = 4 * d + (lane >> 4);
-        const int src = (min(k0 + row, Lk - 1) - k0) * (int)krow + 8 * ((lane & 15) ^ (row & 15));
+        const int src = (min(k0 + row, Lks - 1) - k0) * (int)krow + 8 * ((lane & 15) ^ (row & 15));
         lds_copy16(kb + src, buf + (size_t)d * 1024);
         lds_copy16(vb + src, buf + (size_t)KBP * HD * 2 + (size_t)d * 1024);
       }
@@ -1402,9 +1407,9 @@ void attn_seq_kernel(AttnP p) {
   // the online softmax of block t's scores: P packed for the P.V step; returns whether o must be rescaled
   // by alpha (some query's running maximum moved; alpha = 1 leaves o unchanged bit for bit)
   auto soft = [&](int t, f32x4 (&s)[KT], u32x4 (&pb)[KS], float& alpha) __attribute__((always_inline)) {
-    const int k0 = t * KBP + kp0;  // the part's first key in the sequence
+    const int k0 = t * KBP + kp0;  // the part's first key from the split's first
     float mx = -INFINITY;
-    if (k0 + KPP <= Lk) {
+    if (k0 + KPP <= Lks) {
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
@@ -1417,7 +1422,7 @@ void attn_seq_kernel(AttnP p) {
       for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float v = k0 + 16 * kt + 4 * lg + e < Lk ? s[kt][e] * c2 : -INFINITY;
+          const float v = k0 + 16 * kt + 4 * lg + e < Lks ? s[kt][e] * c2 : -INFINITY;
           s[kt][e] = v;
           mx = fmaxf(mx, v);
         }
@@ -1500,6 +1505,7 @@ void attn_seq_kernel(AttnP p) {
   wait_vmcnt<0>();  // no copy may still be writing LDS when the parts are merged in it
 
   float L = l_run;
+  float Mw = m_run == -INFINITY ? 0.f : m_run;  // o and L are relative to 2^Mw
   if constexpr (KH > 1) {
     // merge the key parts in LDS, in part order (the chunk kernel's merge): parts > 0 leave (m, l) and O^T,
     // part 0 combines them
@@ -1520,6 +1526,7 @@ void attn_seq_kernel(AttnP p) {
     float M = -INFINITY;
     for (int k = 0; k < KH; ++k) M = fmaxf(M, cm[(k * NQW + qw) * 16 + lr]);
     const float Mu = M == -INFINITY ? 0.f : M;
+    Mw = Mu;
     L = 0.f;
     for (int k = 0; k < KH; ++k) L += cl[(k * NQW + qw) * 16 + lr] * __builtin_amdgcn_exp2f(cm[(k * NQW + qw) * 16 + lr] - Mu);
     const float f0 = __builtin_amdgcn_exp2f(cm[qw * 16 + lr] - Mu);
@@ -1530,6 +1537,45 @@ void attn_seq_kernel(AttnP p) {
 #pragma unroll
       for (int dt = 0; dt < DT16; ++dt) o[dt] += co[(((k - 1) * NQW + qw) * DT16 + dt) * 64 + lane] * fk;
     }
+  }
+  if (ns > 1) {
+    // key splits: every split's wave leaves (O, m, l) of its query tile by write-through stores; the last to
+    // arrive (per sequence, kv head and tile) adds the splits in split order, so which one is last does not
+    // change the bits.  The other splits have read their queries from out before they arrived.
+    auto slot = [&](int uu) { return p.part + ((size_t)((uu * p.nkv + g) * XG + x) * NQW + qw) * PSZ; };
+    float* mine = slot(u0 + js);
+#pragma unroll
+    for (int dt = 0; dt < DT16; ++dt) stf4<true>(reinterpret_cast<f32x4*>(mine) + dt * 64 + lane, o[dt]);
+    if (lg == 0) {
+      stf<true>(mine + 16 * HD + lr, Mw);
+      stf<true>(mine + 16 * HD + 16 + lr, L);
+    }
+    wait_memory();  // the stores are acknowledged before the arrival is counted
+    unsigned* cnt = p.seq_cnt + ((b * p.nkv + g) * XG + x) * NQW + qw;
+    unsigned old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old != (unsigned)(ns - 1)) return;
+    if (lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float M = -INFINITY;
+    for (int jj = 0; jj < ns; ++jj) M = fmaxf(M, jj == js ? Mw : ldf<true>(slot(u0 + jj) + 16 * HD + lr));
+    f32x4 ot[DT16];
+#pragma unroll
+    for (int dt = 0; dt < DT16; ++dt) ot[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float Lt = 0.f;
+    for (int jj = 0; jj < ns; ++jj) {
+      const float* q = slot(u0 + jj);
+      const float mj = jj == js ? Mw : ldf<true>(q + 16 * HD + lr);
+      const float lj = jj == js ? L : ldf<true>(q + 16 * HD + 16 + lr);
+      const float f = __builtin_amdgcn_exp2f(mj - M);
+      Lt += lj * f;
+#pragma unroll
+      for (int dt = 0; dt < DT16; ++dt)
+        ot[dt] += (jj == js ? o[dt] : ldf4<true>(reinterpret_cast<const f32x4*>(q) + dt * 64 + lane)) * f;
+    }
+    L = Lt;
+#pragma unroll
+    for (int dt = 0; dt < DT16; ++dt) o[dt] = ot[dt];
   }
   if (!qvalid) return;
   const float inv = 1.0f / L;

@@ -100,6 +100,9 @@ struct fdllm_ctx {
   int prefill_hpw = 0;    // query heads per prefill-attention workgroup (0: chosen per launch)
   int prefill_pair = 1;   // paired-query-block prefill attention (0 off, 1 when it fills the chip, 2 always)
   int seq_attn = 1;       // batched calls: attn_seq_kernel (0: the chunk kernel with key splits + merge)
+  int seq_split = 1;      // attn_seq_kernel splits long sequences' keys over the compute units it leaves idle
+  int ncu = 256;          // compute units of the device
+  unsigned* attn_cnt = nullptr;  // attn_seq_kernel's arrival counters (SEQ_CNT_MAX, zero between launches)
   int fuse_down = 1;      // large-M down launches with k splits: split sum + residual + next RMSNorm in one launch
   // large-M o_proj with a forced k split and its split sum + residual + the next norm in one launch: -1 with
   // three splits up to 256 rows (128-row batched step: 14.8 + 4.8 us norm -> 8.1 + 7.1 us; at 512 rows it
@@ -321,6 +324,15 @@ int run_attention(fdllm_ctx* c, int rows, uint16_t* kc, uint16_t* vc, int ws, in
     return fail(FDLLM_EINVAL, "batched call of %d rows per sequence over %d keys is too long for one step", a.rows, a.Lk);
   a.S = pl.S; a.chunk = pl.chunk; a.target_wgs = target; a.prefill_hpw = c->prefill_hpw; a.prefill_pair = c->prefill_pair;
   a.seq_attn = seq_kernel;
+  if (seq_kernel) {
+    a.seq_cnt = c->attn_cnt;
+    const size_t pf = plan_seq_units(a, c->seq_split ? c->ncu : 0);
+    if (pf) {
+      int rc = ensure_floats(&c->apart, &c->apart_floats, pf);
+      if (rc) return rc;
+      a.part = c->apart;
+    }
+  }
   if (a.S > 1 && !seq_kernel) {
     int rc = ensure_floats(&c->apart, &c->apart_floats, attn_partial_floats(a));
     if (rc) return rc;
@@ -689,6 +701,7 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   if (const char* e = std::getenv("FDLLM_WR_SMALL")) c->mm.wr_small_ops = atoi(e) & 3;
   if (const char* e = std::getenv("FDLLM_WR_FFN")) c->mm.wr_ffn = e[0] != '\0' ? (atoi(e) & 15) : -1;
   if (const char* e = std::getenv("FDLLM_WR3")) c->mm.wr3 = atoi(e) != 0;
+  if (const char* e = std::getenv("FDLLM_SEQ_SPLIT")) c->seq_split = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_WT8")) c->mm.wt8 = atoi(e);
   if (const char* e = std::getenv("FDLLM_PERSISTENT")) c->step_on = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_XFRAG")) c->frag_on = atoi(e) != 0;
@@ -706,13 +719,20 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   c->names.push_back("model.norm.weight");
   if (!f.tie_word_embeddings) c->names.push_back("lm_head.weight");
   c->n_counters = 1 << 16;
-  hipError_t e = hipMalloc((void**)&c->counters, (size_t)c->n_counters * 4 + 64);
-  if (e == hipSuccess) e = hipMemset(c->counters, 0, (size_t)c->n_counters * 4 + 64);
+  const size_t cnt_bytes = ((size_t)c->n_counters + SEQ_CNT_MAX) * 4 + 64;
+  hipError_t e = hipMalloc((void**)&c->counters, cnt_bytes);
+  if (e == hipSuccess) e = hipMemset(c->counters, 0, cnt_bytes);
   if (e != hipSuccess) {
     delete c;
     return fail(FDLLM_EHIP, "workspace allocation failed: %s", hipGetErrorString(e));
   }
-  c->zero_i32 = (int32_t*)(c->counters + c->n_counters);
+  c->attn_cnt = c->counters + c->n_counters;
+  c->zero_i32 = (int32_t*)(c->attn_cnt + SEQ_CNT_MAX);
+  {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->dev) == hipSuccess && cus > 0) c->ncu = cus;
+    else (void)hipGetLastError();
+  }
   {
     // this device's copy of the allocation-free step's scratch array, found once per device
     std::lock_guard<std::mutex> lk(g_scratch_mu);

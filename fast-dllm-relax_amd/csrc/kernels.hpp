@@ -141,6 +141,8 @@ hipError_t launch_resid_norm(int dt, const float* part, int splits, int rows, in
 
 // ---- attention ----------------------------------------------------------------------------------
 constexpr int MAX_SEQS = 64;  // sequences of one batched call
+constexpr int MAX_SEQ_UNITS = 128;      // attn_seq_kernel work units (key splits of the sequences)
+constexpr int SEQ_CNT_MAX = 16384;      // its arrival counters (sequence, kv head, query tile)
 struct AttnP {
   const uint16_t* qkv; int ldq;       // [rows][ldq]: q | k | v, bias added, before RoPE
   int rows, nq, nkv;
@@ -165,9 +167,23 @@ struct AttnP {
   // [0, seq_lk[b]); ws and Lk above then hold the largest window (S and chunk are planned for it)
   int nseq; long long seq_stride;
   int seq_ws[MAX_SEQS]; int seq_lk[MAX_SEQS];
+  // attn_seq_kernel's work units (plan_seq_units), in launch order: a unit is split j of the s splits of
+  // sequence b's 64-key blocks, blocks [tb, te), whose partials sit at index u0 + j (a sequence's splits
+  // take consecutive indices from u0).  unit_a = b | j << 6 | s << 11 | u0 << 16, unit_t = tb | te << 16.
+  // Splits of one sequence leave fp32 partials in part; the last of them to arrive (seq_cnt, zero between
+  // launches) merges them in split order.
+  int nunits;
+  unsigned* seq_cnt;
+  int unit_a[MAX_SEQ_UNITS]; int unit_t[MAX_SEQ_UNITS];
 };
 struct AttnPlan { int chunked; int q_tiles_per_wg; int key_groups; int qg; int S; int chunk; };
 AttnPlan attn_plan(int rows, int nq, int nkv, int Lk, int target_wgs);
+// attn_seq_kernel's units for a batched call (a.nseq, rows, heads, seq_lk and seq_cnt set): each sequence
+// starts as one unit; while fewer than ncu / (nkv x query-tile groups) units exist (one workgroup per
+// compute unit), the sequence with the longest split (lowest index on ties) takes one more split, until
+// the longest split is at most 2 blocks.  ncu 0 or no counters: no splits.  Returns the partial floats
+// the splits need (0 without splits).
+size_t plan_seq_units(AttnP& a, int ncu);
 hipError_t launch_attention(int dt, const AttnP& a, hipStream_t st);
 size_t attn_partial_floats(const AttnP& a);
 

@@ -159,11 +159,15 @@ def test_wide_batched_step_16_sequences(wide2):
 
 
 def test_seq_attention_kernel_matches_chunk_kernel(monkeypatch):
-    """Batched calls take attn_seq_kernel (every key of a sequence streamed through one workgroup, no key
-    splits) by default; FDLLM_SEQ_ATTN=0 keeps the chunk kernel with key splits and the merge launch.  Both
+    """Batched calls take attn_seq_kernel by default: a workgroup streams its sequence's key blocks (the
+    longest sequences' blocks split over the compute units the others leave idle, the splits merged by the
+    last to arrive, in split order); FDLLM_SEQ_SPLIT=0 streams every key of a sequence through one
+    workgroup, and FDLLM_SEQ_ATTN=0 keeps the chunk kernel with key splits and the merge launch.  All three
     append the same RoPE'd K/V rows at layer 0 (bit for bit) and agree on the hidden states, and so on later
-    layers' appended rows, to the bf16 criterion (their fp32 softmax sums run in different orders).  Prefixes off the 64-key block grid, up to 1000
-    keys, full (32-row) and partial (8-row) steps; 16 sequences of the 1.5B width."""
+    layers' appended rows, to the bf16 criterion (their fp32 softmax sums run in different orders).  The
+    split kernel gives the same bits when the call is repeated (the arrival counters return to zero, and
+    which split arrives last does not matter).  Prefixes off the 64-key block grid, up to 1000 keys, full
+    (32-row) and partial (8-row) steps; 16 sequences of the 1.5B width."""
     from fast_dllm_relax_amd.config import FastDLLMConfig
     from fast_dllm_relax_amd.params import from_numpy
     from fast_dllm_relax_amd.vm import HipVM
@@ -172,10 +176,12 @@ def test_seq_attention_kernel_matches_chunk_kernel(monkeypatch):
     kw = WIDE2
     params = from_numpy(random_params(OracleConfig(**kw), 4, "bfloat16"), FastDLLMConfig(**kw), dtype="bfloat16")
     vms = {}
-    for name, on in (("seq", "1"), ("chunk", "0")):
+    for name, on, split in (("seq", "1", "1"), ("nosplit", "1", "0"), ("chunk", "0", "1")):
         monkeypatch.setenv("FDLLM_SEQ_ATTN", on)
+        monkeypatch.setenv("FDLLM_SEQ_SPLIT", split)
         vms[name] = HipVM(FastDLLMConfig(**kw), params, dtype="bfloat16", max_rows=512)
         monkeypatch.delenv("FDLLM_SEQ_ATTN")
+        monkeypatch.delenv("FDLLM_SEQ_SPLIT")
     rng = np.random.default_rng(41)
     prefixes = [1000, 32, 96, 511, 200, 64, 992, 130, 700, 33, 257, 960, 448, 5, 640, 801]
     L, nkv, hd = kw["num_hidden_layers"], kw["num_key_value_heads"], kw["head_dim"]
@@ -193,26 +199,32 @@ def test_seq_attention_kernel_matches_chunk_kernel(monkeypatch):
         off = torch.tensor(prefixes, dtype=torch.int32, device="cuda")
         log(f"case: {name} attention, forward_cached_batch nseq={B} rows={R}")
         h = vm.forward_cached_batch(x, k, v, off, prefixes)
+        if name == "seq":
+            log("case: seq attention, the same call again (same bits)")
+            h2 = vm.forward_cached_batch(x, k, v, off, prefixes)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(to_np(h2).view(np.uint16), to_np(h).view(np.uint16))
         kf, vf = to_np(k), to_np(v)
         offp = torch.tensor([P + 8 for P in prefixes], dtype=torch.int32, device="cuda")
         log(f"case: {name} attention, forward_block_partial_batch rp=8")
         hp = vm.forward_block_partial_batch(8, x[:, 8:16].contiguous(), k, v, offp, prefixes)
         torch.cuda.synchronize()
         out[name] = (to_np(h), kf, vf, to_np(hp))
-    for i, what in ((1, "K cache"), (2, "V cache")):
-        # layer 0's appended rows and every prefix row are the same bits; later layers' appended rows follow
-        # hidden states that agree to the bf16 criterion
-        np.testing.assert_array_equal(out["seq"][i][0], out["chunk"][i][0], err_msg=f"{what}, layer 0")
-        for b, P in enumerate(prefixes):
-            np.testing.assert_array_equal(out["seq"][i][:, b, :P], out["chunk"][i][:, b, :P],
-                                          err_msg=f"{what}, sequence {b} prefix rows")
-            assert (out["seq"][i][:, b, P + R:] == SENTINEL).all(), f"{what}, sequence {b}: rows past its window"
-        bf16_parity(f"seq vs chunk attention, {what} appended rows",
-                    np.stack([out["seq"][i][1:, b, P:P + R] for b, P in enumerate(prefixes)]),
-                    np.stack([out["chunk"][i][1:, b, P:P + R] for b, P in enumerate(prefixes)]))
+    for other in ("chunk", "nosplit"):
+        for i, what in ((1, "K cache"), (2, "V cache")):
+            # layer 0's appended rows and every prefix row are the same bits; later layers' appended rows
+            # follow hidden states that agree to the bf16 criterion
+            np.testing.assert_array_equal(out["seq"][i][0], out[other][i][0], err_msg=f"{what}, layer 0")
+            for b, P in enumerate(prefixes):
+                np.testing.assert_array_equal(out["seq"][i][:, b, :P], out[other][i][:, b, :P],
+                                              err_msg=f"{what}, sequence {b} prefix rows")
+                assert (out["seq"][i][:, b, P + R:] == SENTINEL).all(), f"{what}, sequence {b}: rows past its window"
+            bf16_parity(f"seq vs {other} attention, {what} appended rows",
+                        np.stack([out["seq"][i][1:, b, P:P + R] for b, P in enumerate(prefixes)]),
+                        np.stack([out[other][i][1:, b, P:P + R] for b, P in enumerate(prefixes)]))
+        bf16_parity(f"seq vs {other} attention, full step hidden", out["seq"][0], out[other][0])
+        bf16_parity(f"seq vs {other} attention, partial step hidden", out["seq"][3], out[other][3])
     assert np.isfinite(out["seq"][0]).all() and np.isfinite(out["seq"][3]).all()
-    bf16_parity("seq vs chunk attention, full step hidden", out["seq"][0], out["chunk"][0])
-    bf16_parity("seq vs chunk attention, partial step hidden", out["seq"][3], out["chunk"][3])
     for vm in vms.values():
         vm.close()
 
