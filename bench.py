@@ -372,7 +372,8 @@ def batched_bench(args) -> dict:
 
     from fast_dllm_relax_amd.config import DEFAULT_MASK_ID, fast_dllm_v2_1p5b
     from fast_dllm_relax_amd.params import random_params_torch
-    from fast_dllm_relax_amd.runtime import _embed, batched_shifted_confidence, relax_batched_block_refine
+    from fast_dllm_relax_amd.runtime import (_embed, batched_shifted_confidence, batched_shifted_confidence_rows,
+                                             relax_batched_block_refine)
     from fast_dllm_relax_amd.vm import HipVM
 
     cfg = fast_dllm_v2_1p5b(tie_word_embeddings=False)
@@ -420,6 +421,8 @@ def batched_bench(args) -> dict:
     full_ms = event_ms(lambda: batched_shifted_confidence(vm, vm.forward_cached_batch(emb, k, v, off, a0s)), 10)
     part_ms = event_ms(lambda: batched_shifted_confidence(
         vm, vm.forward_block_partial_batch(8, emb8, k, v, off8, a0s)), 10)
+    # the loop's full step: the same forward, the confidence of one 8-row sub-block per sequence only
+    sub_ms = event_ms(lambda: batched_shifted_confidence_rows(vm, vm.forward_cached_batch(emb, k, v, off, a0s), 8, 16), 10)
 
     H, I, V, L = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.num_hidden_layers
     qkv = (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim
@@ -436,12 +439,14 @@ def batched_bench(args) -> dict:
         "workload": f"BASELINE config 4: 1.5B fp16, seed 3, {BATCH_SEQS} sequences, prefixes U[128, 1024], one "
                     f"32-token block each starting at the prefix rounded down to 32 (the prompt's tail + masks), "
                     f"sub-blocks of 8, threshold 0.9, untied lm_head N(0, 0.5) (BASELINE.json: tied head); the loop's "
-                    f"full steps score only the sub-block's rows (step_full_ms: confidence of all 512 rows)",
+                    f"full steps score only the sub-block's rows (step_full_ms: confidence of all 512 rows; "
+                    f"step_full_subblock_ms: of rows 8..15 of each sequence, as the loop's full steps do)",
         "prefixes": prefixes,
         "tokens_per_s": round(unmasked / refine_s, 2), "tokens": unmasked, "refine_s": round(refine_s, 4),
         "steps": steps, "partial_steps": partial_steps,
         "prefill_ms_mean": round(prefill_s / args.steps * 1e3, 2),
         "step_full_ms": round(full_ms, 4), "step_full_rows": BATCH_SEQS * 32,
+        "step_full_subblock_ms": round(sub_ms, 4),
         "step_full_tflops": round(tf_full, 1), "step_full_mfma_frac": round(tf_full / MFMA_F16_PEAK_TFLOPS, 4),
         "step_partial_ms": round(part_ms, 4), "step_partial_rows": BATCH_SEQS * 8,
         "step_partial_tflops": round(tf_part, 1),
