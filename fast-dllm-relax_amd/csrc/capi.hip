@@ -703,6 +703,7 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   if (const char* e = std::getenv("FDLLM_WR3")) c->mm.wr3 = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_SEQ_SPLIT")) c->seq_split = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_WT8")) c->mm.wt8 = atoi(e);
+  if (const char* e = std::getenv("FDLLM_WT256")) c->mm.wt256 = atoi(e);
   if (const char* e = std::getenv("FDLLM_PERSISTENT")) c->step_on = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_XFRAG")) c->frag_on = atoi(e) != 0;
   c->step_check = step_check_default(c->step_on, std::getenv("FDLLM_STEP_CHECK"));

@@ -170,6 +170,11 @@ using WtBig = WtCfg<4, 6, 2, 2, 4>;
 // of the 20 blocks a stage).  gate_up, us per launch with its norm pass, eight / four waves: 43.4 / 43.8 at
 // 384 rows, 44.4 / 44.7 at 512, 58.8 / 59.6 at 768, 60.6 / 61.4 at 1024; down unchanged (28.6 at 512)
 using WtBig8 = WtCfg<2, 6, 4, 2, 4>;
+// 4 x 2 waves of 64 x 96: a 256 x 192 block, one workgroup per compute unit (189 registers, 112 KB of LDS;
+// waves copy 4 or 3 of a stage's 28 blocks), 30% less data into the compute units than the 128 x 192
+// blocks.  gate_up with its norm pass: 42.5 against 44.3 us at 512 rows (188 workgroups), 41.9 against
+// 43.4 at 384; with four waves of 128 x 96 the same block took 67 against 46
+using WtB256 = WtCfg<4, 6, 4, 2, 4>;
 // register-weight kernel (gemm_wt.hpp, gemm_wr_kernel): four waves of 16 MF rows x TPW tiles, a
 // 16 MF x 64 TPW block, D stages in flight
 template <int MF, int TPW, int D>
@@ -191,7 +196,7 @@ using WrTiny = WrCfg<4, 1, 12>;  // 64 x 64 (4 MFMAs per k step and wave: twelve
 // 64 row blocks of 8192 rows fill 512 slots, two per compute unit, where the 128 x 256 blocks' 384
 // leave half the units with one)
 using WrB3 = WrCfg<8, 3, FD_WR_DEPTH>;
-enum MmId : int { MM_SMALL = 0, MM_WIDE = 1, MM_WIDE_D = 2, MM_BIG = 3, MM_WT = 4, MM_WR = 5, MM_WR_S = 6, MM_WR_M = 7, MM_WR_T = 8, MM_WR_3 = 9, MM_WT_8 = 10 };
+enum MmId : int { MM_SMALL = 0, MM_WIDE = 1, MM_WIDE_D = 2, MM_BIG = 3, MM_WT = 4, MM_WR = 5, MM_WR_S = 6, MM_WR_M = 7, MM_WR_T = 8, MM_WR_3 = 9, MM_WT_8 = 10, MM_WT_256 = 11 };
 struct MmInfo { int bm, bn_tiles, kss; };
 template <class M> constexpr MmInfo mm_info_of() { return MmInfo{M::bm, M::bn_tiles, M::kss}; }
 static MmInfo mm_info(int id) {
@@ -206,6 +211,7 @@ static MmInfo mm_info(int id) {
     case MM_WR_T: return mm_info_of<WrTiny>();
     case MM_WR_3: return mm_info_of<WrB3>();
     case MM_WT_8: return mm_info_of<WtBig8>();
+    case MM_WT_256: return mm_info_of<WtB256>();
     default: return mm_info_of<MmSmall>();
   }
 }
@@ -242,6 +248,7 @@ static int mm_choice(int cfg, int M, int ntiles, const MmPolicy& pol) {
   switch (cfg) {
     case CFG_LM_HEAD: return MM_WIDE;  // one 256-column confidence tile per block column
     case CFG_GATE_UP:
+      if (M > 256 && M <= pol.wt256 && ntiles % WtB256::bn_tiles == 0) return MM_WT_256;
       if (M >= 256 && ntiles % WtBig::bn_tiles == 0) return (pol.wt8 & 1) ? MM_WT_8 : MM_WT;
       return M >= 1024 ? MM_BIG : MM_WIDE;
     case CFG_DOWN:
@@ -280,6 +287,7 @@ GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol) {
       // measured 3.92 against 3.94-3.95 ms per batched step (fewer partials for the split sum; five
       // splits 4.03, ten 3.95)
       if (cfg == CFG_DOWN && a.M > 128) target = target * 7 / 8;
+      if (id == MM_WT_256) target = 0;  // no split
       int split = 1;
       const int max_split = id == MM_WR || id == MM_WR_S || id == MM_WR_M || id == MM_WR_T || id == MM_WR_3 ? 16 : 8;
       if (pol.force_split > 1 && cfg != CFG_LM_HEAD && nst % pol.force_split == 0 && nst / pol.force_split >= pol.min_stages)
@@ -419,6 +427,7 @@ static hipError_t launch_mm(const GemmP& a, const GemmPlan& p, hipStream_t st) {
     return hipErrorInvalidValue;
   }
   if constexpr (CFG == CFG_GATE_UP) {
+    if (p.mm_id == MM_WT_256) return launch_wt_cfg<DT, C::epi, WtB256>(a, p, st);
     if (p.mm_id == MM_WT) return launch_wt_cfg<DT, C::epi, WtBig>(a, p, st);
     if (p.mm_id == MM_WT_8) return launch_wt_cfg<DT, C::epi, WtBig8>(a, p, st);
     if (p.mm_id == MM_BIG) return launch_mm_cfg<DT, C::epi, XF_NONE, MmBig>(a, p, st);

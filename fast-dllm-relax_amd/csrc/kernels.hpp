@@ -78,6 +78,7 @@ struct MmPolicy {
   int force_split = 0;  // > 1: this k split whenever it divides the stages (the fused o_proj + norm)
   int wr3 = 1;          // o_proj / down at the register-weight thresholds: 128 x 192 blocks (0: 128 x 256)
   int wt8 = 1;  // LDS-staged 128 x 192 blocks of eight waves (bit 0 gate_up, bit 1 down) instead of four
+  int wt256 = 512;  // gate_up from 257 up to this many rows on LDS-staged 256 x 192 blocks of eight waves
 };
 GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol = MmPolicy{});
 // whether the plan runs the one-shot register-fragment body, the only one that takes xfrag / yfrag 1

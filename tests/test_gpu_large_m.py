@@ -19,7 +19,7 @@ from helpers import WIDE2, bf16_parity, log
 pytestmark = pytest.mark.gpu
 
 
-def _vm(kw, params, dtype, monkeypatch, wr_ops, max_rows, wr_small=0, wt8=0):
+def _vm(kw, params, dtype, monkeypatch, wr_ops, max_rows, wr_small=0, wt8=0, wt256=0):
     from fast_dllm_relax_amd.config import FastDLLMConfig
     from fast_dllm_relax_amd.vm import HipVM
 
@@ -28,8 +28,9 @@ def _vm(kw, params, dtype, monkeypatch, wr_ops, max_rows, wr_small=0, wt8=0):
     monkeypatch.setenv("FDLLM_MM_TARGET_WGS", "1")
     monkeypatch.setenv("FDLLM_WR_SMALL", str(wr_small))
     monkeypatch.setenv("FDLLM_WT8", str(wt8))
+    monkeypatch.setenv("FDLLM_WT256", str(wt256))
     vm = HipVM(FastDLLMConfig(**kw), params, dtype=dtype, max_rows=max_rows)
-    for k in ("FDLLM_WR_OPS", "FDLLM_WR_MIN_ROWS", "FDLLM_MM_TARGET_WGS", "FDLLM_WR_SMALL", "FDLLM_WT8"):
+    for k in ("FDLLM_WR_OPS", "FDLLM_WR_MIN_ROWS", "FDLLM_MM_TARGET_WGS", "FDLLM_WR_SMALL", "FDLLM_WT8", "FDLLM_WT256"):
         monkeypatch.delenv(k)
     return vm
 
@@ -52,6 +53,8 @@ def test_register_weight_kernel_bit_identical(dtype, monkeypatch):
     vm_small = _vm(kw, params, dtype, monkeypatch, 0, max(sizes), wr_small=3)  # 64 x 128 blocks for qkv, o_proj
     # gate_up and down on the LDS-staged kernel's eight-wave 128 x 192 blocks (waves copy 3 or 2 blocks a stage)
     vm_wt8 = _vm(kw, params, dtype, monkeypatch, 0, max(sizes), wt8=3)
+    # gate_up up to 512 rows on 256 x 192 blocks of eight waves (waves copy 4 or 3 of a stage's 28 blocks)
+    vm_256 = _vm(kw, params, dtype, monkeypatch, 0, max(sizes), wt256=512)  # (the default; vm_old: 0)
     rng = np.random.default_rng(17)
     for S in sizes:
         log(f"case: forward_hidden {S} rows, 1.5B width, 2 layers, {dtype}, register-weight vs LDS-staged")
@@ -61,11 +64,13 @@ def test_register_weight_kernel_bit_identical(dtype, monkeypatch):
         h_wr = vm_wr.forward_hidden(x, None)
         h_small = vm_small.forward_hidden(x, None)
         h_wt8 = vm_wt8.forward_hidden(x, None)
+        h_256 = vm_256.forward_hidden(x, None)
         torch.cuda.synchronize()
         assert torch.isfinite(h_wr.float()).all()
         np.testing.assert_array_equal(_bits(h_wr), _bits(h_old), err_msg=f"S={S}")
         np.testing.assert_array_equal(_bits(h_small), _bits(h_old), err_msg=f"S={S}, 64 x 128 blocks")
         np.testing.assert_array_equal(_bits(h_wt8), _bits(h_old), err_msg=f"S={S}, eight-wave LDS-staged blocks")
+        np.testing.assert_array_equal(_bits(h_256), _bits(h_old), err_msg=f"S={S}, 256 x 192 LDS-staged blocks")
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
