@@ -23,7 +23,7 @@ EXPORTS = (
     "fdllm_forward_block_partial_rp8", "fdllm_forward_block_partial_rp16", "fdllm_forward_block_partial_rp24",
     "fdllm_forward_cached_batch", "fdllm_forward_block_partial_batch", "fdllm_build_prefix_cache_seq",
     "fdllm_get_confidence", "fdllm_confidence_from_logits", "fdllm_unmask", "fdllm_get_confidence_unmask",
-    "fdllm_host_alloc", "fdllm_host_free", "fdllm_bench_op", "fdllm_persistent_steps",
+    "fdllm_host_alloc", "fdllm_host_free", "fdllm_bench_op", "fdllm_group_wait_launches",
     "fdllm_frag_calls",
     "fdllm_last_error",
 )
@@ -71,7 +71,7 @@ _SIGS = {
     "fdllm_host_alloc": ([ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p)], _I),
     "fdllm_host_free": ([_P], None),
     "fdllm_bench_op": ([_P, _I, _I, _I, _I, _P, _P, _I, _I, _P], _I),
-    "fdllm_persistent_steps": ([_P], ctypes.c_longlong),
+    "fdllm_group_wait_launches": ([_P], ctypes.c_longlong),
     "fdllm_frag_calls": ([_P], ctypes.c_longlong),
     "fdllm_last_error": ([], ctypes.c_char_p),
 }

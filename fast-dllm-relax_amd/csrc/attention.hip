@@ -84,9 +84,9 @@ static hipError_t launch_chunk_kh(const AttnP& a, const AttnPlan& p, hipStream_t
   const size_t merge_lds = (size_t)2 * KH * QPW * 16 * 4 + (size_t)(KH - 1) * QPW * (HD / 16) * 64 * 16;
   const size_t lds = std::max(loop_lds, merge_lds);
   if (lds > 160 * 1024) return hipErrorInvalidValue;
+  const int nseq = std::max(a.nseq, 1);
   auto kern = attn_chunk_kernel<DT, QPW, KH, CH, MASK>;
   raise_lds(kern, lds);
-  const int nseq = std::max(a.nseq, 1);
   if (nseq == 1)
     hipLaunchKernelGGL(kern, dim3(attn_chunk_grid_1seq(p.qg, a.nkv, a.S)), dim3(64 * QPW * KH), lds, st, a);
   else

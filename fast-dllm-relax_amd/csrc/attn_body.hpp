@@ -296,19 +296,17 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
 // once, so the chunk costs one memory latency instead of one per 32-key block.  Waves are QPW query
 // tiles times KH key parts.  The output is accumulated transposed, O^T = V^T P^T, so that a lane holds
 // one query (its softmax statistics stay in-lane) and the row reductions use row-swap permutes.  The
-// key parts are merged in LDS; with key splits (gridDim.z > 1) each workgroup stores its partial and
-// attn_merge_kernel, launched next on the stream, combines them across many workgroups.
+// key parts are merged in LDS; with key splits (more than one chunk) each workgroup stores its partial
+// and attn_merge_kernel, launched next on the stream, combines them across many workgroups.  (Merging
+// them inside this launch, the chunks of a (query-tile group, kv head) meeting at a group counter, was
+// bit-identical but slower: 15.0 us against 10.5 + 4.0 us at 32 rows and prefix 2048, 17.5 against
+// 7.6 + 4.8 us at 8 rows.)
 // Body of one workgroup (query-tile group bx, kv head by, key chunk bz; tid = threadIdx.x), in two phases:
 // attn_chunk_load requests the chunk's K/V rows into registers (AttnChunkRegs) and attn_chunk_compute
-// does the rest.  PART selects which rows a load call requests: CHUNK_ALL every row, CHUNK_CACHE only
-// rows read from the cache (they do not depend on this call's qkv projection, so a persistent launch
-// requests them before it waits for the projection) and CHUNK_WINDOW only this call's own rows (from
-// qkv).  With COH the qkv loads and the output stores are agent-scope, for a launch in which other
-// workgroups produce the qkv rows; the kernel below uses plain accesses.
-enum ChunkPart : int { CHUNK_ALL = 0, CHUNK_CACHE = 1, CHUNK_WINDOW = 2 };
+// does the rest.
 
 // WCS: also hold the RoPE (cos, sin) entries of items whose key is one of this call's rows, requested
-// with the K/V (the persistent step, which keeps these registers live across a wait, leaves it off)
+// with the K/V
 template <int QPW, int KH, int CH, bool WCS = false>
 struct AttnChunkRegs {
   static constexpr int NT = 64 * QPW * KH;
@@ -324,7 +322,7 @@ struct AttnChunkRegs {
 // consecutive lanes take 16 key quads x 2 dim chunks of V, so the LDS stores of attn_chunk_compute hit 64 distinct banks
 // per pass (rows are 68 dwords apart, 4 banks on).  Rows past kend read row kbeg and are masked or
 // zeroed later.
-template <int QPW, int KH, int CH, bool COH, int PART, bool WCS = false>
+template <int QPW, int KH, int CH, bool WCS = false>
 __device__ __forceinline__ void attn_chunk_load(const AttnP& a, int by, int bz, AttnChunkRegs<QPW, KH, CH, WCS>& R,
                                                 int tid) {
   typedef AttnChunkRegs<QPW, KH, CH, WCS> Regs;
@@ -343,17 +341,15 @@ __device__ __forceinline__ void attn_chunk_load(const AttnP& a, int by, int bz, 
     key = key < kend ? key : kbeg;
     const bool win = key >= a.ws && key < a.ws + a.rows;
     if (win) {
-      if (PART != CHUNK_CACHE) {
-        const u16* src = kq_base + (size_t)(key - a.ws) * a.ldq;
-        R.klo[it] = ld16<COH>(src + 8 * p);
-        R.khi[it] = ld16<COH>(src + 64 + 8 * p);
-        if constexpr (WCS) {
-          const float* cs = a.rope + (size_t)(key - a.ws) * 128 + 16 * p;
+      const u16* src = kq_base + (size_t)(key - a.ws) * a.ldq;
+      R.klo[it] = ld16<false>(src + 8 * p);
+      R.khi[it] = ld16<false>(src + 64 + 8 * p);
+      if constexpr (WCS) {
+        const float* cs = a.rope + (size_t)(key - a.ws) * 128 + 16 * p;
 #pragma unroll
-          for (int c = 0; c < 4; ++c) R.kcs[it][c] = *reinterpret_cast<const f32x4*>(cs + 4 * c);
-        }
+        for (int c = 0; c < 4; ++c) R.kcs[it][c] = *reinterpret_cast<const f32x4*>(cs + 4 * c);
       }
-    } else if (PART != CHUNK_WINDOW) {
+    } else {
       const u16* src = a.kc + key * krow + g * HD;
       R.klo[it] = *reinterpret_cast<const u32x4*>(src + 8 * p);
       R.khi[it] = *reinterpret_cast<const u32x4*>(src + 64 + 8 * p);
@@ -369,15 +365,15 @@ __device__ __forceinline__ void attn_chunk_load(const AttnP& a, int by, int bz, 
       key = key < kend ? key : kbeg;
       const bool win = key >= a.ws && key < a.ws + a.rows;
       if (win) {
-        if (PART != CHUNK_CACHE) R.vv[it][qq] = ld16<COH>(vq_base + (size_t)(key - a.ws) * a.ldq + 8 * dc);
-      } else if (PART != CHUNK_WINDOW) {
+        R.vv[it][qq] = ld16<false>(vq_base + (size_t)(key - a.ws) * a.ldq + 8 * dc);
+      } else {
         R.vv[it][qq] = *reinterpret_cast<const u32x4*>(a.vc + key * krow + g * HD + 8 * dc);
       }
     }
   }
 }
 
-template <int DT, int QPW, int KH, int CH, int MASK, bool COH, bool WCS = false>
+template <int DT, int QPW, int KH, int CH, int MASK, bool WCS = false>
 __device__ __forceinline__ void attn_chunk_compute(const AttnP& a, int bx, int by, int bz, unsigned char* smem,
                                                    AttnChunkRegs<QPW, KH, CH, WCS>& R, int tid) {
   typedef AttnChunkRegs<QPW, KH, CH, WCS> Regs;
@@ -417,7 +413,7 @@ __device__ __forceinline__ void attn_chunk_compute(const AttnP& a, int bx, int b
   if (!qshare || kh == 0) {
     const u16* qp = a.qkv + (size_t)r * a.ldq + (g * grp + hh) * HD + 8 * lg;
 #pragma unroll
-    for (int ds = 0; ds < 4; ++ds) qf[ds] = ld16<COH>(qp + 32 * ds);
+    for (int ds = 0; ds < 4; ++ds) qf[ds] = ld16<false>(qp + 32 * ds);
     const float* cs = a.rope + (size_t)r * 128;
     rope_tab<DT>(qf[0], qf[2], cs + 16 * lg);
     rope_tab<DT>(qf[1], qf[3], cs + 16 * lg + 64);
@@ -599,7 +595,7 @@ __device__ __forceinline__ void attn_chunk_compute(const AttnP& a, int bx, int b
   // lane output: query row qi (head hh, row r), dims 16 dt + 4 lg .. + 3
   auto store4 = [&](int dt, f32x4 v) {
     u16* dst = out_at(a, r, (g * grp + hh) * HD + 16 * dt + 4 * lg);
-    st8<COH>(dst, u32x2{pack2(from_f32<DT>(v[0]), from_f32<DT>(v[1])), pack2(from_f32<DT>(v[2]), from_f32<DT>(v[3]))});
+    st8<false>(dst, u32x2{pack2(from_f32<DT>(v[0]), from_f32<DT>(v[1])), pack2(from_f32<DT>(v[2]), from_f32<DT>(v[3]))});
   };
   if (a.S == 1) {
     if (kh == 0 && qvalid) {
@@ -615,16 +611,16 @@ __device__ __forceinline__ void attn_chunk_compute(const AttnP& a, int bx, int b
   if (kh == 0 && tile_ok) {
     float* pp = a.part + ((size_t)(g * QT + qt) * a.S + c) * PSZ;
 #pragma unroll
-    for (int dt = 0; dt < DT16; ++dt) stf4<COH>(reinterpret_cast<f32x4*>(pp) + dt * 64 + lane, o[dt]);
-    if (lg == 0) stf2<COH>(pp + 16 * HD + 2 * lr, f32x2_t{Mq, Lq});
+    for (int dt = 0; dt < DT16; ++dt) stf4<false>(reinterpret_cast<f32x4*>(pp) + dt * 64 + lane, o[dt]);
+    if (lg == 0) stf2<false>(pp + 16 * HD + 2 * lr, f32x2_t{Mq, Lq});
   }
 }
 
-template <int DT, int QPW, int KH, int CH, int MASK, bool COH>
+template <int DT, int QPW, int KH, int CH, int MASK>
 __device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, int bz, unsigned char* smem) {
   AttnChunkRegs<QPW, KH, CH, true> R;
-  attn_chunk_load<QPW, KH, CH, COH, CHUNK_ALL, true>(a, by, bz, R, threadIdx.x);
-  attn_chunk_compute<DT, QPW, KH, CH, MASK, COH, true>(a, bx, by, bz, smem, R, threadIdx.x);
+  attn_chunk_load<QPW, KH, CH, true>(a, by, bz, R, threadIdx.x);
+  attn_chunk_compute<DT, QPW, KH, CH, MASK, true>(a, bx, by, bz, smem, R, threadIdx.x);
 }
 
 // Batched call: the view of sequence b (its rows, cache, window and split partials) in a, a copy of the
@@ -661,14 +657,14 @@ __global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP p) {
     const int i = blockIdx.x, round = i >> 3;
     const int pair = (round / qg) * 8 + (i & 7), x = round % qg;
     if (pair >= p.nkv * p.S) return;
-    attn_chunk_body<DT, QPW, KH, CH, MASK, false>(p, x, pair % p.nkv, pair / p.nkv, smem);
+    attn_chunk_body<DT, QPW, KH, CH, MASK>(p, x, pair % p.nkv, pair / p.nkv, smem);
     return;
   }
   const int qg = (int)gridDim.x / p.nseq, b = (int)blockIdx.x / qg;
   AttnP a = p;
   seq_view(a, p, b);
   if ((int)blockIdx.z * a.chunk >= a.Lk) return;  // past this sequence's keys: the merge skips it
-  attn_chunk_body<DT, QPW, KH, CH, MASK, false>(a, (int)blockIdx.x - b * qg, blockIdx.y, blockIdx.z, smem);
+  attn_chunk_body<DT, QPW, KH, CH, MASK>(a, (int)blockIdx.x - b * qg, blockIdx.y, blockIdx.z, smem);
 }
 
 // Merge of the key splits: one wave per (kv head g, query tile qt, 16-dim slice dt).  The split weights
@@ -676,13 +672,18 @@ __global__ __launch_bounds__(64 * QPW * KH) void attn_chunk_kernel(AttnP p) {
 // partials are added in split order.
 // Splits at or past ceil(Lk / chunk) (a shorter sequence of a batched call) hold nothing and are skipped.
 // SR: splits held in registers at once (two loads each), so that up to SR splits cost one round trip.
-template <int DT, bool COH, int SR = 24>
+template <int DT, int SR = 24>
 __device__ __forceinline__ void attn_merge_wave(const AttnP& a, int dt, int qt, int g, int lane) {
   constexpr int SB = 8;   // batch of the two-pass loop for more splits
   const int lr = lane & 15, lg = lane >> 4;
   const int grp = a.nq / a.nkv, QR = grp * a.rows, QT = (QR + 15) / 16;
   const int S = min(a.S, (a.Lk + a.chunk - 1) / a.chunk);  // splits that hold keys
   const float* pt = a.part + (size_t)(g * QT + qt) * a.S * PSZ;
+  // O^T fragment and (m, l) of this lane's query in split q
+  auto ld_o = [&](int q) -> f32x4 {
+    return ldf4<false>(reinterpret_cast<const f32x4*>(pt + (size_t)q * PSZ) + dt * 64 + lane);
+  };
+  auto ld_ml = [&](int q) -> f32x2_t { return ldf2<false>(pt + (size_t)q * PSZ + 16 * HD + 2 * lr); };
   float M = -INFINITY, L = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   if (S <= SR) {
@@ -690,9 +691,8 @@ __device__ __forceinline__ void attn_merge_wave(const AttnP& a, int dt, int qt, 
     f32x2_t ml[SR];  // (m, l) of this lane's query
 #pragma unroll
     for (int q = 0; q < SR; ++q) {
-      const float* ps = pt + (size_t)min(q, S - 1) * PSZ;
-      ov[q] = ldf4<COH>(reinterpret_cast<const f32x4*>(ps) + dt * 64 + lane);
-      ml[q] = ldf2<COH>(ps + 16 * HD + 2 * lr);
+      ov[q] = ld_o(min(q, S - 1));
+      ml[q] = ld_ml(min(q, S - 1));
     }
     // keep every load above issued before the first use (the scheduler would otherwise sink the O loads
     // next to their uses and pay one round trip per pair)
@@ -710,7 +710,7 @@ __device__ __forceinline__ void attn_merge_wave(const AttnP& a, int dt, int qt, 
     for (int s0 = 0; s0 < S; s0 += SB) {
       f32x2_t mv[SB];
 #pragma unroll
-      for (int q = 0; q < SB; ++q) mv[q] = ldf2<COH>(pt + (size_t)min(s0 + q, S - 1) * PSZ + 16 * HD + 2 * lr);
+      for (int q = 0; q < SB; ++q) mv[q] = ld_ml(min(s0 + q, S - 1));
 #pragma unroll
       for (int q = 0; q < SB; ++q) M = fmaxf(M, mv[q][0]);
     }
@@ -720,9 +720,8 @@ __device__ __forceinline__ void attn_merge_wave(const AttnP& a, int dt, int qt, 
       f32x2_t mv[SB];
 #pragma unroll
       for (int q = 0; q < SB; ++q) {
-        const float* ps = pt + (size_t)min(s0 + q, S - 1) * PSZ;
-        ov[q] = ldf4<COH>(reinterpret_cast<const f32x4*>(ps) + dt * 64 + lane);
-        mv[q] = ldf2<COH>(ps + 16 * HD + 2 * lr);
+        ov[q] = ld_o(min(s0 + q, S - 1));
+        mv[q] = ld_ml(min(s0 + q, S - 1));
       }
 #pragma unroll
       for (int q = 0; q < SB; ++q) {
@@ -737,8 +736,8 @@ __device__ __forceinline__ void attn_merge_wave(const AttnP& a, int dt, int qt, 
     const int h = qi / a.rows, r = qi - h * a.rows;
     const float inv = 1.0f / L;
     u16* dst = out_at(a, r, (g * grp + h) * HD + 16 * dt + 4 * lg);
-    st8<COH>(dst, u32x2{pack2(from_f32<DT>(acc[0] * inv), from_f32<DT>(acc[1] * inv)),
-                        pack2(from_f32<DT>(acc[2] * inv), from_f32<DT>(acc[3] * inv))});
+    st8<false>(dst, u32x2{pack2(from_f32<DT>(acc[0] * inv), from_f32<DT>(acc[1] * inv)),
+                          pack2(from_f32<DT>(acc[2] * inv), from_f32<DT>(acc[3] * inv))});
   }
 }
 
@@ -747,13 +746,13 @@ __device__ __forceinline__ void attn_merge_wave(const AttnP& a, int dt, int qt, 
 template <int DT, int SR>
 __global__ __launch_bounds__(64) void attn_merge_kernel(AttnP p) {
   if (p.nseq <= 1) {
-    attn_merge_wave<DT, false, SR>(p, blockIdx.x, blockIdx.y, blockIdx.z, threadIdx.x);
+    attn_merge_wave<DT, SR>(p, blockIdx.x, blockIdx.y, blockIdx.z, threadIdx.x);
     return;
   }
   const int b = (int)blockIdx.z / p.nkv;
   AttnP a = p;
   seq_view(a, p, b);
-  attn_merge_wave<DT, false, SR>(a, blockIdx.x, blockIdx.y, (int)blockIdx.z - b * p.nkv, threadIdx.x);
+  attn_merge_wave<DT, SR>(a, blockIdx.x, blockIdx.y, (int)blockIdx.z - b * p.nkv, threadIdx.x);
 }
 
 

@@ -13,7 +13,7 @@
 
 #include "../../include/fdllm.h"
 #include "kernels.hpp"
-#include "step_status.hpp"
+#include "wait_status.hpp"
 
 using namespace fdllm;
 
@@ -111,22 +111,27 @@ struct fdllm_ctx {
   int down_split = 10;    // cross-workgroup k splits of the down projection (largest divisor of K/32 <= this)
   MmPolicy mm;              // large-M GEMM planning (k splits, register-weight kernel)
   bool frag_on = true;      // one-shot chains keep activations in MFMA-fragment order (FDLLM_XFRAG=0: row-major)
-  // the persistent cached step (step_body.hpp)
-  bool step_on = false;                // FDLLM_PERSISTENT=1 turns it on (measured slower than the kernels)
-  bool step_check = false;             // wait for every persistent launch and check its status (on with FDLLM_PERSISTENT unless FDLLM_STEP_CHECK=0)
-  int step_attn_target = 0;            // attention workgroups aimed for (0: attn_target)
-  int step_grid = 0;                   // workgroups of the launch (compute units, at most 256)
-  long long step_limit = 0;            // wall-clock ticks a barrier wait may take
-  StepLayerW* step_layers = nullptr;   // device table of the layers' weights
-  unsigned* step_sync = nullptr;       // barrier / arrival counters, abort flag
-  size_t step_sync_words = 0;
-  unsigned* step_status = nullptr;     // host-visible (pinned, mapped) abort word
-  unsigned* step_status_dev = nullptr;
-  long long step_launches = 0;         // persistent steps run (fdllm_persistent_steps)
+  // k splits of the one-shot projections summed inside their own launch (GroupWait, kernels.hpp), when the
+  // launch's grid is resident at once
+  bool group_waits = true;             // FDLLM_GROUP_WAITS=0 turns them off (separate split-sum launches)
+  unsigned* gw_cnt = nullptr;          // the counter banks
+  unsigned* wait_fault = nullptr;      // host-visible (pinned, mapped) fault word of those waits
+  unsigned* wait_fault_dev = nullptr;
+  long long wait_limit = 0;            // wall-clock ticks one wait may take (0.2 s)
+  long long group_wait_launches = 0;   // launches that reduced their splits themselves (fdllm_group_wait_launches)
+  int gw_bank = 0;                     // the bank of the next launch
+  int gw_prev = 0;                     // groups the previous launch used (in the other bank)
   long long frag_calls = 0;            // layer loops run in MFMA-fragment order (fdllm_frag_calls)
-  std::string step_trace_path;         // FDLLM_STEP_TRACE: write each launch's barrier timeline there
-  unsigned long long* step_trace = nullptr;
   unsigned char* scratch_dev = nullptr;  // this device's copy of `scratch` (fdllm_forward_cached_noalloc)
+
+  // the group-wait descriptor of the next launch, which uses `groups` counters
+  GroupWait next_group_wait(int groups) {
+    GroupWait g{gw_cnt, wait_fault_dev, wait_limit, gw_bank, gw_prev};
+    gw_bank ^= 1;
+    gw_prev = groups;
+    ++group_wait_launches;
+    return g;
+  }
 
   int qkv_dim() const { return (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim; }
   int q_dim() const { return cfg.num_attention_heads * cfg.head_dim; }
@@ -227,8 +232,19 @@ int run_gemm(fdllm_ctx* c, int cfg, GemmP a, int ksplit, hipStream_t st) {
       return fail(FDLLM_EINVAL, "too many GEMM workgroup groups (%d)", pl.groups * pl.mchunks);
     a.part = c->gpart;
     a.counters = c->counters;
+    // the one-shot register-fragment body sums its k splits inside the launch when the whole grid is
+    // resident at once (one workgroup per compute unit): no split-sum launch
+    const long long grid = (long long)pl.groups * pl.ksplit * pl.mchunks;
+    if (pl.kind == GK_ONESHOT && cfg != CFG_GATE_UP && gemm_takes_frag(cfg, pl) && pl.tiles_per_wg <= 4 &&
+        pl.groups * pl.mchunks <= GW_GROUPS && group_waits_fit(c->group_waits, c->wait_fault, grid, c->ncu)) {
+      a.gw = c->next_group_wait(pl.groups * pl.mchunks);
+    }
   }
-  HIPCHK(launch_gemm(f.dtype, cfg, a, pl, st));
+  if (const hipError_t e = launch_gemm(f.dtype, cfg, a, pl, st); e != hipSuccess) {
+    // a launch that never ran leaves the counter banks out of step: no more in-launch reductions
+    if (a.gw.cnt != nullptr) c->group_waits = false;
+    return fail(FDLLM_EHIP, "launch_gemm: %s", hipGetErrorString(e));
+  }
   return FDLLM_OK;
 }
 
@@ -344,83 +360,6 @@ int run_attention(fdllm_ctx* c, int rows, uint16_t* kc, uint16_t* vc, int ws, in
   return FDLLM_OK;
 }
 
-// The layers of a one-sequence cached step (at most 32 rows, no mask) as one persistent cooperative launch
-// (step_body.hpp), when the model and the call fit its plan.  *done tells whether it ran; when it did
-// not, the caller runs the per-operator kernels.  h / ssq and the RoPE table must hold the call's rows.
-int try_step(fdllm_ctx* c, int rows, uint16_t* kbase, uint16_t* vbase, size_t layer_stride, int write_start,
-             int attend_len, hipStream_t st, bool* done) {
-  *done = false;
-  if (!c->step_on || rows > 32) return FDLLM_OK;
-  const fdllm_config& f = c->cfg;
-  StepP p{};
-  p.layers = c->step_layers; p.L = f.num_hidden_layers;
-  p.H = f.hidden_size; p.I = f.intermediate_size; p.nq = f.num_attention_heads; p.nkv = f.num_key_value_heads;
-  p.qkv_dim = c->qkv_dim(); p.q_dim = c->q_dim(); p.eps = f.rms_norm_eps; p.M = rows;
-  p.h = c->h; p.ssq = c->ssq; p.ssq_ld = c->ws_rows; p.qkv = c->qkv; p.attn = c->attn; p.act = c->act;
-  AttnP& a = p.at;
-  a.qkv = c->qkv; a.ldq = c->qkv_dim(); a.rows = rows; a.nq = p.nq; a.nkv = p.nkv; a.rope = c->rope;
-  a.ws = write_start; a.Lk = attend_len; a.scale = 1.0f / std::sqrt((float)f.head_dim); a.mask = 0; a.nseq = 1;
-  a.block = f.bd_size;
-  a.target_wgs = c->step_attn_target > 0 ? c->step_attn_target : c->attn_target;
-  const AttnPlan pl = attn_plan(rows, p.nq, p.nkv, attend_len, a.target_wgs);
-  if (!pl.chunked || pl.q_tiles_per_wg != 4 || pl.key_groups != 2) return FDLLM_OK;
-  a.S = pl.S; a.chunk = pl.chunk; a.out = c->attn;
-  p.qg = pl.qg;
-  p.kbase = kbase; p.vbase = vbase; p.layer_stride = (long long)layer_stride;
-  p.nt_q = c->qkv_dim() / 16; p.nt_o = f.hidden_size / 16; p.np_u = f.intermediate_size / 16;
-  // down: the one-shot kernel's tile groups and k split
-  GemmP dp = gemm_args(nullptr, d_tiles(c), f.hidden_size, f.intermediate_size, nullptr, f.intermediate_size, rows);
-  const GemmPlan dpl = gemm_plan(CFG_DOWN, dp, 1, c->mm);
-  if (dpl.kind != GK_ONESHOT || dpl.tiles_per_wg != STEP_DNT) return FDLLM_OK;
-  p.d_groups = dpl.groups; p.d_splits = dpl.ksplit;
-  p.sync.ctr = c->step_sync;
-  p.sync.la = c->step_sync + BAR_CTRS * BAR_STRIDE;
-  p.sync.abort_f = p.sync.la + 256 * BAR_STRIDE;
-  p.sync.status = c->step_status_dev;
-  p.sync.limit = c->step_limit;
-  const StepPlan sp = step_plan(p, c->step_grid);
-  if (!sp.ok || p.d_groups > 256) return FDLLM_OK;
-  if (a.S > 1) {
-    const int rc = ensure_floats(&c->apart, &c->apart_floats, attn_partial_floats(a));
-    if (rc) return rc;
-    a.part = c->apart;
-  }
-  {
-    const int rc = ensure_floats(&c->gpart, &c->gpart_floats, (size_t)p.d_groups * p.d_splits * STEP_DNT * 2 * 64 * 4);
-    if (rc) return rc;
-    p.dpart = c->gpart;
-  }
-  constexpr int kTraceBars = 256;
-  if (!c->step_trace_path.empty()) {
-    if (c->step_trace == nullptr) HIPCHK(hipMalloc((void**)&c->step_trace, (size_t)256 * kTraceBars * 16));
-    HIPCHK(launch_fill_u32((unsigned*)c->step_trace, (size_t)256 * kTraceBars * 4, 0u, st));
-    p.sync.trace = c->step_trace;
-    p.sync.trace_bars = kTraceBars;
-  }
-  HIPCHK(launch_fill_u32(c->step_sync, c->step_sync_words, 0u, st));
-  HIPCHK(launch_step(f.dtype, p, c->step_grid, sp.lds, st));
-  if (c->step_trace != nullptr && !c->step_trace_path.empty()) {
-    // timeline of this launch: header (grid, barriers per row, layers, merge stage), then the rows
-    std::vector<unsigned long long> tr((size_t)c->step_grid * kTraceBars * 2);
-    HIPCHK(hipMemcpyAsync(tr.data(), c->step_trace, tr.size() * 8, hipMemcpyDeviceToHost, st));
-    HIPCHK(hipStreamSynchronize(st));
-    if (FILE* fp = std::fopen(c->step_trace_path.c_str(), "wb")) {
-      const long long hdr[4] = {c->step_grid, kTraceBars, f.num_hidden_layers, a.S > 1 ? 1 : 0};
-      std::fwrite(hdr, sizeof(hdr), 1, fp);
-      std::fwrite(tr.data(), 8, tr.size(), fp);
-      std::fclose(fp);
-    }
-  }
-  if (c->step_check) {
-    HIPCHK(hipStreamSynchronize(st));
-    if (take_step_abort(c->step_status, &c->step_on))
-      return fail(FDLLM_EHIP, "persistent step aborted: a grid barrier wait timed out");
-  }
-  ++c->step_launches;
-  *done = true;
-  return FDLLM_OK;
-}
-
 // The four projections of layer L at `rows` rows, as the layer loop launches them.  frag: the one-shot
 // chain's activations (h, the attention output, SiLU * up) are in MFMA-fragment order.
 struct LayerGemms { GemmP q, o, gu, d; int dsplit; };
@@ -480,22 +419,11 @@ int run_layers(fdllm_ctx* c, const void* x_in, int rows, uint16_t* kbase, uint16
   const fdllm_config& f = c->cfg;
   const int H = f.hidden_size;
   const int ssq_ld = c->ws_rows;
-  // the persistent step (when it may run) and batched calls keep the activations row-major
-  const bool step_may = sb == nullptr && mask == 0 && bias == nullptr && c->step_on;
-  const bool frag = sb == nullptr && !step_may && frag_chain(c, rows);
+  // batched calls keep the activations row-major
+  const bool frag = sb == nullptr && frag_chain(c, rows);
   HIPCHK(launch_load_rows(f.dtype, (const uint16_t*)x_in, rows, H, c->h, c->ssq, ssq_ld, st, frag));
   int rc = rope_table(c, rows, pos_dev, sb ? sb->rows : rows, st);
   if (rc) return rc;
-  if (step_may) {
-    bool done = false;
-    rc = try_step(c, rows, kbase, vbase, layer_stride, write_start, attend_len, st, &done);
-    if (rc) return rc;
-    if (done) {
-      if (out != nullptr)
-        HIPCHK(launch_norm_rows(f.dtype, c->h, rows, H, c->ssq, ssq_ld, c->final_norm, f.rms_norm_eps, (uint16_t*)out, st));
-      return FDLLM_OK;
-    }
-  }
   if (frag) ++c->frag_calls;
   // xn_ready: the previous layer's down launch also normalised this layer's qkv input into c->xn
   // (run_resid_fused), in the layout the qkv launch takes; final_done: the last one wrote out
@@ -573,11 +501,11 @@ int check_ready(const fdllm_ctx* c) {
   return FDLLM_OK;
 }
 
-// An earlier persistent launch timed out at a barrier (its outputs are wrong): report it once and run the
-// per-operator kernels from now on (step_status.hpp).
-int pending_step_abort(fdllm_ctx* c) {
-  if (take_step_abort(c->step_status, &c->step_on))
-    return fail(FDLLM_EHIP, "an earlier persistent step aborted (grid barrier timeout); its results are invalid");
+// A group wait of an earlier launch timed out (its outputs are wrong): report it once and reduce every
+// split with the separate kernels from now on (wait_status.hpp).
+int pending_wait_fault(fdllm_ctx* c) {
+  if (take_wait_fault(c->wait_fault, &c->group_waits))
+    return fail(FDLLM_EHIP, "a group wait of an earlier launch timed out; the results of that call are invalid");
   return FDLLM_OK;
 }
 
@@ -585,7 +513,7 @@ int cached_step(fdllm_ctx* c, const void* x, int rows, void* k, void* v, int cap
                 int64_t prefix_len, int write_rel, int attend_rel, void* out, void* stream) {
   int rc = check_ready(c);
   if (rc) return rc;
-  rc = pending_step_abort(c);
+  rc = pending_wait_fault(c);
   if (rc) return rc;
   if (!x || !k || !v || !off || !out) return fail(FDLLM_EINVAL, "null tensor argument");
   if (rows <= 0) return fail(FDLLM_EINVAL, "active rows must be positive, got %d", rows);
@@ -613,6 +541,8 @@ int cached_step(fdllm_ctx* c, const void* x, int rows, void* k, void* v, int cap
 int cached_step_batch(fdllm_ctx* c, const void* x, int nseq, int rows, void* k, void* v, int cap, const int32_t* off,
                       const int64_t* prefix_lens, int write_rel, int attend_rel, void* out, void* stream) {
   int rc = check_ready(c);
+  if (rc) return rc;
+  rc = pending_wait_fault(c);
   if (rc) return rc;
   if (!x || !k || !v || !off || !prefix_lens || !out) return fail(FDLLM_EINVAL, "null tensor argument");
   if (nseq <= 0 || nseq > MAX_SEQS) return fail(FDLLM_EINVAL, "batch of %d sequences (1 .. %d supported)", nseq, MAX_SEQS);
@@ -704,11 +634,8 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   if (const char* e = std::getenv("FDLLM_SEQ_SPLIT")) c->seq_split = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_WT8")) c->mm.wt8 = atoi(e);
   if (const char* e = std::getenv("FDLLM_WT256")) c->mm.wt256 = atoi(e);
-  if (const char* e = std::getenv("FDLLM_PERSISTENT")) c->step_on = atoi(e) != 0;
+  if (const char* e = std::getenv("FDLLM_GROUP_WAITS")) c->group_waits = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_XFRAG")) c->frag_on = atoi(e) != 0;
-  c->step_check = step_check_default(c->step_on, std::getenv("FDLLM_STEP_CHECK"));
-  if (const char* e = std::getenv("FDLLM_STEP_ATTN_TARGET")) c->step_attn_target = std::max(0, atoi(e));
-  if (const char* e = std::getenv("FDLLM_STEP_TRACE")) c->step_trace_path = e;
   c->names.push_back("model.embed_tokens.weight");
   for (int i = 0; i < f.num_hidden_layers; ++i) {
     std::string p = "model.layers." + std::to_string(i);
@@ -720,7 +647,8 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   c->names.push_back("model.norm.weight");
   if (!f.tie_word_embeddings) c->names.push_back("lm_head.weight");
   c->n_counters = 1 << 16;
-  const size_t cnt_bytes = ((size_t)c->n_counters + SEQ_CNT_MAX) * 4 + 64;
+  constexpr size_t gw_words = (size_t)2 * GW_GROUPS * GW_STRIDE;  // two banks of group counters
+  const size_t cnt_bytes = ((size_t)c->n_counters + SEQ_CNT_MAX + gw_words) * 4 + 64;
   hipError_t e = hipMalloc((void**)&c->counters, cnt_bytes);
   if (e == hipSuccess) e = hipMemset(c->counters, 0, cnt_bytes);
   if (e != hipSuccess) {
@@ -728,7 +656,8 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
     return fail(FDLLM_EHIP, "workspace allocation failed: %s", hipGetErrorString(e));
   }
   c->attn_cnt = c->counters + c->n_counters;
-  c->zero_i32 = (int32_t*)(c->attn_cnt + SEQ_CNT_MAX);
+  c->gw_cnt = c->attn_cnt + SEQ_CNT_MAX;
+  c->zero_i32 = (int32_t*)(c->gw_cnt + gw_words);
   {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->dev) == hipSuccess && cus > 0) c->ncu = cus;
@@ -750,23 +679,19 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
       c->scratch_dev = (unsigned char*)g_scratch_ptr[c->dev];
     }
   }
-  if (c->step_on) {
-    // the persistent step needs a cooperative launch of one workgroup per compute unit
-    int coop = 0, cus = 0, khz = 0;
-    (void)hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, c->dev);
-    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->dev);
+  {
+    // the fault word of the group waits; without it every split is reduced by a separate kernel
+    int khz = 0;
     (void)hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, c->dev);
-    c->step_grid = std::min(cus, 256);
-    c->step_limit = (long long)std::max(khz, 1000) * 200;  // 0.2 s
-    c->step_sync_words = (size_t)BAR_CTRS * BAR_STRIDE + 256 * BAR_STRIDE + BAR_STRIDE;
-    if (!coop || c->step_grid < 64 ||
-        hipMalloc((void**)&c->step_sync, c->step_sync_words * 4) != hipSuccess ||
-        hipHostMalloc((void**)&c->step_status, 64, hipHostMallocMapped) != hipSuccess ||
-        hipHostGetDevicePointer((void**)&c->step_status_dev, c->step_status, 0) != hipSuccess) {
+    c->wait_limit = (long long)std::max(khz, 1000) * 200;  // 0.2 s
+    if (hipHostMalloc((void**)&c->wait_fault, 64, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess ||
+        hipHostGetDevicePointer((void**)&c->wait_fault_dev, c->wait_fault, 0) != hipSuccess) {
       (void)hipGetLastError();
-      c->step_on = false;
+      if (c->wait_fault) (void)hipHostFree(c->wait_fault);
+      c->wait_fault = c->wait_fault_dev = nullptr;
+      c->group_waits = false;
     } else {
-      *c->step_status = 0u;
+      *c->wait_fault = 0u;
     }
   }
   int rc = ensure_rows(c, std::max(1, f.max_rows));
@@ -787,9 +712,9 @@ void fdllm_destroy(fdllm_ctx* c) {
   if (!c) return;
   (void)hipDeviceSynchronize();
   for (void* p : {c->ws, (void*)c->gpart, (void*)c->apart, c->stats, (void*)c->counters, (void*)c->packed,
-                  (void*)c->rope, (void*)c->step_layers, (void*)c->step_sync, (void*)c->step_trace})
+                  (void*)c->rope})
     if (p) (void)hipFree(p);
-  if (c->step_status) (void)hipHostFree(c->step_status);
+  if (c->wait_fault) (void)hipHostFree(c->wait_fault);
   delete c;
 }
 
@@ -817,15 +742,6 @@ int fdllm_bind_weights(fdllm_ctx* c, const void* const* ptrs, int n) {
   c->bound = false;
   int rc = pack_all(c);
   if (rc) return rc;
-  if (c->step_on) {
-    std::vector<StepLayerW> tab(c->cfg.num_hidden_layers);
-    for (int i = 0; i < c->cfg.num_hidden_layers; ++i) {
-      const Layer& L = c->layers[i];
-      tab[i] = StepLayerW{L.pqkv, L.bqkv, L.po, L.pgu, L.pd, L.ln_in, L.ln_post};
-    }
-    if (c->step_layers == nullptr) HIPCHK(hipMalloc((void**)&c->step_layers, tab.size() * sizeof(StepLayerW)));
-    HIPCHK(hipMemcpy(c->step_layers, tab.data(), tab.size() * sizeof(StepLayerW), hipMemcpyHostToDevice));
-  }
   c->bound = true;
   return FDLLM_OK;
 }
@@ -842,6 +758,8 @@ int fdllm_embed(fdllm_ctx* c, const int32_t* ids, int n, void* out, void* stream
 int fdllm_forward_hidden(fdllm_ctx* c, const void* x, int S, const float* bias, void* out, void* stream) {
   int rc = check_ready(c);
   if (rc) return rc;
+  rc = pending_wait_fault(c);
+  if (rc) return rc;
   if (S <= 0) return fail(FDLLM_EINVAL, "seq_len must be positive, got %d", S);
   if (!x || !out) return fail(FDLLM_EINVAL, "null tensor argument");
   rc = ensure_rows(c, S);
@@ -852,7 +770,7 @@ int fdllm_forward_hidden(fdllm_ctx* c, const void* x, int S, const float* bias, 
 int fdllm_get_logits(fdllm_ctx* c, const void* hidden, int rows, float* logits, void* stream) {
   int rc = check_ready(c);
   if (rc) return rc;
-  rc = pending_step_abort(c);
+  rc = pending_wait_fault(c);
   if (rc) return rc;
   if (rows <= 0 || !hidden || !logits) return fail(FDLLM_EINVAL, "invalid get_logits arguments");
   return run_lm_head(c, (const uint16_t*)hidden, rows, logits, false, (hipStream_t)stream);
@@ -861,6 +779,8 @@ int fdllm_get_logits(fdllm_ctx* c, const void* hidden, int rows, float* logits, 
 int fdllm_build_prefix_cache(fdllm_ctx* c, const void* x, int P, const float* bias, void* k, void* v, int cap,
                              void* stream) {
   int rc = check_ready(c);
+  if (rc) return rc;
+  rc = pending_wait_fault(c);
   if (rc) return rc;
   if (P <= 0 || !x || !k || !v) return fail(FDLLM_EINVAL, "invalid build_prefix_cache arguments");
   if (P > cap) return fail(FDLLM_EINVAL, "KV write [0, %d) outside cache capacity %d", P, cap);
@@ -887,19 +807,18 @@ struct ScratchView {
   float *ssq, *gpart, *apart, *rope;
   size_t gpart_floats, apart_floats, rope_floats;
   int ws_rows;
-  bool step_on;
   explicit ScratchView(fdllm_ctx* ctx) : c(ctx) {
     h = c->h; qkv = c->qkv; attn = c->attn; act = c->act; kscr = c->kscr; vscr = c->vscr; xn = c->xn;
     ssq = c->ssq; gpart = c->gpart; apart = c->apart; rope = c->rope;
     gpart_floats = c->gpart_floats; apart_floats = c->apart_floats; rope_floats = c->rope_floats;
-    ws_rows = c->ws_rows; step_on = c->step_on;
+    ws_rows = c->ws_rows;
     t_no_alloc = true;
   }
   ~ScratchView() {
     c->h = h; c->qkv = qkv; c->attn = attn; c->act = act; c->kscr = kscr; c->vscr = vscr; c->xn = xn;
     c->ssq = ssq; c->gpart = gpart; c->apart = apart; c->rope = rope;
     c->gpart_floats = gpart_floats; c->apart_floats = apart_floats; c->rope_floats = rope_floats;
-    c->ws_rows = ws_rows; c->step_on = step_on;
+    c->ws_rows = ws_rows;
     t_no_alloc = false;
   }
 };
@@ -950,7 +869,6 @@ int fdllm_forward_cached_noalloc(fdllm_ctx* c, const void* x, int rows, void* k,
   c->rope_floats = R * 128;
   c->gpart_floats = noalloc_gemm_partials(c);
   c->gpart = (float*)take(c->gpart_floats * 4);
-  c->step_on = false;  // the persistent step sizes its own buffers
   if (off_b >= NOALLOC_SCRATCH_BYTES)
     return fail(FDLLM_EINVAL, "the model's workspace (%zu bytes) exceeds the allocation-free step's scratch (%zu bytes)",
                 off_b, NOALLOC_SCRATCH_BYTES);
@@ -1000,6 +918,8 @@ int fdllm_build_prefix_cache_seq(fdllm_ctx* c, const void* x, int P, const float
                                  int nseq, int seq, void* stream) {
   int rc = check_ready(c);
   if (rc) return rc;
+  rc = pending_wait_fault(c);
+  if (rc) return rc;
   if (P <= 0 || !x || !k || !v) return fail(FDLLM_EINVAL, "invalid build_prefix_cache arguments");
   if (nseq <= 0 || seq < 0 || seq >= nseq) return fail(FDLLM_EINVAL, "sequence %d of a batch of %d", seq, nseq);
   if (P > cap) return fail(FDLLM_EINVAL, "KV write [0, %d) outside cache capacity %d", P, cap);
@@ -1017,7 +937,7 @@ int fdllm_get_confidence(fdllm_ctx* c, const void* hidden, int rows, int32_t* id
                          void* stream) {
   int rc = check_ready(c);
   if (rc) return rc;
-  rc = pending_step_abort(c);
+  rc = pending_wait_fault(c);
   if (rc) return rc;
   if (rows <= 0 || !hidden || !ids || !maxp) return fail(FDLLM_EINVAL, "invalid get_confidence arguments");
   rc = ensure_stats(c, rows);
@@ -1059,7 +979,7 @@ static UnmaskP unmask_args(const fdllm_ctx* c, int rows, int row0, int32_t* bloc
 int fdllm_unmask(fdllm_ctx* c, const int32_t* ids, const float* maxp, int rows, int row0, int32_t* block, int s0,
                  int sub_rows, int32_t mask_id, float threshold, int32_t* report, int32_t seq, void* stream) {
   if (!c) return fail(FDLLM_EINVAL, "null context");
-  int rc = pending_step_abort(c);
+  int rc = pending_wait_fault(c);
   if (rc) return rc;
   if (!ids || !maxp) return fail(FDLLM_EINVAL, "null confidence argument");
   rc = check_unmask(c, rows, row0, block, s0, sub_rows, threshold);
@@ -1074,7 +994,7 @@ int fdllm_get_confidence_unmask(fdllm_ctx* c, const void* hidden, int rows, int 
                                 int32_t* report, int32_t seq, void* stream) {
   int rc = check_ready(c);
   if (rc) return rc;
-  rc = pending_step_abort(c);
+  rc = pending_wait_fault(c);
   if (rc) return rc;
   if (!hidden) return fail(FDLLM_EINVAL, "null hidden states");
   if ((ids == nullptr) != (maxp == nullptr)) return fail(FDLLM_EINVAL, "ids and maxp must both be given or both be null");
@@ -1112,7 +1032,7 @@ void fdllm_host_free(void* host_ptr) {
   if (host_ptr) (void)hipHostFree(host_ptr);
 }
 
-long long fdllm_persistent_steps(const fdllm_ctx* c) { return c ? c->step_launches : 0; }
+long long fdllm_group_wait_launches(const fdllm_ctx* c) { return c ? c->group_wait_launches : 0; }
 
 long long fdllm_frag_calls(const fdllm_ctx* c) { return c ? c->frag_calls : 0; }
 
@@ -1131,7 +1051,7 @@ int fdllm_bench_op(fdllm_ctx* c, int op, int rows, int layer, int iters, void* k
   hipStream_t st = (hipStream_t)stream;
   const size_t stride = (size_t)cap * f.num_key_value_heads * f.head_dim;
   // the launches a cached step of `rows` rows makes (layout included), on whatever the buffers hold
-  const bool frag = !c->step_on && frag_chain(c, rows);
+  const bool frag = frag_chain(c, rows);
   for (int it = 0; it < iters && rc == FDLLM_OK; ++it) {
     // consecutive launches walk the layers, as a step does, so no weight is re-read from cache
     const int li = (layer + it) % f.num_hidden_layers;

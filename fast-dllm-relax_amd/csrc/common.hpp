@@ -5,6 +5,8 @@
 
 #include <type_traits>
 
+#include "kernels.hpp"
+
 namespace fdllm {
 
 typedef uint16_t u16;
@@ -255,6 +257,64 @@ __device__ __forceinline__ void stf2(float* p, f32x2_t v) {
 template <bool COH>
 __device__ __forceinline__ void stf4(f32x4* p, f32x4 v) {
   st16<COH>(p, u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])});
+}
+
+// Agent-coherent 16-byte accesses through a buffer resource (one instruction per lane with the sc1 cache
+// policy, where the agent-scope atomics above take two 8-byte ones), addressed by a byte offset from a
+// base that is uniform across the wave.
+struct CohBuf {
+  __amdgpu_buffer_rsrc_t r;
+};
+__device__ __forceinline__ CohBuf coh_buf(const void* base, unsigned bytes) {
+  return CohBuf{__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000)};
+}
+constexpr int CPOL_SC1 = 16;
+__device__ __forceinline__ f32x4 coh_ldf4(const CohBuf& b, unsigned off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(b.r, (int)off, 0, CPOL_SC1));
+}
+__device__ __forceinline__ f32x2_t coh_ldf2(const CohBuf& b, unsigned off) {
+  return __builtin_bit_cast(f32x2_t, __builtin_amdgcn_raw_buffer_load_b64(b.r, (int)off, 0, CPOL_SC1));
+}
+__device__ __forceinline__ void coh_stf4(const CohBuf& b, unsigned off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), b.r, (int)off, 0, CPOL_SC1);
+}
+__device__ __forceinline__ void coh_stf2(const CohBuf& b, unsigned off, f32x2_t v) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), b.r, (int)off, 0, CPOL_SC1);
+}
+
+// ---- group waits inside one launch (GroupWait, kernels.hpp) ----
+// Workgroup i (linear index, any thread) zeroes counter i of the other bank when the previous launch used it.
+__device__ __forceinline__ void group_clear_other(const GroupWait& gw, int i) {
+  if (i < gw.clear)
+    __hip_atomic_store(gw.cnt + (size_t)((1 - gw.bank) * GW_GROUPS + i) * GW_STRIDE, 0u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+// The workgroup's stores are acknowledged, then it counts its arrival on group k and waits until all
+// `members` have arrived.  Returns false in every thread when the wait timed out: the fault word is set
+// and the caller skips the work that needed the group.  Wave 0 polls (uniform control flow: the count is
+// read into a scalar register).
+__device__ __forceinline__ bool group_arrive_wait(const GroupWait& gw, int k, unsigned members, int* lds_flag) {
+  wait_memory();
+  __syncthreads();
+  unsigned* ctr = gw.cnt + (size_t)(gw.bank * GW_GROUPS + k) * GW_STRIDE;
+  if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) == 0) {
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const long long t0 = wall_clock64();
+    int ok = 1;
+    while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) < members) {
+      if (wall_clock64() - t0 > gw.limit) {
+        ok = 0;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (threadIdx.x == 0) {
+      if (!ok) __hip_atomic_store(gw.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      *lds_flag = ok;
+    }
+  }
+  __syncthreads();
+  return *lds_flag != 0;
 }
 
 __device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned expected, int* lds_flag) {

@@ -349,7 +349,7 @@ static hipError_t launch_os(const GemmP& a, const GemmPlan& p, hipStream_t st) {
       (void)hipGetLastError();
   }
   hipLaunchKernelGGL(kern, dim3(p.groups, p.ksplit, p.mchunks), dim3(512), lds, st, a);
-  if (p.ksplit > 1) {
+  if (p.ksplit > 1 && a.gw.cnt == nullptr) {
     constexpr int units = (C::epi == EPI_SILU_PAIR ? C::nt / 2 : C::nt) * MT;
     hipLaunchKernelGGL((gemm_os_epilogue_kernel<DT, C::epi, MT, C::nt>), dim3(p.groups, 1, p.mchunks), dim3(64 * units), 0,
                        st, a, p.ksplit);
@@ -485,6 +485,9 @@ hipError_t launch_gemm(int dt, int cfg, const GemmP& a, const GemmPlan& p, hipSt
   if ((a.xfrag == 1 || a.yfrag == 1) && !gemm_takes_frag(cfg, p)) return hipErrorInvalidValue;
   if ((a.xfrag == 2 || a.yfrag == 2) && !gemm_takes_blocks(p)) return hipErrorInvalidValue;
   if (a.yfrag == 2 && cfg != CFG_GATE_UP) return hipErrorInvalidValue;
+  // a k split summed inside the launch: only the register-fragment body does it
+  if (a.gw.cnt != nullptr && !(gemm_takes_frag(cfg, p) && p.ksplit > 1 && os_info(cfg).nt <= 4 && cfg != CFG_GATE_UP))
+    return hipErrorInvalidValue;
   if (dt == DT_BF16) return launch_dt<DT_BF16>(cfg, a, p, st);
   return launch_dt<DT_F16>(cfg, a, p, st);
 }

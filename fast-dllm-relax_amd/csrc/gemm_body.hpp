@@ -737,14 +737,48 @@ __device__ __forceinline__ void gemm_os_direct_body(const GemmP& a, int bx, int 
     }
   }
 
-  // 6. cross-workgroup k splits: the unit's partial, summed by the epilogue body
+  // 6. cross-workgroup k splits: the unit's partial, summed by the epilogue body (a separate launch), or,
+  //    with a.gw, inside this launch: the tile group's splits meet at its counter and unit u of the group
+  //    is summed by wave u / gy of split u % gy, in split order (gemm_os_epilogue_body's arithmetic)
   if (gy > 1) {
-    if (has_unit) {
-      const size_t grp = (size_t)bz * a.ngroups + bx;
-      constexpr int per = NT * MT * 64;
-      f32x4* part = reinterpret_cast<f32x4*>(a.part) + (grp * gy + by) * per;
+    const size_t grp = (size_t)bz * a.ngroups + bx;
+    constexpr int per = NT * MT * 64;
+    f32x4* part = reinterpret_cast<f32x4*>(a.part) + (grp * gy + by) * per;
+    if (a.gw.cnt == nullptr) {
+      if (has_unit) {
 #pragma unroll
-      for (int q = 0; q < TPU; ++q) part[((ut + q) * MT + umt) * 64 + lane] = v[q];
+        for (int q = 0; q < TPU; ++q) part[((ut + q) * MT + umt) * 64 + lane] = v[q];
+      }
+      return;
+    }
+    if (has_unit) {
+      const CohBuf pb = coh_buf(part, per * 16);
+#pragma unroll
+      for (int q = 0; q < TPU; ++q) coh_stf4(pb, (unsigned)(((ut + q) * MT + umt) * 64 + lane) * 16u, v[q]);
+    }
+    __shared__ int ok_s;
+    if (threadIdx.x == 0) group_clear_other(a.gw, (int)((bz * gy + by) * a.ngroups + bx));
+    if (!group_arrive_wait(a.gw, (int)grp, (unsigned)gy, &ok_s)) return;
+    const CohBuf gb = coh_buf(reinterpret_cast<const f32x4*>(a.part) + grp * gy * per, (unsigned)(gy * per * 16));
+    for (int u = w * gy + by; u < UNITS; u += NW * gy) {
+      const int sut = (u / MT) * TPU, sumt = u % MT;
+      f32x4 sv[TPU];
+#pragma unroll
+      for (int q = 0; q < TPU; ++q) {
+        constexpr int SB = 16;
+        const unsigned o = (unsigned)(((sut + q) * MT + sumt) * 64 + lane) * 16u;
+        f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int y0 = 0; y0 < gy; y0 += SB) {
+          f32x4 pv[SB];
+#pragma unroll
+          for (int y = 0; y < SB; ++y) pv[y] = coh_ldf4(gb, (unsigned)min(y0 + y, gy - 1) * (per * 16u) + o);
+#pragma unroll
+          for (int y = 0; y < SB; ++y)
+            if (y0 + y < gy) sum = (y0 + y == 0) ? pv[y] : sum + pv[y];
+        }
+        sv[q] = sum;
+      }
+      os_epilogue<DT, EPI, TPU, false>(a, sv, m0 + 16 * sumt + lr, t0 + sut, lg);
     }
     return;
   }

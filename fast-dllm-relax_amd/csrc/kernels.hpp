@@ -15,6 +15,30 @@ namespace fdllm {
 enum PackMode : int { PACK_ROWS = 0, PACK_PAIRS = 1 };
 hipError_t launch_pack(const uint16_t* src, int N, int K, int ntiles, int mode, uint16_t* dst, hipStream_t st);
 
+// ---- workgroups of one launch waiting on each other ----------------------------------------------
+// The one-shot projections' k splits (down) are reduced inside their own launch: the
+// workgroups of a group store their fp32 partials with agent-scope stores, count their arrival on the
+// group's counter and wait until the group's last member has arrived; then each sums a share of the
+// group's outputs.  Such a launch is planned only when its whole grid is resident at once (at most one
+// workgroup per compute unit), so every member of a group runs.  Every wait is still bounded: past
+// `limit` ticks of the 100 MHz wall clock a workgroup gives up, sets *fault (pinned host memory,
+// written with a system-scope store) and skips its share, so a broken launch ends with a reported
+// fault instead of a hung GPU.
+// Counters: two banks of GW_GROUPS counters GW_STRIDE words apart (group k of bank b at
+// (b GW_GROUPS + k) GW_STRIDE).  Launches that use a region alternate banks; each launch's workgroup i
+// zeroes counter i of the other bank, for i < clear (the groups the previous launch used), since that
+// launch has finished (launches of a context are stream-ordered).  So no arrival has to return a value
+// and nothing is reset on a wait's critical path.
+constexpr int GW_STRIDE = 32;
+constexpr int GW_GROUPS = 256;  // groups of one launch (counters in each bank)
+struct GroupWait {
+  unsigned* cnt;      // the region's two banks; nullptr: the launch reduces with a separate kernel
+  unsigned* fault;    // device address of the host-visible fault word
+  long long limit;    // wall-clock ticks one wait may take
+  int bank;           // bank of this launch
+  int clear;          // counters of the other bank to zero
+};
+
 // ---- skinny GEMM over packed weights ------------------------------------------------------------
 // Y[M, N] = X[M, K] . W[N, K]^T for M <= 32 per m-chunk (gridDim.z chunks of 32 rows).
 enum Epilogue : int { EPI_BIAS = 0, EPI_RESID = 1, EPI_SILU_PAIR = 2, EPI_LOGITS = 3 };
@@ -42,6 +66,9 @@ struct GemmP {
   // large-M k splits: 1 stores the split sums row-major (part[split][M][N], N a multiple of 4) and launches
   // no split-sum kernel; the caller sums them (launch_resid_norm)
   int part_rows;
+  // one-shot k splits: gw.cnt set, the splits of each tile group are summed inside the launch (the host
+  // sets it only when the grid is resident at once); otherwise gemm_os_epilogue_kernel sums them
+  GroupWait gw;
 };
 
 // Launch configurations (see gemm.hip); the host picks one per projection.
@@ -188,51 +215,5 @@ size_t plan_seq_units(AttnP& a, int ncu);
 hipError_t launch_attention(int dt, const AttnP& a, hipStream_t st);
 size_t attn_partial_floats(const AttnP& a);
 
-// ---- the cached step as one persistent launch (step_body.hpp) -------------------------------------
-struct StepSync {
-  unsigned* ctr;      // 32 barrier counters, 32 words apart; zero at launch
-  unsigned* la;       // down tile-group arrival counters, 32 words apart; zero at launch
-  unsigned* abort_f;  // nonzero: some wait timed out; every workgroup leaves at its next wait
-  unsigned* status;   // host-visible word: set to 1 when the launch aborted
-  long long limit;    // wall-clock ticks a wait may take
-  unsigned long long* trace;  // optional: per workgroup and barrier n, the wall clock at arrival and release
-  int trace_bars;             // barriers per workgroup row of trace (slot 0: kernel start / end)
-};
-constexpr int BAR_CTRS = 32;
-constexpr int BAR_STRIDE = 32;  // words between counters (128 B)
-
-struct StepLayerW {
-  const uint16_t *pqkv, *bqkv, *po, *pgu, *pd, *ln_in, *ln_post;  // packed weights, bias, norm weights
-};
-
-// Upper bounds of the register-resident weight slices (step_plan checks a model fits them).
-constexpr int STEP_KPW = 6;    // k steps per wave of qkv / o_proj / gate_up (K <= 8 x 6 x 32 = 1536)
-constexpr int STEP_PAIRS = 3;  // gate_up tile pairs per workgroup
-constexpr int STEP_DNT = 4;    // down tiles per group (the one-shot kernel's grouping)
-constexpr int STEP_DKPW = 4;   // down k steps per wave (splits of at most 32 k steps)
-
-struct StepP {
-  const StepLayerW* layers; int L;
-  int H, I, nq, nkv, qkv_dim, q_dim;
-  float eps;
-  int M;                      // active rows (<= 32)
-  uint16_t* h; float* ssq; int ssq_ld;
-  uint16_t* qkv; uint16_t* attn; uint16_t* act;
-  float* dpart;               // down split partials
-  AttnP at;                   // attention of the call (kc / vc set per layer from the bases below)
-  uint16_t* kbase; uint16_t* vbase; long long layer_stride;
-  int qg;                     // query-tile groups of the attention (4 tiles each)
-  int nt_q, nt_o, np_u;       // qkv tiles, o_proj tiles, gate_up pairs
-  int d_groups, d_splits;     // down: tile groups of STEP_DNT tiles, k splits
-  StepSync sync;
-};
-// Whether the launch fits G co-resident workgroups and the kernel's register slices; the LDS it needs.
-// why: the reason when it does not.
-struct StepPlan { bool ok; const char* why; size_t lds; };
-StepPlan step_plan(const StepP& p, int G);
-size_t step_sync_words(const StepP& p);  // words of the sync area (barrier + arrival counters, abort)
-// A cooperative launch of G workgroups (all co-resident, or the launch fails).
-hipError_t launch_step(int dt, const StepP& p, int G, size_t lds, hipStream_t st);
-hipError_t launch_fill_u32(unsigned* p, size_t n, unsigned v, hipStream_t st);
 
 }  // namespace fdllm

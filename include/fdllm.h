@@ -204,11 +204,12 @@ void fdllm_host_free(void* host_ptr);
 int fdllm_bench_op(fdllm_ctx* ctx, int op, int rows, int layer, int iters, void* k_cache, void* v_cache, int cap,
                    int attend_len, void* stream);
 
-/* Diagnostic; it has no counterpart in the reference.  Number of cached steps this context has run as one
- * persistent launch (all layers in one cooperative kernel).  That path is off unless the environment
- * variable FDLLM_PERSISTENT=1 is set when the context is created; otherwise every step runs the
- * per-operator kernels. */
-long long fdllm_persistent_steps(const fdllm_ctx* ctx);
+/* Diagnostic; it has no counterpart in the reference.  Number of launches this context has run that
+ * reduced their own splits (the down projection's k splits, the decode attention's key splits) instead of
+ * handing them to a separate split-sum or merge launch.  Such a launch is planned when its whole grid is
+ * resident at once (at most one workgroup per compute unit); FDLLM_GROUP_WAITS=0 at fdllm_create turns
+ * it off, and so does a timed-out wait (reported by the next entry point as FDLLM_EHIP). */
+long long fdllm_group_wait_launches(const fdllm_ctx* ctx);
 
 /* Diagnostic; it has no counterpart in the reference.  Number of layer-loop calls (cached steps, short
  * stateless forwards) this context has run with the activations in MFMA-fragment order: calls of at

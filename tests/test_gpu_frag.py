@@ -26,7 +26,6 @@ def _pair_of_vms(kw, seed, monkeypatch, dtype):
 
     cfg = FastDLLMConfig(**kw)
     params = from_numpy(random_params(OracleConfig(**kw), seed, dtype), cfg, dtype=dtype)
-    monkeypatch.delenv("FDLLM_PERSISTENT", raising=False)
     monkeypatch.delenv("FDLLM_XFRAG", raising=False)
     vm_f = HipVM(cfg, params, dtype=dtype, max_rows=64)
     monkeypatch.setenv("FDLLM_XFRAG", "0")
