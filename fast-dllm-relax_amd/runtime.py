@@ -409,7 +409,9 @@ def relax_greedy_generate(vm: HipVM, prompt_token_ids, *, max_new_tokens: int, b
     and the host reads only the step's report.  ``decisions`` (optional) then receives, per cached
     refinement step, the report's sub-block view: the rows that were masked, their shifted probabilities
     and ids, and the rows the device selected (and {"kind": "append", "token": t} per block append).  Without it, each step reads the confidence back and
-    applies the rule on the host, as the reference does."""
+    applies the rule on the host, as the reference does, and ``decisions`` receives the same view of the
+    host's decision; a stateless step (the first block of a prompt shorter than a block) records
+    {"kind": "stateless", ...} with its float64 probabilities."""
     if temperature != 0.0:
         raise NotImplementedError("Fast-dLLM Relax runner currently supports only temperature=0.")
     if top_p <= 0:
@@ -534,6 +536,10 @@ def relax_greedy_generate(vm: HipVM, prompt_token_ids, *, max_new_tokens: int, b
                         x_t[a0 + s0 + r] = int(bids[r])
                         unmask_updates += 1
                     log("partial" if use_partial else "full", s0, tuple(rows), tuple(int(bids[r]) for r in rows))
+                    if decisions is not None:
+                        decisions.append({"kind": "partial" if use_partial else "full", "s0": s0, "masked": local,
+                                          "probs": np.asarray(bp, np.float32), "ids": [int(t) for t in bids],
+                                          "selected": rows})
                 else:
                     _, shifted = score_sequence_block(vm, x_t, block_size=block_size)
                     block_recomputes += 1
@@ -554,6 +560,9 @@ def relax_greedy_generate(vm: HipVM, prompt_token_ids, *, max_new_tokens: int, b
                         x_t[a0 + s0 + r] = int(chosen[r])
                         unmask_updates += 1
                     log("stateless", s0, tuple(rows), tuple(int(chosen[r]) for r in rows))
+                    if decisions is not None:
+                        decisions.append({"kind": "stateless", "s0": s0, "masked": local, "probs": cp,
+                                          "ids": [int(t) for t in chosen], "selected": rows})
                 if len(x_t) - plen0 >= max_new_tokens:
                     break
             if len(x_t) - plen0 >= max_new_tokens:
@@ -574,9 +583,13 @@ def relax_greedy_generate(vm: HipVM, prompt_token_ids, *, max_new_tokens: int, b
         elif use_cache:
             _, _, nxt, prefix_cache = score_active_block_cached_fast(vm, generated[a0:], prefix_cache)
             block_kv_valid = False
+            if decisions is not None:
+                decisions.append({"kind": "append", "token": nxt})
         else:
             cur, _ = score_sequence_block(vm, generated, block_size=block_size)
             nxt = int(cur[0, -1, :].argmax())
+            if decisions is not None:
+                decisions.append({"kind": "append", "token": nxt})
         log("append", prefix_cache.prefix_len if use_cache else 0, nxt)
         block_recomputes += 1
         generated.append(nxt)

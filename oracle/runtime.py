@@ -157,8 +157,9 @@ def greedy_generate(model: OracleModel, prompt_ids, *, max_new_tokens: int, bloc
                     small_block_size: int = 8, threshold: float = 0.9, use_block_cache: bool = True,
                     mask_id: int, stop_token: int | None, trace: list | None = None, decisions: list | None = None):
     """relax_greedy_generate (runtime.py:591-880), temperature 0.  ``trace`` collects one tuple per call;
-    ``decisions`` (optional) one dict per cached refinement step: the sub-block's masked rows, shifted
-    probabilities and ids, the selected rows, and each row's gap between its two largest logits."""
+    ``decisions`` (optional) one dict per refinement step (cached or stateless): the sub-block's masked
+    rows, shifted probabilities (float64 on the stateless path) and ids, the selected rows, and each row's
+    gap between its two largest logits; and one per block append after the first call."""
     generated = list(prompt_ids)
     plen0 = len(generated)
     stats = dict(unmask_updates=0, block_recomputes=0, partial_recomputes=0, block_appends=0)
@@ -263,6 +264,11 @@ def greedy_generate(model: OracleModel, prompt_ids, *, max_new_tokens: int, bloc
                         x_t[a0 + s0 + r] = int(chosen[r])
                         stats["unmask_updates"] += 1
                     log("stateless", s0, tuple(rows), tuple(int(chosen[r]) for r in rows))
+                    if decisions is not None:
+                        top2 = np.sort(small, axis=-1)[:, -2:]
+                        decisions.append({"kind": "stateless", "s0": s0, "masked": local, "probs": cp,
+                                          "ids": [int(t) for t in chosen], "selected": rows,
+                                          "gap": top2[:, 1] - top2[:, 0]})
                 if len(x_t) - plen0 >= max_new_tokens:
                     break
             if len(x_t) - plen0 >= max_new_tokens:
@@ -282,6 +288,9 @@ def greedy_generate(model: OracleModel, prompt_ids, *, max_new_tokens: int, bloc
         else:
             cur, _ = score_sequence_block(model, generated, block_size=block_size)
             nxt = int(cur[0, -1, :].argmax())
+            if decisions is not None:
+                top2 = np.sort(cur[0, -1, :])[-2:]
+                decisions.append({"kind": "append", "token": nxt, "gap": float(top2[1] - top2[0])})
         log("append", cache.prefix_len if use_cache else 0, nxt)
         stats["block_recomputes"] += 1
         generated.append(nxt)

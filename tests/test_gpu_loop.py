@@ -148,7 +148,9 @@ def test_fused_confidence_unmask_equals_confidence(small_pair):
 
 
 def _check_decisions(decisions):
-    """Every device decision is fd_unmask of that step's own probabilities (bit-exact given the logits)."""
+    """Every cached decision is fd_unmask of that step's own fp32 probabilities (bit-exact given the
+    logits); a stateless one (runtime.py:806-837) unmasks the masked rows whose float64 probability
+    exceeds the threshold, else the first of the largest."""
     n = 0
     for d in decisions:
         if d["kind"] == "append":
@@ -156,8 +158,16 @@ def _check_decisions(decisions):
         sub = len(d["ids"])
         masked = np.zeros(sub, bool)
         masked[d["masked"]] = True
-        sel = oconf.unmask(np.asarray(d["probs"], np.float32), masked, THR)
-        assert list(np.nonzero(sel)[0]) == list(d["selected"]), d
+        if d["kind"] == "stateless":
+            p = np.asarray(d["probs"], np.float64)
+            sel = [r for r in d["masked"] if p[r] > THR]
+            if not sel:
+                g = np.where(masked, p, -np.inf)
+                sel = [int(np.argmax(g))]
+            assert list(sel) == list(d["selected"]), d
+        else:
+            sel = oconf.unmask(np.asarray(d["probs"], np.float32), masked, THR)
+            assert list(np.nonzero(sel)[0]) == list(d["selected"]), d
         n += 1
     return n
 
@@ -182,17 +192,30 @@ def _fragile(od, delta):
     return False
 
 
-def _loop_vs_oracle(ref, vm, prompt, new_tokens, mask_id, delta):
+class _LoggedTrace(list):
+    """A trace list that prints each call as it is logged (a long oracle loop then shows progress)."""
+
+    def __init__(self, name):
+        super().__init__()
+        self.name = name
+
+    def append(self, item):
+        super().append(item)
+        if len(self) % 8 == 1:
+            log(f"    {self.name} call {len(self)}: {item[0]}")
+
+
+def _loop_vs_oracle(ref, vm, prompt, new_tokens, mask_id, delta, device_loop=True, verbose=False):
     _, rt = _rt()
     common = dict(max_new_tokens=new_tokens, block_size=32, small_block_size=8, threshold=THR, mask_id=mask_id,
                   stop_token=None)
     tr_h, dec_h = [], []
-    out_h, st_h = rt.relax_greedy_generate(vm, prompt, trace=tr_h, decisions=dec_h, **common)
-    log(f"  HIP loop: {len(out_h)} tokens, {st_h}")
+    out_h, st_h = rt.relax_greedy_generate(vm, prompt, trace=tr_h, decisions=dec_h, device_loop=device_loop, **common)
+    log(f"  HIP loop ({'device' if device_loop else 'host'} rule): {len(out_h)} tokens, {st_h}")
     n = _check_decisions(dec_h)
-    log(f"  {n} device unmask decisions equal fd_unmask on their own probabilities")
+    log(f"  {n} unmask decisions equal the rule applied to their own probabilities")
     assert sum(len(d["selected"]) > 1 for d in dec_h if d["kind"] != "append") > 0, "no step crossed the threshold"
-    tr_o, dec_o = [], []
+    tr_o, dec_o = (_LoggedTrace("oracle") if verbose else []), []
     out_o, st_o = greedy_generate(ref, prompt, trace=tr_o, decisions=dec_o, **common)
     log(f"  oracle loop: {len(out_o)} tokens, {st_o}")
     first = next((i for i, (a, b) in enumerate(zip(tr_h, tr_o)) if a != b), None)
@@ -247,4 +270,63 @@ def test_decode_loop_cfg3_shape_matches_oracle():
     prompt = [int(t) for t in np.random.default_rng(2).integers(0, 150000, 2048)]
     delta = _measured_logit_error(ref, vm, prompt, DEFAULT_MASK_ID)
     _loop_vs_oracle(ref, vm, prompt, 64, DEFAULT_MASK_ID, delta)
+    vm.close()
+
+
+def test_host_loop_small_matches_oracle(small_pair):
+    """relax_greedy_generate with the reference's host rule (device_loop=False): score_active_block_refine /
+    _partial_perlayer / _cached_fast and the threshold decision on the host, as runtime.py:794-805."""
+    ref, vm = small_pair
+    prompt = [int(t) for t in np.random.default_rng(22).integers(0, 999, 64)]
+    delta = _measured_logit_error(ref, vm, prompt, 999)
+    _loop_vs_oracle(ref, vm, prompt, 96, 999, delta, device_loop=False)
+
+
+def test_host_loop_small_unaligned_prompt(small_pair):
+    ref, vm = small_pair
+    prompt = [int(t) for t in np.random.default_rng(23).integers(0, 999, 77)]
+    delta = _measured_logit_error(ref, vm, prompt, 999)
+    _loop_vs_oracle(ref, vm, prompt, 64, 999, delta, device_loop=False)
+
+
+@pytest.mark.parametrize("device_loop", [True, False])
+def test_loop_short_prompt_stateless_first_block(small_pair, device_loop):
+    """A 20-token prompt: the first block is refined statelessly (score_sequence_block, float64 probabilities
+    and the gated argmax, runtime.py:719-721, 806-837), then the block is appended and the loop turns to
+    the cache."""
+    ref, vm = small_pair
+    prompt = [int(t) for t in np.random.default_rng(24).integers(0, 999, 20)]
+    # the stateless block's logit error: a dense forward over the prompt and its masks
+    from oracle.runtime import score_sequence_block as o_ssb
+
+    _, rt = _rt()
+    seq = prompt + [999] * 12
+    _, sh_o = o_ssb(ref, seq, block_size=32)
+    _, sh_h = rt.score_sequence_block(vm, seq, block_size=32)
+    delta = float(np.abs(np.asarray(sh_h, np.float32) - sh_o).max())
+    log(f"  stateless block logit error: max |dlogit| = {delta:.4g}")
+    _loop_vs_oracle(ref, vm, prompt, 64, 999, delta, device_loop=device_loop)
+
+
+@pytest.mark.timeout(900)
+def test_decode_loop_cfg3_full_depth():
+    """BASELINE cfg3 at full depth: the 28-layer 1.5B model with bench.py's weights (seed 2, untied lm_head
+    N(0, 0.5)), a 2048-token prompt and 64 new tokens, on the device loop, against the bf16 oracle loop
+    under the divergence rule above (the measured logit error of one cached step at this depth sets it)."""
+    from fast_dllm_relax_amd.config import DEFAULT_MASK_ID, fast_dllm_v2_1p5b
+    from fast_dllm_relax_amd.params import param_names, random_params_torch
+    from fast_dllm_relax_amd.vm import HipVM
+    from oracle.model import OracleConfig, OracleModel
+
+    cfg = fast_dllm_v2_1p5b(tie_word_embeddings=False)
+    log("setup: 1.5B bf16, 28 layers, seed 2, lm_head N(0, 0.5)")
+    params = random_params_torch(cfg, 2, dtype="bfloat16", device="cuda", lm_head_std=0.5)
+    vm = HipVM(cfg, params, dtype="bfloat16", max_rows=2048)
+    ocfg = OracleConfig(vocab_size=cfg.vocab_size, hidden_size=cfg.hidden_size, intermediate_size=cfg.intermediate_size,
+                        num_hidden_layers=cfg.num_hidden_layers, num_attention_heads=cfg.num_attention_heads,
+                        num_key_value_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim, tie_word_embeddings=False)
+    ref = OracleModel(ocfg, {n: p.float().cpu().numpy() for n, p in zip(param_names(cfg), params)}, "bfloat16")
+    prompt = [int(t) for t in np.random.default_rng(2).integers(0, 150000, 2048)]
+    delta = _measured_logit_error(ref, vm, prompt, DEFAULT_MASK_ID)
+    _loop_vs_oracle(ref, vm, prompt, 64, DEFAULT_MASK_ID, delta, verbose=True)
     vm.close()

@@ -93,6 +93,8 @@ def test_prefill_and_cached_step_match_oracle(tiny):
 
 
 def test_forward_hidden_matches_oracle_and_dense_equals_cached(tiny):
+    """forward_hidden against the oracle (explicit bias and the arithmetic block-causal rule), and the
+    HIP path's cached and partial rows against its own dense block-causal rows."""
     ref, vm = tiny
     rng = np.random.default_rng(4)
     S = 96
@@ -106,6 +108,19 @@ def test_forward_hidden_matches_oracle_and_dense_equals_cached(tiny):
     log("case: forward_hidden S=96 arithmetic block-causal")
     h2 = to_np(vm.forward_hidden(x, None))
     np.testing.assert_allclose(h2, h, rtol=1e-2, atol=1e-2)
+    # the reference's invariant (tests/test_tiny_compile.py:264-290): the cached step's rows equal the
+    # dense block-causal forward's rows, and each partial step equals the full cached step's rows for its
+    # sub-block (the cached path runs other attention kernels, hence the bf16 tolerance)
+    log("case: cached rows == dense block-causal rows, partial rows == cached rows")
+    P, L, nkv = 64, TINY["num_hidden_layers"], TINY["num_key_value_heads"]
+    k = torch.zeros((L, 1, 128, nkv, 128), dtype=torch.bfloat16, device="cuda")
+    v = torch.zeros_like(k)
+    vm.build_prefix_cache(x[:, :P], None, k, v)
+    hc = to_np(vm.forward_cached(x[:, P:], k, v, _off(P), P))
+    np.testing.assert_allclose(hc, h2[:, P:], **TOL)
+    for rp in (0, 8, 16, 24):
+        hp = to_np(vm[f"forward_block_partial_rp{rp}"](x[:, P + rp:P + rp + 8].contiguous(), k, v, _off(P + rp), P))
+        np.testing.assert_allclose(hp, hc[:, rp:rp + 8], **TOL, err_msg=f"rp{rp}")
 
 
 def test_write_window_errors(tiny):
