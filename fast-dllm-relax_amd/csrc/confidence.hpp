@@ -86,8 +86,11 @@ __device__ __forceinline__ void unmask_wave(const int32_t* ids, const float* max
     rep[REP_LEFT] = __popcll(mm & ~sm);
     rep[REP_COUNT] = __popcll(sm);
     rep[REP_LAST] = ids[u.rows - 1];
+    // the 64-bit row masks as (low, high) word pairs: sub-blocks of up to 64 rows
     rep[REP_BLOCK + u.bd + 2 * u.sub] = (int32_t)(unsigned)mm;
-    rep[REP_BLOCK + u.bd + 2 * u.sub + 1] = (int32_t)(unsigned)sm;
+    rep[REP_BLOCK + u.bd + 2 * u.sub + 1] = (int32_t)(unsigned)(mm >> 32);
+    rep[REP_BLOCK + u.bd + 2 * u.sub + 2] = (int32_t)(unsigned)sm;
+    rep[REP_BLOCK + u.bd + 2 * u.sub + 3] = (int32_t)(unsigned)(sm >> 32);
   }
   // the report may be host memory the caller polls: every lane's stores reach it before lane 0
   // publishes the sequence number

@@ -123,9 +123,10 @@ hipError_t launch_confidence_tiles(const float* logits, int ld, int vocab, int r
 // ---- the decode loop's threshold unmask (unmask.hip, confidence.hpp) ------------------------------
 // Words of an unmask report (int32): the sequence number (written last), masks left in the sub-block,
 // rows unmasked, the unshifted argmax of the last confidence row, the block after the update, then the
-// sub-block's shifted ids and probabilities (fp32 bits) and the masked / selected row bitmasks.
+// sub-block's shifted ids and probabilities (fp32 bits) and the masked / selected row bitmasks (64 bits
+// each, as a low and a high word).
 constexpr int REP_SEQ = 0, REP_LEFT = 1, REP_COUNT = 2, REP_LAST = 3, REP_BLOCK = 4;
-__host__ __device__ constexpr int report_words(int bd, int sub) { return REP_BLOCK + bd + 2 * sub + 2; }
+__host__ __device__ constexpr int report_words(int bd, int sub) { return REP_BLOCK + bd + 2 * sub + 4; }
 
 struct UnmaskP {
   int rows;            // confidence rows of the call

@@ -232,7 +232,7 @@ class DeviceBlock:
         self.mask_id, self.thr = int(mask_id), threshold_f32(threshold)
         self.buf = torch.zeros(self.bd + 1 + self.bd // self.sub, dtype=torch.int32, device="cuda")
         self.block = self.buf[:self.bd]
-        self.words = 4 + self.bd + 2 * self.sub + 2
+        self.words = 4 + self.bd + 2 * self.sub + 4
         host, dev = ctypes.c_void_p(), ctypes.c_void_p()
         _lib.check(self.lib.fdllm_host_alloc(self.words * 4, ctypes.byref(host), ctypes.byref(dev)))
         self._host, self._dev = host, dev
@@ -295,9 +295,13 @@ class DeviceBlock:
                     torch.cuda.synchronize()  # surfaces a device error, if there is one
                     if rep[0] != seq:
                         raise RuntimeError(f"device unmask report {seq} did not arrive")
-        words = rep[:4 + self.bd + 2 * sub + 2].copy()
+        words = rep[:4 + self.bd + 2 * sub + 4].copy()
         b = 4 + self.bd
-        masked_bits, sel_bits = int(words[b + 2 * sub]) & 0xFFFFFFFF, int(words[b + 2 * sub + 1]) & 0xFFFFFFFF
+
+        def mask64(i):  # a (low, high) word pair
+            return (int(words[i]) & 0xFFFFFFFF) | (int(words[i + 1]) & 0xFFFFFFFF) << 32
+
+        masked_bits, sel_bits = mask64(b + 2 * sub), mask64(b + 2 * sub + 2)
         return UnmaskReport(block=words[4:b].tolist(), selected=[r for r in range(sub) if sel_bits >> r & 1],
                             masked=[r for r in range(sub) if masked_bits >> r & 1], ids=words[b:b + sub].tolist(),
                             probs=words[b + sub:b + 2 * sub].view(np.float32).copy(), left=int(words[1]),

@@ -167,12 +167,13 @@ int fdllm_confidence_from_logits(fdllm_ctx* ctx, const float* logits, int rows, 
  *               0 for a partial step.  The selected rows are overwritten with their predicted ids.
  *   threshold   compared as `p > threshold` in fp32 (pass the fp32 rounding toward -inf of the host
  *               threshold to reproduce numpy's fp32-vs-Python-float comparison).
- *   report      optional int32 [4 + bd_size + 2 sub_rows + 2] (device memory, or host memory from
+ *   report      optional int32 [4 + bd_size + 2 sub_rows + 4] (device memory, or host memory from
  *               fdllm_host_alloc that the host polls): word 0 = seq, written after everything else;
  *               1 = masked rows left in the sub-block; 2 = rows unmasked; 3 = unshifted argmax of the
  *               last confidence row (the append step's next token, runtime.py:360-363); 4.. = the block
  *               after the update; then the sub-block's shifted ids, their probabilities (fp32 bits), and
- *               bitmasks of the rows that were masked and that were selected.
+ *               the 64-bit masks of the rows that were masked and that were selected, each as a low and
+ *               a high word (bit r: sub-block row r).
  * sub_rows = 0 updates nothing (an append step that only needs the report).  bd_size must be <= 64. */
 int fdllm_unmask(fdllm_ctx* ctx, const int32_t* ids, const float* maxp, int rows, int row0, int32_t* block, int s0,
                  int sub_rows, int32_t mask_id, float threshold, int32_t* report, int32_t seq, void* stream);

@@ -89,7 +89,7 @@ def test_unmask_rule_bit_exact_random(small_pair):
         blk[mk] = mask_id
         blk_h[i] = blk
         cases.append((rows, row0, s0))
-    words = 4 + bd + 2 * sub + 2
+    words = 4 + bd + 2 * sub + 4
     ids_d = torch.from_numpy(ids_h).cuda()
     p_d = torch.from_numpy(p_h).cuda()
     blk_d = torch.from_numpy(blk_h).cuda()
@@ -108,9 +108,41 @@ def test_unmask_rule_bit_exact_random(small_pair):
         assert r[1] == int((masked & ~sel).sum()) and r[2] == int(sel.sum())
         assert r[3] == ids_h[i, rows - 1]
         np.testing.assert_array_equal(r[4 + bd + sub:4 + bd + 2 * sub].view(np.float32), p)
-        assert (int(r[4 + bd + 2 * sub]) & 0xFF) == sum(1 << j for j in range(sub) if masked[j])
-        assert (int(r[4 + bd + 2 * sub + 1]) & 0xFF) == sum(1 << j for j in range(sub) if sel[j])
+        m64 = (int(r[4 + bd + 2 * sub]) & 0xFFFFFFFF) | (int(r[4 + bd + 2 * sub + 1]) & 0xFFFFFFFF) << 32
+        s64 = (int(r[4 + bd + 2 * sub + 2]) & 0xFFFFFFFF) | (int(r[4 + bd + 2 * sub + 3]) & 0xFFFFFFFF) << 32
+        assert m64 == sum(1 << j for j in range(sub) if masked[j])
+        assert s64 == sum(1 << j for j in range(sub) if sel[j])
     log(f"  {n} random unmask cases bit-exact with fd_unmask")
+
+
+def test_unmask_sub_block_past_32_rows():
+    """A 64-row block refined as one 64-row sub-block: the report's masked / selected masks carry all 64
+    rows (a low and a high word each), and the block update matches fd_unmask."""
+    _lib, rt = _rt()
+    _, vm = make_pair(dict(SMALL, bd_size=64), 25, "bfloat16", max_rows=64)
+    rng = np.random.default_rng(26)
+    thr32 = np.float32(rt.threshold_f32(THR))
+    bd = sub = 64
+    for i, frac in enumerate((0.6, 1.0, 0.2)):
+        ids_h = rng.integers(0, 999, 64).astype(np.int32)
+        p_h = rng.random(64).astype(np.float32)
+        p_h[rng.integers(32, 64, 5)] = np.float32(0.95)  # rows past 32 crossing the threshold
+        blk_h = rng.integers(0, 999, bd).astype(np.int32)
+        blk_h[rng.random(bd) < frac] = 999
+        ids_d, p_d, blk_d = (torch.from_numpy(a).cuda() for a in (ids_h, p_h, blk_h))
+        rep_d = torch.zeros(4 + bd + 2 * sub + 4, dtype=torch.int32, device="cuda")
+        _lib.check(vm.lib.fdllm_unmask(vm.ctx, ids_d.data_ptr(), p_d.data_ptr(), 64, 0, blk_d.data_ptr(), 0, sub, 999,
+                                       float(thr32), rep_d.data_ptr(), i + 1, _stream()))
+        torch.cuda.synchronize()
+        want, sel, masked, _ = _expected(ids_h, p_h, blk_h, 0, 0, sub, 999)
+        r = rep_d.cpu().numpy()
+        np.testing.assert_array_equal(blk_d.cpu().numpy(), want)
+        m64 = (int(r[4 + bd + 2 * sub]) & 0xFFFFFFFF) | (int(r[4 + bd + 2 * sub + 1]) & 0xFFFFFFFF) << 32
+        s64 = (int(r[4 + bd + 2 * sub + 2]) & 0xFFFFFFFF) | (int(r[4 + bd + 2 * sub + 3]) & 0xFFFFFFFF) << 32
+        assert m64 == sum(1 << j for j in range(sub) if masked[j])
+        assert s64 == sum(1 << j for j in range(sub) if sel[j])
+        assert r[1] == int((masked & ~sel).sum()) and r[2] == int(sel.sum())
+    vm.close()
 
 
 def test_unmask_rejects_bad_windows(small_pair):

@@ -1,6 +1,7 @@
 """The allocation-free cached step (fdllm_forward_cached_noalloc, include/fdllm.h) against
-fdllm_forward_cached: the same hidden states and cache rows, bit for bit, on two calls in a row (the
-second smaller), called through the C ABI.  Marked gpu."""
+fdllm_forward_cached: the same hidden states and cache rows, bit for bit, on calls in a row, each
+smaller than the one before (the first at the documented limit of 8192 attended keys), called through
+the C ABI.  Marked gpu."""
 
 from __future__ import annotations
 
@@ -41,8 +42,11 @@ def test_noalloc_step_equals_forward_cached():
     ref, vm = make_pair(WIDE2, 7, "bfloat16", max_rows=2048)
     lib = vm.lib
     rng = np.random.default_rng(7)
+    long_prompt = [int(t) for t in rng.integers(0, 150000, 8160)]
+    log("case: noalloc 32 rows at prefix 8160 (8192 keys, the documented limit: 64 key chunks of partials)")
+    _step_both(vm, lib, _lib, long_prompt, [int(t) for t in rng.integers(0, 150000, 32)], 8192)
     prompt = [int(t) for t in rng.integers(0, 150000, 2016)]
-    log("case: noalloc 32 rows at prefix 2016")
+    log("case: noalloc 32 rows at prefix 2016 (a smaller call after it)")
     _step_both(vm, lib, _lib, prompt, [int(t) for t in rng.integers(0, 150000, 32)], 2048)
     log("case: noalloc 8 rows at prefix 480 (a smaller second call)")
     _step_both(vm, lib, _lib, prompt[:480], [int(t) for t in rng.integers(0, 150000, 8)], 512)
