@@ -128,7 +128,7 @@ constexpr int PAIR_TQ = 3, PAIR_DEPTH = 3;
 
 template <int DT, int MASK>
 static hipError_t launch_prefill(const AttnP& a, hipStream_t st) {
-  hipLaunchKernelGGL(rope_kv_kernel<DT>, dim3(a.rows), dim3(128), 0, st, a);
+  if (!a.roped) hipLaunchKernelGGL(rope_kv_kernel<DT>, dim3(a.rows), dim3(128), 0, st, a);
   const int nqb = (a.rows + 31) / 32, grp = a.nq / a.nkv;
   const int pairs = (nqb + 1) / 2;
   if (grp == 2 * PAIR_TQ && (a.prefill_pair == 2 || (a.prefill_pair == 1 && pairs * a.nkv >= 256))) {
@@ -206,7 +206,7 @@ size_t plan_seq_units(AttnP& a, int ncu) {
 template <int DT>
 static hipError_t launch_seq(const AttnP& a, hipStream_t st) {
   if (a.nunits < a.nseq || a.nunits > MAX_SEQ_UNITS) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(rope_kv_kernel<DT>, dim3(a.nseq * a.rows), dim3(128), 0, st, a);
+  if (!a.roped) hipLaunchKernelGGL(rope_kv_kernel<DT>, dim3(a.nseq * a.rows), dim3(128), 0, st, a);
   const int QT = ((a.nq / a.nkv) * a.rows + 15) / 16, xg = (QT + SEQ_NQW - 1) / SEQ_NQW;
   const int pairs = a.nunits * a.nkv;
   auto kern = attn_seq_kernel<DT, SEQ_DEPTH, SEQ_NQW, SEQ_KH>;
@@ -216,9 +216,16 @@ static hipError_t launch_seq(const AttnP& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+bool attn_takes_roped(const AttnP& a) {
+  if (a.nseq > 1 && a.seq_attn && a.mask == 0) return true;
+  const AttnPlan p = attn_plan(a.rows, a.nq, a.nkv, a.Lk, a.target_wgs);
+  return !p.chunked && a.nseq <= 1 && a.rows >= PREFILL_MIN_ROWS && a.mask != 2;
+}
+
 template <int DT>
 static hipError_t launch_dt(const AttnP& a, hipStream_t st) {
   const AttnPlan p = attn_plan(a.rows, a.nq, a.nkv, a.Lk, a.target_wgs);
+  if (a.roped && !attn_takes_roped(a)) return hipErrorInvalidValue;
   if (p.S != a.S || p.chunk != a.chunk) return hipErrorInvalidValue;
   if (a.ofrag && (a.nseq > 1 || a.rows > 32)) return hipErrorInvalidValue;
   if (a.nseq > MAX_SEQS) return hipErrorInvalidValue;

@@ -108,6 +108,9 @@ struct fdllm_ctx {
   // three splits up to 256 rows (128-row batched step: 14.8 + 4.8 us norm -> 8.1 + 7.1 us; at 512 rows it
   // measured slower, 3.88 -> 3.94 ms per step with two splits), 0 never, N > 1 with N splits at any size
   int fuse_oproj = -1;
+  // large-M calls whose attention starts with the RoPE / KV-append pass (prefill, batched sequences): that
+  // pass done by qkv's epilogue instead (FDLLM_QKV_ROPE=0: the separate pass)
+  int qkv_rope = 1;
   int down_split = 10;    // cross-workgroup k splits of the down projection (largest divisor of K/32 <= this)
   MmPolicy mm;              // large-M GEMM planning (k splits, register-weight kernel)
   bool frag_on = true;      // one-shot chains keep activations in MFMA-fragment order (FDLLM_XFRAG=0: row-major)
@@ -308,12 +311,12 @@ int rope_table(fdllm_ctx* c, int rows, const int32_t* pos, int rows_per_seq, hip
   return FDLLM_OK;
 }
 
-// Attention of the call's rows; the RoPE table (rope_table) must hold the call's positions.  With sb,
-// the rows are sb->nseq sequences of sb->rows (ws and Lk are then ignored).
-int run_attention(fdllm_ctx* c, int rows, uint16_t* kc, uint16_t* vc, int ws, int Lk, int mask,
-                  const float* bias, long long bias_ld, hipStream_t st, const SeqBatch* sb = nullptr, bool frag = false) {
+// The attention launch of the call's rows, planned into a; the RoPE table (rope_table) must hold the
+// call's positions.  With sb, the rows are sb->nseq sequences of sb->rows (ws and Lk are then ignored).
+int plan_attention(fdllm_ctx* c, AttnP& a, int rows, uint16_t* kc, uint16_t* vc, int ws, int Lk, int mask,
+                   const float* bias, long long bias_ld, const SeqBatch* sb, bool frag) {
   const fdllm_config& f = c->cfg;
-  AttnP a{};
+  a = AttnP{};
   a.qkv = c->qkv; a.ldq = c->qkv_dim(); a.rows = rows; a.nq = f.num_attention_heads; a.nkv = f.num_key_value_heads;
   a.rope = c->rope;
   a.kc = kc; a.vc = vc; a.ws = ws; a.Lk = Lk; a.scale = 1.0f / std::sqrt((float)f.head_dim);
@@ -356,7 +359,15 @@ int run_attention(fdllm_ctx* c, int rows, uint16_t* kc, uint16_t* vc, int ws, in
   }
   a.out = c->attn;
   a.ofrag = frag;
-  HIPCHK(launch_attention(f.dtype, a, st));
+  return FDLLM_OK;
+}
+
+int run_attention(fdllm_ctx* c, int rows, uint16_t* kc, uint16_t* vc, int ws, int Lk, int mask,
+                  const float* bias, long long bias_ld, hipStream_t st, const SeqBatch* sb = nullptr, bool frag = false) {
+  AttnP a;
+  int rc = plan_attention(c, a, rows, kc, vc, ws, Lk, mask, bias, bias_ld, sb, frag);
+  if (rc) return rc;
+  HIPCHK(launch_attention(c->cfg.dtype, a, st));
   return FDLLM_OK;
 }
 
@@ -439,10 +450,26 @@ int run_layers(fdllm_ctx* c, const void* x_in, int rows, uint16_t* kbase, uint16
       g.q.nw = nullptr;
       g.q.xfrag = xn_layout;
     }
+    AttnP at;
+    rc = plan_attention(c, at, rows, kc, vc, write_start, attend_len, mask, bias, bias_ld, sb, frag);
+    if (rc) return rc;
+    if (!frag && rows > 32 && c->qkv_rope && attn_takes_roped(at)) {
+      // the queries RoPE'd and the K/V rows appended by qkv's epilogue, when its kernel takes that
+      GemmP tq = g.q;
+      const GemmPlan pq = gemm_plan(CFG_QKV, tq, 1, c->mm);
+      if (gemm_ropes_in_epilogue(CFG_QKV, pq) && g.q.ntiles % 8 == 0) {
+        RopeOut& ro = g.q.ro;
+        ro.rope = c->rope; ro.q = at.out; ro.kc = kc; ro.vc = vc;
+        ro.nq = f.num_attention_heads; ro.nkv = f.num_key_value_heads;
+        ro.rows = at.nseq > 1 ? at.rows : rows;
+        ro.seq_stride = at.nseq > 1 ? at.seq_stride : 0;
+        for (int b = 0; b < at.nseq; ++b) ro.ws[b] = at.nseq > 1 ? at.seq_ws[b] : at.ws;
+        at.roped = 1;
+      }
+    }
     rc = run_gemm(c, CFG_QKV, g.q, 1, st);
     if (rc) return rc;
-    rc = run_attention(c, rows, kc, vc, write_start, attend_len, mask, bias, bias_ld, st, sb, frag);
-    if (rc) return rc;
+    HIPCHK(launch_attention(f.dtype, at, st));
     // o_proj + the post-attention norm: with a forced k split, when gate_up takes normalised rows
     bool gu_ready = false;
     const int oproj_split = c->fuse_oproj > 1 ? c->fuse_oproj : (c->fuse_oproj < 0 && rows <= 256 ? 3 : 0);
@@ -623,6 +650,7 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   if (const char* e = std::getenv("FDLLM_SEQ_ATTN")) c->seq_attn = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_FUSE_DOWN")) c->fuse_down = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_FUSE_OPROJ")) c->fuse_oproj = e[0] != '\0' ? std::max(0, atoi(e)) : -1;
+  if (const char* e = std::getenv("FDLLM_QKV_ROPE")) c->qkv_rope = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_DOWN_SPLIT")) c->down_split = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_MM_TARGET_WGS")) c->mm.target_wgs = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_MM_MIN_STAGES")) c->mm.min_stages = std::max(1, atoi(e));

@@ -192,6 +192,9 @@ using WrBig = WrCfg<8, 4, FD_WR_DEPTH>;  // 128 x 256
 using WrSmall = WrCfg<4, 2, FD_WR_SMALL_DEPTH>;  // 64 x 128
 using WrMid = WrCfg<8, 2, 6>;    // 128 x 128 (six stages: 56 KB of LDS)
 using WrTiny = WrCfg<4, 1, 12>;  // 64 x 64 (4 MFMAs per k step and wave: twelve stages in flight)
+// (qkv with RoPE in the epilogue exchanges rotation partners between waves through the stage buffers)
+static_assert(WrTiny::lds >= (size_t)4 * 1 * 4 * 64 * 8 && WrSmall::lds >= (size_t)4 * 2 * 4 * 64 * 8,
+              "the RoPE exchange fits the stage buffers");
 // 128 x 192 (o_proj / down from the register-weight thresholds: 1536 columns make 8 column blocks, so
 // 64 row blocks of 8192 rows fill 512 slots, two per compute unit, where the 128 x 256 blocks' 384
 // leave half the units with one)
@@ -480,11 +483,18 @@ bool gemm_takes_blocks(const GemmPlan& p) {
   return p.kind == GK_MM && p.mm_id >= MM_WT;
 }
 
+// (the 64-row blocks only: on the 128 x 256 blocks, which have no registers left to request the table
+// early, the 8192-row prefill took 30.30 against 30.16 ms with the separate pass)
+bool gemm_ropes_in_epilogue(int cfg, const GemmPlan& p) {
+  return cfg == CFG_QKV && p.kind == GK_MM && p.ksplit == 1 && (p.mm_id == MM_WR_T || p.mm_id == MM_WR_S);
+}
+
 hipError_t launch_gemm(int dt, int cfg, const GemmP& a, const GemmPlan& p, hipStream_t st) {
   if (a.part_rows && (p.kind != GK_MM || a.N % 4)) return hipErrorInvalidValue;
   if ((a.xfrag == 1 || a.yfrag == 1) && !gemm_takes_frag(cfg, p)) return hipErrorInvalidValue;
   if ((a.xfrag == 2 || a.yfrag == 2) && !gemm_takes_blocks(p)) return hipErrorInvalidValue;
   if (a.yfrag == 2 && cfg != CFG_GATE_UP) return hipErrorInvalidValue;
+  if (a.ro.rope != nullptr && !(gemm_ropes_in_epilogue(cfg, p) && a.ntiles % 8 == 0 && a.ro.rows > 0)) return hipErrorInvalidValue;
   // a k split summed inside the launch: only the register-fragment body does it
   if (a.gw.cnt != nullptr && !(gemm_takes_frag(cfg, p) && p.ksplit > 1 && os_info(cfg).nt <= 4 && cfg != CFG_GATE_UP))
     return hipErrorInvalidValue;

@@ -185,6 +185,81 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_wt_kernel(GemmP a, int nbm,
 // wave (stages past the last re-read the last), weights first, and the issue is fenced against compiler
 // motion, so "all but the (D - 1) VPS most recent" is exactly "stage st has landed"; the last nst % R
 // stages, after the loop, wait for all.
+// The qkv epilogue with RoPE and the KV append (RopeOut): the block's sums + bias (rbias, requested early
+// with the table entries rcs) rounded to the model dtype (EPI_BIAS), then per element rope_kv_kernel's arithmetic (rope_pairs: lo' = rnd(x1 c) + rnd(-x2 s), hi' =
+// rnd(x2 c) + rnd(x1 s), x1 / x2 the values at dims d and d + 64 of the head, (c, s) the table entry d of
+// the row) and its destinations.  The tiles arrive in perm8 order, so the partner of this wave's tile j is
+// tile j of wave w ^ 1 (two tiles per wave) or w ^ 2 (one), read through the stage buffers (free once the
+// k loop ended).  The same lane holds the same row and the same
+// four dims of both.
+template <int DT, int MF, int TPW>
+__device__ __forceinline__ void wr_qkv_rope(const GemmP& a, const f32x4 (&acc)[TPW][MF], int m0, int tw0, int lane,
+                                            int w, unsigned char* smem, const f32x4 (&rcs)[TPW][MF][2],
+                                            const u32x2 (&rbias)[TPW]) {
+  static_assert(TPW == 1 || TPW == 2, "rotation pairs in two waves of the block");
+  const int lr = lane & 15, lg = lane >> 4;
+  const RopeOut& ro = a.ro;
+  u32x2 x[TPW][MF];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    const float bv[4] = {lo_f32<DT>(rbias[j][0]), hi_f32<DT>(rbias[j][0]), lo_f32<DT>(rbias[j][1]), hi_f32<DT>(rbias[j][1])};
+#pragma unroll
+    for (int f = 0; f < MF; ++f) {
+      u16 out[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) out[i] = from_f32<DT>(acc[j][f][i] + bv[i]);
+      x[j][f] = u32x2{pack2(out[0], out[1]), pack2(out[2], out[3])};
+    }
+  }
+  u32x2 y[TPW][MF];
+  u32x2* xb = reinterpret_cast<u32x2*>(smem);  // [4 waves][TPW][MF][64 lanes]
+  __syncthreads();  // every wave is done reading the stage buffers
+#pragma unroll
+  for (int j = 0; j < TPW; ++j)
+#pragma unroll
+    for (int f = 0; f < MF; ++f) xb[((w * TPW + j) * MF + f) * 64 + lane] = x[j][f];
+  __syncthreads();
+  const int pw = TPW == 2 ? (w ^ 1) : (w ^ 2);
+#pragma unroll
+  for (int j = 0; j < TPW; ++j)
+#pragma unroll
+    for (int f = 0; f < MF; ++f) y[j][f] = xb[((pw * TPW + j) * MF + f) * 64 + lane];
+  const size_t krow = (size_t)ro.nkv * 128;
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    const int t = perm8(tw0 + j);
+    const int hd = t >> 3, dh = 16 * (t & 7) + 4 * lg;  // head; first of the lane's four dims in it
+    const bool lo = dh < 64;
+    const int dl = dh & 63;
+#pragma unroll
+    for (int f = 0; f < MF; ++f) {
+      const int m = m0 + 16 * f + lr;
+      if (m >= a.M || 16 * t >= a.N) continue;
+      const int b = m / ro.rows, rl = m - b * ro.rows;
+      u16* kvrow = nullptr;
+      if (hd >= ro.nq) kvrow = (hd < ro.nq + ro.nkv ? ro.kc : ro.vc) + b * ro.seq_stride + (size_t)(ro.ws[b] + rl) * krow;
+      if (hd >= ro.nq + ro.nkv) {
+        *reinterpret_cast<u32x2*>(kvrow + (hd - ro.nq - ro.nkv) * 128 + dh) = x[j][f];
+        continue;
+      }
+      const f32x4 t0 = rcs[j][f][0], t1 = rcs[j][f][1];
+      const float cs[8] = {t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
+      const u32x2 v1 = lo ? x[j][f] : y[j][f], v2 = lo ? y[j][f] : x[j][f];  // dims dl .., dl + 64 ..
+      const float x1[4] = {lo_f32<DT>(v1[0]), hi_f32<DT>(v1[0]), lo_f32<DT>(v1[1]), hi_f32<DT>(v1[1])};
+      const float x2[4] = {lo_f32<DT>(v2[0]), hi_f32<DT>(v2[0]), lo_f32<DT>(v2[1]), hi_f32<DT>(v2[1])};
+      u16 o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float c = cs[2 * i], sn = cs[2 * i + 1];
+        o[i] = lo ? from_f32<DT>(rnd<DT>(x1[i] * c) + rnd<DT>(-x2[i] * sn))
+                  : from_f32<DT>(rnd<DT>(x2[i] * c) + rnd<DT>(x1[i] * sn));
+      }
+      u16* dst = hd < ro.nq ? ro.q + (size_t)m * ro.nq * 128 + hd * 128 + dh : kvrow + (hd - ro.nq) * 128 + dh;
+      *reinterpret_cast<u32x2*>(dst) = u32x2{pack2(o[0], o[1]), pack2(o[2], o[3])};
+    }
+  }
+}
+
 template <int DT, int EPI, int MF, int TPW, int D>
 // (up to 32 accumulator tiles per wave, two workgroups per compute unit: at most 256 registers per lane,
 // accumulators included; more tiles, one workgroup)
@@ -229,9 +304,12 @@ void gemm_wr_kernel(GemmP a, int nbm, int nbn) {
       xstep[q] = 32;
     }
   }
+  // qkv with RoPE in the epilogue takes its tiles in perm8 order (RopeOut)
+  const bool rope = EPI == EPI_BIAS && a.ro.rope != nullptr;
   const u16* ws[TPW];
 #pragma unroll
-  for (int j = 0; j < TPW; ++j) ws[j] = a.W + ((size_t)min(tw0 + j, tlast) * a.KS + kb) * 512 + 8 * lane;
+  for (int j = 0; j < TPW; ++j)
+    ws[j] = a.W + ((size_t)min(rope ? perm8(tw0 + j) : tw0 + j, tlast) * a.KS + kb) * 512 + 8 * lane;
 
   u32x4 wv[R][TPW];
   auto issue = [&](int st, u32x4 (&dst)[TPW], int buf) {
@@ -250,6 +328,27 @@ void gemm_wr_kernel(GemmP a, int nbm, int nbn) {
   for (int j = 0; j < TPW; ++j)
 #pragma unroll
     for (int f = 0; f < MF; ++f) acc[j][f] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // qkv with RoPE in the epilogue: the table entries and the bias values the epilogue takes, requested
+  // before the pipeline (older than every stage's copies, so stage 0's counted wait covers them)
+  constexpr bool RPRE = EPI == EPI_BIAS && TPW <= 2;
+  f32x4 rcs[RPRE ? TPW : 1][RPRE ? MF : 1][2];
+  u32x2 rbias[RPRE ? TPW : 1];
+  if constexpr (RPRE) {
+    if (rope) {
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) {
+        const int t = perm8(tw0 + j), n = 16 * t + 4 * lg, dl = (16 * (t & 7) + 4 * lg) & 63;
+        rbias[j] = *reinterpret_cast<const u32x2*>(a.bias + min(n, a.N - 4));
+#pragma unroll
+        for (int f = 0; f < MF; ++f) {
+          const float* cs = a.ro.rope + (size_t)min(m0 + 16 * f + lr, mlast) * 128 + 2 * dl;
+          rcs[j][f][0] = *reinterpret_cast<const f32x4*>(cs);
+          rcs[j][f][1] = *reinterpret_cast<const f32x4*>(cs + 4);
+        }
+      }
+    }
+  }
 
 #pragma unroll
   for (int u = 0; u < D; ++u) issue(u, wv[u], u);
@@ -357,6 +456,14 @@ void gemm_wr_kernel(GemmP a, int nbm, int nbn) {
         os_epilogue<DT, EPI, 2, false>(a, v, m0 + 16 * f + lr, tw0 + 2 * p, lg);
       }
   } else {
+    if constexpr (EPI == EPI_BIAS) {
+      if constexpr (RPRE) {
+        if (rope) {
+          wr_qkv_rope<DT, MF, TPW>(a, acc, m0, tw0, lane, w, smem, rcs, rbias);
+          return;
+        }
+      }
+    }
 #pragma unroll
     for (int j = 0; j < TPW; ++j)
 #pragma unroll

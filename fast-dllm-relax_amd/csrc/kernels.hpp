@@ -39,10 +39,26 @@ struct GroupWait {
   int clear;          // counters of the other bank to zero
 };
 
+constexpr int MAX_SEQS = 64;  // sequences of one batched call
+
 // ---- skinny GEMM over packed weights ------------------------------------------------------------
 // Y[M, N] = X[M, K] . W[N, K]^T for M <= 32 per m-chunk (gridDim.z chunks of 32 rows).
 enum Epilogue : int { EPI_BIAS = 0, EPI_RESID = 1, EPI_SILU_PAIR = 2, EPI_LOGITS = 3 };
 enum XForm : int { XF_NONE = 0, XF_RMS = 1 };
+
+// The qkv projection of a call whose attention takes its queries and new keys already RoPE'd (the
+// prefill and batched-sequence kernels, which otherwise start with rope_kv_kernel): its epilogue applies
+// rope_kv_kernel's arithmetic (bias, rounding, RoPE of the q and k heads from the table rope, [rows][64][2])
+// and writes the q heads to q ([rows][nq x 128]) and the k / v heads of row r of sequence b = r / rows to
+// the cache rows ws[b] + r % rows of kc / vc + b seq_stride ([cap][nkv][128]), instead of Y.  The
+// register-weight kernel then takes its 16-column tiles in the order perm8 (each head's tiles 0, 1, 4, 5,
+// 2, 3, 6, 7), so that the two halves of every rotation pair sit in one wave or in two waves of one block.
+struct RopeOut {
+  const float* rope; uint16_t* q; uint16_t* kc; uint16_t* vc;
+  int nq, nkv, rows; long long seq_stride;
+  int ws[MAX_SEQS];
+};
+__host__ __device__ constexpr int perm8(int t) { return (t & ~6) | ((t & 2) << 1) | ((t & 4) >> 1); }
 
 struct GemmP {
   const uint16_t* W; int KS;          // packed weights, k steps (K / 32)
@@ -69,6 +85,7 @@ struct GemmP {
   // one-shot k splits: gw.cnt set, the splits of each tile group are summed inside the launch (the host
   // sets it only when the grid is resident at once); otherwise gemm_os_epilogue_kernel sums them
   GroupWait gw;
+  RopeOut ro;                         // EPI_BIAS (qkv) on the register-weight kernel: ro.rope set, see RopeOut
 };
 
 // Launch configurations (see gemm.hip); the host picks one per projection.
@@ -112,6 +129,8 @@ GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol = Mm
 bool gemm_takes_frag(int cfg, const GemmPlan& p);
 // whether the plan runs the large-M LDS-staged kernel, the only one that takes xfrag 2
 bool gemm_takes_blocks(const GemmPlan& p);
+// whether the qkv plan's kernel applies RoPE in its epilogue when GemmP::ro is set
+bool gemm_ropes_in_epilogue(int cfg, const GemmPlan& p);
 hipError_t launch_gemm(int dt, int cfg, const GemmP& a, const GemmPlan& p, hipStream_t st);
 
 // ---- confidence ---------------------------------------------------------------------------------
@@ -169,7 +188,6 @@ hipError_t launch_resid_norm(int dt, const float* part, int splits, int rows, in
                              int ssq_ld, const uint16_t* w, float eps, uint16_t* y, int yblk, hipStream_t st);
 
 // ---- attention ----------------------------------------------------------------------------------
-constexpr int MAX_SEQS = 64;  // sequences of one batched call
 constexpr int MAX_SEQ_UNITS = 128;      // attn_seq_kernel work units (key splits of the sequences)
 constexpr int SEQ_CNT_MAX = 16384;      // its arrival counters (sequence, kv head, query tile)
 struct AttnP {
@@ -204,9 +222,14 @@ struct AttnP {
   int nunits;
   unsigned* seq_cnt;
   int unit_a[MAX_SEQ_UNITS]; int unit_t[MAX_SEQ_UNITS];
+  // the qkv epilogue has already RoPE'd the queries into out and appended the K/V rows (GemmP::ro): the
+  // launch skips rope_kv_kernel
+  int roped;
 };
 struct AttnPlan { int chunked; int q_tiles_per_wg; int key_groups; int qg; int S; int chunk; };
 AttnPlan attn_plan(int rows, int nq, int nkv, int Lk, int target_wgs);
+// whether launch_attention starts with rope_kv_kernel for a (the batched-sequence and prefill kernels)
+bool attn_takes_roped(const AttnP& a);
 // attn_seq_kernel's units for a batched call (a.nseq, rows, heads, seq_lk and seq_cnt set): each sequence
 // starts as one unit; while fewer than ncu / (nkv x query-tile groups) units exist (one workgroup per
 // compute unit), the sequence with the longest split (lowest index on ties) takes one more split, until

@@ -269,3 +269,66 @@ def test_fused_down_norm_bit_identical(dtype, monkeypatch):
         bf16_parity(what, out["fused"][i].float().cpu().numpy(), out["separate"][i].float().cpu().numpy())
     for vm in vms.values():
         vm.close()
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_qkv_rope_epilogue_bit_identical(dtype, monkeypatch):
+    """Calls whose attention starts with the RoPE / KV-append pass (prefill and forward_hidden from 128 rows,
+    the batched-sequence kernel) have qkv's register-weight epilogue do that pass instead: rope_kv_kernel's
+    arithmetic on the rounded qkv values, with the tiles taken in perm8 order so that both halves of each
+    rotation pair are in one block (64 x 64 blocks up to 512 rows, 64 x 128 below 4096, 128 x 256 above).
+    Hidden states, caches and the batched step must agree bit for bit with the separate pass
+    (FDLLM_QKV_ROPE=0), at ragged row counts too."""
+    from fast_dllm_relax_amd.config import FastDLLMConfig
+    from fast_dllm_relax_amd.params import from_numpy
+    from fast_dllm_relax_amd.vm import HipVM
+    from oracle.model import OracleConfig, random_params, build_prefix_block_attention_bias
+
+    kw = WIDE2
+    params = from_numpy(random_params(OracleConfig(**kw), 14, dtype), FastDLLMConfig(**kw), dtype=dtype)
+    tdt = torch.bfloat16 if dtype == "bfloat16" else torch.float16
+    vms = {}
+    for name, on in (("epilogue", "1"), ("separate", "0")):
+        monkeypatch.setenv("FDLLM_QKV_ROPE", on)
+        vms[name] = HipVM(FastDLLMConfig(**kw), params, dtype=dtype, max_rows=4200)
+        monkeypatch.delenv("FDLLM_QKV_ROPE")
+    rng = np.random.default_rng(37)
+    L, nkv, hd = kw["num_hidden_layers"], kw["num_key_value_heads"], kw["head_dim"]
+    for S in (130, 300, 512, 2080, 4160):
+        log(f"case: forward_hidden {S} rows and build_prefix_cache, {dtype}, RoPE in qkv's epilogue vs rope_kv")
+        ids = torch.tensor(rng.integers(0, kw["vocab_size"] - 1, S), dtype=torch.int32, device="cuda")
+        x = vms["separate"].embed(ids)[None]
+        h = {name: vm.forward_hidden(x, None) for name, vm in vms.items()}
+        caches = {}
+        for name, vm in vms.items():
+            k = torch.zeros((L, 1, S, nkv, hd), dtype=tdt, device="cuda")
+            v = torch.zeros_like(k)
+            vm.build_prefix_cache(x, None, k, v)
+            caches[name] = (k, v)
+        torch.cuda.synchronize()
+        assert torch.isfinite(h["epilogue"].float()).all()
+        np.testing.assert_array_equal(_bits(h["epilogue"]), _bits(h["separate"]), err_msg=f"hidden S={S}")
+        for i, what in enumerate(("K", "V")):
+            np.testing.assert_array_equal(_bits(caches["epilogue"][i]), _bits(caches["separate"][i]),
+                                          err_msg=f"{what} cache S={S}")
+    prefixes = [int(p) for p in 32 * rng.integers(1, 9, 16)]
+    cap = max(prefixes) + 32
+    ids = [rng.integers(0, kw["vocab_size"] - 1, P + 32) for P in prefixes]
+    k0 = torch.zeros((L, 16, cap, nkv, hd), dtype=tdt, device="cuda")
+    v0 = torch.zeros_like(k0)
+    for b, P in enumerate(prefixes):
+        vms["separate"].build_prefix_cache_seq(
+            vms["separate"].embed(torch.tensor(ids[b][:P], dtype=torch.int32, device="cuda"))[None], None, k0, v0, b)
+    out = {}
+    for name, vm in vms.items():
+        log(f"case: batched step of 16 x 32 rows, {dtype}, {name}")
+        k, v = k0.clone(), v0.clone()
+        x = torch.stack([vm.embed(torch.tensor(ids[b][P:], dtype=torch.int32, device="cuda"))
+                         for b, P in enumerate(prefixes)])
+        hf = vm.forward_cached_batch(x, k, v, torch.tensor(prefixes, dtype=torch.int32, device="cuda"), prefixes)
+        torch.cuda.synchronize()
+        out[name] = (hf, k, v)
+    for i, what in enumerate(("batched hidden", "K cache", "V cache")):
+        np.testing.assert_array_equal(_bits(out["epilogue"][i]), _bits(out["separate"][i]), err_msg=what)
+    for vm in vms.values():
+        vm.close()
