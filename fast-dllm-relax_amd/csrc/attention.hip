@@ -122,21 +122,35 @@ static hipError_t launch_prefill_cfg(const AttnP& a, int hpw, hipStream_t st) {
   return hipGetLastError();
 }
 
-// The paired-query-block kernel (all heads of a kv head per workgroup, tiles per wave) for models with
-// 6 query heads per kv head, and its K/V blocks in flight.
+// The paired-query-block kernel for models with 6 query heads per kv head: all heads of a kv head per
+// workgroup (PAIR_TQ tiles per wave) from PAIR_WHOLE_MIN workgroups, below that the heads split over
+// three workgroups (one tile per wave) from PAIR_SPLIT_MIN_BLOCKS query blocks, below that
+// attn_prefill_kernel; and its K/V blocks in flight.  Measured (1.5B bf16 build_prefix_cache, ms; the
+// one-block kernel / split / whole): 512 rows 3.31 / 3.38 / 3.82, 1024 4.95 / 4.89 / 5.58, 2048 8.44 /
+// 8.03 / 9.12, 4096 16.68 / 15.93 / 15.58, 8192 34.2 / 34.3 / 29.4.
 constexpr int PAIR_TQ = 3, PAIR_DEPTH = 3;
+constexpr int PAIR_WHOLE_MIN = 128, PAIR_SPLIT_MIN_BLOCKS = 32;
+
+template <int DT, int MASK, int TQ>
+static hipError_t launch_pair(const AttnP& a, int pairs, int groups, hipStream_t st) {
+  auto kern = attn_prefill_pair_kernel<DT, MASK, TQ, PAIR_DEPTH>;
+  constexpr size_t lds = (size_t)(PAIR_DEPTH + 1) * 2 * 64 * HD * 2;  // K and V of D + 1 key blocks
+  raise_lds(kern, lds);
+  hipLaunchKernelGGL(kern, dim3(pairs, a.nkv, groups), dim3(256), lds, st, a);
+  return hipGetLastError();
+}
 
 template <int DT, int MASK>
 static hipError_t launch_prefill(const AttnP& a, hipStream_t st) {
   if (!a.roped) hipLaunchKernelGGL(rope_kv_kernel<DT>, dim3(a.rows), dim3(128), 0, st, a);
   const int nqb = (a.rows + 31) / 32, grp = a.nq / a.nkv;
   const int pairs = (nqb + 1) / 2;
-  if (grp == 2 * PAIR_TQ && (a.prefill_pair == 2 || (a.prefill_pair == 1 && pairs * a.nkv >= 256))) {
-    auto kern = attn_prefill_pair_kernel<DT, MASK, PAIR_TQ, PAIR_DEPTH>;
-    constexpr size_t lds = (size_t)(PAIR_DEPTH + 1) * 2 * 64 * HD * 2;  // K and V of D + 1 key blocks
-    raise_lds(kern, lds);
-    hipLaunchKernelGGL(kern, dim3(pairs, a.nkv), dim3(256), lds, st, a);
-    return hipGetLastError();
+  if (grp == 2 * PAIR_TQ) {
+    // prefill_pair: 0 off, 1 by size, 2 always all heads per workgroup, 3 always the split form
+    const bool whole = a.prefill_pair == 2 || (a.prefill_pair == 1 && pairs * a.nkv >= PAIR_WHOLE_MIN);
+    const bool split = a.prefill_pair == 3 || (a.prefill_pair == 1 && !whole && nqb >= PAIR_SPLIT_MIN_BLOCKS);
+    if (whole) return launch_pair<DT, MASK, PAIR_TQ>(a, pairs, 1, st);
+    if (split) return launch_pair<DT, MASK, 1>(a, pairs, PAIR_TQ, st);
   }
   int hpw = grp % 2 == 0 && nqb * (grp / 2) * a.nkv >= 1024 ? 2 : 1;
   const int ph = a.prefill_hpw;

@@ -1004,9 +1004,11 @@ __global__ __launch_bounds__(64 * NWQ) void attn_prefill_kernel(AttnP a, int hpw
 // g and the pair of 32-row query blocks nqb - 1 - p and p: under the block-causal mask their key ranges
 // add up to the same number of 64-key blocks for every pair, so with one workgroup per compute unit all
 // finish together (one block per workgroup, as in attn_prefill_kernel, leaves the longest query block
-// alone on its compute unit at the end).  All grp heads of the kv head are in the workgroup (2 grp query
-// tiles, TQ per wave), so each K/V block fetched serves all of them, and a wave reads each K or V
-// fragment from LDS once for its TQ tiles.  Per query the key blocks, their order and every rounding are
+// alone on its compute unit at the end).  The workgroup's 4 TQ query tiles (TQ per wave) are tiles
+// 4 TQ z .. of the kv head's 2 grp (blockIdx.z = z): with TQ = grp / 2 all heads of the kv head are in one
+// workgroup, so each K/V block fetched serves all of them; shorter prefills, with too few pairs to fill
+// the chip, split the heads over 2 grp / (4 TQ) workgroups.  A wave reads each K or V fragment from LDS
+// once for its TQ tiles.  Per query the key blocks, their order and every rounding are
 // those of attn_prefill_kernel, so the results are the same bits.
 //
 // The work is a list of tasks t = (query block, key block): the first block's key blocks, then the
@@ -1034,9 +1036,10 @@ void attn_prefill_pair_kernel(AttnP a) {
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int lr = lane & 15, lg = lane >> 4;
-  const int grp = a.nq / a.nkv;  // = NWQ TQ / 2 (the launcher checks)
+  const int grp = a.nq / a.nkv;  // = NWQ TQ gridDim.z / 2 (the launcher checks)
   const int nqb = (a.rows + 31) / 32;
   const int p = blockIdx.x, g = blockIdx.y;
+  const int tq0 = (int)blockIdx.z * NWQ * TQ;  // the workgroup's first query tile of the kv head
   const int qA = nqb - 1 - p, qB = p;  // qA == qB: the middle block of an odd count, alone
   const int rlast = a.rows - 1;
   const size_t krow = (size_t)a.nkv * HD;
@@ -1051,6 +1054,11 @@ void attn_prefill_pair_kernel(AttnP a) {
   auto kend_blk = [&](int qb) { return kend_of(min(qb * 32 + 31, rlast)); };
   const int keA = kend_blk(qA), keB = kend_blk(qB);
   const int nA = (keA + KBP - 1) / KBP;
+  // this lane's K fragment byte offsets within a buffer: row lr, chunk lg + 4 ds (swizzled; + 4096 bytes
+  // per 16-row score tile)
+  uint32_t koff[4];
+#pragma unroll
+  for (int ds = 0; ds < 4; ++ds) koff[ds] = 2 * (lr * HD + 8 * ((lg + 4 * ds) ^ lr));
   const int T = nA + (qA == qB ? 0 : (keB + KBP - 1) / KBP);
 
   // ---- copies of task t (tasks past the last re-read the last) into buffer t % R: this wave's 1 KB
@@ -1082,7 +1090,7 @@ void attn_prefill_pair_kernel(AttnP a) {
     kend_min = kend_of(q0);
 #pragma unroll
     for (int i = 0; i < TQ; ++i) {
-      const int t = w * TQ + i, hh = t / 2;
+      const int t = tq0 + w * TQ + i, hh = t / 2;
       const int r = min(q0 + 16 * (t % 2) + lr, rlast);
       kend_q[i] = kend_of(r);
       const u16* qp = a.out + (size_t)r * a.nq * HD + (g * grp + hh) * HD + 8 * lg;
@@ -1102,7 +1110,7 @@ void attn_prefill_pair_kernel(AttnP a) {
     const int q0 = qb * 32;
 #pragma unroll
     for (int i = 0; i < TQ; ++i) {
-      const int t = w * TQ + i, hh = t / 2;
+      const int t = tq0 + w * TQ + i, hh = t / 2;
       const int r = q0 + 16 * (t % 2) + lr;
       if (r > rlast) continue;
       const float inv = 1.0f / l_run[i];
@@ -1119,20 +1127,56 @@ void attn_prefill_pair_kernel(AttnP a) {
     const u16* kbuf = lds16 + (size_t)(t % R) * BUFE;
     const u16* vbuf = kbuf + KBP * HD;
     const int k0 = (t < nA ? t : t - nA) * KBP;
-    // S^T = K Q^T: lane holds S^T[key k0 + 16 kt + 4 lg + e][query lr]; K row 16 kt + lr, chunk lg + 4 ds
+    // S^T = K Q^T: lane holds S^T[key k0 + 16 kt + 4 lg + e][query lr]; K row 16 kt + lr, chunk lg + 4 ds.
+    // The four fragments of score tile kt + 1 are requested (asm reads, one wait for the four) before tile
+    // kt's MFMAs, so each wait finds them landed (the compiler's own order read one fragment, waited the
+    // whole LDS latency and issued its TQ MFMAs, sixteen times per block)
     f32x4 s[TQ][4];
+    const uint32_t kbb = lds_addr(kbuf);
+    u32x4 kf0[4], kf1[4];
+    auto rdk = [&](auto ktc, u32x4 (&f)[4]) __attribute__((always_inline)) {
+      constexpr int KT = decltype(ktc)::value;
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
+      for (int ds = 0; ds < 4; ++ds) f[ds] = ds_read16<KT * 4096>(kbb + koff[ds]);
+    };
+    auto mmk = [&](int kt, const u32x4 (&f)[4]) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < TQ; ++i) s[i][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const u16* kp = kbuf + (16 * kt + lr) * HD;
 #pragma unroll
-      for (int ds = 0; ds < 4; ++ds) {
-        const u32x4 kf = *reinterpret_cast<const u32x4*>(kp + 8 * ((lg + 4 * ds) ^ lr));
+      for (int ds = 0; ds < 4; ++ds)
 #pragma unroll
-        for (int i = 0; i < TQ; ++i) s[i][kt] = mfma16<DT>(kf, qf[i][ds], s[i][kt]);
-      }
-    }
+        for (int i = 0; i < TQ; ++i) s[i][kt] = mfma16<DT>(f[ds], qf[i][ds], s[i][kt]);
+    };
+    rdk(std::integral_constant<int, 0>{}, kf0);
+    lds_wait(kf0);
+    rdk(std::integral_constant<int, 1>{}, kf1);
+    mmk(0, kf0);
+    lds_wait(kf1);
+    rdk(std::integral_constant<int, 2>{}, kf0);
+    mmk(1, kf1);
+    lds_wait(kf0);
+    rdk(std::integral_constant<int, 3>{}, kf1);
+    mmk(2, kf0);
+    lds_wait(kf1);
+    mmk(3, kf1);
+    // V^T fragments of k step ks by transposing reads (ds_read_tr16: the builtin would make the compiler
+    // wait for every copy in flight first): this lane supplies key 32 ks + 4 lg + lr / 4 (+ 16 for the
+    // second half), dims 16 dt + 4 (lr % 4) .. + 3.  k step 0's reads are issued here and land during the
+    // softmax; k step 1's during k step 0's MFMAs (both k steps' P.V after each tile's own softmax
+    // measured the same, with 30 more registers)
+    const uint32_t vbase = lds_addr(vbuf);
+    auto rdv = [&](int ks, u32x2 (&vh)[DT16 * 2]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int dt = 0; dt < DT16; ++dt)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const int row = 32 * ks + 16 * hf + 4 * lg + (lr >> 2);
+          const int dim = 16 * dt + 4 * (lr & 3);
+          vh[dt * 2 + hf] = ds_read_tr16(vbase + 2 * (row * HD + 8 * ((dim >> 3) ^ (row & 15)) + (dim & 7)));
+        }
+    };
+    u32x2 vh0[DT16 * 2], vh1[DT16 * 2];
+    rdv(0, vh0);
     u32x4 pb[TQ][2];
     const bool whole = k0 + KBP <= kend_min;  // no key of the block is masked for any query of the block
 #pragma unroll
@@ -1186,30 +1230,20 @@ void attn_prefill_pair_kernel(AttnP a) {
                           pack_f32x2<DT>(s[i][2 * ks + 1][0], s[i][2 * ks + 1][1]),
                           pack_f32x2<DT>(s[i][2 * ks + 1][2], s[i][2 * ks + 1][3])};
     }
-    // O^T += V^T P^T over the block's two 32-key k steps.  Transposing reads (ds_read_tr16: the builtin
-    // would make the compiler wait for every copy in flight first): this lane supplies key
-    // 32 ks + 4 lg + lr / 4 (+ 16 for the second half), dims 16 dt + 4 (lr % 4) .. + 3; one k step's 16
-    // reads, then one wait
-    const uint32_t vbase = lds_addr(vbuf);
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      u32x2 vh[DT16 * 2];
-#pragma unroll
-      for (int dt = 0; dt < DT16; ++dt)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const int row = 32 * ks + 16 * hf + 4 * lg + (lr >> 2);
-          const int dim = 16 * dt + 4 * (lr & 3);
-          vh[dt * 2 + hf] = ds_read_tr16(vbase + 2 * (row * HD + 8 * ((dim >> 3) ^ (row & 15)) + (dim & 7)));
-        }
-      lds_wait(vh);
+    // O^T += V^T P^T over the block's two 32-key k steps
+    auto mmv = [&](int ks, const u32x2 (&vh)[DT16 * 2]) __attribute__((always_inline)) {
 #pragma unroll
       for (int dt = 0; dt < DT16; ++dt) {
         const u32x4 vf = u32x4{vh[2 * dt][0], vh[2 * dt][1], vh[2 * dt + 1][0], vh[2 * dt + 1][1]};
 #pragma unroll
         for (int i = 0; i < TQ; ++i) o[i][dt] = mfma16<DT>(vf, pb[i][ks], o[i][dt]);
       }
-    }
+    };
+    lds_wait(vh0);
+    rdv(1, vh1);
+    mmv(0, vh0);
+    lds_wait(vh1);
+    mmv(1, vh1);
   };
 
   // ---- task t: wait for its copies, free buffer (t - 1) % R, issue task t + D into it, compute.

@@ -98,7 +98,7 @@ struct fdllm_ctx {
   float* rope = nullptr; size_t rope_floats = 0;  // RoPE (cos, sin) table of the current call's rows
   int attn_target = 64;   // attention workgroups aimed for when splitting the keys
   int prefill_hpw = 0;    // query heads per prefill-attention workgroup (0: chosen per launch)
-  int prefill_pair = 1;   // paired-query-block prefill attention (0 off, 1 when it fills the chip, 2 always)
+  int prefill_pair = 1;   // paired-query-block prefill attention (0 off, 1 by size, 2 always all heads, 3 always split)
   int seq_attn = 1;       // batched calls: attn_seq_kernel (0: the chunk kernel with key splits + merge)
   int seq_split = 1;      // attn_seq_kernel splits long sequences' keys over the compute units it leaves idle
   int ncu = 256;          // compute units of the device
@@ -646,7 +646,7 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   (void)hipGetDevice(&c->dev);
   if (const char* e = std::getenv("FDLLM_ATTN_TARGET")) c->attn_target = std::max(1, atoi(e));
   if (const char* e = std::getenv("FDLLM_PREFILL_HPW")) c->prefill_hpw = std::max(0, atoi(e));
-  if (const char* e = std::getenv("FDLLM_PREFILL_PAIR")) c->prefill_pair = std::min(2, std::max(0, atoi(e)));
+  if (const char* e = std::getenv("FDLLM_PREFILL_PAIR")) c->prefill_pair = std::min(3, std::max(0, atoi(e)));
   if (const char* e = std::getenv("FDLLM_SEQ_ATTN")) c->seq_attn = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_FUSE_DOWN")) c->fuse_down = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_FUSE_OPROJ")) c->fuse_oproj = e[0] != '\0' ? std::max(0, atoi(e)) : -1;

@@ -204,7 +204,8 @@ struct AttnP {
   int S, chunk;                       // key splits (gridDim.z), keys per split (multiple of 32)
   int target_wgs;                     // workgroups the plan aims for (attn_plan)
   int prefill_hpw;                    // query heads per workgroup of the prefill kernel (0: chosen per launch)
-  int prefill_pair;                   // paired-query-block prefill kernel: 0 off, 1 when it fills the chip, 2 always
+  int prefill_pair;                   // paired-query-block prefill kernel: 0 off, 1 by size, 2 always all heads per
+                                      // workgroup, 3 always the heads split over workgroups
   int seq_attn;                       // batched calls without a mask: attn_seq_kernel (no key splits) instead of chunks + merge
   float* part;                        // split partials (merged by attn_merge_kernel)
   uint16_t* out;                      // [rows][nq * 128]

@@ -119,11 +119,13 @@ def _prefill_vm(kw, params, dtype, monkeypatch, pair, max_rows):
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
 def test_prefill_pair_kernel_bit_identical(dtype, monkeypatch):
-    """The paired-query-block prefill attention (FDLLM_PREFILL_PAIR=2 forces it at every size; by default
-    it runs once its workgroups fill the chip, from about 8192 rows) against attn_prefill_kernel: the same
-    key blocks in the same order per query, so hidden states and caches agree bit for bit.  Odd and even
-    query-block counts, a ragged last block, the block-causal mask (forward_hidden, build_prefix_cache)
-    and the unmasked form (a cached forward of 200 rows after a prefix)."""
+    """The paired-query-block prefill attention, with all six heads of a kv head per workgroup
+    (FDLLM_PREFILL_PAIR=2 forces it at every size; by default it runs once its workgroups fill the chip,
+    from 4096 rows) and with the heads split over three workgroups (=3 forces it; by default from 32
+    query blocks below that), against attn_prefill_kernel: the same key blocks in the same order per query,
+    so hidden states and caches agree bit for bit.  Odd and even query-block counts, a ragged last block,
+    the block-causal mask (forward_hidden, build_prefix_cache) and the unmasked form (a cached forward of
+    200 rows after a prefix)."""
     from fast_dllm_relax_amd.config import FastDLLMConfig
     from fast_dllm_relax_amd.params import from_numpy
     from oracle.model import OracleConfig, random_params
@@ -132,24 +134,27 @@ def test_prefill_pair_kernel_bit_identical(dtype, monkeypatch):
     tdt = torch.bfloat16 if dtype == "bfloat16" else torch.float16
     params = from_numpy(random_params(OracleConfig(**kw), 6, dtype), FastDLLMConfig(**kw), dtype=dtype)
     vm_pair = _prefill_vm(kw, params, dtype, monkeypatch, 2, 2080)
+    vm_split = _prefill_vm(kw, params, dtype, monkeypatch, 3, 2080)
     vm_old = _prefill_vm(kw, params, dtype, monkeypatch, 0, 2080)
     rng = np.random.default_rng(23)
     for S in (300, 1056, 2080):
-        log(f"case: forward_hidden {S} rows, 1.5B width, 2 layers, {dtype}, paired vs one-block prefill attention")
+        log(f"case: forward_hidden {S} rows, 1.5B width, 2 layers, {dtype}, paired (whole / split) vs one-block")
         ids = torch.tensor(rng.integers(0, kw["vocab_size"] - 1, S), dtype=torch.int32, device="cuda")
         x = vm_old.embed(ids)[None]
         h_old = vm_old.forward_hidden(x, None)
         h_pair = vm_pair.forward_hidden(x, None)
+        h_split = vm_split.forward_hidden(x, None)
         torch.cuda.synchronize()
         assert torch.isfinite(h_pair.float()).all()
         np.testing.assert_array_equal(_bits(h_pair), _bits(h_old), err_msg=f"forward_hidden S={S}")
+        np.testing.assert_array_equal(_bits(h_split), _bits(h_old), err_msg=f"forward_hidden S={S}, split")
 
     P, R = 1000, 200
     L, nkv, hd = kw["num_hidden_layers"], kw["num_key_value_heads"], kw["head_dim"]
     log(f"case: build_prefix_cache {P} rows + forward_cached {R} rows, {dtype}, paired vs one-block")
     ids = torch.tensor(rng.integers(0, kw["vocab_size"] - 1, P + R), dtype=torch.int32, device="cuda")
     caches = {}
-    for name, vm in (("pair", vm_pair), ("old", vm_old)):
+    for name, vm in (("pair", vm_pair), ("split", vm_split), ("old", vm_old)):
         k = torch.zeros((L, 1, P + R + 32, nkv, hd), dtype=tdt, device="cuda")
         v = torch.zeros_like(k)
         vm.build_prefix_cache(vm.embed(ids[:P])[None], None, k, v)
@@ -159,6 +164,7 @@ def test_prefill_pair_kernel_bit_identical(dtype, monkeypatch):
         caches[name] = (k, v, h)
     for i, what in enumerate(("k cache", "v cache", "cached-forward hidden")):
         np.testing.assert_array_equal(_bits(caches["pair"][i]), _bits(caches["old"][i]), err_msg=what)
+        np.testing.assert_array_equal(_bits(caches["split"][i]), _bits(caches["old"][i]), err_msg=f"{what}, split")
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
