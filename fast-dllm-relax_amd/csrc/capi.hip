@@ -756,8 +756,12 @@ const char* fdllm_param_name(const fdllm_ctx* c, int i) {
 int fdllm_bind_weights(fdllm_ctx* c, const void* const* ptrs, int n) {
   if (!c || !ptrs) return fail(FDLLM_EINVAL, "null argument");
   if (n != (int)c->names.size()) return fail(FDLLM_EINVAL, "expected %d params, got %d", (int)c->names.size(), n);
-  for (int i = 0; i < n; ++i)
+  for (int i = 0; i < n; ++i) {
     if (!ptrs[i]) return fail(FDLLM_EINVAL, "param %d (%s) is null", i, c->names[i].c_str());
+    // the kernels read norm weights, biases and embedding rows with 16-byte loads
+    if ((uintptr_t)ptrs[i] % 16)
+      return fail(FDLLM_EINVAL, "param %d (%s) is not 16-byte aligned", i, c->names[i].c_str());
+  }
   c->params.assign((const uint16_t* const*)ptrs, (const uint16_t* const*)ptrs + n);
   c->embed = c->params[0];
   c->layers.resize(c->cfg.num_hidden_layers);

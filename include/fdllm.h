@@ -65,7 +65,8 @@ int fdllm_num_params(const fdllm_ctx* ctx);
 const char* fdllm_param_name(const fdllm_ctx* ctx, int index);
 
 /* Binds the packed `params` list (cuda.py:807, "param_mode": "packed"): n device pointers in
- * fdllm_param_name order.  The caller keeps them alive while the context uses them. */
+ * fdllm_param_name order, each 16-byte aligned (FDLLM_EINVAL otherwise).  The caller keeps them alive
+ * while the context uses them. */
 int fdllm_bind_weights(fdllm_ctx* ctx, const void* const* ptrs, int n);
 
 /* embed (cuda.py:698-699): ids [seq_len] int32 -> out [seq_len, hidden]. */

@@ -138,6 +138,27 @@ def test_write_window_errors(tiny):
         vm.forward_block_partial_rp24(xs, k, v, _off(56), 40)
 
 
+def test_bind_rejects_misaligned_params(tiny):
+    """fdllm_bind_weights checks that every parameter is 16-byte aligned (the kernels read norm weights,
+    biases and embedding rows in 16-byte units): a 2-byte-offset view is rejected with FDLLM_EINVAL, and
+    the context keeps the weights it had (its logits are unchanged)."""
+    _, vm = tiny
+    ids = _dev_ids(np.arange(32) % (TINY["vocab_size"] - 1))
+    h = vm.embed(ids)[None]
+    before = vm.get_logits(h).float().cpu()
+    params = list(vm.params)
+    i = 2  # a norm weight
+    shifted = torch.empty(params[i].numel() + 1, dtype=params[i].dtype, device="cuda")[1:].view_as(params[i])
+    shifted.copy_(params[i])
+    bad = params[:i] + [shifted] + params[i + 1:]
+    log("case: bind with a 2-byte-offset parameter")
+    with pytest.raises(ValueError, match="not 16-byte aligned"):
+        vm.bind(bad)
+    vm.params = params
+    after = vm.get_logits(h).float().cpu()
+    assert torch.equal(before, after)
+
+
 def test_confidence_bit_exact_given_logits(tiny):
     ref, vm = tiny
     rng = np.random.default_rng(5)
