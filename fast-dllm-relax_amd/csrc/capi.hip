@@ -2,6 +2,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <initializer_list>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -522,6 +523,15 @@ int run_layers(fdllm_ctx* c, const void* x_in, int rows, uint16_t* kbase, uint16
   return FDLLM_OK;
 }
 
+// Activations, caches and logits are read and written in 16-byte units (the caches also by 16-byte
+// global-to-LDS copies): such a tensor argument that is not 16-byte aligned is refused.
+int check_aligned(std::initializer_list<const void*> ps) {
+  for (const void* p : ps)
+    if (p != nullptr && (uintptr_t)p % 16)
+      return fail(FDLLM_EINVAL, "tensor arguments (activations, caches, logits) must be 16-byte aligned");
+  return FDLLM_OK;
+}
+
 int check_ready(const fdllm_ctx* c) {
   if (!c) return fail(FDLLM_EINVAL, "null context");
   if (!c->bound) return fail(FDLLM_ESTATE, "weights are not bound (fdllm_bind_weights)");
@@ -543,6 +553,8 @@ int cached_step(fdllm_ctx* c, const void* x, int rows, void* k, void* v, int cap
   rc = pending_wait_fault(c);
   if (rc) return rc;
   if (!x || !k || !v || !off || !out) return fail(FDLLM_EINVAL, "null tensor argument");
+  rc = check_aligned({x, k, v, out});
+  if (rc) return rc;
   if (rows <= 0) return fail(FDLLM_EINVAL, "active rows must be positive, got %d", rows);
   int64_t write_start = prefix_len + write_rel, attend_len = prefix_len + attend_rel;
   // fast_dllm.attn_inplace guard (runtime.py:69-70) and the write-window check (runtime.py:56-57)
@@ -572,6 +584,8 @@ int cached_step_batch(fdllm_ctx* c, const void* x, int nseq, int rows, void* k, 
   rc = pending_wait_fault(c);
   if (rc) return rc;
   if (!x || !k || !v || !off || !prefix_lens || !out) return fail(FDLLM_EINVAL, "null tensor argument");
+  rc = check_aligned({x, k, v, out});
+  if (rc) return rc;
   if (nseq <= 0 || nseq > MAX_SEQS) return fail(FDLLM_EINVAL, "batch of %d sequences (1 .. %d supported)", nseq, MAX_SEQS);
   if (rows <= 0) return fail(FDLLM_EINVAL, "active rows must be positive, got %d", rows);
   const fdllm_config& f = c->cfg;
@@ -794,6 +808,8 @@ int fdllm_forward_hidden(fdllm_ctx* c, const void* x, int S, const float* bias, 
   if (rc) return rc;
   if (S <= 0) return fail(FDLLM_EINVAL, "seq_len must be positive, got %d", S);
   if (!x || !out) return fail(FDLLM_EINVAL, "null tensor argument");
+  rc = check_aligned({x, out});
+  if (rc) return rc;
   rc = ensure_rows(c, S);
   if (rc) return rc;
   return run_layers(c, x, S, c->kscr, c->vscr, 0, 0, c->zero_i32, S, bias ? 2 : 1, bias, S, out, (hipStream_t)stream);
@@ -805,6 +821,8 @@ int fdllm_get_logits(fdllm_ctx* c, const void* hidden, int rows, float* logits, 
   rc = pending_wait_fault(c);
   if (rc) return rc;
   if (rows <= 0 || !hidden || !logits) return fail(FDLLM_EINVAL, "invalid get_logits arguments");
+  rc = check_aligned({hidden, logits});
+  if (rc) return rc;
   return run_lm_head(c, (const uint16_t*)hidden, rows, logits, false, (hipStream_t)stream);
 }
 
@@ -815,6 +833,8 @@ int fdllm_build_prefix_cache(fdllm_ctx* c, const void* x, int P, const float* bi
   rc = pending_wait_fault(c);
   if (rc) return rc;
   if (P <= 0 || !x || !k || !v) return fail(FDLLM_EINVAL, "invalid build_prefix_cache arguments");
+  rc = check_aligned({x, k, v});
+  if (rc) return rc;
   if (P > cap) return fail(FDLLM_EINVAL, "KV write [0, %d) outside cache capacity %d", P, cap);
   rc = ensure_rows(c, P);
   if (rc) return rc;
@@ -953,6 +973,8 @@ int fdllm_build_prefix_cache_seq(fdllm_ctx* c, const void* x, int P, const float
   rc = pending_wait_fault(c);
   if (rc) return rc;
   if (P <= 0 || !x || !k || !v) return fail(FDLLM_EINVAL, "invalid build_prefix_cache arguments");
+  rc = check_aligned({x, k, v});
+  if (rc) return rc;
   if (nseq <= 0 || seq < 0 || seq >= nseq) return fail(FDLLM_EINVAL, "sequence %d of a batch of %d", seq, nseq);
   if (P > cap) return fail(FDLLM_EINVAL, "KV write [0, %d) outside cache capacity %d", P, cap);
   rc = ensure_rows(c, P);
@@ -972,6 +994,8 @@ int fdllm_get_confidence(fdllm_ctx* c, const void* hidden, int rows, int32_t* id
   rc = pending_wait_fault(c);
   if (rc) return rc;
   if (rows <= 0 || !hidden || !ids || !maxp) return fail(FDLLM_EINVAL, "invalid get_confidence arguments");
+  rc = check_aligned({hidden, logits});
+  if (rc) return rc;
   rc = ensure_stats(c, rows);
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
@@ -1029,6 +1053,8 @@ int fdllm_get_confidence_unmask(fdllm_ctx* c, const void* hidden, int rows, int 
   rc = pending_wait_fault(c);
   if (rc) return rc;
   if (!hidden) return fail(FDLLM_EINVAL, "null hidden states");
+  rc = check_aligned({hidden});
+  if (rc) return rc;
   if ((ids == nullptr) != (maxp == nullptr)) return fail(FDLLM_EINVAL, "ids and maxp must both be given or both be null");
   rc = check_unmask(c, rows, row0, block, s0, sub_rows, threshold);
   if (rc) return rc;

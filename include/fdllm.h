@@ -9,7 +9,9 @@
  * Conventions
  *   - All pointers are device pointers unless stated; `stream` is a hipStream_t (NULL = default).
  *   - Activations/weights/caches are in the context's dtype (bf16 or fp16, 2-byte elements);
- *     logits are fp32; token ids are int32.
+ *     logits are fp32; token ids are int32.  Weights, activations, caches and logits must be
+ *     16-byte aligned (FDLLM_EINVAL otherwise); id, offset and bias arrays need only their
+ *     element alignment.
  *   - KV caches: [num_layers, 1, cap, num_kv_heads, head_dim] rows (contract "inplace_bsnh_v1",
  *     export_utils.py:21-34).
  *   - Return value: 0 on success; FDLLM_EINVAL for a rejected argument (the reference raises

@@ -138,10 +138,11 @@ def test_write_window_errors(tiny):
         vm.forward_block_partial_rp24(xs, k, v, _off(56), 40)
 
 
-def test_bind_rejects_misaligned_params(tiny):
+def test_misaligned_arguments_rejected(tiny):
     """fdllm_bind_weights checks that every parameter is 16-byte aligned (the kernels read norm weights,
     biases and embedding rows in 16-byte units): a 2-byte-offset view is rejected with FDLLM_EINVAL, and
-    the context keeps the weights it had (its logits are unchanged)."""
+    the context keeps the weights it had (its logits are unchanged).  The entry points that take
+    activations, caches or logits refuse such views the same way."""
     _, vm = tiny
     ids = _dev_ids(np.arange(32) % (TINY["vocab_size"] - 1))
     h = vm.embed(ids)[None]
@@ -157,6 +158,15 @@ def test_bind_rejects_misaligned_params(tiny):
     vm.params = params
     after = vm.get_logits(h).float().cpu()
     assert torch.equal(before, after)
+    log("case: forward_hidden / forward_cached with a 2-byte-offset activation view")
+    xs = torch.empty(h.numel() + 1, dtype=h.dtype, device="cuda")[1:].view_as(h)
+    xs.copy_(h)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        vm.forward_hidden(xs, None)
+    k = torch.zeros((2, 1, 64, 2, 128), dtype=torch.bfloat16, device="cuda")
+    v = torch.zeros_like(k)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        vm.forward_cached(xs, k, v, _off(0), 0)
 
 
 def test_confidence_bit_exact_given_logits(tiny):
