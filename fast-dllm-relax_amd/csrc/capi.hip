@@ -229,7 +229,7 @@ int run_gemm(fdllm_ctx* c, int cfg, GemmP a, int ksplit, hipStream_t st) {
     a.nw = nullptr;
     a.xfrag = blocks ? 2 : 0;
   }
-  if (pl.ksplit > 1) {
+  if (pl.ksplit > 1 || pl.tail_split > 1) {
     int rc = ensure_floats(&c->gpart, &c->gpart_floats, pl.part_floats);
     if (rc) return rc;
     if (pl.groups * pl.mchunks > c->n_counters)
@@ -704,6 +704,8 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->dev) == hipSuccess && cus > 0) c->ncu = cus;
     else (void)hipGetLastError();
+    c->mm.lm_tail_cus = c->ncu;
+    if (const char* e = std::getenv("FDLLM_LM_TAIL")) c->mm.lm_tail_cus = atoi(e) != 0 ? c->ncu : 0;
   }
   {
     // this device's copy of the allocation-free step's scratch array, found once per device

@@ -326,6 +326,24 @@ GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol) {
   p.groups = (a.ntiles + tiles - 1) / tiles;
   p.part_floats = p.ksplit > 1 ? (size_t)p.groups * p.mchunks * p.ksplit * tiles * 2 * 64 * 4 : 0;
   a.ngroups = p.groups;
+  // The lm_head's 256-column groups stream 768 KB of weights each (1.5B: 594 groups).  On 256 compute units
+  // whole rounds give every unit two and the last 82 units a third, which sets the launch time; split over
+  // three workgroups in k, those 82 groups add a third of a group to 246 units instead (measured at 32 rows:
+  // 512 groups alone 76 us, all 594 98 us).  The splits meet in the last arriver, which adds them in split
+  // order and runs the epilogue.
+  a.tail_full = a.tail_split = 0;
+  if (cfg == CFG_LM_HEAD && p.kind == GK_STREAM && p.ksplit == 1 && p.mchunks == 1 && pol.lm_tail_cus > 0) {
+    const int full = p.groups / pol.lm_tail_cus * pol.lm_tail_cus, rem = p.groups - full;
+    int s = rem > 0 ? std::min(3, pol.lm_tail_cus / rem) : 0;
+    while (s > 1 && a.KS % s != 0) --s;
+    if (s > 1) {
+      a.tail_full = full;
+      a.tail_split = s;
+      p.part_floats = (size_t)rem * s * tiles * 2 * 64 * 4;
+    }
+  }
+  p.tail_full = a.tail_full;
+  p.tail_split = a.tail_split;
   return p;
 }
 
@@ -335,7 +353,8 @@ static hipError_t launch_cfg(const GemmP& a, const GemmPlan& p, hipStream_t st) 
   if (C::kw > 1) lds = (size_t)(C::kw - 1) * C::tw * C::tpw * MT * 64 * 16;
   if (C::epi == EPI_LOGITS) lds = (size_t)32 * 256 * 4;
   auto kern = gemm_pk_kernel<DT, C::epi, C::xf, MT, C::tpw, C::tw, C::kw, C::u>;
-  hipLaunchKernelGGL(kern, dim3(p.groups, p.ksplit, p.mchunks), dim3(64 * C::tw * C::kw), lds, st, a);
+  const int gx = p.tail_split > 1 ? p.tail_full + (p.groups - p.tail_full) * p.tail_split : p.groups;
+  hipLaunchKernelGGL(kern, dim3(gx, p.ksplit, p.mchunks), dim3(64 * C::tw * C::kw), lds, st, a);
   return hipGetLastError();
 }
 

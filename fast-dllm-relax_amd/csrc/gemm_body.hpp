@@ -160,9 +160,24 @@ __global__ __launch_bounds__(64 * TW * KW) void gemm_pk_kernel(GemmP a) {
   const int tw = w % TW, kw = w / TW;
   const int lr = lane & 15, lg = lane >> 4;
   const int m0 = blockIdx.z * 32;
-  const int t0 = (blockIdx.x * TW + tw) * TPW;
-  const int kq = a.kps / KW, kr = a.kps % KW;
-  const int wb = blockIdx.y * a.kps + kw * kq + min(kw, kr);
+  // the workgroup's column group bx and k split by of ny: (blockIdx.x, blockIdx.y) of gridDim.y, except in
+  // a tail split, where workgroups tail_full + j take column group tail_full + j / tail_split, split
+  // j % tail_split of the k steps
+  int bx = blockIdx.x, by = blockIdx.y, ny = gridDim.y, kps = a.kps;
+  if (a.tail_split > 1 && bx >= a.tail_full) {
+    const int j = bx - a.tail_full;
+    bx = a.tail_full + j / a.tail_split;
+    by = j % a.tail_split;
+    ny = a.tail_split;
+    kps = a.KS / a.tail_split;
+    // its compute unit also runs two whole groups: ahead of them in issue, a split finishes its third of
+    // the k steps early and its hand-off and epilogue run while they stream, off the launch's critical
+    // path (at equal priority all three finish together and the last arriver's hand-off comes last)
+    __builtin_amdgcn_s_setprio(2);
+  }
+  const int t0 = (bx * TW + tw) * TPW;
+  const int kq = kps / KW, kr = kps % KW;
+  const int wb = by * kps + kw * kq + min(kw, kr);
   const int wn = kq + (kw < kr ? 1 : 0);
 
   // Every load below is unconditional and in bounds, so the compiler can count outstanding loads
@@ -285,36 +300,38 @@ __global__ __launch_bounds__(64 * TW * KW) void gemm_pk_kernel(GemmP a) {
     }
   }
 
-  // ---- cross-workgroup k splits: the last arriver adds them in split order ----
-  if (gridDim.y > 1) {
-    const size_t grp = (size_t)blockIdx.z * gridDim.x + blockIdx.x;
-    const size_t per = (size_t)TW * TPW * MT * 64;
-    f32x4* part = reinterpret_cast<f32x4*>(a.part) + grp * gridDim.y * per;
+  // ---- cross-workgroup k splits: the last arriver adds them in split order (its own from registers) ----
+  if (ny > 1) {
+    const size_t grp = (size_t)blockIdx.z * a.ngroups + bx;
+    // the partials of the tail's groups only (tail_split: one row chunk), or of every group
+    const size_t pgrp = a.tail_split > 1 ? (size_t)(bx - a.tail_full) : grp;
+    constexpr unsigned per = TW * TPW * MT * 64;  // f32x4 per split partial
+    const CohBuf pb = coh_buf(reinterpret_cast<f32x4*>(a.part) + pgrp * ny * per, (unsigned)ny * per * 16u);
     if (kw == 0) {
 #pragma unroll
       for (int j = 0; j < TPW; ++j)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
-          st_agent4(part + blockIdx.y * per + ((tw * TPW + j) * MT + mt) * 64 + lane, acc[j][mt]);
+          coh_stf4(pb, ((unsigned)by * per + ((tw * TPW + j) * MT + mt) * 64 + lane) * 16u, acc[j][mt]);
     }
-    if (!arrive_last(a.counters + grp, gridDim.y, &flag_s)) return;
+    if (!arrive_last(a.counters + grp, ny, &flag_s)) return;
     if (kw == 0) {
-      // every split's partial is requested before any is added (one memory round trip per 16 splits)
+      // every other split's partial is requested before any is added (one memory round trip per 16 splits)
       constexpr int SB = 16;
 #pragma unroll
       for (int j = 0; j < TPW; ++j)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          const size_t o = ((tw * TPW + j) * MT + mt) * 64 + lane;
+          const unsigned o = (((tw * TPW + j) * MT + mt) * 64 + lane) * 16u;
           f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
-          for (int y0 = 0; y0 < (int)gridDim.y; y0 += SB) {
+          for (int y0 = 0; y0 < ny; y0 += SB) {
             f32x4 v[SB];
 #pragma unroll
             for (int q = 0; q < SB; ++q)
-              v[q] = y0 + q < (int)gridDim.y ? ld_agent4(part + (y0 + q) * per + o) : f32x4{0.f, 0.f, 0.f, 0.f};
+              v[q] = y0 + q < ny && y0 + q != by ? coh_ldf4(pb, (unsigned)(y0 + q) * per * 16u + o) : acc[j][mt];
 #pragma unroll
             for (int q = 0; q < SB; ++q)
-              if (y0 + q < (int)gridDim.y) s = (y0 + q == 0) ? v[q] : s + v[q];
+              if (y0 + q < ny) s = (y0 + q == 0) ? v[q] : s + v[q];
           }
           acc[j][mt] = s;
         }
@@ -331,7 +348,7 @@ __global__ __launch_bounds__(64 * TW * KW) void gemm_pk_kernel(GemmP a) {
       for (int mt = 0; mt < MT; ++mt) {
         const int m = 16 * mt + lr;
         const int nl = 16 * (tw * TPW + j) + 4 * lg;
-        const int n = blockIdx.x * 256 + nl;
+        const int n = bx * 256 + nl;
         float v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = rnd<DT>(acc[j][mt][i]);
@@ -349,7 +366,7 @@ __global__ __launch_bounds__(64 * TW * KW) void gemm_pk_kernel(GemmP a) {
       }
     if (a.stat_m == nullptr) return;
     __syncthreads();
-    logits_tile_stats<DT, 16 * MT, TW * KW>(a, tile, m0, (int)blockIdx.x, w, lane);
+    logits_tile_stats<DT, 16 * MT, TW * KW>(a, tile, m0, bx, w, lane);
   } else if constexpr (EPI == EPI_SILU_PAIR) {
     if (kw != 0) return;
     const int p = t0 / 2;  // tiles t0 (gate) and t0 + 1 (up) of pair p

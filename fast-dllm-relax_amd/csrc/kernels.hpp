@@ -74,7 +74,10 @@ struct GemmP {
   float* logits; int ldl;             // EPI_LOGITS (optional)
   float* stat_m; int32_t* stat_a; float* stat_s; int stat_tiles;  // EPI_LOGITS confidence statistics
   float* part; unsigned* counters;    // cross-workgroup split partials / arrival counters
-  int ngroups;                        // tile groups of the one-shot launch (its gridDim.x)
+  int ngroups;                        // tile groups of the one-shot and streaming launches
+  // streaming kernel, one gridDim.y: column groups tail_full .. ngroups - 1 each split k tail_split ways
+  // over workgroups tail_full + tail_split (group - tail_full) + split (tail_split <= 1: no tail split)
+  int tail_full, tail_split;
   // 1: one-shot chains (M <= 32, the register-fragment body only): X, and Y of EPI_RESID /
   // EPI_SILU_PAIR, in MFMA-fragment order (frag_off) instead of row-major; 2: X, and the Y of
   // EPI_SILU_PAIR, in the large-M LDS-staged kernel's fragment blocks (frag_blk_off)
@@ -104,6 +107,7 @@ enum GemmKind : int { GK_STREAM = 0, GK_ONESHOT = 1, GK_MM = 2 };
 struct GemmPlan {
   int kind; int ksplit; int tiles_per_wg; int groups; int mchunks; size_t part_floats;
   int mm_id; int nbm; int nbn;
+  int tail_full, tail_split;  // GK_STREAM: see GemmP (set in both)
 };
 // How large-M launches are planned.  target_wgs / min_stages: k is split only while the launch has fewer
 // than target_wgs workgroups, and only into splits of at least min_stages stages.  wr_ops: the
@@ -123,6 +127,10 @@ struct MmPolicy {
   int wr3 = 1;          // o_proj / down at the register-weight thresholds: 128 x 192 blocks (0: 128 x 256)
   int wt8 = 1;  // LDS-staged 128 x 192 blocks of eight waves (bit 0 gate_up, bit 1 down) instead of four
   int wt256 = 512;  // gate_up from 257 up to this many rows on LDS-staged 256 x 192 blocks of eight waves
+  // the streaming lm_head of up to 32 rows: the column groups past the last whole round over this many
+  // compute units (one group per unit per round) split k up to 3 ways, so that every unit streams about
+  // the same bytes (0: off)
+  int lm_tail_cus = 0;
 };
 GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol = MmPolicy{});
 // whether the plan runs the one-shot register-fragment body, the only one that takes xfrag / yfrag 1

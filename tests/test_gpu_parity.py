@@ -241,6 +241,55 @@ def test_wide_cached_step_and_logits(wide2):
 
 
 
+def test_lm_head_tail_split(wide2, monkeypatch):
+    """The lm_head of up to 32 rows runs its 256-column groups in whole rounds of one per compute unit and
+    splits the groups past the last round three ways in k (1.5B: 82 of 594 groups on 256 units).  The
+    other groups' logits are the unsplit kernel's bits; the split groups' differ only by the fp32 order
+    of the three partial sums, so an entry can move to the neighbouring bf16 value, and few do.  The
+    confidence stays bit-exact given the logits."""
+    from fast_dllm_relax_amd.config import FastDLLMConfig
+    from fast_dllm_relax_amd.params import from_numpy
+    from fast_dllm_relax_amd.vm import HipVM
+
+    ref, vm = wide2
+    cfg = FastDLLMConfig(**WIDE2)
+    monkeypatch.setenv("FDLLM_LM_TAIL", "0")
+    vm_off = HipVM(cfg, from_numpy(ref.p, cfg, dtype="bfloat16"), dtype="bfloat16", max_rows=64)
+    monkeypatch.delenv("FDLLM_LM_TAIL")
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
+    groups = -(-WIDE2["vocab_size"] // 256)
+    c0 = groups // ncu * ncu * 256  # first column of the split groups
+    assert 0 < c0 < WIDE2["vocab_size"]
+    g = torch.Generator(device="cuda").manual_seed(13)
+    try:
+        for rows in (32, 17, 8, 1):
+            log(f"case: lm_head tail split, {rows} rows, split from column {c0}")
+            h = (torch.randn((1, rows, WIDE2["hidden_size"]), generator=g, device="cuda") * 2).to(torch.bfloat16)
+            lg = to_np(vm.get_logits(h))
+            lg0 = to_np(vm_off.get_logits(h))
+            np.testing.assert_array_equal(lg[..., :c0], lg0[..., :c0])
+            d = np.abs(lg[..., c0:] - lg0[..., c0:])
+            moved = float(np.mean(d > 0))
+            log(f"  split groups: {moved:.2e} of the entries moved, max |d| {d.max():.3g}")
+            # a moved entry is the neighbouring bf16 value, or, where the sum cancels to near zero, within
+            # the fp32 sums' own error
+            u1 = (lg[..., c0:].view(np.uint32) >> 16).astype(np.int64)
+            u0 = (lg0[..., c0:].view(np.uint32) >> 16).astype(np.int64)
+            adjacent = ((u1 >> 15) == (u0 >> 15)) & (np.abs(u1 - u0) <= 1)
+            assert np.all(adjacent | (d <= 1e-4)), "moved by more than one bf16 step"
+            assert moved < 1e-2
+            if rows == 32:
+                assert moved > 0, "the split groups gave the unsplit bits everywhere: was the split taken?"
+            logits = torch.empty((1, rows, WIDE2["vocab_size"]), dtype=torch.float32, device="cuda")
+            ids, maxp = vm.get_confidence(h, logits=logits)
+            np.testing.assert_array_equal(to_np(logits), lg)
+            wid, wp = oconf.confidence(lg[0])
+            np.testing.assert_array_equal(ids.cpu().numpy()[0], wid)
+            np.testing.assert_array_equal(maxp.cpu().numpy()[0].view(np.uint32), wp.view(np.uint32))
+    finally:
+        vm_off.close()
+
+
 def test_wide_forward_hidden_large_m(wide2):
     """Large-M projections (the MFMA block kernel) at the 1.5B layer shapes: a stateless block-causal
     forward over 160 rows (64-row blocks with k splits) and 1056 rows (128-row blocks, ragged last
