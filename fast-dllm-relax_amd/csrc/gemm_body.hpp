@@ -52,6 +52,18 @@ template <int DT, int XF>
 __device__ __forceinline__ u32x4 xform(u32x4 raw, u32x4 wv, float inv) {
   if constexpr (XF == XF_NONE) {
     return raw;
+  } else if constexpr (DT == DT_BF16) {
+    // the same two roundings per value as below, each pair rounded by one packed conversion and the
+    // products unpacked by a shift and a mask (the per-value form took 15 instructions per pair, this
+    // one 10: one-shot qkv and gate_up transform every activation of the call in each workgroup)
+    u32x4 o;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t r = pack_f32x2<DT>(__uint_as_float(raw[c] << 16) * inv, __uint_as_float(raw[c] & 0xffff0000u) * inv);
+      o[c] = pack_f32x2<DT>(__uint_as_float(wv[c] << 16) * __uint_as_float(r << 16),
+                            __uint_as_float(wv[c] & 0xffff0000u) * __uint_as_float(r & 0xffff0000u));
+    }
+    return o;
   } else {
     u32x4 o;
 #pragma unroll
