@@ -661,19 +661,24 @@ __device__ __forceinline__ void gemm_os_direct_body(const GemmP& a, int bx, int 
 
   // A wave may have at most 63 loads outstanding, and a load waits for every older one.  With the norm
   // transform the activation path (KPW x MT fragments, 12 sums-of-squares loads, one norm-weight chunk)
-  // goes first: it is short enough that the weight slice (gate_up's 36 blocks per wave) still fits
-  // behind it, and the norm is done while the weights stream.  Without it, a wide slice (down's 20
-  // blocks) goes first and the fragments arrive while it streams.
+  // goes first, then the weights.  A wave's load instructions issue only as fast as its compute unit
+  // takes data in, so a wave that requested gate_up's 36 weight blocks at once sat in that issue until
+  // most of them had arrived (about 9 us, per-wave clock marks in a probe build) and only then reached
+  // the transform, which ran after the stream instead of during it: a wide slice is requested in two
+  // parts, the first W1 k steps (12 blocks) before the transform and the rest after it.  Without the
+  // transform, a wide slice (down's 20 blocks) goes first and the fragments arrive while it streams.
   constexpr bool W_FIRST = XF != XF_RMS && NT * KPW > 16;
+  constexpr int W1 = XF == XF_RMS && NT * KPW > 16 ? (12 + NT - 1) / NT : KPW;
   u32x4 A[KPW][NT];
-  auto issue_w = [&]() {
+  auto issue_w = [&](int s0, int s1) {
 #pragma unroll
     for (int s = 0; s < KPW; ++s)
+      if (s >= s0 && s < s1)
 #pragma unroll
-      for (int j = 0; j < NT; ++j)
-        A[s][j] = FD_WLOAD(wblock(a.W, a.KS, t0 + j, kb + ws + min(s, max(wn, 1) - 1)));
+        for (int j = 0; j < NT; ++j)
+          A[s][j] = FD_WLOAD(wblock(a.W, a.KS, t0 + j, kb + ws + min(s, max(wn, 1) - 1)));
   };
-  if constexpr (W_FIRST) issue_w();
+  if constexpr (W_FIRST) issue_w(0, KPW);
   // 1. the activation path: the wave's fragments, the rows' sums of squares (threads 0 .. 255: row
   //    tid / 8, tiles tid % 8 + 8q) and the split's norm weights (one 16-byte chunk per thread)
   u32x4 X[KPW][MT];
@@ -703,8 +708,9 @@ __device__ __forceinline__ void gemm_os_direct_body(const GemmP& a, int bx, int 
     }
     if (nw_ld) nwv = *reinterpret_cast<const u32x4*>(a.nw + 32 * kb + 8 * threadIdx.x);
   }
-  // 2. the weight slice: KPW k steps x NT tiles per wave, all requested at once
-  if constexpr (!W_FIRST) issue_w();
+  // 2. the weight slice: KPW k steps x NT tiles per wave, all requested at once (with the transform, its
+  //    first W1 steps)
+  if constexpr (!W_FIRST) issue_w(0, W1);
 
   // 3. 1 / rms of the chunk's rows (gemm_os_body's order), then the transform in registers
   if constexpr (XF == XF_RMS) {
@@ -727,6 +733,10 @@ __device__ __forceinline__ void gemm_os_direct_body(const GemmP& a, int bx, int 
 #pragma unroll
       for (int s = 0; s < KPW; ++s) X[s][mt] = xform<DT, XF>(X[s][mt], nw_s[(ws + min(s, max(wn, 1) - 1)) * 4 + lg], inv);
     }
+  }
+  if constexpr (!W_FIRST && W1 < KPW) {
+    __builtin_amdgcn_sched_barrier(0);  // not hoisted above the transform
+    issue_w(W1, KPW);
   }
 
   // 4. multiply
