@@ -678,6 +678,11 @@ int fdllm_create(const fdllm_config* cfg, fdllm_ctx** out) {
   if (const char* e = std::getenv("FDLLM_WT256")) c->mm.wt256 = atoi(e);
   if (const char* e = std::getenv("FDLLM_GROUP_WAITS")) c->group_waits = atoi(e) != 0;
   if (const char* e = std::getenv("FDLLM_XFRAG")) c->frag_on = atoi(e) != 0;
+  if (const char* e = std::getenv("FDLLM_OS_HALF")) c->mm.os_half = atoi(e) & 3;
+  // fp16 keeps whole 32-row chunks: its norm transform compiles to a different mix of fp16 rounding
+  // instructions (v_fma_mixlo_f16 or an fp32 multiply and a conversion) for 16-row chunks, which changed
+  // results in the last bit; no fp16 workload here runs the one-shot chain at 17-32 rows
+  if (f.dtype == FDLLM_DTYPE_F16) c->mm.os_half = 0;
   c->names.push_back("model.embed_tokens.weight");
   for (int i = 0; i < f.num_hidden_layers; ++i) {
     std::string p = "model.layers." + std::to_string(i);

@@ -305,7 +305,14 @@ GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol) {
     }
   }
   const OsInfo o = os_info(cfg);
-  const int mt = a.M <= 16 ? 1 : 2;
+  // One-shot qkv and o_proj keep one weight tile per workgroup (128 / 96 workgroups at the 1.5B shapes),
+  // so with 32 rows a compute unit takes in twice as many activation bytes (96 KB) as weight bytes.
+  // Two 16-row m-chunks halve that on twice the workgroups, and the pair of workgroups that shares a
+  // tile (linear indices 8 x groups apart) runs on one XCD, so the second reads its weights from L2.
+  // Each row's arithmetic is unchanged (same k partition and sums): the same bits.
+  const bool half = a.M > 16 && a.M <= 32 && ((pol.os_half >> cfg) & 1) && o.nt == 1;
+  const int mt = a.M <= 16 || half ? 1 : 2;
+  p.mrows = 32;
   if (o.nt > 0 && a.M <= 32 && a.ntiles % o.nt == 0) {
     // the largest k split <= the preferred one that divides the k steps, raised until every wave's share
     // fits the kernel's KPW steps; the activation slice must fit the staging (kps * MT * 64 fragments
@@ -317,6 +324,10 @@ GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol) {
     if (split > 0 && split <= a.KS && (a.KS / split) * mt <= 96) {
       p.kind = GK_ONESHOT;
       p.ksplit = split;
+      if (half && split == 1) {
+        p.mrows = 16;
+        p.mchunks = 2;
+      }
     }
   }
   if (p.kind != GK_ONESHOT) p.ksplit = stream_split;
@@ -471,7 +482,7 @@ static hipError_t launch_mt(const GemmP& a, const GemmPlan& p, hipStream_t st) {
   if (p.kind == GK_MM) return launch_mm<DT, CFG, C>(a, p, st);
   if constexpr (O::nt > 0) {
     if (p.kind == GK_ONESHOT) {
-      if (a.M <= 16) return launch_os<DT, O, 1>(a, p, st);
+      if (a.M <= 16 || p.mrows == 16) return launch_os<DT, O, 1>(a, p, st);
       return launch_os<DT, O, 2>(a, p, st);
     }
   }
@@ -495,7 +506,7 @@ static hipError_t launch_dt(int cfg, const GemmP& a, const GemmPlan& p, hipStrea
 // register-fragment body
 bool gemm_takes_frag(int cfg, const GemmPlan& p) {
   const int nt = os_info(cfg).nt;
-  return p.kind == GK_ONESHOT && p.mchunks == 1 && nt > 0 && (nt <= 4 || (cfg == CFG_GATE_UP && p.ksplit == 1));
+  return p.kind == GK_ONESHOT && p.mchunks * p.mrows <= 32 && nt > 0 && (nt <= 4 || (cfg == CFG_GATE_UP && p.ksplit == 1));
 }
 
 bool gemm_takes_blocks(const GemmPlan& p) {

@@ -499,7 +499,7 @@ __device__ __forceinline__ void gemm_os_body(const GemmP& a, int bx, int by, int
   __shared__ float inv_s[32];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int lr = lane & 15, lg = lane >> 4;
-  const int m0 = bz * 32, mlast = a.M - 1;
+  const int m0 = bz * 16 * MT, mlast = a.M - 1;  // m-chunks of 16 MT rows
   const int t0 = bx * NT;
   const int kb = by * a.kps;  // first k step of the split
   const int kq = a.kps / NW, kr = a.kps % NW;
@@ -653,7 +653,7 @@ __device__ __forceinline__ void gemm_os_direct_body(const GemmP& a, int bx, int 
   __shared__ float inv_s[32];
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lr = lane & 15, lg = lane >> 4;
-  const int m0 = bz * 32, mlast = a.M - 1;
+  const int m0 = bz * 16 * MT, mlast = a.M - 1;  // m-chunks of 16 MT rows
   const int t0 = bx * NT;
   const int kb = by * a.kps;  // first k step of the split
   const int kq = a.kps / NW, kr = a.kps % NW;
@@ -689,7 +689,7 @@ __device__ __forceinline__ void gemm_os_direct_body(const GemmP& a, int bx, int 
       // row-major: the row (clamped to the last; rows past it are never stored); fragment order: the
       // whole 1 KB block (m0 = 0)
       const int m = min(m0 + 16 * mt + lr, mlast), ks = kb + ws + min(s, max(wn, 1) - 1);
-      const size_t off = a.xfrag ? (size_t)((2 * ks + mt) * 64 + lane) * 8 : (size_t)m * a.ldx + 32 * ks + 8 * lg;
+      const size_t off = a.xfrag ? (size_t)((2 * ks + (m0 >> 4) + mt) * 64 + lane) * 8 : (size_t)m * a.ldx + 32 * ks + 8 * lg;
       X[s][mt] = *reinterpret_cast<const u32x4*>(a.X + off);
     }
   constexpr int SQ = 12;  // unrolled sums-of-squares loads (96 tiles: hidden 1536); the rest in a loop
@@ -871,7 +871,7 @@ __device__ __forceinline__ void gemm_os_epilogue_body(const GemmP& a, int splits
     }
     v[q] = sum;
   }
-  os_epilogue<DT, EPI, TPU, COH>(a, v, bz * 32 + 16 * umt + lr, bx * NT + ut, lg);
+  os_epilogue<DT, EPI, TPU, COH>(a, v, bz * 16 * MT + 16 * umt + lr, bx * NT + ut, lg);
 }
 
 template <int DT, int EPI, int MT, int NT>

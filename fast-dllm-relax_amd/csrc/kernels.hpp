@@ -108,6 +108,7 @@ struct GemmPlan {
   int kind; int ksplit; int tiles_per_wg; int groups; int mchunks; size_t part_floats;
   int mm_id; int nbm; int nbn;
   int tail_full, tail_split;  // GK_STREAM: see GemmP (set in both)
+  int mrows;                  // GK_ONESHOT: rows per m-chunk (blockIdx.z), 32, or 16 for half-row chunks
 };
 // How large-M launches are planned.  target_wgs / min_stages: k is split only while the launch has fewer
 // than target_wgs workgroups, and only into splits of at least min_stages stages.  wr_ops: the
@@ -131,6 +132,9 @@ struct MmPolicy {
   // compute units (one group per unit per round) split k up to 3 ways, so that every unit streams about
   // the same bytes (0: off)
   int lm_tail_cus = 0;
+  // one-shot projections (bit cfg) of 17 to 32 rows run as two 16-row m-chunks: each workgroup takes in
+  // half the activations for the same weight tile
+  int os_half = (1 << CFG_QKV) | (1 << CFG_OPROJ);
 };
 GemmPlan gemm_plan(int cfg, GemmP& a, int stream_split, const MmPolicy& pol = MmPolicy{});
 // whether the plan runs the one-shot register-fragment body, the only one that takes xfrag / yfrag 1

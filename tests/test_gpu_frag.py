@@ -1,4 +1,5 @@
-"""Activations in MFMA-fragment order against the row-major layout.
+"""Activations in MFMA-fragment order against the row-major layout (and the one-shot GEMMs' half-row
+m-chunks against whole 32-row chunks, the same way).
 
 A call of at most 32 rows whose four projections all take the one-shot GEMM keeps h, the attention
 output and SiLU * up in the order the GEMMs load their operand fragments (the default); FDLLM_XFRAG=0
@@ -18,7 +19,8 @@ from helpers import TINY, WIDE2, log
 pytestmark = pytest.mark.gpu
 
 
-def _pair_of_vms(kw, seed, monkeypatch, dtype):
+def _pair_of_vms(kw, seed, monkeypatch, dtype, env="FDLLM_XFRAG"):
+    """The default context and one with the switch `env` set to 0, on the same weights."""
     from fast_dllm_relax_amd.config import FastDLLMConfig
     from fast_dllm_relax_amd.params import from_numpy
     from fast_dllm_relax_amd.vm import HipVM
@@ -26,11 +28,11 @@ def _pair_of_vms(kw, seed, monkeypatch, dtype):
 
     cfg = FastDLLMConfig(**kw)
     params = from_numpy(random_params(OracleConfig(**kw), seed, dtype), cfg, dtype=dtype)
-    monkeypatch.delenv("FDLLM_XFRAG", raising=False)
+    monkeypatch.delenv(env, raising=False)
     vm_f = HipVM(cfg, params, dtype=dtype, max_rows=64)
-    monkeypatch.setenv("FDLLM_XFRAG", "0")
+    monkeypatch.setenv(env, "0")
     vm_r = HipVM(cfg, params, dtype=dtype, max_rows=64)
-    monkeypatch.delenv("FDLLM_XFRAG")
+    monkeypatch.delenv(env)
     return vm_f, vm_r
 
 
@@ -42,8 +44,9 @@ def _same(a, b, what):
     np.testing.assert_array_equal(_bits(a), _bits(b), err_msg=what)
 
 
-def _run_case(kw, seed, P, monkeypatch, dtype="bfloat16"):
-    vm_f, vm_r = _pair_of_vms(kw, seed, monkeypatch, dtype)
+def _run_case(kw, seed, P, monkeypatch, dtype="bfloat16", env="FDLLM_XFRAG"):
+    vm_f, vm_r = _pair_of_vms(kw, seed, monkeypatch, dtype, env)
+    frag_r = 0 if env == "FDLLM_XFRAG" else 1  # the other switches keep the fragment order
     tdt = torch.bfloat16 if dtype == "bfloat16" else torch.float16
     L, nkv, hd = kw["num_hidden_layers"], kw["num_key_value_heads"], kw["head_dim"]
     cap = (P + 32 + 31) // 32 * 32 + 32
@@ -62,7 +65,7 @@ def _run_case(kw, seed, P, monkeypatch, dtype="bfloat16"):
     hr = vm_r.forward_cached(x, *caches["r"], off, P)
     torch.cuda.synchronize()
     assert vm_f.lib.fdllm_frag_calls(vm_f.ctx) == 1, "the fragment-order path did not run"
-    assert vm_r.lib.fdllm_frag_calls(vm_r.ctx) == 0
+    assert vm_r.lib.fdllm_frag_calls(vm_r.ctx) == frag_r
     _same(hf, hr, "hidden R=32")
     _same(caches["f"][0], caches["r"][0], "K cache")
     _same(caches["f"][1], caches["r"][1], "V cache")
@@ -85,7 +88,7 @@ def _run_case(kw, seed, P, monkeypatch, dtype="bfloat16"):
     _same(vm_f.forward_hidden(xs, bias), vm_r.forward_hidden(xs, bias), "forward_hidden bias")
     torch.cuda.synchronize()
     assert vm_f.lib.fdllm_frag_calls(vm_f.ctx) == 7
-    assert vm_r.lib.fdllm_frag_calls(vm_r.ctx) == 0
+    assert vm_r.lib.fdllm_frag_calls(vm_r.ctx) == 7 * frag_r
     assert bool(torch.isfinite(hf.float()).all())
 
 
@@ -110,3 +113,10 @@ def test_frag_wide(monkeypatch):
 def test_frag_wide_long_prefix(monkeypatch):
     """Prefix 3000: 24 key chunks, the split merge writes the attention output."""
     _run_case(WIDE2, 2, 3000, monkeypatch)
+
+
+def test_half_row_chunks_bit_identical(monkeypatch):
+    """One-shot qkv and o_proj of 17 to 32 rows as two 16-row m-chunks (the default for bf16) against one
+    32-row chunk (FDLLM_OS_HALF=0): each row's arithmetic is the same, so every result is the same bits."""
+    _run_case(WIDE2, 5, 700, monkeypatch, env="FDLLM_OS_HALF")
+    _run_case(dict(TINY, num_hidden_layers=3), 6, 130, monkeypatch, env="FDLLM_OS_HALF")
