@@ -315,7 +315,38 @@ struct AttnChunkRegs {
   static constexpr bool wcs = WCS;
   u32x4 klo[KIT], khi[KIT], vv[VIT][4];
   f32x4 kcs[WCS ? KIT : 1][4];
+  u32x4 qf[4];        // the lane's query (before RoPE) and its RoPE table entries, requested first
+  f32x4 qcs[2][4];
 };
+
+// The lane's query row and its RoPE (cos, sin) entries, requested before the chunk's K/V: a wave's loads
+// issue only as fast as the compute unit takes data in, and requested after the 64 KB of K/V (as they
+// were) they landed last and the query RoPE waited for all of it.
+template <int QPW, int KH, int CH, bool WCS>
+__device__ __forceinline__ void attn_chunk_qload(const AttnP& a, int bx, int by, AttnChunkRegs<QPW, KH, CH, WCS>& R,
+                                                 int tid) {
+  const int lane = tid & 63, w = tid >> 6;
+  const int qw = w % QPW, kh = w / QPW;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int grp = a.nq / a.nkv, QR = grp * a.rows, QT = (QR + 15) / 16;
+  const int qt = bx * QPW + qw;
+  const int qi = qt * 16 + lr;
+  const bool qvalid = qt < QT && qi < QR;
+  const int hh = qvalid ? qi / a.rows : 0;
+  const int r = qvalid ? qi - hh * a.rows : 0;
+  const bool qshare = KH > 1 && a.nseq <= 1;
+  if (!qshare || kh == 0) {
+    const u16* qp = a.qkv + (size_t)r * a.ldq + (by * grp + hh) * HD + 8 * lg;
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) R.qf[ds] = ld16<false>(qp + 32 * ds);
+    const float* cs = a.rope + (size_t)r * 128 + 16 * lg;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      R.qcs[0][c] = *reinterpret_cast<const f32x4*>(cs + 4 * c);
+      R.qcs[1][c] = *reinterpret_cast<const f32x4*>(cs + 64 + 4 * c);
+    }
+  }
+}
 
 // Item -> (key, chunk) maps: 16 consecutive lanes take 16 keys of one K chunk (with, for this call's own
 // rows, the key's RoPE table entries, so the RoPE at staging waits for no further load), and 32
@@ -407,16 +438,12 @@ __device__ __forceinline__ void attn_chunk_compute(const AttnP& a, int bx, int b
   const int r = qvalid ? qi - hh * a.rows : 0;
   // (a batched call runs three or more workgroup rounds: it skips the sharing, whose 16 KB of LDS would
   // keep a second workgroup off each compute unit, and every wave loads its queries itself)
-  u32x4 qf[4];
+  u32x4 qf[4] = {R.qf[0], R.qf[1], R.qf[2], R.qf[3]};  // requested by attn_chunk_qload
   u32x4* qbuf = reinterpret_cast<u32x4*>(vbuf + HD * VLDC);  // [QPW][4][64] (KH > 1)
   const bool qshare = KH > 1 && a.nseq <= 1;
   if (!qshare || kh == 0) {
-    const u16* qp = a.qkv + (size_t)r * a.ldq + (g * grp + hh) * HD + 8 * lg;
-#pragma unroll
-    for (int ds = 0; ds < 4; ++ds) qf[ds] = ld16<false>(qp + 32 * ds);
-    const float* cs = a.rope + (size_t)r * 128;
-    rope_tab<DT>(qf[0], qf[2], cs + 16 * lg);
-    rope_tab<DT>(qf[1], qf[3], cs + 16 * lg + 64);
+    rope_pairs<DT>(qf[0], qf[2], R.qcs[0]);
+    rope_pairs<DT>(qf[1], qf[3], R.qcs[1]);
     if (qshare) {
 #pragma unroll
       for (int ds = 0; ds < 4; ++ds) qbuf[(qw * 4 + ds) * 64 + lane] = qf[ds];
@@ -619,6 +646,7 @@ __device__ __forceinline__ void attn_chunk_compute(const AttnP& a, int bx, int b
 template <int DT, int QPW, int KH, int CH, int MASK>
 __device__ __forceinline__ void attn_chunk_body(const AttnP& a, int bx, int by, int bz, unsigned char* smem) {
   AttnChunkRegs<QPW, KH, CH, true> R;
+  attn_chunk_qload<QPW, KH, CH, true>(a, bx, by, R, threadIdx.x);
   attn_chunk_load<QPW, KH, CH, true>(a, by, bz, R, threadIdx.x);
   attn_chunk_compute<DT, QPW, KH, CH, MASK, true>(a, bx, by, bz, smem, R, threadIdx.x);
 }
