@@ -5,24 +5,28 @@
 
 namespace fdllm {
 
-// key parts per workgroup of the chunked kernel (waves = 4 query tiles x ATTN_KH)
-constexpr int ATTN_KH = 2;
+// The chunked kernel's workgroup for one sequence: 2 query tiles times key parts of 32 keys (4 for 128-key
+// chunks, 2 for 64-key ones), eight or four waves.  Measured per layer (chunk + merge, 1.5B, prefix 2048)
+// against 4 query tiles x 2 key parts: 32 rows 13.0 -> 11.9 us, 8 rows 11.2 -> 10.8 us (2 x 2: 12.3 /
+// 11.2).  More query-tile groups put more compute units on each chunk's keys, and with more workgroups
+// the 8-row step keeps 128-key chunks (half the split partials).  Batched calls keep 4 query tiles x 2
+// key parts: their 128-row partial step took 2.73 against 2.54 ms the other way.
 
 // Launch plan: short row blocks (the cached decode step) use attn_chunk_kernel with one key chunk of
 // CH keys per workgroup; long row blocks (prefill, stateless forward) use attn_kernel with few, long
 // key ranges per workgroup.
-AttnPlan attn_plan(int rows, int nq, int nkv, int Lk, int target_wgs) {
+AttnPlan attn_plan(int rows, int nq, int nkv, int Lk, int target_wgs, int nseq) {
   AttnPlan p{};
   const int QT = ((nq / nkv) * rows + 15) / 16;
   // chunked: 128 keys per workgroup unless that leaves fewer workgroups than aimed for; at most 64
   // chunks, so the split merge stays small (longer contexts take the loop kernel)
   if (QT <= 12 && (Lk + 127) / 128 <= 64) {
     p.chunked = 1;
-    p.q_tiles_per_wg = 4;
-    p.key_groups = 2;
-    p.qg = (QT + 3) / 4;
+    p.q_tiles_per_wg = nseq > 1 ? 4 : 2;
+    p.qg = (QT + p.q_tiles_per_wg - 1) / p.q_tiles_per_wg;
     p.chunk = 128;
     if (p.qg * nkv * ((Lk + 127) / 128) < target_wgs && (Lk + 63) / 64 <= 64) p.chunk = 64;
+    p.key_groups = nseq > 1 ? 2 : p.chunk / 32;
     p.S = (Lk + p.chunk - 1) / p.chunk;
     return p;
   }
@@ -75,9 +79,8 @@ static hipError_t launch_loop(const AttnP& a, const AttnPlan& p, hipStream_t st)
   return hipGetLastError();
 }
 
-template <int DT, int CH, int KH, int MASK>
+template <int DT, int CH, int KH, int MASK, int QPW>
 static hipError_t launch_chunk_kh(const AttnP& a, const AttnPlan& p, hipStream_t st) {
-  constexpr int QPW = 4;
   // K and V^T of the chunk, then (one-sequence calls) the queries the first key part shares
   const size_t loop_lds = (size_t)CH * KLD * 2 + (size_t)HD * (CH + 8) * 2 +
                           (KH > 1 && a.nseq <= 1 ? (size_t)QPW * 4 * 64 * 16 : 0);
@@ -98,12 +101,19 @@ static hipError_t launch_chunk_kh(const AttnP& a, const AttnPlan& p, hipStream_t
   return hipGetLastError();
 }
 
+// attn_plan's workgroup shape: 2 query tiles x CH / 32 key parts (one sequence) or 4 x 2 (batched)
+template <int DT, int CH, int MASK>
+static hipError_t launch_chunk_shape(const AttnP& a, const AttnPlan& p, hipStream_t st) {
+  if (p.q_tiles_per_wg == 2 && p.key_groups == CH / 32) return launch_chunk_kh<DT, CH, CH / 32, MASK, 2>(a, p, st);
+  if (p.q_tiles_per_wg == 4 && p.key_groups == 2) return launch_chunk_kh<DT, CH, 2, MASK, 4>(a, p, st);
+  return hipErrorInvalidValue;
+}
 template <int DT, int CH>
 static hipError_t launch_chunk_mask(const AttnP& a, const AttnPlan& p, hipStream_t st) {
   switch (a.mask) {
-    case 0: return launch_chunk_kh<DT, CH, ATTN_KH, 0>(a, p, st);
-    case 1: return launch_chunk_kh<DT, CH, ATTN_KH, 1>(a, p, st);
-    default: return launch_chunk_kh<DT, CH, ATTN_KH, 2>(a, p, st);
+    case 0: return launch_chunk_shape<DT, CH, 0>(a, p, st);
+    case 1: return launch_chunk_shape<DT, CH, 1>(a, p, st);
+    default: return launch_chunk_shape<DT, CH, 2>(a, p, st);
   }
 }
 
@@ -232,13 +242,13 @@ static hipError_t launch_seq(const AttnP& a, hipStream_t st) {
 
 bool attn_takes_roped(const AttnP& a) {
   if (a.nseq > 1 && a.seq_attn && a.mask == 0) return true;
-  const AttnPlan p = attn_plan(a.rows, a.nq, a.nkv, a.Lk, a.target_wgs);
+  const AttnPlan p = attn_plan(a.rows, a.nq, a.nkv, a.Lk, a.target_wgs, a.nseq);
   return !p.chunked && a.nseq <= 1 && a.rows >= PREFILL_MIN_ROWS && a.mask != 2;
 }
 
 template <int DT>
 static hipError_t launch_dt(const AttnP& a, hipStream_t st) {
-  const AttnPlan p = attn_plan(a.rows, a.nq, a.nkv, a.Lk, a.target_wgs);
+  const AttnPlan p = attn_plan(a.rows, a.nq, a.nkv, a.Lk, a.target_wgs, a.nseq);
   if (a.roped && !attn_takes_roped(a)) return hipErrorInvalidValue;
   if (p.S != a.S || p.chunk != a.chunk) return hipErrorInvalidValue;
   if (a.ofrag && (a.nseq > 1 || a.rows > 32)) return hipErrorInvalidValue;

@@ -333,7 +333,7 @@ int plan_attention(fdllm_ctx* c, AttnP& a, int rows, uint16_t* kc, uint16_t* vc,
     }
     target = std::max(1, target / sb->nseq);
   }
-  const AttnPlan pl = attn_plan(a.rows, a.nq, a.nkv, a.Lk, target);
+  const AttnPlan pl = attn_plan(a.rows, a.nq, a.nkv, a.Lk, target, a.nseq);
   // batched calls without a mask take attn_seq_kernel (every key of a sequence in one workgroup, no
   // partials) from 32 rows per sequence, or when the chunk plan cannot cover the longest sequence in one
   // step; otherwise the chunk kernel.  Measured on config 4 (16 sequences, prefixes up to 1024): 32 rows

@@ -240,7 +240,7 @@ struct AttnP {
   int roped;
 };
 struct AttnPlan { int chunked; int q_tiles_per_wg; int key_groups; int qg; int S; int chunk; };
-AttnPlan attn_plan(int rows, int nq, int nkv, int Lk, int target_wgs);
+AttnPlan attn_plan(int rows, int nq, int nkv, int Lk, int target_wgs, int nseq);
 // whether launch_attention starts with rope_kv_kernel for a (the batched-sequence and prefill kernels)
 bool attn_takes_roped(const AttnP& a);
 // attn_seq_kernel's units for a batched call (a.nseq, rows, heads, seq_lk and seq_cnt set): each sequence
