@@ -7,6 +7,7 @@
 namespace fdllm {
 
 constexpr int UNMASK_MAX_ROWS = 1024;  // confidence rows one fused launch combines
+constexpr int CONF_NT = 10;            // tiles per lane held in registers (594 for the 1.5B vocabulary)
 
 // One workgroup: its waves combine the rows' tile statistics (wave w takes rows w, w + nw, ...), then
 // wave 0 applies the rule to the sub-block.
@@ -16,11 +17,7 @@ __global__ __launch_bounds__(1024) void confidence_unmask_kernel(const float* st
   __shared__ int32_t ids_l[UNMASK_MAX_ROWS];
   __shared__ float maxp_l[UNMASK_MAX_ROWS];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  for (int r = w; r < u.rows; r += nw) {
-    int32_t id;
-    float p;
-    confidence_row(stat_m + (size_t)r * tiles, stat_a + (size_t)r * tiles, stat_s + (size_t)r * tiles, tiles, lane,
-                   &id, &p);
+  auto put = [&](int r, int32_t id, float p) {
     if (lane == 0) {
       ids_l[r] = id;
       maxp_l[r] = p;
@@ -28,6 +25,25 @@ __global__ __launch_bounds__(1024) void confidence_unmask_kernel(const float* st
         ids_out[r] = id;
         maxp_out[r] = p;
       }
+    }
+  };
+  if (tiles <= 64 * CONF_NT && u.rows <= 2 * nw) {
+    // a decode step's rows (up to 32 on 16 waves): rows w and w + nw together, every statistic in one
+    // round trip (about 10 us -> 4 us for 32 rows of the 1.5B vocabulary)
+    int32_t id[2];
+    float p[2];
+    const int nr = (w < u.rows ? 1 : 0) + (w + nw < u.rows ? 1 : 0);  // rows w and w + nw
+    confidence_rows<2, CONF_NT>(stat_m + (size_t)w * tiles, stat_a + (size_t)w * tiles, stat_s + (size_t)w * tiles,
+                                tiles, nw * tiles, nr, lane, id, p);
+    if (nr > 0) put(w, id[0], p[0]);
+    if (nr > 1) put(w + nw, id[1], p[1]);
+  } else {
+    for (int r = w; r < u.rows; r += nw) {
+      int32_t id;
+      float p;
+      confidence_row(stat_m + (size_t)r * tiles, stat_a + (size_t)r * tiles, stat_s + (size_t)r * tiles, tiles, lane,
+                     &id, &p);
+      put(r, id, p);
     }
   }
   __syncthreads();
