@@ -17,8 +17,14 @@ __global__ __launch_bounds__(64) void confidence_combine_kernel(const float* sta
   if (r >= rows) return;
   int32_t id;
   float p;
-  confidence_row(stat_m + (size_t)r * tiles, stat_a + (size_t)r * tiles, stat_s + (size_t)r * tiles, tiles, lane, &id,
-                 &p);
+  if (tiles <= 64 * 10) {
+    // the row's statistics requested together: one memory round trip (the 1.5B vocabulary's 594 tiles)
+    confidence_rows<1, 10>(stat_m + (size_t)r * tiles, stat_a + (size_t)r * tiles, stat_s + (size_t)r * tiles, tiles,
+                           tiles, 1, lane, &id, &p);
+  } else {
+    confidence_row(stat_m + (size_t)r * tiles, stat_a + (size_t)r * tiles, stat_s + (size_t)r * tiles, tiles, lane,
+                   &id, &p);
+  }
   if (lane == 0) {
     ids[r] = id;
     maxp[r] = p;
