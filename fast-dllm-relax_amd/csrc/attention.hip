@@ -5,12 +5,14 @@
 
 namespace fdllm {
 
-// The chunked kernel's workgroup for one sequence: 2 query tiles times key parts of 32 keys (4 for 128-key
-// chunks, 2 for 64-key ones), eight or four waves.  Measured per layer (chunk + merge, 1.5B, prefix 2048)
-// against 4 query tiles x 2 key parts: 32 rows 13.0 -> 11.9 us, 8 rows 11.2 -> 10.8 us (2 x 2: 12.3 /
-// 11.2).  More query-tile groups put more compute units on each chunk's keys, and with more workgroups
-// the 8-row step keeps 128-key chunks (half the split partials).  Batched calls keep 4 query tiles x 2
-// key parts: their 128-row partial step took 2.73 against 2.54 ms the other way.
+// The chunked kernel's workgroup: query tiles x 2 key parts, 2 query tiles for one sequence and 4 for a
+// batched call.  A query's arithmetic does not depend on how many tiles share its workgroup, so the
+// results are those of the 4-tile workgroups; with twice the workgroups more compute units take each
+// chunk's keys (one sequence, 1.5B, prefix 2048, chunk + merge per layer: 13.0 -> 12.3 us at 32 rows).
+// The chunk length is chosen on the 4-tile count for both, so that it, and with it every result, stays
+// the same.  (4 key parts of 32 keys measured faster still, 11.9 us, but a key part's online softmax
+// then runs over other blocks, which changes the rounding; batched calls on 2 tiles: 128-row partial
+// step 2.73 against 2.54 ms.)
 
 // Launch plan: short row blocks (the cached decode step) use attn_chunk_kernel with one key chunk of
 // CH keys per workgroup; long row blocks (prefill, stateless forward) use attn_kernel with few, long
@@ -22,11 +24,11 @@ AttnPlan attn_plan(int rows, int nq, int nkv, int Lk, int target_wgs, int nseq) 
   // chunks, so the split merge stays small (longer contexts take the loop kernel)
   if (QT <= 12 && (Lk + 127) / 128 <= 64) {
     p.chunked = 1;
+    p.key_groups = 2;
+    p.chunk = 128;
+    if ((QT + 3) / 4 * nkv * ((Lk + 127) / 128) < target_wgs && (Lk + 63) / 64 <= 64) p.chunk = 64;
     p.q_tiles_per_wg = nseq > 1 ? 4 : 2;
     p.qg = (QT + p.q_tiles_per_wg - 1) / p.q_tiles_per_wg;
-    p.chunk = 128;
-    if (p.qg * nkv * ((Lk + 127) / 128) < target_wgs && (Lk + 63) / 64 <= 64) p.chunk = 64;
-    p.key_groups = nseq > 1 ? 2 : p.chunk / 32;
     p.S = (Lk + p.chunk - 1) / p.chunk;
     return p;
   }
@@ -101,11 +103,12 @@ static hipError_t launch_chunk_kh(const AttnP& a, const AttnPlan& p, hipStream_t
   return hipGetLastError();
 }
 
-// attn_plan's workgroup shape: 2 query tiles x CH / 32 key parts (one sequence) or 4 x 2 (batched)
+// attn_plan's workgroup shape: 2 (one sequence) or 4 (batched) query tiles x 2 key parts
 template <int DT, int CH, int MASK>
 static hipError_t launch_chunk_shape(const AttnP& a, const AttnPlan& p, hipStream_t st) {
-  if (p.q_tiles_per_wg == 2 && p.key_groups == CH / 32) return launch_chunk_kh<DT, CH, CH / 32, MASK, 2>(a, p, st);
-  if (p.q_tiles_per_wg == 4 && p.key_groups == 2) return launch_chunk_kh<DT, CH, 2, MASK, 4>(a, p, st);
+  if (p.key_groups != 2) return hipErrorInvalidValue;
+  if (p.q_tiles_per_wg == 2) return launch_chunk_kh<DT, CH, 2, MASK, 2>(a, p, st);
+  if (p.q_tiles_per_wg == 4) return launch_chunk_kh<DT, CH, 2, MASK, 4>(a, p, st);
   return hipErrorInvalidValue;
 }
 template <int DT, int CH>
