@@ -21,6 +21,7 @@ EXPORTS = (
     "fdllm_embed", "fdllm_forward_hidden", "fdllm_get_logits", "fdllm_build_prefix_cache",
     "fdllm_forward_cached", "fdllm_forward_cached_noalloc", "fdllm_forward_block_partial", "fdllm_forward_block_partial_rp0",
     "fdllm_forward_block_partial_rp8", "fdllm_forward_block_partial_rp16", "fdllm_forward_block_partial_rp24",
+    "fdllm_kv_write", "fdllm_attn_inplace",
     "fdllm_forward_cached_batch", "fdllm_forward_block_partial_batch", "fdllm_build_prefix_cache_seq",
     "fdllm_get_confidence", "fdllm_confidence_from_logits", "fdllm_unmask", "fdllm_get_confidence_unmask",
     "fdllm_host_alloc", "fdllm_host_free", "fdllm_bench_op", "fdllm_group_wait_launches",
@@ -61,6 +62,8 @@ _SIGS = {
     "fdllm_forward_block_partial_rp8": ([_P, _P, _I, _P, _P, _I, _P, _I64, _P, _P], _I),
     "fdllm_forward_block_partial_rp16": ([_P, _P, _I, _P, _P, _I, _P, _I64, _P, _P], _I),
     "fdllm_forward_block_partial_rp24": ([_P, _P, _I, _P, _P, _I, _P, _I64, _P, _P], _I),
+    "fdllm_kv_write": ([_P, _P, _P, _I, _P, _P, _I, _I, _I64, _P], _I),
+    "fdllm_attn_inplace": ([_P, _P, _P, _P, _I, _P, _P, _I, _I, _I64, _I, _I, _P, _P], _I),
     "fdllm_forward_cached_batch": ([_P, _P, _I, _I, _P, _P, _I, _P, ctypes.POINTER(_I64), _P, _P], _I),
     "fdllm_forward_block_partial_batch": ([_P, _I, _P, _I, _I, _P, _P, _I, _P, ctypes.POINTER(_I64), _P, _P], _I),
     "fdllm_build_prefix_cache_seq": ([_P, _P, _I, _P, _P, _P, _I, _I, _I, _P], _I),

@@ -97,9 +97,11 @@ __global__ __launch_bounds__(64 * QPW * KSW) void attn_kernel(AttnP a) {
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds)
       qf[ds] = qvalid ? *reinterpret_cast<const u32x4*>(qp + 32 * ds) : u32x4{0u, 0u, 0u, 0u};
-    const float* cs = a.rope + (size_t)r * 128;
-    rope_tab<DT>(qf[0], qf[2], cs + 16 * lg);
-    rope_tab<DT>(qf[1], qf[3], cs + 16 * lg + 64);
+    if (a.rope != nullptr) {  // null: the queries arrive rotated (fdllm_attn_inplace)
+      const float* cs = a.rope + (size_t)r * 128;
+      rope_tab<DT>(qf[0], qf[2], cs + 16 * lg);
+      rope_tab<DT>(qf[1], qf[3], cs + 16 * lg + 64);
+    }
   }
   const int qpos_blk = a.mask == 1 ? (a.q_pos0 + r) / a.block : 0;
   const float* brow = a.mask == 2 ? a.bias + (long long)r * a.bias_ld : nullptr;
@@ -339,11 +341,13 @@ __device__ __forceinline__ void attn_chunk_qload(const AttnP& a, int bx, int by,
     const u16* qp = a.qkv + (size_t)r * a.ldq + (by * grp + hh) * HD + 8 * lg;
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) R.qf[ds] = ld16<false>(qp + 32 * ds);
-    const float* cs = a.rope + (size_t)r * 128 + 16 * lg;
+    if (a.rope != nullptr) {  // null: the queries arrive rotated (fdllm_attn_inplace)
+      const float* cs = a.rope + (size_t)r * 128 + 16 * lg;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      R.qcs[0][c] = *reinterpret_cast<const f32x4*>(cs + 4 * c);
-      R.qcs[1][c] = *reinterpret_cast<const f32x4*>(cs + 64 + 4 * c);
+      for (int c = 0; c < 4; ++c) {
+        R.qcs[0][c] = *reinterpret_cast<const f32x4*>(cs + 4 * c);
+        R.qcs[1][c] = *reinterpret_cast<const f32x4*>(cs + 64 + 4 * c);
+      }
     }
   }
 }
@@ -442,8 +446,10 @@ __device__ __forceinline__ void attn_chunk_compute(const AttnP& a, int bx, int b
   u32x4* qbuf = reinterpret_cast<u32x4*>(vbuf + HD * VLDC);  // [QPW][4][64] (KH > 1)
   const bool qshare = KH > 1 && a.nseq <= 1;
   if (!qshare || kh == 0) {
-    rope_pairs<DT>(qf[0], qf[2], R.qcs[0]);
-    rope_pairs<DT>(qf[1], qf[3], R.qcs[1]);
+    if (a.rope != nullptr) {
+      rope_pairs<DT>(qf[0], qf[2], R.qcs[0]);
+      rope_pairs<DT>(qf[1], qf[3], R.qcs[1]);
+    }
     if (qshare) {
 #pragma unroll
       for (int ds = 0; ds < 4; ++ds) qbuf[(qw * 4 + ds) * 64 + lane] = qf[ds];

@@ -957,6 +957,82 @@ FD_PARTIAL(16)
 FD_PARTIAL(24)
 #undef FD_PARTIAL
 
+// ---- the reference's attention callbacks (fast_dllm_relax/runtime.py:51-80), for a model that computes
+// its own projections and RoPE and calls out for the cache write and the attention ----
+
+static int check_kv_call(const fdllm_ctx* c, int rows, int cap, int layer) {
+  if (!c) return fail(FDLLM_EINVAL, "null context");
+  if (rows < 0) return fail(FDLLM_EINVAL, "rows must not be negative, got %d", rows);
+  if (cap <= 0) return fail(FDLLM_EINVAL, "cache capacity must be positive, got %d", cap);
+  if (layer < 0 || layer >= c->cfg.num_hidden_layers)
+    return fail(FDLLM_EINVAL, "layer %d outside [0, %d)", layer, c->cfg.num_hidden_layers);
+  return FDLLM_OK;
+}
+
+// _write_rows (runtime.py:51-60): rows [start, start + rows) of the layer's cache get k and v byte for
+// byte (a cache row is nkv x head_dim contiguous elements, so the window is one contiguous range).
+static int write_kv_rows(const fdllm_ctx* c, const void* k, const void* v, int rows, void* kc, void* vc, int cap,
+                         int layer, int64_t start, hipStream_t st) {
+  if (start < 0 || start + rows > cap)
+    return fail(FDLLM_EINVAL, "KV write [%lld, %lld) outside cache capacity %d", (long long)start,
+                (long long)(start + rows), cap);
+  if (rows == 0) return FDLLM_OK;
+  const size_t row = (size_t)c->cfg.num_key_value_heads * c->cfg.head_dim;
+  const size_t off = ((size_t)layer * cap + (size_t)start) * row, bytes = (size_t)rows * row * sizeof(uint16_t);
+  HIPCHK(hipMemcpyAsync((uint16_t*)kc + off, k, bytes, hipMemcpyDeviceToDevice, st));
+  HIPCHK(hipMemcpyAsync((uint16_t*)vc + off, v, bytes, hipMemcpyDeviceToDevice, st));
+  return FDLLM_OK;
+}
+
+int fdllm_kv_write(fdllm_ctx* c, const void* k, const void* v, int rows, void* k_cache, void* v_cache, int cap,
+                   int layer, int64_t start, void* stream) {
+  int rc = check_kv_call(c, rows, cap, layer);
+  if (rc) return rc;
+  if (!k || !v || !k_cache || !v_cache) return fail(FDLLM_EINVAL, "null tensor argument");
+  return write_kv_rows(c, k, v, rows, k_cache, v_cache, cap, layer, start, (hipStream_t)stream);
+}
+
+// fast_dllm.attn_inplace (runtime.py:63-73): the write of _write_rows, then attention of the given
+// (already rotated) queries over cache rows [0, prefix_len + attend_rel) with no mask (_attend,
+// runtime.py:30-48).  The chunk and loop kernels take the queries from q (AttnP::rope null: no RoPE, and
+// ws = Lk: no rows of the call are read from q's buffer or appended, the cache already holds them); the
+// prefill kernels (128 rows and more) read rotated queries from the output buffer, where they are
+// copied first.
+int fdllm_attn_inplace(fdllm_ctx* c, const void* q, const void* k, const void* v, int rows, void* k_cache,
+                       void* v_cache, int cap, int layer, int64_t prefix_len, int write_rel, int attend_rel, void* out,
+                       void* stream) {
+  int rc = check_kv_call(c, rows, cap, layer);
+  if (rc) return rc;
+  if (!q || !k || !v || !k_cache || !v_cache || !out) return fail(FDLLM_EINVAL, "null tensor argument");
+  rc = check_aligned({q, k_cache, v_cache, out});
+  if (rc) return rc;
+  const int64_t write_start = prefix_len + write_rel, attend_len = prefix_len + attend_rel;
+  if (write_start + rows > attend_len)
+    return fail(FDLLM_EINVAL, "KV write [%lld, %lld) past the attended rows [0, %lld)", (long long)write_start,
+                (long long)(write_start + rows), (long long)attend_len);
+  const hipStream_t st = (hipStream_t)stream;
+  rc = write_kv_rows(c, k, v, rows, k_cache, v_cache, cap, layer, write_start, st);
+  if (rc || rows == 0) return rc;
+  // the reference attends over the slice k_cache[layer, :, :attend_len], which stops at the capacity
+  const int Lk = (int)std::min<int64_t>(attend_len, cap);
+  const fdllm_config& f = c->cfg;
+  const size_t stride = (size_t)cap * f.num_key_value_heads * f.head_dim;
+  AttnP a;
+  rc = plan_attention(c, a, rows, (uint16_t*)k_cache + layer * stride, (uint16_t*)v_cache + layer * stride, Lk, Lk,
+                      0, nullptr, 0, nullptr, false);
+  if (rc) return rc;
+  a.qkv = (const uint16_t*)q;
+  a.ldq = f.num_attention_heads * f.head_dim;
+  a.rope = nullptr;
+  a.out = (uint16_t*)out;
+  if (attn_takes_roped(a)) {
+    HIPCHK(hipMemcpyAsync(out, q, (size_t)rows * a.ldq * sizeof(uint16_t), hipMemcpyDeviceToDevice, st));
+    a.roped = 1;
+  }
+  HIPCHK(launch_attention(f.dtype, a, st));
+  return FDLLM_OK;
+}
+
 int fdllm_forward_cached_batch(fdllm_ctx* c, const void* x, int nseq, int rows, void* k, void* v, int cap,
                                const int32_t* off, const int64_t* prefix_lens, void* out, void* stream) {
   return cached_step_batch(c, x, nseq, rows, k, v, cap, off, prefix_lens, 0, rows, out, stream);

@@ -205,7 +205,9 @@ constexpr int SEQ_CNT_MAX = 16384;      // its arrival counters (sequence, kv he
 struct AttnP {
   const uint16_t* qkv; int ldq;       // [rows][ldq]: q | k | v, bias added, before RoPE
   int rows, nq, nkv;
-  const float* rope;                  // [rows][64][2] RoPE (cos, sin) of row r (position pos_offset + r), model-dtype values
+  const float* rope;                  // [rows][64][2] RoPE (cos, sin) of row r (position pos_offset + r), model-dtype values;
+                                      // null (chunk and loop kernels): the queries arrive rotated and ws >= Lk (no rows taken
+                                      // from qkv or appended)
   uint16_t* kc; uint16_t* vc;         // this layer's cache [cap][nkv][128]
   int ws;                             // rows [ws, ws + rows) are this call's: taken from qkv, written to the cache
   int Lk;                             // attended keys [0, Lk)

@@ -197,6 +197,45 @@ class HipVM:
         return self._partial(24, active_embed, k_cache, v_cache, cache_offset, prefix_len)
 
     # ---- batched steps (no reference counterpart: the reference is batch 1, cuda.py:796-836) ----
+    # ---- the reference's attention callbacks (runtime.py:19-80) ------------------------------
+    def _check_bsnh(self, t: torch.Tensor, heads: int, name: str) -> int:
+        hd = self.cfg.head_dim
+        if (t.dim() != 4 or t.shape[0] != 1 or t.shape[2] != heads or t.shape[3] != hd or t.dtype != self.torch_dtype
+                or not t.is_cuda or not t.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous {self.torch_dtype} device tensor [1, rows, {heads}, {hd}], "
+                             f"got {tuple(t.shape)} {t.dtype}")
+        return int(t.shape[1])
+
+    def kv_write(self, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, layer: int,
+                 start: int):
+        """fast_dllm.kv_write (runtime.py:76-80): k / v [1, rows, nkv, hd] into cache rows [start, + rows) of
+        `layer`, byte for byte; returns the caches (aliases)."""
+        nkv = self.cfg.num_key_value_heads
+        rows = self._check_bsnh(k, nkv, "k")
+        if self._check_bsnh(v, nkv, "v") != rows:
+            raise ValueError("k and v rows differ")
+        cap = self._check_cache(k_cache, v_cache)
+        _lib.check(self.lib.fdllm_kv_write(self.ctx, _ptr(k), _ptr(v), rows, _ptr(k_cache), _ptr(v_cache), cap,
+                                           int(layer), int(start), _stream()))
+        return k_cache, v_cache
+
+    def attn_inplace(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
+                     v_cache: torch.Tensor, layer: int, prefix_len: int, write_rel: int, attend_rel: int):
+        """fast_dllm.attn_inplace (runtime.py:63-73): write k / v at cache rows [prefix_len + write_rel,
+        + rows), then attend the rotated queries q [1, rows, nq, hd] over rows [0, prefix_len + attend_rel)
+        with no mask.  Returns (k_cache, v_cache, out [1, rows, nq, hd])."""
+        c = self.cfg
+        rows = self._check_bsnh(q, c.num_attention_heads, "q")
+        if self._check_bsnh(k, c.num_key_value_heads, "k") != rows or \
+                self._check_bsnh(v, c.num_key_value_heads, "v") != rows:
+            raise ValueError("q, k and v rows differ")
+        cap = self._check_cache(k_cache, v_cache)
+        out = torch.empty_like(q)
+        _lib.check(self.lib.fdllm_attn_inplace(self.ctx, _ptr(q), _ptr(k), _ptr(v), rows, _ptr(k_cache), _ptr(v_cache),
+                                               cap, int(layer), int(prefix_len), int(write_rel), int(attend_rel),
+                                               _ptr(out), _stream()))
+        return k_cache, v_cache, out
+
     def _check_batch_cache(self, k: torch.Tensor, v: torch.Tensor, nseq: int) -> int:
         c = self.cfg
         exp = (c.num_hidden_layers, nseq, k.shape[2] if k.dim() == 5 else -1, c.num_key_value_heads, c.head_dim)

@@ -127,6 +127,28 @@ int fdllm_forward_block_partial_rp24(fdllm_ctx* ctx, const void* active_embed, i
                                      void* v_cache, int cap, const int32_t* cache_offset, int64_t prefix_len,
                                      void* out, void* stream);
 
+/* The reference's attention callbacks, for a model that computes its own projections and RoPE and calls
+ * out once per layer for the cache write and the attention (fast_dllm_relax/runtime.py:19-80, called
+ * from model/cuda.py through rx.call_inplace_packed).  Tensors are BSNH with batch 1, in the context's
+ * dtype: k / v [rows, nkv, head_dim], q / out [rows, nq, head_dim]; the caches [L, 1, cap, nkv,
+ * head_dim] are the ones the other entry points take.  Neither call needs bound weights.
+ *
+ * fast_dllm.kv_write (runtime.py:76-80, _write_rows :51-60): k / v copied byte for byte to cache rows
+ * [start, start + rows) of `layer`.  FDLLM_EINVAL: "KV write [s, e) outside cache capacity cap". */
+int fdllm_kv_write(fdllm_ctx* ctx, const void* k, const void* v, int rows, void* k_cache, void* v_cache, int cap,
+                   int layer, int64_t start, void* stream);
+
+/* fast_dllm.attn_inplace (runtime.py:63-73): the write of fdllm_kv_write at rows [prefix_len + write_rel,
+ * + rows), then out = softmax(q K^T / sqrt(head_dim)) V over cache rows [0, prefix_len + attend_rel) of
+ * `layer`, no mask, query head h on kv head h / (nq / nkv) (_attend, runtime.py:30-48); like the
+ * reference's slice of the cache, the attended rows stop at the capacity.  q must already be rotated.
+ * FDLLM_EINVAL: "KV write [s, e) past the attended rows [0, n)" when the written rows end past the
+ * attended ones, and the capacity error of fdllm_kv_write.  q, the caches and out must be 16-byte
+ * aligned. */
+int fdllm_attn_inplace(fdllm_ctx* ctx, const void* q, const void* k, const void* v, int rows, void* k_cache,
+                       void* v_cache, int cap, int layer, int64_t prefix_len, int write_rel, int attend_rel,
+                       void* out, void* stream);
+
 /* Batched steps: no counterpart in the reference, whose entry points are batch 1
  * (fast_dllm_relax/model/cuda.py:796-836); they serve callers that refine one block per sequence
  * for many sequences at once.  nseq (<= 64) sequences share one cache tensor [L, nseq, cap, nkv, hd]

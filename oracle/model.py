@@ -248,25 +248,45 @@ class OracleModel:
             v_cache[i, 0, :n] = v
             h = self._layer_tail(i, h, self.attend(q, k, v, bias))
 
+    @staticmethod
+    def kv_write(k: np.ndarray, v: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, layer: int, start: int):
+        """fast_dllm.kv_write (runtime.py:76-80) with _write_rows (:51-60): k / v [1, rows, nkv, hd] copied
+        to cache rows [start, start + rows) of `layer` (caches [L, 1, cap, nkv, hd])."""
+        rows = k.shape[1]
+        if start < 0 or start + rows > k_cache.shape[2]:
+            raise ValueError(f"KV write [{start}, {start + rows}) outside cache capacity {k_cache.shape[2]}")
+        k_cache[layer, :, start:start + rows] = k
+        v_cache[layer, :, start:start + rows] = v
+        return k_cache, v_cache
+
+    def attn_inplace(self, q: np.ndarray, k: np.ndarray, v: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
+                     layer: int, prefix_len: int, write_rel: int, attend_rel: int):
+        """fast_dllm.attn_inplace (runtime.py:63-73): write k / v at rows [prefix_len + write_rel, + rows),
+        then attend q [1, rows, nq, hd] (already rotated) over the cache slice [0, prefix_len + attend_rel)
+        of `layer` (a slice: past the capacity it stops there), no mask (_attend, runtime.py:30-48).
+        Returns (k_cache, v_cache, out [1, rows, nq, hd])."""
+        write_start, attend_len = prefix_len + write_rel, prefix_len + attend_rel
+        rows = k.shape[1]
+        if write_start + rows > attend_len:
+            raise ValueError(f"KV write [{write_start}, {write_start + rows}) past the attended rows [0, {attend_len})")
+        self.kv_write(k, v, k_cache, v_cache, layer, write_start)
+        out = self.attend(q[0], k_cache[layer, 0, :attend_len], v_cache[layer, 0, :attend_len])
+        return k_cache, v_cache, out[None]
+
     def forward_cached(self, active_embed: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
                        cache_offset: int, prefix_len: int, write_rel: int = 0,
                        attend_rel: int | None = None) -> np.ndarray:
-        """cuda.py:639-666 with the attn_inplace callback semantics of runtime.py:51-73."""
+        """cuda.py:639-666: per layer, the projections and RoPE, then the attn_inplace callback
+        (runtime.py:51-73)."""
         h = np.asarray(active_embed, dtype=F32)[0]
         rows = h.shape[0]
         attend_rel = rows if attend_rel is None else attend_rel
-        start, attend_len = prefix_len + write_rel, prefix_len + attend_rel
-        if start + rows > attend_len:
-            raise ValueError(f"KV write [{start}, {start + rows}) past the attended rows [0, {attend_len})")
-        if start < 0 or start + rows > k_cache.shape[2]:
-            raise ValueError(f"KV write [{start}, {start + rows}) outside cache capacity {k_cache.shape[2]}")
         for i in range(self.cfg.num_hidden_layers):
             xn = self.rmsnorm(h, self.p[f"model.layers.{i}.input_layernorm.weight"])
             q, k, v = self._qkv(i, xn, int(cache_offset))
-            k_cache[i, 0, start:start + rows] = k
-            v_cache[i, 0, start:start + rows] = v
-            attn = self.attend(q, k_cache[i, 0, :attend_len], v_cache[i, 0, :attend_len])
-            h = self._layer_tail(i, h, attn)
+            _, _, attn = self.attn_inplace(q[None], k[None], v[None], k_cache, v_cache, i, prefix_len, write_rel,
+                                           attend_rel)
+            h = self._layer_tail(i, h, attn[0])
         return self.rmsnorm(h, self.p["model.norm.weight"])[None]
 
     def forward_block_partial(self, rp: int, active_embed, k_cache, v_cache, cache_offset, prefix_len):

@@ -170,6 +170,55 @@ def test_attention_matches_torch_sdpa_gqa(tiny32):
     np.testing.assert_allclose(got, want, rtol=0, atol=2e-6)
 
 
+def _torch_callbacks(q, k, v, kc, vc, layer, prefix_len, write_rel, attend_rel):
+    """fast_dllm.attn_inplace's body (runtime.py:51-73) on torch tensors: torch's slice-assignment for the
+    write, torch's slice for the attended rows and torch's SDPA with GQA (the reference's fallback
+    _attend, runtime.py:38-48)."""
+    kc, vc = torch.from_numpy(kc.copy()), torch.from_numpy(vc.copy())
+    start, attend_len, rows = prefix_len + write_rel, prefix_len + attend_rel, k.shape[1]
+    kc[layer, :, start:start + rows].copy_(torch.from_numpy(k))
+    vc[layer, :, start:start + rows].copy_(torch.from_numpy(v))
+    out = torch.nn.functional.scaled_dot_product_attention(
+        torch.from_numpy(q).transpose(1, 2), kc[layer, :, :attend_len].transpose(1, 2),
+        vc[layer, :, :attend_len].transpose(1, 2), enable_gqa=True).transpose(1, 2)
+    return kc.numpy(), vc.numpy(), out.numpy()
+
+
+@pytest.mark.parametrize("rows,P,write_rel,attend_rel,cap", [
+    (8, 40, 0, 8, 64), (8, 40, 16, 32, 96), (5, 10, 3, 9, 32),
+    (8, 40, 0, 30, 56),  # attended rows past the capacity: the slice stops at 56
+])
+def test_attn_callbacks_against_torch(tiny32, rows, P, write_rel, attend_rel, cap):
+    cfg, _, model = tiny32
+    rng = np.random.default_rng(rows * 100 + P)
+    q = rng.standard_normal((1, rows, cfg.num_attention_heads, cfg.head_dim)).astype(np.float32)
+    k, v = rng.standard_normal((2, 1, rows, cfg.num_key_value_heads, cfg.head_dim)).astype(np.float32)
+    shape = (cfg.num_hidden_layers, 1, cap, cfg.num_key_value_heads, cfg.head_dim)
+    kc, vc = rng.standard_normal((2,) + shape).astype(np.float32)
+    want_k, want_v, want = _torch_callbacks(q, k, v, kc, vc, 1, P, write_rel, attend_rel)
+    got_k, got_v, got = model.attn_inplace(q, k, v, kc, vc, 1, P, write_rel, attend_rel)
+    assert got_k is kc and got_v is vc  # written in place, returned as aliases
+    np.testing.assert_array_equal(kc, want_k)
+    np.testing.assert_array_equal(vc, want_v)
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-6)
+
+
+def test_attn_callback_errors(tiny32):
+    cfg, _, model = tiny32
+    k = np.zeros((1, 8, cfg.num_key_value_heads, cfg.head_dim), np.float32)
+    q = np.zeros((1, 8, cfg.num_attention_heads, cfg.head_dim), np.float32)
+    kc = np.zeros((cfg.num_hidden_layers, 1, 32, cfg.num_key_value_heads, cfg.head_dim), np.float32)
+    vc = kc.copy()
+    # the reference's messages (runtime.py:56-57, 69-70)
+    with pytest.raises(ValueError, match=r"^KV write \[20, 28\) past the attended rows \[0, 24\)$"):
+        model.attn_inplace(q, k, k, kc, vc, 0, 16, 4, 8)
+    with pytest.raises(ValueError, match=r"^KV write \[28, 36\) outside cache capacity 32$"):
+        model.attn_inplace(q, k, k, kc, vc, 0, 24, 4, 12)
+    with pytest.raises(ValueError, match=r"^KV write \[-2, 6\) outside cache capacity 32$"):
+        model.kv_write(k, k, kc, vc, 0, -2)
+    assert not kc.any()
+
+
 def test_shift_and_block_bias_closed_forms():
     bias = build_prefix_block_attention_bias(0, 96, block_size=32)[0, 0]
     q, k = np.meshgrid(np.arange(96), np.arange(96), indexing="ij")
