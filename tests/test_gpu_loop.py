@@ -179,6 +179,42 @@ def test_fused_confidence_unmask_equals_confidence(small_pair):
         np.testing.assert_array_equal(blk.cpu().numpy(), want)
 
 
+def test_fused_unmask_without_confidence_outputs(small_pair):
+    """Without the ids / maxp outputs the fused kernel combines only the rows the rule reads (the shifted
+    sub-block and, for the report, the last row): the block update and the report equal the rule applied
+    to the full confidence, including the report-only call (sub 0)."""
+    _lib, rt = _rt()
+    _, vm = small_pair
+    torch.manual_seed(4)
+    thr = rt.threshold_f32(THR)
+    bd = 32
+    for rows, row0, s0, sub in [(32, 0, 0, 8), (32, 8, 8, 8), (32, 24, 24, 8), (8, 0, 16, 8), (32, 5, 3, 20),
+                                (32, 0, 0, 0), (8, 0, 0, 0)]:
+        log(f"case: fused unmask rows={rows} row0={row0} s0={s0} sub={sub}")
+        hidden = (torch.randn((1, rows, 256)) * 2).to(torch.bfloat16).cuda()
+        ids_u, p_u = vm.get_confidence(hidden)
+        ids_h, p_h = ids_u.cpu().numpy()[0], p_u.cpu().numpy()[0]
+        blk = torch.full((bd,), 999, dtype=torch.int32, device="cuda")
+        blk[::3] = 5
+        blk0 = blk.cpu().numpy()
+        rep = torch.zeros(4 + bd + 2 * sub + 4, dtype=torch.int32, device="cuda")
+        _lib.check(vm.lib.fdllm_get_confidence_unmask(vm.ctx, hidden.data_ptr(), rows, row0, blk.data_ptr(), s0, sub,
+                                                      999, thr, None, None, rep.data_ptr(), 7, _stream()))
+        torch.cuda.synchronize()
+        if sub:
+            want, sel, masked, _ = _expected(ids_h, p_h, blk0, row0, s0, sub, 999)
+        else:
+            want, sel, masked = blk0, np.zeros(0, bool), np.zeros(0, bool)
+        np.testing.assert_array_equal(blk.cpu().numpy(), want)
+        r = rep.cpu().numpy()
+        assert r[0] == 7 and r[3] == ids_h[rows - 1]
+        np.testing.assert_array_equal(r[4:4 + bd], want)
+        src = [max(row0 + j - 1, 0) for j in range(sub)]
+        np.testing.assert_array_equal(r[4 + bd:4 + bd + sub], ids_h[src])
+        np.testing.assert_array_equal(r[4 + bd + sub:4 + bd + 2 * sub], p_h[src].view(np.int32))
+        assert r[2] == int(sel.sum()) and r[1] == int((masked & ~sel).sum())
+
+
 def _check_decisions(decisions):
     """Every cached decision is fd_unmask of that step's own fp32 probabilities (bit-exact given the
     logits); a stateless one (runtime.py:806-837) unmasks the masked rows whose float64 probability
