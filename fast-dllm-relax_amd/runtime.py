@@ -238,6 +238,7 @@ class DeviceBlock:
         self._host, self._dev = host, dev
         self.rep = np.ctypeslib.as_array(ctypes.cast(host, ctypes.POINTER(ctypes.c_int32)), shape=(self.words,))
         self.seq = int(self.rep[0])
+        self._pre = None  # the block's rows embedded after the last update (see unmask)
 
     def close(self) -> None:
         if self._host is not None:
@@ -258,8 +259,12 @@ class DeviceBlock:
         if len(vals) != self.buf.numel():
             raise ValueError(f"block of {len(ids)} ids, expected {self.bd}")
         self.buf.copy_(torch.tensor(vals, dtype=torch.int32).pin_memory(), non_blocking=True)
+        self._pre = None
 
     def _embed(self, start: int, rows: int) -> torch.Tensor:
+        pre = self._pre
+        if pre is not None:
+            return pre[start:start + rows][None]
         return self.vm.embed_unchecked(self.block[start:start + rows])[None]
 
     def forward_full(self, cache: PrefixCache) -> torch.Tensor:
@@ -285,6 +290,10 @@ class DeviceBlock:
         self._lib.check(self.lib.fdllm_get_confidence_unmask(
             self.vm.ctx, _ptr(hidden), rows, row0, _ptr(self.block), s0, sub, self.mask_id, self.thr, None, None,
             self._dev, seq, _stream()))
+        # the next step of this block embeds rows of the block as this update leaves it: embedding all of
+        # them now, behind the update on the stream, takes the embed launch off the host's path between
+        # two model calls (the next call slices its rows from this buffer; load() drops it)
+        self._pre = self.vm.embed_unchecked(self.block) if sub > 0 else None
         rep = self.rep
         if rep[0] != seq:
             deadline = time.perf_counter() + self.REPORT_TIMEOUT_S
@@ -515,7 +524,8 @@ def relax_greedy_generate(vm: HipVM, prompt_token_ids, *, max_new_tokens: int, b
                     x_t[a0:a0 + block_size] = rep.block
                     rows = rep.selected
                     unmask_updates += len(rows)
-                    log("partial" if use_partial else "full", s0, tuple(rows), tuple(rep.ids[r] for r in rows))
+                    if trace is not None:
+                        log("partial" if use_partial else "full", s0, tuple(rows), tuple(rep.ids[r] for r in rows))
                     if decisions is not None:
                         decisions.append({"kind": "partial" if use_partial else "full", "s0": s0,
                                           "masked": rep.masked, "probs": rep.probs, "ids": rep.ids,
