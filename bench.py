@@ -85,11 +85,14 @@ def main() -> int:
     ap.add_argument("--no-prefix512", action="store_true")
     ap.add_argument("--no-long-context", action="store_true")
     ap.add_argument("--cpu-iters", type=int, default=5)
-    ap.add_argument("--profile-target", choices=("batched", "prefill8192", "decode"),
+    ap.add_argument("--profile-target", choices=("batched", "prefill8192", "decode", "decode-gaps"),
                     help="only run a short workload for rocprofv3: 'batched' = config 4's 512-row and 128-row "
                          "batched steps (5 each), 'prefill8192' = two 8192-row prefills, 'decode' = config 3's "
                          "decode loop (one warm-up and one timed generation of --new-tokens after the prompt; "
-                         "--host-loop runs the loop with the host-side unmask instead of the device one)")
+                         "--host-loop runs the loop with the host-side unmask instead of the device one); "
+                         "'decode-gaps' runs three generations without a profiler and prints the GPU time between "
+                         "model calls, from events recorded after each call's last launch and before the next "
+                         "call's first (device loop only)")
     ap.add_argument("--host-loop", action="store_true",
                     help="decode with the host-side unmask (a readback per step) instead of the device loop")
     ap.add_argument("--trace-gaps", metavar="KERNEL_TRACE_CSV",
@@ -482,6 +485,9 @@ def profile_target(which: str, args) -> int:
             log(f"profile target: generation {i + 1}/2 done ({len(out)} tokens, {stats['block_recomputes']} calls)")
         return 0
 
+    if which == "decode-gaps":
+        return decode_gap_events(args)
+
     if which == "prefill8192":
         cfg = fast_dllm_v2_1p5b()
         vm = HipVM(cfg, random_params_torch(cfg, 4, dtype="bfloat16", device="cuda"), dtype="bfloat16", max_rows=8192)
@@ -515,14 +521,75 @@ def profile_target(which: str, args) -> int:
     return 0
 
 
+def decode_gap_events(args) -> int:
+    """GPU time between the decode loop's model calls without a profiler: the C ABI calls of the device
+    loop go through a wrapper that records an event on the stream right after each call's fused
+    confidence + unmask launch and right before the next call's first launch.  The time between the two
+    events is the GPU's idle time plus what the stream runs in between (the embedding of the next rows),
+    and the events' own recording adds about a microsecond."""
+    import numpy as np
+    import torch
+
+    from fast_dllm_relax_amd.config import DEFAULT_MASK_ID, fast_dllm_v2_1p5b
+    from fast_dllm_relax_amd.params import random_params_torch
+    from fast_dllm_relax_amd.runtime import relax_greedy_generate
+    from fast_dllm_relax_amd.vm import HipVM
+
+    cfg = fast_dllm_v2_1p5b(tie_word_embeddings=False)
+    params = random_params_torch(cfg, SEED, dtype="bfloat16", device="cuda", std=0.02, lm_head_std=0.5)
+    vm = HipVM(cfg, params, dtype="bfloat16", max_rows=args.prefix)
+    prompt = np.random.default_rng(SEED).integers(0, 150000, args.prefix).tolist()
+    lib, marks = vm.lib, []
+
+    def mark(kind):
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        marks.append((kind, e))
+
+    class Marked:
+        def __getattr__(self, name):
+            return getattr(lib, name)
+
+        def fdllm_get_confidence_unmask(self, *a):
+            rc = lib.fdllm_get_confidence_unmask(*a)
+            mark("end")
+            return rc
+
+        def fdllm_forward_cached(self, *a):
+            mark("start")
+            return lib.fdllm_forward_cached(*a)
+
+        def fdllm_forward_block_partial(self, *a):
+            mark("start")
+            return lib.fdllm_forward_block_partial(*a)
+
+    vm.lib = Marked()
+    res = []
+    for i in range(3):
+        marks.clear()
+        _, stats = relax_greedy_generate(vm, prompt, max_new_tokens=args.new_tokens, block_size=32,
+                                         small_block_size=8, threshold=0.9, mask_id=DEFAULT_MASK_ID, stop_token=None)
+        torch.cuda.synchronize()
+        gaps = sorted(e1.elapsed_time(e2) * 1e3 for (k1, e1), (k2, e2) in zip(marks, marks[1:])
+                      if k1 == "end" and k2 == "start")
+        q = lambda v, f: v[min(len(v) - 1, int(f * len(v)))]  # noqa: E731
+        res.append({"generation": i, "calls": stats["block_recomputes"], "gaps": len(gaps),
+                    "gap_us_median": round(statistics.median(gaps), 1), "gap_us_p10": round(q(gaps, 0.1), 1),
+                    "gap_us_p90": round(q(gaps, 0.9), 1), "gap_ms_sum": round(sum(gaps) / 1e3, 3)})
+        log(json.dumps(res[-1]))
+    print(json.dumps({"decode_gaps": res}))
+    return 0
+
+
 def trace_gaps(path: str) -> int:
     """GPU idle time between model calls of the decode loop, from a rocprofv3 kernel trace (csv).
 
-    A model call starts with its embedding gather (embed_kernel) and ends with the confidence reduction
-    (confidence_unmask_kernel on the device loop, confidence_combine_kernel on the host loop).  The gap
-    is the time from the end of one call's last kernel to the start of the next call's first, over the
-    calls of the last generation in the trace (the loop's steady state); it holds whatever the host
-    does in between (readback, unmask, uploads, launch of the next call)."""
+    A model call starts with its first layer-loop kernel (load_rows_kernel) and ends with the confidence
+    reduction (confidence_unmask_kernel on the device loop, confidence_combine_kernel on the host loop).
+    The gap is the time from the end of one call's last kernel to the start of the next call's first,
+    over the calls of the last generation in the trace (the loop's steady state); it holds whatever the
+    host does in between (readback, unmask, uploads, the embedding of the next rows, the launch of the
+    next call)."""
     import csv
 
     rows = []
@@ -532,7 +599,7 @@ def trace_gaps(path: str) -> int:
     rows.sort()
     calls, cur = [], None
     for s, e, n in rows:
-        if "embed_kernel" in n:
+        if "load_rows_kernel" in n:
             cur = [s, None, 0]
         if cur is None:
             continue
