@@ -191,6 +191,21 @@ def main() -> int:
     bytes_r32 = cfg.step_bytes(32, P)
     bytes_r8 = cfg.step_bytes(8, P)
 
+    # ---- the attention callback alone (fdllm_attn_inplace): one call per layer over the same cache,
+    # with rotated queries and the block's K/V rows of a refinement step ---------------------------------
+    q_cb = torch.randn((1, 32, cfg.num_attention_heads, cfg.head_dim), device="cuda").to(torch.bfloat16)
+    kv_cb = torch.randn((1, 32, cfg.num_key_value_heads, cfg.head_dim), device="cuda").to(torch.bfloat16)
+    o_cb = vm.attn_inplace(q_cb, kv_cb, kv_cb, cache.k, cache.v, 0, P, 0, 32)[2]  # checked once, then raw calls
+    cb_args = (q_cb.data_ptr(), kv_cb.data_ptr(), kv_cb.data_ptr(), 32, cache.k.data_ptr(), cache.v.data_ptr(),
+               cache.capacity)
+    cb_stream = torch.cuda.current_stream().cuda_stream
+
+    def attn_layers():
+        for layer in range(cfg.num_hidden_layers):
+            _lib.check(vm.lib.fdllm_attn_inplace(vm.ctx, *cb_args, layer, P, 0, 32, o_cb.data_ptr(), cb_stream))
+
+    attn_cb_us = event_ms(attn_layers, 10) / cfg.num_hidden_layers * 1e3
+
     # ---- dominant kernel alone (gate_up + SiLU), events on the launch stream ------------------------
     stream = torch.cuda.current_stream().cuda_stream
     lib = vm.lib
@@ -257,6 +272,9 @@ def main() -> int:
                      "step_traffic": step_traffic,
                      "step_traffic_ratio": round(step_traffic / bytes_r32, 4) if step_traffic else None,
                      "step_counter_gbps": round(step_traffic / (refine_ms * 1e-3) / 1e9, 1) if step_traffic else None},
+        "attention_callback": {"workload": f"fdllm_attn_inplace (fast_dllm.attn_inplace): 32 rotated query rows, "
+                                           f"K/V rows written at {P}, attention over {P + 32} keys, one call per "
+                                           f"layer", "us_per_call": round(attn_cb_us, 2)},
         "cpu_baseline": cpu,
         "prefix512": prefix512,
         "long_context": long_context,
