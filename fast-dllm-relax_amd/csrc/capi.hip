@@ -979,8 +979,13 @@ static int write_kv_rows(const fdllm_ctx* c, const void* k, const void* v, int r
   if (rows == 0) return FDLLM_OK;
   const size_t row = (size_t)c->cfg.num_key_value_heads * c->cfg.head_dim;
   const size_t off = ((size_t)layer * cap + (size_t)start) * row, bytes = (size_t)rows * row * sizeof(uint16_t);
-  HIPCHK(hipMemcpyAsync((uint16_t*)kc + off, k, bytes, hipMemcpyDeviceToDevice, st));
-  HIPCHK(hipMemcpyAsync((uint16_t*)vc + off, v, bytes, hipMemcpyDeviceToDevice, st));
+  uint16_t *kd = (uint16_t*)kc + off, *vd = (uint16_t*)vc + off;
+  if (((uintptr_t)k | (uintptr_t)v | (uintptr_t)kd | (uintptr_t)vd | bytes) % 16 == 0 && bytes / 16 <= INT32_MAX) {
+    HIPCHK(launch_kv_copy(k, v, kd, vd, bytes, st));  // one launch for both
+  } else {
+    HIPCHK(hipMemcpyAsync(kd, k, bytes, hipMemcpyDeviceToDevice, st));
+    HIPCHK(hipMemcpyAsync(vd, v, bytes, hipMemcpyDeviceToDevice, st));
+  }
   return FDLLM_OK;
 }
 

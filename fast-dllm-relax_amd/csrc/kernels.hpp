@@ -179,6 +179,8 @@ hipError_t launch_confidence_unmask(const float* sm, const int32_t* sa, const fl
 hipError_t launch_unmask(const int32_t* ids, const float* maxp, const UnmaskP& u, hipStream_t st);
 
 // ---- row kernels --------------------------------------------------------------------------------
+// k and v (bytes each, 16-byte multiples at 16-byte aligned addresses) copied to kd and vd in one launch
+hipError_t launch_kv_copy(const void* k, const void* v, void* kd, void* vd, size_t bytes, hipStream_t st);
 hipError_t launch_embed(const int32_t* ids, int n, const uint16_t* table, int vocab, int hidden, uint16_t* out,
                         hipStream_t st);
 // copy the input rows into the residual stream and emit their per-16-column sums of squares; hfrag: h

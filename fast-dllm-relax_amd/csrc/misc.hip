@@ -206,6 +206,25 @@ __global__ __launch_bounds__(64) void rope_table_kernel(const int32_t* pos_offse
   tab[((size_t)r * 64 + i) * 2 + 1] = rnd<DT>(sinf(fr));
 }
 
+// The cache write of fast_dllm.kv_write / attn_inplace (_write_rows, fast_dllm_relax/runtime.py:51-60):
+// the k and v rows into their cache windows in one launch, 16 bytes per thread and tensor (a copy: the
+// bytes are the caller's).  The host takes this path when every pointer and the size are 16-byte
+// multiples.
+__global__ __launch_bounds__(256) void kv_copy_kernel(const u32x4* k, const u32x4* v, u32x4* kd, u32x4* vd, int n16) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n16) {
+    kd[i] = k[i];
+    vd[i] = v[i];
+  }
+}
+
+hipError_t launch_kv_copy(const void* k, const void* v, void* kd, void* vd, size_t bytes, hipStream_t st) {
+  const int n16 = (int)(bytes / 16);
+  hipLaunchKernelGGL(kv_copy_kernel, dim3((n16 + 255) / 256), dim3(256), 0, st, (const u32x4*)k, (const u32x4*)v,
+                     (u32x4*)kd, (u32x4*)vd, n16);
+  return hipGetLastError();
+}
+
 hipError_t launch_embed(const int32_t* ids, int n, const uint16_t* table, int vocab, int hidden, uint16_t* out,
                         hipStream_t st) {
   hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, st, ids, table, vocab, hidden, out);

@@ -106,6 +106,15 @@ def test_kv_write_byte_exact_and_errors(heads12):
     ref.kv_write(k, v, kc, vc, 1, 50)
     np.testing.assert_array_equal(to_np(dvc), vc)
     np.testing.assert_array_equal(np.isnan(to_np(dkc)), np.isnan(kc))
+    log("case: kv_write from rows that are not 16-byte aligned (the two-copy path)")
+    flat = torch.zeros(13 * 2 * 128 + 8, dtype=torch.bfloat16, device="cuda")
+    ku = flat[1:1 + 13 * 2 * 128].view(1, 13, 2, 128)
+    ku.copy_(dk)
+    assert ku.data_ptr() % 16 != 0
+    vm.kv_write(ku, dv, dkc, dvc, 0, 20)
+    assert torch.equal(dkc[0, 0, 20:33].reshape(13, -1).view(torch.int16), bits_k[0].reshape(13, -1))
+    assert torch.equal(dvc[0, 0, 20:33], dv[0])
+    want_k = dkc.clone()
     log("case: window errors")
     with pytest.raises(ValueError, match=r"KV write \[70, 83\) outside cache capacity 80"):
         vm.kv_write(dk, dv, dkc, dvc, 0, 70)
