@@ -361,13 +361,15 @@ def long_context_bench() -> dict:
     def score():
         logits, _ = score_masked_continuation(vm, prefix, cont, block_size=32, mask_id=DEFAULT_MASK_ID,
                                               cached_prefix=(prefix, cache))
-        x = torch.from_numpy(logits).double()
+        # the reference's reduction (runners.py:876-880): fp32 log-softmax of the host logits, then a gather
+        x = torch.from_numpy(np.asarray(logits, dtype=np.float32))
         return torch.log_softmax(x, dim=-1)[torch.arange(C), torch.tensor(cont)].numpy()
 
     score()  # warm-up
     logprobs, score_s = timed(score, 5)
     res = {"workload": f"BASELINE config 5: 1.5B bf16, seed 4, prefix {P} via build_prefix_cache, {C}-token "
-                       "continuation scored by score_masked_continuation + log-softmax",
+                       "continuation scored by score_masked_continuation + the fp32 log-softmax and gather of "
+                       "runners.py:876-880",
            "prefill_ms": round(prefill_s * 1e3, 2), "prefill_tokens_per_s": round(P / prefill_s, 1),
            "scoring_ms": round(score_s * 1e3, 3), "loglikelihood": round(float(logprobs.sum()), 4)}
     log(f"long_context: scoring {score_s * 1e3:.2f} ms")
