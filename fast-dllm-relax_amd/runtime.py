@@ -730,6 +730,8 @@ def relax_batched_block_refine(vm: HipVM, prompts, *, mask_id: int, block_size: 
     for b in range(nseq):
         vm.build_prefix_cache_seq(_embed(vm, xs[b][:a0s[b]]), None, k, v, b)
     off_full = torch.tensor(a0s, dtype=torch.int32, device=dev)
+    # the partial steps' RoPE offsets, uploaded once (one host-to-device copy per step otherwise)
+    off_part = {s0: off_full + s0 for s0 in range(0, block_size, small_block_size)}
     if timing is not None:
         torch.cuda.synchronize()
         timing["prefill_s"] = time.perf_counter() - t0
@@ -746,8 +748,7 @@ def relax_batched_block_refine(vm: HipVM, prompts, *, mask_id: int, block_size: 
             if use_partial:
                 ids = [t for x, a0 in zip(xs, a0s) for t in x[a0 + s0:a0 + s1]]
                 emb = _embed(vm, ids).view(nseq, s1 - s0, -1)
-                off = torch.tensor([a0 + s0 for a0 in a0s], dtype=torch.int32, device=dev)
-                hidden = vm.forward_block_partial_batch(s0, emb, k, v, off, a0s)
+                hidden = vm.forward_block_partial_batch(s0, emb, k, v, off_part[s0], a0s)
                 partial_steps += 1
                 sids, sprobs = batched_shifted_confidence(vm, hidden)
             else:
