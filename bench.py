@@ -774,8 +774,8 @@ def measured_traffic():
 
 def hf_reference_model(cfg, params, dtype):
     """transformers' Qwen2ForCausalLM built from a Qwen2Config (no download) with the weights of ``params``
-    (host tensors in the packed parameter order), q/k/v and gate/up split back out of the fused tensors
-    (the "HF reference forward").  Constructed on the meta device and then given the
+    (host tensors in the packed parameter order), q/k/v and gate/up split back out of the fused tensors:
+    the reference model's HF counterpart on the host.  Constructed on the meta device and then given the
     weights, so no random initialisation is spent on 1.5B parameters."""
     import torch
     from transformers import Qwen2Config, Qwen2ForCausalLM
@@ -844,7 +844,7 @@ def hf_cached_step(model, k_prefix, v_prefix, block_ids, P):
 
 
 def cpu_baseline(vm, params, cache, block, P, iters, tokens_per_call):
-    """The CPU baseline of BASELINE.md section 3, on the same weights and KV-cache prefix as the GPU run,
+    """The CPU baseline: the reference model's step on the host, on the same weights and KV-cache prefix as the GPU run,
     all host cores: the HF reference forward (transformers' Qwen2, one 32-row cached forward + lm_head
     against the P-row prefix) in bf16 and fp32, and this build's numpy oracle for the same step.  Medians
     of ``iters`` (>= 5) after one warm-up each; tokens/s uses the GPU loop's tokens per model call."""
@@ -904,7 +904,7 @@ def cpu_baseline(vm, params, cache, block, P, iters, tokens_per_call):
             "value_fp32": round(tokens_per_call / res["fp32"], 3),
             "port_step_s": round(port_s, 4), "port_value": round(tokens_per_call / port_s, 3), "port_cores": int(blas),
             "host_cpus": os.cpu_count(),
-            "sample": f"HF reference forward (BASELINE.md section 3): transformers {_hf_version()} Qwen2ForCausalLM "
+            "sample": f"HF reference forward: transformers {_hf_version()} Qwen2ForCausalLM "
                       f"from a Qwen2Config with the bench weights, one 32-row cached forward + lm_head against a "
                       f"{P}-row DynamicCache (the GPU-built prefix), torch threads = {threads}; median of {iters} "
                       f"after 1 warm-up, bf16 (value) and fp32; tokens/s = {tokens_per_call:.3f} tokens per model "
